@@ -1,0 +1,250 @@
+// common.hpp -- device helpers shared by the gfx950 kernels of liblux3d_fused:
+// dtype traits with 16-byte vector I/O, f32<->bf16/f16 conversions, and
+// wavefront reductions built on DPP and the gfx950 permlane swaps.
+//
+// Element I/O model: every kernel moves "chunks" of 8 consecutive elements
+// per lane (one 16-byte load for bf16/f16, two for f32), so a wavefront's
+// load instruction covers a contiguous 1 KiB (2-byte types) or 2 KiB (f32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lux3d_fused.h"
+
+namespace lux3d {
+
+// ---------------------------------------------------------------------------
+// Scalar conversions
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t v) { return __uint_as_float(v << 16); }
+
+// f32 -> bf16, round-to-nearest-even; NaN keeps sign and top payload bits and
+// is forced quiet. Bit-identical to half::bf16::from_f32 (used where results
+// must be bit-exact: Q8_0 dequant).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits_exact(float f) {
+  uint32_t x = __float_as_uint(f);
+  uint32_t r = (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+  return ((x & 0x7FFFFFFFu) > 0x7F800000u) ? ((x >> 16) | 0x40u) : r;
+}
+
+// Two f32 -> packed bf16x2 with the gfx950 hardware convert (v_cvt_pk_bf16_f32,
+// round-to-nearest-even). Identical to the exact conversion for every non-NaN
+// input.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  f32x2_t v = {lo, hi};
+  bf16x2_t r = __builtin_convertvector(v, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  f32x2_t v = {lo, hi};
+  f16x2_t r = __builtin_convertvector(v, f16x2_t);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+}
+
+// ---------------------------------------------------------------------------
+// dtype tags and 8-element chunk I/O
+// ---------------------------------------------------------------------------
+
+struct F32 { static constexpr int code = LUX3D_F32; static constexpr int bytes = 4; };
+struct BF16 { static constexpr int code = LUX3D_BF16; static constexpr int bytes = 2; };
+struct F16 { static constexpr int code = LUX3D_F16; static constexpr int bytes = 2; };
+
+template <typename T> struct Chunk;
+
+template <> struct Chunk<BF16> {
+  __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
+    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+  __device__ __forceinline__ static void store(void *p, const float (&v)[8]) {
+    uint4 u;
+    u.x = pack_bf16x2(v[0], v[1]);
+    u.y = pack_bf16x2(v[2], v[3]);
+    u.z = pack_bf16x2(v[4], v[5]);
+    u.w = pack_bf16x2(v[6], v[7]);
+    *reinterpret_cast<uint4 *>(p) = u;
+  }
+  // value as it reads back after a store (for outputs that are re-read)
+  __device__ __forceinline__ static float round_trip(float f) {
+    return __uint_as_float(pack_bf16x2(f, 0.f) << 16);
+  }
+};
+
+template <> struct Chunk<F16> {
+  __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
+    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+      v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  }
+  __device__ __forceinline__ static void store(void *p, const float (&v)[8]) {
+    uint4 u;
+    u.x = pack_f16x2(v[0], v[1]);
+    u.y = pack_f16x2(v[2], v[3]);
+    u.z = pack_f16x2(v[4], v[5]);
+    u.w = pack_f16x2(v[6], v[7]);
+    *reinterpret_cast<uint4 *>(p) = u;
+  }
+  __device__ __forceinline__ static float round_trip(float f) {
+    return f16_bits_to_f32(pack_f16x2(f, 0.f) & 0xFFFFu);
+  }
+};
+
+template <> struct Chunk<F32> {
+  __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+    float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ __forceinline__ static void store(void *p, const float (&v)[8]) {
+    float4 *q = reinterpret_cast<float4 *>(p);
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  __device__ __forceinline__ static float round_trip(float f) { return f; }
+};
+
+// Scalar element access for the unaligned / odd-size fallback kernels.
+template <typename T> __device__ __forceinline__ float load1(const void *p, int64_t i);
+template <> __device__ __forceinline__ float load1<F32>(const void *p, int64_t i) {
+  return reinterpret_cast<const float *>(p)[i];
+}
+template <> __device__ __forceinline__ float load1<BF16>(const void *p, int64_t i) {
+  return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+}
+template <> __device__ __forceinline__ float load1<F16>(const void *p, int64_t i) {
+  return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+}
+template <typename T> __device__ __forceinline__ void store1(void *p, int64_t i, float v);
+template <> __device__ __forceinline__ void store1<F32>(void *p, int64_t i, float v) {
+  reinterpret_cast<float *>(p)[i] = v;
+}
+template <> __device__ __forceinline__ void store1<BF16>(void *p, int64_t i, float v) {
+  reinterpret_cast<uint16_t *>(p)[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+}
+template <> __device__ __forceinline__ void store1<F16>(void *p, int64_t i, float v) {
+  reinterpret_cast<uint16_t *>(p)[i] = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
+}
+
+// Per-channel parameters of any supported float dtype (runtime code, uniform
+// across the wavefront). `dt < 0` means "absent" and yields `dflt`.
+__device__ __forceinline__ float param1(const void *p, int dt, int64_t i, float dflt) {
+  if (dt == LUX3D_F32) return reinterpret_cast<const float *>(p)[i];
+  if (dt == LUX3D_BF16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+  if (dt == LUX3D_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+  return dflt;
+}
+
+// 8 consecutive parameters starting at element i (i a multiple of 8 and the
+// base 16-byte aligned: checked on the host before a vector kernel is chosen).
+__device__ __forceinline__ void param8(const void *p, int dt, int64_t i, float dflt, float (&v)[8]) {
+  if (dt == LUX3D_F32) {
+    Chunk<F32>::load(reinterpret_cast<const float *>(p) + i, v);
+  } else if (dt == LUX3D_BF16) {
+    Chunk<BF16>::load(reinterpret_cast<const uint16_t *>(p) + i, v);
+  } else if (dt == LUX3D_F16) {
+    Chunk<F16>::load(reinterpret_cast<const uint16_t *>(p) + i, v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = dflt;
+  }
+}
+
+template <typename T> __device__ __forceinline__ const char *cptr(const void *p) {
+  return reinterpret_cast<const char *>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane exchange and reductions (wave64, gfx950)
+// ---------------------------------------------------------------------------
+
+// DPP controls: quad_perm [1,0,3,2] = xor 1, quad_perm [2,3,0,1] = xor 2,
+// row_half_mirror (lane i of 8 <- 7-i), row_mirror (lane i of 16 <- 15-i).
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of 8 / 16 lanes. Every lane of a group ends with
+// the bit-identical total (each step adds two equal-valued halves).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  return v;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+  v = group8_sum(v);
+  v += dpp<DPP_MIRROR>(v);
+  return v;
+}
+// Whole-wave sum: 16-lane rows are combined with v_permlane16_swap (rows
+// 0<->1, 2<->3) and v_permlane32_swap (lanes 0-31 <-> 32-63).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group16_sum(v);
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  return v;
+}
+
+template <int LANES> __device__ __forceinline__ float group_sum(float v) {
+  static_assert(LANES == 8 || LANES == 16 || LANES == 64, "group size");
+  if constexpr (LANES == 8) return group8_sum(v);
+  else if constexpr (LANES == 16) return group16_sum(v);
+  else return wave_sum(v);
+}
+
+// Value held by lane (lane ^ M).
+template <int M> __device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 1) return dpp<DPP_XOR1>(v);
+  else if constexpr (M == 2) return dpp<DPP_XOR2>(v);
+  else return __shfl_xor(v, M, 64);
+}
+
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Segment of row r given int64 offsets [nseg+1] (largest s with off[s] <= r),
+// or equal segments of `rows_per_seg` rows when `off` is NULL. Always returns
+// a value in [0, nseg-1], whatever the offsets hold.
+__device__ __forceinline__ int64_t segment_of(const int64_t *off, int64_t nseg, int64_t rows_per_seg,
+                                              int64_t r) {
+  if (!off) {
+    int64_t s = r / rows_per_seg;
+    return s < nseg ? s : nseg - 1;
+  }
+  int64_t lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    int64_t mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace lux3d

@@ -1,0 +1,97 @@
+// kernels.hpp -- host-side launch interface between the C ABI (abi.cpp) and
+// the gfx950 kernels. Everything here is internal to liblux3d_fused.so: the
+// ABI validates descriptors, resolves strides and dtypes, fills one of these
+// parameter blocks and calls the launcher, which picks the kernel variant.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace lux3d {
+
+// ---- row family: LayerNorm / residual+LayerNorm / AdaLN modulate / gate ----
+enum RowMode : int { ROW_LN = 0, ROW_RESID_LN = 1, ROW_MODULATE = 2, ROW_GATE = 3 };
+
+// A modulation piece p[s, c] (+ base[c]); dt < 0 when absent.
+struct ModPiece {
+  const void *p = nullptr;
+  int64_t ld = 0;
+  int dt = -1;
+  const void *base = nullptr;
+  int base_dt = -1;
+};
+
+struct RowParams {
+  const void *x = nullptr;  int64_t x_rs = 0;   // input rows
+  const void *a = nullptr;  int64_t a_rs = 0;   // residual branch (RESID) or h (GATE)
+  void *h = nullptr;        int64_t h_rs = 0;   // RESID: stored residual stream
+  void *y = nullptr;        int64_t y_rs = 0;   // output rows
+  int64_t rows = 0, d = 0;
+  float eps = 0.f;
+  const void *w = nullptr; int w_dt = -1;       // LN weight
+  const void *b = nullptr; int b_dt = -1;       // LN bias
+  const void *g = nullptr; int g_dt = -1;       // LayerScale gamma
+  const int64_t *seg_off = nullptr;             // [nseg+1] or NULL
+  int64_t nseg = 1, rows_per_seg = 1;
+  ModPiece shift, scale, gate;
+};
+
+// Returns hipSuccess or the launch error. `vec` selects the 16-byte vector
+// kernels (the caller has checked alignment and d % 8 == 0).
+hipError_t launch_rows(int mode, int dt, const RowParams &p, bool vec, hipStream_t s);
+
+// ---- head family: per-head norm + rotary on [B, H, N, D] views ------------
+enum HeadNorm : int { HN_NONE = 0, HN_LN = 1, HN_RMS = 2, HN_L2 = 3 };
+enum HeadRot : int {
+  HR_NONE = 0,
+  HR_R1_TAB = 1,   // VGGT 2D RoPE, [B, N, D] cos / sin_alt tables
+  HR_R1_POS = 2,   // VGGT 2D RoPE from integer positions [B, N, 2]
+  HR_R2_TAB = 3,   // TRELLIS.2 3D RoPE, [N, D/2] cos / sin tables
+  HR_R2_COORD = 4, // TRELLIS.2 3D RoPE from int32 coords [N, 3]
+  HR_R3_TAB = 5    // DINOv3 2D RoPE, [N - prefix, D] tables, prefix untouched
+};
+
+struct HeadIO {
+  const void *x = nullptr; int64_t sB = 0, sH = 0, sN = 0;  // input view
+  void *y = nullptr;       int64_t oB = 0, oH = 0, oN = 0;  // output view
+  const void *p0 = nullptr; int p0_dt = -1;                 // LN w / RMS w / L2 gamma
+  const void *p1 = nullptr; int p1_dt = -1;                 // LN b
+};
+
+struct HeadParams {
+  HeadIO io[2];
+  int ntens = 1;
+  int64_t B = 0, H = 0, N = 0, D = 0;
+  float eps = 0.f;
+  // rotation source
+  const void *tab_c = nullptr, *tab_s = nullptr; int tab_dt = -1;
+  int64_t tab_sB = 0, tab_sN = 0;               // element (b, n, j) at b*sB + n*sN + j
+  const void *pos = nullptr; int pos_dt = -1;
+  int64_t pos_sB = 0, pos_sN = 0, pos_sC = 0;   // positions/coords element strides
+  float freq[64] = {};
+  int nfreq = 0;
+  int64_t prefix = 0;
+};
+
+hipError_t launch_heads(int norm, int rot, int dt, const HeadParams &p, hipStream_t s);
+
+// ---- table builders ---------------------------------------------------------
+hipError_t launch_rope2d_tables(const void *pos, int pos_dt, int64_t psB, int64_t psN,
+                                int64_t psC, int64_t B, int64_t N, int64_t D,
+                                const float *inv_freq, float *cos_full, float *sin_alt,
+                                hipStream_t s);
+hipError_t launch_rope3d_tables(const int32_t *coords, int64_t csN, int64_t csC, int64_t N,
+                                int64_t half, int64_t fd, const float *freq, float *cos,
+                                float *sin, hipStream_t s);
+
+// ---- elementwise -------------------------------------------------------------
+enum Act : int { ACT_GELU_ERF = 0, ACT_GELU_TANH = 1, ACT_SILU = 2 };
+hipError_t launch_act(int act, int dt, const void *x, void *y, int64_t n, bool vec, hipStream_t s);
+
+hipError_t launch_timestep(const float *t, int64_t n, const float *freqs, int64_t dim,
+                           int cos_first, float neg_log_period, float *out, hipStream_t s);
+
+hipError_t launch_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *y,
+                               bool vec, hipStream_t s);
+
+}  // namespace lux3d

@@ -1,0 +1,250 @@
+// pointwise.hip -- streaming kernels for gfx950: GELU (erf / tanh), SiLU,
+// sinusoidal timestep embeddings and the bit-exact GGML Q8_0 dequant.
+//
+// Activations are pure HBM streams (one read, one write per element). Each
+// thread moves kUnroll chunks of 8 elements; the loads of all chunks are
+// issued before any arithmetic, and consecutive lanes touch consecutive
+// 16-byte chunks, so each wavefront keeps 4 KiB (bf16) in flight. The
+// transcendental work is kept to one exp2 + one reciprocal per element for
+// the tanh GELU and SiLU (hardware v_exp_f32 / v_rcp_f32).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lux3d {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+template <int ACT> __device__ __forceinline__ float act(float x) {
+  if constexpr (ACT == ACT_GELU_TANH) {
+    // 0.5*x*(1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi)*x*(1 + 0.044715*x^2):
+    // the sigmoid form has no cancellation for x << 0.
+    constexpr float k = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2*sqrt(2/pi)*log2(e)
+    const float u = x * (1.0f + 0.044715f * x * x);
+    return x * fast_rcp(1.0f + fast_exp2(k * u));
+  } else if constexpr (ACT == ACT_GELU_ERF) {
+    // 0.5*x*(1 + erf(x/sqrt2)) evaluated through erfc(|x|/sqrt2), which keeps
+    // full relative accuracy in the negative tail (x*Phi(x) -> 0).
+    const float e = erfcf(fabsf(x) * 0.7071067811865476f);
+    const float h = 0.5f * x * e;
+    return x >= 0.f ? x - h : h;
+  } else {
+    constexpr float k = -1.4426950408889634f;  // -log2(e)
+    return x * fast_rcp(1.0f + fast_exp2(k * x));
+  }
+}
+
+template <typename T, int ACT>
+__global__ __launch_bounds__(kBlock) void act_kernel(const void *x, void *y, int64_t nchunks) {
+  constexpr int EB = T::bytes;
+  const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
+  float v[kUnroll][8];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = base + u * kBlock;
+    if (c < nchunks) Chunk<T>::load(reinterpret_cast<const char *>(x) + c * 8 * EB, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = base + u * kBlock;
+    if (c < nchunks) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[u][k] = act<ACT>(v[u][k]);
+      Chunk<T>::store(reinterpret_cast<char *>(y) + c * 8 * EB, v[u]);
+    }
+  }
+}
+
+// Elements [first, n) one per thread (tails and unaligned tensors).
+template <typename T, int ACT>
+__global__ __launch_bounds__(kBlock) void act_kernel_any(const void *x, void *y, int64_t first,
+                                                         int64_t n) {
+  const int64_t i = first + (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) store1<T>(y, i, act<ACT>(load1<T>(x, i)));
+}
+
+template <typename T, int ACT>
+hipError_t launch_act_t(const void *x, void *y, int64_t n, bool vec, hipStream_t s) {
+  int64_t first = 0;
+  if (vec) {
+    const int64_t nchunks = n / 8;
+    if (nchunks > 0) {
+      const int64_t per_block = (int64_t)kBlock * kUnroll;
+      hipLaunchKernelGGL((act_kernel<T, ACT>), dim3((unsigned)((nchunks + per_block - 1) / per_block)),
+                         dim3(kBlock), 0, s, x, y, nchunks);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    first = nchunks * 8;
+  }
+  const int64_t rest = n - first;
+  if (rest > 0) {
+    hipLaunchKernelGGL((act_kernel_any<T, ACT>), dim3((unsigned)((rest + kBlock - 1) / kBlock)),
+                       dim3(kBlock), 0, s, x, y, first, n);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+template <typename T>
+hipError_t launch_act_dt(int a, const void *x, void *y, int64_t n, bool vec, hipStream_t s) {
+  switch (a) {
+    case ACT_GELU_ERF: return launch_act_t<T, ACT_GELU_ERF>(x, y, n, vec, s);
+    case ACT_GELU_TANH: return launch_act_t<T, ACT_GELU_TANH>(x, y, n, vec, s);
+    case ACT_SILU: return launch_act_t<T, ACT_SILU>(x, y, n, vec, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---- timestep embedding ------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void timestep_kernel(const float *t, int64_t n,
+                                                          const float *freqs, int64_t dim,
+                                                          int cos_first, float neg_log_period,
+                                                          float *out) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n * dim) return;
+  const int64_t r = e / dim, j = e % dim;
+  const int64_t half = dim / 2;
+  if (j >= 2 * half) {  // odd dim: zero pad (cos-first convention only)
+    out[e] = 0.f;
+    return;
+  }
+  const int64_t i = j < half ? j : j - half;
+  float f;
+  if (freqs) {
+    f = freqs[i];
+  } else {
+    // exp(-ln(1e4)*i/half): the f32 argument is formed exactly as the
+    // reference does; the exponential is evaluated in f64 and rounded once.
+    const float x = neg_log_period * (float)i / (float)half;
+    f = (float)exp((double)x);
+  }
+  const float arg = t[r] * f;
+  float sv, cv;
+  sincosf(arg, &sv, &cv);
+  const bool first_half = j < half;
+  out[e] = cos_first ? (first_half ? cv : sv) : (first_half ? sv : cv);
+}
+
+// ---- Q8_0 dequant ------------------------------------------------------------
+// Thread g produces output chunk g (8 values): block g/4, quarter g%4. The
+// 34-byte blocks are only 2-byte aligned, so the scale and the 8 quants are
+// read as 16-bit words; the stores are 16-byte (bf16/f16) or 32-byte (f32).
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits_exact(float v) {
+  // IEEE binary16 round-to-nearest-even; NaN quiet with its top payload.
+  const uint32_t x = __float_as_uint(v);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t exp = (x >> 23) & 0xFFu;
+  const uint32_t man = x & 0x7FFFFFu;
+  if (exp == 0xFFu) return sign | 0x7C00u | (man ? (0x0200u | (man >> 13)) : 0u);
+  const int e = (int)exp - 127 + 15;
+  if (e >= 0x1F) return sign | 0x7C00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    const uint32_t m = man | 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    uint32_t hm = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u);
+    const uint32_t halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (hm & 1u))) hm += 1u;
+    return sign | hm;
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rem = man & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+  return h;
+}
+
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void dequant_q8_0_kernel(const uint8_t *blocks, int64_t nchunks,
+                                                              void *y, int vec) {
+  const int64_t g = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (g >= nchunks) return;
+  const int64_t blk = g >> 2;
+  const int q = (int)(g & 3);
+  const uint16_t *w = reinterpret_cast<const uint16_t *>(blocks + blk * 34);
+  const float d = f16_bits_to_f32(w[0]);
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint16_t pair = w[1 + q * 4 + k];
+    v[2 * k] = (float)(int8_t)(pair & 0xFFu) * d;
+    v[2 * k + 1] = (float)(int8_t)(pair >> 8) * d;
+  }
+  if constexpr (OUT == LUX3D_F32) {
+    float *o = reinterpret_cast<float *>(y) + g * 8;
+    if (vec) {
+      Chunk<F32>::store(o, v);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = v[k];
+    }
+  } else {
+    uint32_t hb[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      hb[k] = OUT == LUX3D_BF16 ? f32_to_bf16_bits_exact(v[k]) : f32_to_f16_bits_exact(v[k]);
+    uint16_t *o = reinterpret_cast<uint16_t *>(y) + g * 8;
+    if (vec) {
+      uint4 u;
+      u.x = hb[0] | (hb[1] << 16);
+      u.y = hb[2] | (hb[3] << 16);
+      u.z = hb[4] | (hb[5] << 16);
+      u.w = hb[6] | (hb[7] << 16);
+      *reinterpret_cast<uint4 *>(o) = u;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = (uint16_t)hb[k];
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_act(int a, int dt, const void *x, void *y, int64_t n, bool vec, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  switch (dt) {
+    case LUX3D_F32: return launch_act_dt<F32>(a, x, y, n, vec, s);
+    case LUX3D_BF16: return launch_act_dt<BF16>(a, x, y, n, vec, s);
+    case LUX3D_F16: return launch_act_dt<F16>(a, x, y, n, vec, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_timestep(const float *t, int64_t n, const float *freqs, int64_t dim, int cos_first,
+                           float neg_log_period, float *out, hipStream_t s) {
+  const int64_t total = n * dim;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(timestep_kernel, dim3((unsigned)((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, s,
+                     t, n, freqs, dim, cos_first, neg_log_period, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *y, bool vec,
+                               hipStream_t s) {
+  const int64_t nchunks = nblocks * 4;
+  if (nchunks <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((nchunks + kBlock - 1) / kBlock));
+  switch (out_dt) {
+    case LUX3D_F32:
+      hipLaunchKernelGGL(dequant_q8_0_kernel<LUX3D_F32>, grid, dim3(kBlock), 0, s, blocks, nchunks, y, (int)vec);
+      break;
+    case LUX3D_BF16:
+      hipLaunchKernelGGL(dequant_q8_0_kernel<LUX3D_BF16>, grid, dim3(kBlock), 0, s, blocks, nchunks, y, (int)vec);
+      break;
+    case LUX3D_F16:
+      hipLaunchKernelGGL(dequant_q8_0_kernel<LUX3D_F16>, grid, dim3(kBlock), 0, s, blocks, nchunks, y, (int)vec);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lux3d

@@ -1,0 +1,336 @@
+"""Tensor-level mirror of candle-3d's operator surface on the fused HIP ops.
+
+Each function keeps the name, argument meaning and error behaviour of the
+reference helper or candle op it replaces (cited per function; paths are
+relative to crates/lux3d-core/src/ of the candle-3d tree). Like a candle
+CustomOp, every op borrows its inputs and allocates its outputs; torch tensors
+on a ROCm device are used only as device memory and streams. All arithmetic
+happens in liblux3d_fused.so; invalid arguments raise Lux3dError, exactly as
+the reference's `candle_core::bail!` sites return an error.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16,
+       torch.int32: _lib.I32, torch.int64: _lib.I64, torch.uint8: _lib.U8}
+
+
+def desc(t: Optional[torch.Tensor]):
+    """lux3d_tensor_t pointer for a torch tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if t.dtype not in _DT:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    if t.dim() == 0:
+        t = t.reshape(1)
+    d = _lib.descriptor(t.data_ptr(), _DT[t.dtype], list(t.shape), list(t.stride()))
+    return ctypes.pointer(d)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _keep(*ts):
+    """Descriptors hold raw pointers: keep the tensors alive for the call."""
+    return ts
+
+
+# ---------------------------------------------------------------------------
+# Row family
+# ---------------------------------------------------------------------------
+
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+               eps: float) -> torch.Tensor:
+    """candle_nn::ops::layer_norm(x, w, b, eps) (upstream candle-nn), the op
+    behind every `layer_norm(dim, eps, vb)` LayerNorm::forward in the
+    reference (e.g. runtime/pi3_encoder.rs:67, runtime/vggt.rs:104)."""
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.call("lux3d_layer_norm", desc(x), desc(weight), desc(bias), eps, desc(y), _stream(x))
+    return y
+
+
+def layer_norm_no_affine(xs: torch.Tensor, eps: float) -> torch.Tensor:
+    """layer_norm_no_affine (runtime/trellis2_blocks.rs:280-286)."""
+    return layer_norm(xs, None, None, eps)
+
+
+def residual_layer_norm(x: torch.Tensor, a: torch.Tensor, ls_gamma: Optional[torch.Tensor],
+                        weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float,
+                        h_out: Optional[torch.Tensor] = None):
+    """`h = x + ls(a)`, `y = norm(h)`: LayerScale::forward
+    (runtime/nn_blocks.rs:210-214) + residual + LayerNorm::forward as in
+    VggtBlock::forward (runtime/vggt.rs:113-124). Returns (h, y)."""
+    h = torch.empty(x.shape, dtype=x.dtype, device=x.device) if h_out is None else h_out
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.call("lux3d_residual_layer_norm", desc(x), desc(a), desc(ls_gamma), desc(weight), desc(bias),
+              eps, desc(h), desc(y), _stream(x))
+    return h, y
+
+
+def adaln_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                   gate: Optional[torch.Tensor] = None, *, shift_base=None, scale_base=None,
+                   gate_base=None, seg_offsets: Optional[torch.Tensor] = None,
+                   eps: float = 1e-6) -> torch.Tensor:
+    """`layer_norm_no_affine(x)*(1 + scale) + shift` (optionally
+    `gate*(...) + x`), per batch element or ragged segment:
+    runtime/trellis2_blocks.rs:617-630 (with `modulation + t_emb` via the
+    *_base vectors) and runtime/vggt.rs:399-405 (gate variant)."""
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.call("lux3d_adaln_modulate", desc(x), desc(seg_offsets), desc(shift), desc(shift_base),
+              desc(scale), desc(scale_base), desc(gate), desc(gate_base), eps, desc(y), _stream(x))
+    return y
+
+
+def gated_residual(x: torch.Tensor, h: torch.Tensor, gate: torch.Tensor, *, gate_base=None,
+                   seg_offsets: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """`xs.add(h.broadcast_mul(gate))` (runtime/trellis2_blocks.rs:632-633)."""
+    o = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    _lib.call("lux3d_gated_residual", desc(x), desc(h), desc(seg_offsets), desc(gate), desc(gate_base),
+              desc(o), _stream(x))
+    return o
+
+
+def chunk_modulation(mod_vec: torch.Tensor):
+    """chunk_modulation (runtime/trellis2_blocks.rs:264-277): six [B, 1, C]
+    views (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp)
+    of a [B, 6C] vector, without copies (the fused ops read the views)."""
+    b, c6 = mod_vec.shape
+    if c6 % 6:
+        raise ValueError("adaLN modulation must chunk into 6")
+    return [p.unsqueeze(1) for p in mod_vec.chunk(6, dim=-1)]
+
+
+# ---------------------------------------------------------------------------
+# VGGT / Pi3 2D RoPE (attention_math.rs)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class RopeEmbeddings:
+    """RopeEmbeddings (runtime/attention_math.rs:88-95): cos_full and
+    sin_alt_full, each [b, 1, n, token_dim] f32."""
+
+    cos_full: torch.Tensor
+    sin_alt_full: torch.Tensor
+
+
+class Rope2d:
+    """Rope2d (runtime/attention_math.rs:4-86)."""
+
+    def __init__(self, base: float):
+        self.base = float(base)
+
+    def embeddings(self, positions: torch.Tensor, token_dim: int) -> RopeEmbeddings:
+        half = token_dim // 2
+        if half % 2 != 0:
+            raise _lib.Lux3dError("Rope2d::embeddings", _lib.ERR_VALUE,
+                                  f"rope token_dim must be divisible by 4, got {token_dim}")
+        b, n, _ = positions.shape
+        cos = torch.empty((b, 1, n, token_dim), dtype=torch.float32, device=positions.device)
+        sin = torch.empty_like(cos)
+        _lib.call("lux3d_rope2d_tables", desc(positions), self.base, desc(cos), desc(sin), _stream(cos))
+        return RopeEmbeddings(cos, sin)
+
+
+def _heads_out(q: torch.Tensor) -> torch.Tensor:
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+
+def layernorm_rope_fused(q: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float,
+                         cos_full: torch.Tensor, sin_alt_full: torch.Tensor) -> torch.Tensor:
+    """candle_nn::ops::layernorm_rope_fused (the fork's CustomOp3, routed at
+    runtime/attention_math.rs:139-146): LN(64)+affine then 2D RoPE on a
+    (possibly strided) [b, h, n, d] head view; contiguous output."""
+    out = _heads_out(q)
+    _lib.call("lux3d_qk_layernorm_rope2d", desc(q), desc(weight), desc(bias), None, None, None, eps,
+              desc(cos_full), desc(sin_alt_full), desc(out), None, _stream(q))
+    return out
+
+
+def rope_fused(x: torch.Tensor, cos_full: torch.Tensor, sin_alt_full: torch.Tensor) -> torch.Tensor:
+    """candle_nn::ops::rope_fused (runtime/attention_math.rs:162)."""
+    out = _heads_out(x)
+    _lib.call("lux3d_qk_layernorm_rope2d", desc(x), None, None, None, None, None, 0.0,
+              desc(cos_full), desc(sin_alt_full), desc(out), None, _stream(x))
+    return out
+
+
+def apply_layernorm_rope(q: torch.Tensor, q_norm, embeddings: RopeEmbeddings) -> torch.Tensor:
+    """apply_layernorm_rope (runtime/attention_math.rs:127-150); q_norm is
+    (weight, bias, eps)."""
+    w, b, eps = q_norm
+    return layernorm_rope_fused(q, w, b, eps, embeddings.cos_full, embeddings.sin_alt_full)
+
+
+def apply_rope(tokens: torch.Tensor, embeddings: RopeEmbeddings) -> torch.Tensor:
+    """apply_rope (runtime/attention_math.rs:155-165)."""
+    return rope_fused(tokens, embeddings.cos_full, embeddings.sin_alt_full)
+
+
+def qk_layernorm_rope2d(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm,
+                        embeddings: Optional[RopeEmbeddings] = None, *,
+                        positions: Optional[torch.Tensor] = None, base: float = 100.0):
+    """Both apply_layernorm_rope calls of VggtAttention::forward
+    (runtime/vggt.rs:170-181) in one launch. Rotation from the tables, or,
+    with `positions`, computed in-kernel (no table traffic)."""
+    qw, qb, eps = q_norm
+    kw, kb, _ = k_norm
+    qo, ko = _heads_out(q), _heads_out(k)
+    if positions is not None:
+        _lib.call("lux3d_qk_layernorm_rope2d_pos", desc(q), desc(qw), desc(qb), desc(k), desc(kw), desc(kb),
+                  eps, desc(positions), base, desc(qo), desc(ko), _stream(q))
+    else:
+        _lib.call("lux3d_qk_layernorm_rope2d", desc(q), desc(qw), desc(qb), desc(k), desc(kw), desc(kb),
+                  eps, desc(embeddings.cos_full), desc(embeddings.sin_alt_full), desc(qo), desc(ko),
+                  _stream(q))
+    return qo, ko
+
+
+# ---------------------------------------------------------------------------
+# TripoSG
+# ---------------------------------------------------------------------------
+
+def rms_norm_heads(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                   k: Optional[torch.Tensor] = None, k_weight: Optional[torch.Tensor] = None):
+    """RmsNormHeads::rms_norm_heads (runtime/triposg_dit.rs:509-522) on a
+    [B, H, L, D] head view (strided views accepted: the transpose/contiguous
+    before it is fused). With `k`, both norms run in one launch."""
+    qo = _heads_out(x)
+    ko = _heads_out(k) if k is not None else None
+    _lib.call("lux3d_rms_norm_heads", desc(x), desc(weight), desc(k), desc(k_weight), eps, desc(qo),
+              desc(ko), _stream(x))
+    return qo if k is None else (qo, ko)
+
+
+# ---------------------------------------------------------------------------
+# TRELLIS.2
+# ---------------------------------------------------------------------------
+
+class Trellis2QkRmsNorm:
+    """Trellis2QkRmsNorm (runtime/trellis2_blocks.rs:288-320)."""
+
+    def __init__(self, gamma: torch.Tensor):
+        self.gamma = gamma
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        out = _heads_out(xs)
+        _lib.call("lux3d_qk_l2norm_rope3d", desc(xs), desc(self.gamma), None, None, None, None, None, 0.0,
+                  desc(out), None, _stream(xs))
+        return out
+
+
+class Trellis2Rope3d:
+    """Trellis2Rope3d (runtime/trellis2_blocks.rs:84-161)."""
+
+    def __init__(self, head_dim: int, rope_base: float = 10000.0):
+        self.head_dim = int(head_dim)
+        self.rope_base = float(rope_base)
+
+    def cos_sin(self, coords: torch.Tensor):
+        """coords int32 [L, 3] on the device -> (cos, sin) [L, head_dim/2]."""
+        n = coords.shape[0]
+        cos = torch.empty((n, self.head_dim // 2), dtype=torch.float32, device=coords.device)
+        sin = torch.empty_like(cos)
+        _lib.call("lux3d_rope3d_tables", desc(coords), self.head_dim, self.rope_base, desc(cos), desc(sin),
+                  _stream(cos))
+        return cos, sin
+
+    def apply(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        out = _heads_out(x)
+        _lib.call("lux3d_qk_l2norm_rope3d", desc(x), None, None, None, desc(cos), desc(sin), None, 0.0,
+                  desc(out), None, _stream(x))
+        return out
+
+
+def qk_l2norm_rope3d(q: torch.Tensor, k: torch.Tensor, q_gamma: Optional[torch.Tensor],
+                     k_gamma: Optional[torch.Tensor], *, coords: Optional[torch.Tensor] = None,
+                     cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                     rope_base: float = 10000.0):
+    """Trellis2SelfAttention::attention's q/k stage
+    (runtime/trellis2_blocks.rs:423-430) on [B, L, H, D] views, one launch."""
+    qo, ko = _heads_out(q), _heads_out(k)
+    _lib.call("lux3d_qk_l2norm_rope3d", desc(q), desc(q_gamma), desc(k), desc(k_gamma), desc(cos), desc(sin),
+              desc(coords), rope_base, desc(qo), desc(ko), _stream(q))
+    return qo, ko
+
+
+def apply_rotary_to_patches(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                            num_prefix: int):
+    """apply_rotary_to_patches (runtime/trellis2_dino.rs:406-436)."""
+    qo, ko = _heads_out(q), _heads_out(k)
+    _lib.call("lux3d_dinov3_rope", desc(q), desc(k), desc(cos), desc(sin), int(num_prefix), desc(qo),
+              desc(ko), _stream(q))
+    return qo, ko
+
+
+# ---------------------------------------------------------------------------
+# Activations, timestep embedding, Q8_0
+# ---------------------------------------------------------------------------
+
+def _act(name: str, x: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    _lib.call(name, desc(x), desc(y), _stream(x))
+    return y
+
+
+def gelu_erf(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tensor::gelu_erf (runtime/nn_blocks.rs:233)."""
+    return _act("lux3d_gelu_erf", x, out)
+
+
+def gelu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tensor::gelu, the tanh approximation (runtime/trellis2_blocks.rs:560)."""
+    return _act("lux3d_gelu_tanh", x, out)
+
+
+def silu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tensor::silu (runtime/trellis2_blocks.rs:236,257)."""
+    return _act("lux3d_silu", x, out)
+
+
+_LIBM = ctypes.CDLL("libm.so.6")
+_LIBM.expf.restype = ctypes.c_float
+_LIBM.expf.argtypes = [ctypes.c_float]
+_LIBM.logf.restype = ctypes.c_float
+_LIBM.logf.argtypes = [ctypes.c_float]
+
+
+def host_timestep_freqs(dim: int) -> list:
+    """The frequency vector the reference builds on the host,
+    exp(-ln(10000) * i / half) with f32 arithmetic and libm expf
+    (runtime/trellis2_blocks.rs:190-194; runtime/triposg_dit.rs:288-291)."""
+    half = dim // 2
+    nlp = ctypes.c_float(-math.log(10000.0)).value
+    out = []
+    for i in range(half):
+        x = ctypes.c_float(ctypes.c_float(nlp * float(i)).value / float(half)).value
+        out.append(_LIBM.expf(x))
+    return out
+
+
+def timestep_embedding(t: torch.Tensor, dim: int, cos_first: bool = True,
+                       freqs: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """timestep_embedding (runtime/trellis2_blocks.rs:184-204, cos first)
+    or TripoSgDiT::timestep_embedding (runtime/triposg_dit.rs:280-297, sin
+    first) for a batch of f32 timesteps t [n] -> [n, dim] f32."""
+    out = torch.empty((t.numel(), dim), dtype=torch.float32, device=t.device)
+    _lib.call("lux3d_timestep_embedding", desc(t.reshape(-1)), desc(freqs), int(dim), 1 if cos_first else 0,
+              desc(out), _stream(t))
+    return out
+
+
+def dequantize_q8_0(blocks: torch.Tensor, shape, dtype=torch.bfloat16) -> torch.Tensor:
+    """QTensor::dequantize for a GGML Q8_0 tensor (runtime/nn_blocks.rs:140):
+    u8 blocks [nblocks*34] -> dtype tensor of `shape`, bit-exact."""
+    y = torch.empty(tuple(shape), dtype=dtype, device=blocks.device)
+    _lib.call("lux3d_dequant_q8_0", desc(blocks.reshape(-1)), desc(y), _stream(y))
+    return y

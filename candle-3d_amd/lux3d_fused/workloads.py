@@ -1,0 +1,396 @@
+"""The fused ops at BASELINE.json's config shapes, as benchmark workloads.
+
+Each workload owns `sets` independent input/output buffer sets whose total
+size exceeds the MI355X's 256 MB Infinity Cache several times, and `launch(i)`
+runs the op once on set i % sets, so consecutive launches never find their
+inputs cache-resident. `bytes` is the op's algorithmic HBM traffic per launch:
+every input read once and every output written once at its natural dtype,
+broadcast parameters counted once.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable, List
+
+import numpy as np
+import torch
+
+from . import ops, synth
+
+MALL_BYTES = 256 << 20
+ROTATION_TARGET = 3 * MALL_BYTES      # total bytes touched by one pass over all sets
+MAX_SETS = 64
+
+
+@dataclass
+class Workload:
+    name: str
+    config: int
+    kernel: str          # HIP kernel family that implements it
+    dtype: str
+    bytes: int           # algorithmic bytes per launch
+    shape: str
+    launch: Callable[[int], object] = field(repr=False)
+    sets: int = 1
+    ideal_note: str = ""
+
+
+def _cur() -> int:
+    """The current HIP stream (read at launch time so graph capture works)."""
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _n_sets(bytes_per_set: int) -> int:
+    return int(min(MAX_SETS, max(2, math.ceil(ROTATION_TARGET / max(bytes_per_set, 1)))))
+
+
+def _t(a: np.ndarray, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t.to(dtype) if dtype is not None else t
+
+
+def _normal(seed, shape, dev, dtype, mean=0.0, std=1.0):
+    """Seeded N(mean, std) device tensor, generated on the device (the
+    benchmark needs the distribution, not the oracle's exact draws), f32
+    then rounded to `dtype`."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(int(seed))
+    t = torch.randn(tuple(shape), generator=g, device=dev, dtype=torch.float32)
+    return (t * std + mean).to(dtype)
+
+
+def _fill_like(base: torch.Tensor, k: int) -> torch.Tensor:
+    """A different-but-deterministic copy for rotation set k (roll the data)."""
+    if k == 0:
+        return base
+    flat = base.reshape(-1)
+    return torch.roll(flat, shifts=int(k * 7919) % max(flat.numel(), 1)).reshape(base.shape).contiguous()
+
+
+# ---------------------------------------------------------------------------
+
+def cfg0_layer_norm(dev) -> Workload:
+    rows, d = 1374, 1024
+    s = synth.config_seed(0)
+    x0 = _normal(s, (rows, d), dev, torch.float32)
+    w = _normal(s + 1, (d,), dev, torch.float32, 1.0, 0.02)
+    b = _normal(s + 2, (d,), dev, torch.float32, 0.0, 0.02)
+    nbytes = rows * d * 8 + 2 * d * 4
+    n = _n_sets(nbytes)
+    xs = [_fill_like(x0, k) for k in range(n)]
+    ys = [torch.empty_like(x0) for _ in range(n)]
+    from . import _lib
+    dw, db = ops.desc(w), ops.desc(b)
+    dx = [ops.desc(x) for x in xs]
+    dy = [ops.desc(y) for y in ys]
+
+    def launch(i):
+        k = i % n
+        _lib.call("lux3d_layer_norm", dx[k], dw, db, 1e-6, dy[k], _cur())
+    wl = Workload("layer_norm", 0, "row_kernel<F32,LN>", "f32", nbytes, f"[{rows},{d}]", launch, n)
+    wl._keep = (xs, ys, w, b, dx, dy, dw, db)
+    return wl
+
+
+def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps) -> Workload:
+    from . import _lib
+    s = synth.config_seed(cfg)
+    d = shape[-1]
+    x0 = _normal(s, shape, dev, dt)
+    a0 = _normal(s + 100, shape, dev, dt)
+    g = _normal(s + 200, (d,), dev, torch.float32, *gamma_ms)
+    w = _normal(s + 300, (d,), dev, torch.float32, 1.0, 0.02)
+    b = _normal(s + 400, (d,), dev, torch.float32, 0.0, 0.02)
+    esz = x0.element_size()
+    nbytes = x0.numel() * esz * 4 + 3 * d * 4
+    n = _n_sets(nbytes)
+    xs = [_fill_like(x0, k) for k in range(n)]
+    as_ = [_fill_like(a0, k + 1) for k in range(n)]
+    hs = [torch.empty_like(x0) for _ in range(n)]
+    ys = [torch.empty_like(x0) for _ in range(n)]
+    D = [(ops.desc(xs[k]), ops.desc(as_[k]), ops.desc(hs[k]), ops.desc(ys[k])) for k in range(n)]
+    dg, dw, dbb = ops.desc(g), ops.desc(w), ops.desc(b)
+
+    def launch(i):
+        dx, da, dh, dy = D[i % n]
+        _lib.call("lux3d_residual_layer_norm", dx, da, dg, dw, dbb, eps, dh, dy, _cur())
+    name = "residual_layer_norm"
+    wl = Workload(name, cfg, "row_kernel<RESID_LN>", "bf16" if dt == torch.bfloat16 else "f32", nbytes,
+                  str(list(shape)), launch, n)
+    wl._keep = (xs, as_, hs, ys, g, w, b, D, dg, dw, dbb)
+    return wl
+
+
+def cfg1_residual_layer_norm(dev) -> Workload:
+    return _residual_ln(dev, 1, (8, 1374, 1024), torch.bfloat16, (1.0, 0.02), 1e-5)
+
+
+def cfg4_residual_layer_norm(dev) -> Workload:
+    return _residual_ln(dev, 4, (1, 1029, 1024), torch.float32, (1e-5, 1e-6), 1e-5)
+
+
+def cfg1_qk_layernorm_rope2d(dev, tables: bool = False) -> Workload:
+    from . import _lib
+    B, N, H, D = 8, 1374, 16, 64
+    s = synth.config_seed(1)
+    qkv0 = _normal(s + 7, (B, N, 3, H, D), dev, torch.bfloat16)
+    qw = _normal(s + 21, (D,), dev, torch.float32, 1.0, 0.02)
+    qb = _normal(s + 22, (D,), dev, torch.float32, 0.0, 0.02)
+    kw = _normal(s + 23, (D,), dev, torch.float32, 1.0, 0.02)
+    kb = _normal(s + 24, (D,), dev, torch.float32, 0.0, 0.02)
+    pos = _t(synth.vggt_positions(B, 37, 37), dev)
+    emb = ops.Rope2d(100.0).embeddings(pos, D) if tables else None
+    qk_elems = B * N * H * D
+    nbytes = 2 * qk_elems * 2 * 2 + 4 * D * 4
+    nbytes += (2 * B * N * D * 4) if tables else (B * N * 2 * 4)
+    n = _n_sets(nbytes + qk_elems * 2)  # + the v third that shares the qkv buffer
+    qkvs = [_fill_like(qkv0, k) for k in range(n)]
+    outs = [(torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev),
+             torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev)) for _ in range(n)]
+    Ds = []
+    for k in range(n):
+        perm = qkvs[k].permute(2, 0, 3, 1, 4)
+        Ds.append((ops.desc(perm[0]), ops.desc(perm[1]), ops.desc(outs[k][0]), ops.desc(outs[k][1])))
+    dqw, dqb, dkw, dkb = ops.desc(qw), ops.desc(qb), ops.desc(kw), ops.desc(kb)
+    dpos = ops.desc(pos)
+    dc = ops.desc(emb.cos_full) if tables else None
+    ds = ops.desc(emb.sin_alt_full) if tables else None
+
+    def launch(i):
+        dq, dk, dqo, dko = Ds[i % n]
+        if tables:
+            _lib.call("lux3d_qk_layernorm_rope2d", dq, dqw, dqb, dk, dkw, dkb, 1e-5, dc, ds, dqo, dko, _cur())
+        else:
+            _lib.call("lux3d_qk_layernorm_rope2d_pos", dq, dqw, dqb, dk, dkw, dkb, 1e-5, dpos, 100.0, dqo, dko,
+                      _cur())
+    name = "qk_layernorm_rope2d" + ("_tables" if tables else "")
+    wl = Workload(name, 1, "head_kernel<BF16,64,LN,R1>", "bf16", nbytes, f"q,k [{B},{H},{N},{D}] in qkv", launch, n)
+    wl._keep = (qkvs, outs, Ds, qw, qb, kw, kb, pos, emb, dqw, dqb, dkw, dkb, dpos, dc, ds)
+    return wl
+
+
+def cfg2_timestep_embedding(dev) -> Workload:
+    from . import _lib
+    t = _t(synth.uniform(synth.config_seed(2) + 4, 2, 0.0, 1000.0), dev)
+    freqs = torch.tensor(ops.host_timestep_freqs(256), dtype=torch.float32, device=dev)
+    out = torch.empty((2, 256), dtype=torch.float32, device=dev)
+    dt_, df, do = ops.desc(t), ops.desc(freqs), ops.desc(out)
+
+    def launch(i):
+        _lib.call("lux3d_timestep_embedding", dt_, df, 256, 1, do, _cur())
+    wl = Workload("timestep_embedding", 2, "timestep_kernel", "f32", 2 * 4 + 128 * 4 + 2 * 256 * 4, "[2]->[2,256]",
+                  launch, 1, "latency-bound: report us only")
+    wl._keep = (t, freqs, out, dt_, df, do)
+    return wl
+
+
+def _modulate(dev, cfg, rows_per_seg, C, gate_only=False) -> Workload:
+    from . import _lib
+    S = len(rows_per_seg)
+    rows = sum(rows_per_seg)
+    s = synth.config_seed(cfg)
+    x0 = _normal(s, (rows, C), dev, torch.bfloat16)
+    shift = _normal(s + 1, (S, C), dev, torch.float32, 0.0, 0.1)
+    scale = _normal(s + 2, (S, C), dev, torch.float32, 0.0, 0.1)
+    gate = _normal(s + 3, (S, C), dev, torch.float32, 0.0, 0.1)
+    ragged = len(set(rows_per_seg)) > 1
+    offs = _t(np.concatenate([[0], np.cumsum(rows_per_seg)]).astype(np.int64), dev) if ragged else None
+    if gate_only:
+        h0 = _normal(s + 9, (rows, C), dev, torch.bfloat16)
+        nbytes = rows * C * 2 * 3 + S * C * 4
+    else:
+        nbytes = rows * C * 2 * 2 + 2 * S * C * 4
+    if ragged:
+        nbytes += (S + 1) * 8
+    n = _n_sets(nbytes)
+    xs = [_fill_like(x0, k) for k in range(n)]
+    hs = [_fill_like(h0, k + 1) for k in range(n)] if gate_only else None
+    ys = [torch.empty_like(x0) for _ in range(n)]
+    dx = [ops.desc(v) for v in xs]
+    dh = [ops.desc(v) for v in hs] if gate_only else None
+    dy = [ops.desc(v) for v in ys]
+    dsh, dsc, dg, do = ops.desc(shift), ops.desc(scale), ops.desc(gate), ops.desc(offs)
+
+    def launch(i):
+        k = i % n
+        if gate_only:
+            _lib.call("lux3d_gated_residual", dx[k], dh[k], do, dg, None, dy[k], _cur())
+        else:
+            _lib.call("lux3d_adaln_modulate", dx[k], do, dsh, None, dsc, None, None, None, 1e-6, dy[k], _cur())
+    name = ("gated_residual" if gate_only else "adaln_modulate") + ("_ragged" if ragged else "")
+    kern = "row_kernel<BF16,GATE>" if gate_only else "row_kernel<BF16,MODULATE>"
+    wl = Workload(name, cfg, kern, "bf16", nbytes, f"[{rows},{C}] segs {list(rows_per_seg)}", launch, n)
+    wl._keep = (xs, hs, ys, shift, scale, gate, offs, dx, dh, dy, dsh, dsc, dg, do)
+    return wl
+
+
+def cfg2_adaln_modulate(dev) -> Workload:
+    return _modulate(dev, 2, (2048, 2048), 2048)
+
+
+def cfg2_gated_residual(dev) -> Workload:
+    return _modulate(dev, 2, (2048, 2048), 2048, gate_only=True)
+
+
+def cfg3_adaln_modulate_ragged(dev) -> Workload:
+    return _modulate(dev, 3, (24000, 40000), 1536)
+
+
+def cfg3_gated_residual_ragged(dev) -> Workload:
+    return _modulate(dev, 3, (24000, 40000), 1536, gate_only=True)
+
+
+def cfg2_rms_norm_heads(dev) -> Workload:
+    from . import _lib
+    B, L, H, D = 2, 2048, 16, 128
+    s = synth.config_seed(2)
+    qkv0 = _normal(s + 9, (B, L, H, 3 * D), dev, torch.bfloat16)
+    wq = _normal(41, (D,), dev, torch.float32, 1.0, 0.02)
+    wk = _normal(42, (D,), dev, torch.float32, 1.0, 0.02)
+    nbytes = 2 * B * L * H * D * 2 * 2 + 2 * D * 4
+    n = _n_sets(nbytes + B * L * H * D * 2)
+    qkvs = [_fill_like(qkv0, k) for k in range(n)]
+    outs = [(torch.empty((B, H, L, D), dtype=torch.bfloat16, device=dev),
+             torch.empty((B, H, L, D), dtype=torch.bfloat16, device=dev)) for _ in range(n)]
+    Ds = [(ops.desc(qkvs[k][..., 0:D].transpose(1, 2)), ops.desc(qkvs[k][..., D:2 * D].transpose(1, 2)),
+           ops.desc(outs[k][0]), ops.desc(outs[k][1])) for k in range(n)]
+    dwq, dwk = ops.desc(wq), ops.desc(wk)
+
+    def launch(i):
+        dq, dk, dqo, dko = Ds[i % n]
+        _lib.call("lux3d_rms_norm_heads", dq, dwq, dk, dwk, 1e-6, dqo, dko, _cur())
+    wl = Workload("rms_norm_heads", 2, "head_kernel<BF16,128,RMS>", "bf16", nbytes,
+                  f"q,k [{B},{H},{L},{D}] in qkv", launch, n)
+    wl._keep = (qkvs, outs, Ds, wq, wk, dwq, dwk)
+    return wl
+
+
+def _act(dev, name, entry) -> Workload:
+    from . import _lib
+    shape = (2, 2048, 8192)
+    x0 = _normal(synth.config_seed(2) + 3, shape, dev, torch.bfloat16)
+    nbytes = x0.numel() * 4
+    n = _n_sets(nbytes)
+    xs = [_fill_like(x0, k) for k in range(n)]
+    ys = [torch.empty_like(x0) for _ in range(n)]
+    dx = [ops.desc(v) for v in xs]
+    dy = [ops.desc(v) for v in ys]
+
+    def launch(i):
+        k = i % n
+        _lib.call(entry, dx[k], dy[k], _cur())
+    wl = Workload(name, 2, f"act_kernel<BF16,{name}>", "bf16", nbytes, str(list(shape)), launch, n)
+    wl._keep = (xs, ys, dx, dy)
+    return wl
+
+
+def cfg2_gelu_tanh(dev) -> Workload:
+    return _act(dev, "gelu_tanh", "lux3d_gelu_tanh")
+
+
+def cfg2_gelu_erf(dev) -> Workload:
+    return _act(dev, "gelu_erf", "lux3d_gelu_erf")
+
+
+def cfg2_silu(dev) -> Workload:
+    return _act(dev, "silu", "lux3d_silu")
+
+
+def cfg3_qk_l2norm_rope3d(dev) -> Workload:
+    from . import _lib
+    H, D = 12, 128
+    sizes = (24000, 40000)
+    N = sum(sizes)
+    coords = np.concatenate([synth.unique_voxels(synth.config_seed(3) + 10 * i, n, 64)
+                             for i, n in enumerate(sizes)], axis=0)
+    s = synth.config_seed(3)
+    qkv0 = _normal(s + 5, (1, N, 3, H, D), dev, torch.bfloat16)
+    gq = _normal(51, (H, D), dev, torch.float32, 1.0, 0.02)
+    gk = _normal(52, (H, D), dev, torch.float32, 1.0, 0.02)
+    cd = _t(coords, dev)
+    nbytes = 2 * N * H * D * 2 * 2 + N * 3 * 4 + 2 * H * D * 4
+    n = _n_sets(nbytes + N * H * D * 2)
+    qkvs = [_fill_like(qkv0, k) for k in range(n)]
+    outs = [(torch.empty((1, N, H, D), dtype=torch.bfloat16, device=dev),
+             torch.empty((1, N, H, D), dtype=torch.bfloat16, device=dev)) for _ in range(n)]
+    Ds = [(ops.desc(qkvs[k][:, :, 0]), ops.desc(qkvs[k][:, :, 1]), ops.desc(outs[k][0]), ops.desc(outs[k][1]))
+          for k in range(n)]
+    dgq, dgk, dcd = ops.desc(gq), ops.desc(gk), ops.desc(cd)
+
+    def launch(i):
+        dq, dk, dqo, dko = Ds[i % n]
+        _lib.call("lux3d_qk_l2norm_rope3d", dq, dgq, dk, dgk, None, None, dcd, 10000.0, dqo, dko, _cur())
+    wl = Workload("qk_l2norm_rope3d_ragged", 3, "head_kernel<BF16,128,L2,R2>", "bf16", nbytes,
+                  f"q,k [1,{N},{H},{D}] in qkv, coords [{N},3]", launch, n)
+    wl._keep = (qkvs, outs, Ds, gq, gk, cd, dgq, dgk, dcd)
+    return wl
+
+
+def cfg4_dequant_q8_0(dev) -> Workload:
+    from . import _lib
+    rows, cols = 4096, 1024
+    nb = rows * cols // 32
+    blocks0 = _t(synth.q8_0_blocks(synth.config_seed(4), nb), dev)
+    nbytes = nb * 34 + rows * cols * 2
+    n = _n_sets(nbytes)
+    bs = [_fill_like(blocks0, 34 * k) if k else blocks0 for k in range(n)]
+    ys = [torch.empty((rows, cols), dtype=torch.bfloat16, device=dev) for _ in range(n)]
+    db = [ops.desc(v) for v in bs]
+    dy = [ops.desc(v) for v in ys]
+
+    def launch(i):
+        k = i % n
+        _lib.call("lux3d_dequant_q8_0", db[k], dy[k], _cur())
+    wl = Workload("dequant_q8_0", 4, "dequant_q8_0_kernel<BF16>", "u8->bf16", nbytes, f"[{rows},{cols}]", launch, n)
+    wl._keep = (bs, ys, db, dy)
+    return wl
+
+
+def cfg4_dinov3_rope(dev) -> Workload:
+    from . import _lib
+    B, H, S, D = 1, 16, 1029, 64
+    s = synth.config_seed(4)
+    q0 = _normal(s + 71, (B, S, H, D), dev, torch.float32)
+    k0 = _normal(s + 72, (B, S, H, D), dev, torch.float32)
+    cos = _normal(s + 73, (S - 5, D), dev, torch.float32)
+    sin = _normal(s + 74, (S - 5, D), dev, torch.float32)
+    nbytes = 2 * B * S * H * D * 4 * 2 + 2 * (S - 5) * D * 4
+    n = _n_sets(nbytes)
+    qs = [_fill_like(q0, k) for k in range(n)]
+    ks = [_fill_like(k0, k + 1) for k in range(n)]
+    outs = [(torch.empty((B, H, S, D), device=dev), torch.empty((B, H, S, D), device=dev)) for _ in range(n)]
+    Ds = [(ops.desc(qs[k].transpose(1, 2)), ops.desc(ks[k].transpose(1, 2)), ops.desc(outs[k][0]),
+           ops.desc(outs[k][1])) for k in range(n)]
+    dc, dsn = ops.desc(cos), ops.desc(sin)
+
+    def launch(i):
+        dq, dk, dqo, dko = Ds[i % n]
+        _lib.call("lux3d_dinov3_rope", dq, dk, dc, dsn, 5, dqo, dko, _cur())
+    wl = Workload("dinov3_rope", 4, "head_kernel<F32,64,R3>", "f32", nbytes, f"q,k [{B},{H},{S},{D}]", launch, n)
+    wl._keep = (qs, ks, outs, Ds, cos, sin, dc, dsn)
+    return wl
+
+
+# The configs[1..4] ops BASELINE.md names (the >=70%-of-peak targets), then extras.
+TARGETS: List[Callable] = [
+    cfg1_residual_layer_norm,
+    cfg1_qk_layernorm_rope2d,
+    cfg2_adaln_modulate,
+    cfg2_gated_residual,
+    cfg2_rms_norm_heads,
+    cfg2_gelu_tanh,
+    cfg3_adaln_modulate_ragged,
+    cfg3_qk_l2norm_rope3d,
+    cfg4_residual_layer_norm,
+    cfg4_dequant_q8_0,
+]
+EXTRAS: List[Callable] = [
+    cfg0_layer_norm,
+    cfg2_timestep_embedding,
+    lambda dev: cfg1_qk_layernorm_rope2d(dev, tables=True),
+    cfg2_gelu_erf,
+    cfg2_silu,
+    cfg3_gated_residual_ragged,
+    cfg4_dinov3_rope,
+]

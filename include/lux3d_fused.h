@@ -1,0 +1,275 @@
+/*
+ * lux3d_fused.h -- C ABI of the MI355X (gfx950) fused transformer-layer ops
+ * for candle-3d (Lux3D). This is the drop-in boundary: a Rust CustomOp (or any
+ * FFI caller) passes borrowed device buffers described by lux3d_tensor_t and a
+ * HIP stream; every entry point validates its arguments on the host, enqueues
+ * exactly one kernel on that stream, never synchronises and never allocates.
+ *
+ * Each entry names the reference function(s) it replaces (paths relative to
+ * crates/lux3d-core/src/ of the candle-3d tree; "candle" = the candle fork the
+ * reference depends on, Cargo.toml:23-25).
+ *
+ * Conventions
+ *  - Tensors: `data` points at the first element (candle's Layout start
+ *    offset already applied); strides are in elements. All kernels require
+ *    the innermost stride to be 1 unless stated otherwise.
+ *  - Activations: f32, bf16 or f16. Per-channel parameters (LayerNorm w/b,
+ *    LayerScale gamma, RMS weights, modulation vectors, RoPE tables): f32,
+ *    bf16 or f16 (loaded and widened to f32). Outputs have the activation's
+ *    dtype. All arithmetic is f32; bf16/f16 outputs are rounded once
+ *    (round-to-nearest-even).
+ *  - Return value: LUX3D_OK (0) or a negative lux3d_status; the message is
+ *    available from lux3d_last_error() on the calling thread. Argument errors
+ *    are detected before anything is enqueued.
+ *  - Thread safety: no global mutable state besides the thread-local error
+ *    message; results are deterministic (no atomics, fixed reduction order).
+ */
+#ifndef LUX3D_FUSED_H
+#define LUX3D_FUSED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LUX3D_ABI_VERSION 1
+#define LUX3D_MAX_RANK 5
+
+typedef enum {
+  LUX3D_F32 = 0,
+  LUX3D_BF16 = 1,
+  LUX3D_F16 = 2,
+  LUX3D_I32 = 3,
+  LUX3D_I64 = 4,
+  LUX3D_U8 = 5
+} lux3d_dtype;
+
+typedef enum {
+  LUX3D_OK = 0,
+  LUX3D_ERR_NULL = -1,     /* a required pointer/descriptor is NULL */
+  LUX3D_ERR_SHAPE = -2,    /* shapes disagree or are unsupported */
+  LUX3D_ERR_DTYPE = -3,    /* unsupported dtype or dtype mismatch */
+  LUX3D_ERR_LAYOUT = -4,   /* unsupported strides */
+  LUX3D_ERR_HIP = -5,      /* the kernel launch failed */
+  LUX3D_ERR_VALUE = -6     /* a scalar argument is out of range */
+} lux3d_status;
+
+/* A borrowed device tensor (candle Storage + Layout). */
+typedef struct {
+  void *data;
+  int32_t dtype;  /* lux3d_dtype */
+  int32_t rank;   /* 1..LUX3D_MAX_RANK */
+  int64_t shape[LUX3D_MAX_RANK];
+  int64_t stride[LUX3D_MAX_RANK];
+} lux3d_tensor_t;
+
+/* A hipStream_t; NULL is the null stream. */
+typedef void *lux3d_stream_t;
+
+int lux3d_abi_version(void);
+const char *lux3d_last_error(void);
+
+/* --------------------------------------------------------------------------
+ * Row LayerNorm over the last dim (rows = all leading dims, which must form a
+ * uniform row stride).
+ *   w, b non-NULL: candle_nn::ops::layer_norm / LayerNorm::forward, reached
+ *     from layer_norm(dim, eps, vb): runtime/pi3_encoder.rs:67,70,153;
+ *     runtime/vggt.rs:104,107,346,356; runtime/triposg_dit.rs:323,332-336;
+ *     runtime/triposg_dino.rs:208,211; runtime/trellis2_dino.rs:324,327;
+ *     runtime/trellis2_blocks.rs:587.
+ *   w = b = NULL: layer_norm_no_affine (runtime/trellis2_blocks.rs:280-286),
+ *     adaln_norm (runtime/vggt.rs:432-437), non_affine_layer_norm
+ *     (runtime/trellis2_dino.rs:448-454).
+ *   y may alias x.                                                          */
+int lux3d_layer_norm(const lux3d_tensor_t *x, const lux3d_tensor_t *w,
+                     const lux3d_tensor_t *b, float eps,
+                     const lux3d_tensor_t *y, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Fused LayerScale + residual + LayerNorm:
+ *   h = x + a*ls_gamma (ls_gamma NULL: h = x + a), stored in h_out;
+ *   y = LayerNorm(h; w, b, eps) computed from the stored (rounded) h.
+ * Replaces LayerScale::forward (runtime/nn_blocks.rs:210-214) + the residual
+ * add + the next norm in VggtBlock::forward (runtime/vggt.rs:113-124),
+ * dinov2 Block::forward (runtime/pi3_encoder.rs:78-89), DinoLayer::forward
+ * (runtime/trellis2_dino.rs:344-355, runtime/triposg_dino.rs:218-228) and
+ * DiTBlock::forward (runtime/triposg_dit.rs:364-379). w/b may be NULL
+ * (non-affine norm). h_out may alias x.                                     */
+int lux3d_residual_layer_norm(const lux3d_tensor_t *x, const lux3d_tensor_t *a,
+                              const lux3d_tensor_t *ls_gamma,
+                              const lux3d_tensor_t *w, const lux3d_tensor_t *b,
+                              float eps, const lux3d_tensor_t *h_out,
+                              const lux3d_tensor_t *y, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * AdaLN modulate on dense or ragged token rows:
+ *   n = LayerNorm_no_affine(x, eps)
+ *   y = n*(scale + 1) + shift                       (gate == NULL)
+ *   y = gate*(n*(scale + 1) + shift) + x            (gate != NULL)
+ * with every modulation piece p in {shift, scale, gate} read per segment s
+ * as p[s, c] (+ p_base[c] when p_base is given: the block's `modulation`
+ * parameter added to t_emb, runtime/trellis2_blocks.rs:617).
+ *   x: [rows, C] (or [B, L, C]); p: [S, C] views (any row stride, so the
+ *   chunks of a [S, 6C] modulation vector are passed without a copy);
+ *   p_base: [C] or NULL.
+ *   seg_offsets: int64 [S+1] device array of row offsets (ragged TRELLIS.2
+ *   voxel batches); NULL means S equal segments of rows/S rows (x [B, L, C]
+ *   with S = B). Rows past offsets[S] use segment S-1.
+ * Replaces Trellis2DenseBlock/Trellis2SparseBlock modulate chains
+ * (runtime/trellis2_blocks.rs:617-630, 639-642, 693-714; chunk order per
+ * chunk_modulation :264-277) and the VGGT camera-head poseLN modulation
+ * (runtime/vggt.rs:399-405, gate variant).                                  */
+int lux3d_adaln_modulate(const lux3d_tensor_t *x, const lux3d_tensor_t *seg_offsets,
+                         const lux3d_tensor_t *shift, const lux3d_tensor_t *shift_base,
+                         const lux3d_tensor_t *scale, const lux3d_tensor_t *scale_base,
+                         const lux3d_tensor_t *gate, const lux3d_tensor_t *gate_base,
+                         float eps, const lux3d_tensor_t *y, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Gated residual: out = x + h*gate, gate per segment as in
+ * lux3d_adaln_modulate. Replaces `h.broadcast_mul(gate)` + `xs.add(h)` at
+ * runtime/trellis2_blocks.rs:632-633, 644-645, 708-717. out may alias x.     */
+int lux3d_gated_residual(const lux3d_tensor_t *x, const lux3d_tensor_t *h,
+                         const lux3d_tensor_t *seg_offsets,
+                         const lux3d_tensor_t *gate, const lux3d_tensor_t *gate_base,
+                         const lux3d_tensor_t *out, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * VGGT/Pi3 2D RoPE (R1) on Q and K head views, optionally after a per-head
+ * affine LayerNorm (the q_norm/k_norm of the attention).
+ *   q, k: [B, H, N, D] views with any outer strides (e.g. the permuted
+ *     [B, N, 3, H, D] qkv buffer), D = 64 or 128; k may be NULL.
+ *   q_w/q_b (k_w/k_b): [D] LayerNorm affine, or all NULL for RoPE only.
+ *   cos_full, sin_alt_full: [B, N, D] or [B, 1, N, D] f32 tables as built by
+ *     Rope2d::embeddings (sin table with the rotate-half negation folded in).
+ *   q_out, k_out: contiguous [B, H, N, D].
+ *   out[j] = y[j]*cos_full[j] + y[partner(j)]*sin_alt_full[j], partner =
+ *   the other quarter of j's half.
+ * Replaces candle_nn::ops::layernorm_rope_fused / rope_fused (the fork's
+ * CustomOp3s routed at runtime/attention_math.rs:132-146, 156-162) and the
+ * composed path they short-cut (LayerNorm::forward on the strided view +
+ * .contiguous() + rope_apply, runtime/attention_math.rs:104-118,148-149).  */
+int lux3d_qk_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w,
+                              const lux3d_tensor_t *q_b, const lux3d_tensor_t *k,
+                              const lux3d_tensor_t *k_w, const lux3d_tensor_t *k_b,
+                              float eps, const lux3d_tensor_t *cos_full,
+                              const lux3d_tensor_t *sin_alt_full,
+                              const lux3d_tensor_t *q_out, const lux3d_tensor_t *k_out,
+                              lux3d_stream_t stream);
+
+/* Same, with the rotation computed in-kernel from integer positions
+ * [B, N, 2] (int32 or int64, (y, x) order; specials at (0, 0)) and `base`,
+ * i.e. Rope2d::embeddings (runtime/attention_math.rs:14-58) fused into the
+ * apply: no [B, N, D] tables are read and no device->host position max is
+ * needed (attention_math.rs:24).                                           */
+int lux3d_qk_layernorm_rope2d_pos(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w,
+                                  const lux3d_tensor_t *q_b, const lux3d_tensor_t *k,
+                                  const lux3d_tensor_t *k_w, const lux3d_tensor_t *k_b,
+                                  float eps, const lux3d_tensor_t *positions, float base,
+                                  const lux3d_tensor_t *q_out, const lux3d_tensor_t *k_out,
+                                  lux3d_stream_t stream);
+
+/* Rope2d::embeddings (runtime/attention_math.rs:14-58) on the device:
+ * positions [B, N, 2] int32/int64 -> cos_full, sin_alt_full contiguous
+ * [B, N, D] f32 (D = token_dim, divisible by 4).                            */
+int lux3d_rope2d_tables(const lux3d_tensor_t *positions, float base,
+                        const lux3d_tensor_t *cos_full, const lux3d_tensor_t *sin_alt_full,
+                        lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * TripoSG per-head RMSNorm (N1) on Q and K head views:
+ *   y = x / sqrt(mean(x^2) + eps) * w      (w: [D])
+ *   q, k: [B, H, L, D] views with any outer strides (the per-head thirds of
+ *   TripoSGAttnProcessor's cat([q,k,v]) need no transpose/contiguous copy);
+ *   k may be NULL; outputs contiguous [B, H, L, D].
+ * Replaces RmsNormHeads::rms_norm_heads (runtime/triposg_dit.rs:509-522)
+ * and the .transpose(1,2).contiguous() before it (:446-453, 478-497).      */
+int lux3d_rms_norm_heads(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w,
+                         const lux3d_tensor_t *k, const lux3d_tensor_t *k_w,
+                         float eps, const lux3d_tensor_t *q_out,
+                         const lux3d_tensor_t *k_out, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * TRELLIS.2 q/k L2 "RMS" norm (N2) and/or 3D RoPE (R2) on [B, L, H, D] head
+ * views (any outer strides; D = 64 or 128), q and k in one launch:
+ *   N2 (gamma [H, D] given): y = x / clamp(||x||, 1e-12, 1e30) * gamma * sqrt(D)
+ *   R2 (phases given): pairs (y[2i], y[2i+1]) rotated by phase i of token l,
+ *     from tables cos/sin [L, D/2] (Trellis2Rope3d::cos_sin layout) or
+ *     computed in-kernel from int32 coords [L, 3] and `base`.
+ *   Both NULL skips that stage; q_out/k_out contiguous [B, L, H, D].
+ * Replaces Trellis2QkRmsNorm::forward (runtime/trellis2_blocks.rs:306-319),
+ * Trellis2Rope3d::apply (:139-160) and their use in
+ * Trellis2SelfAttention::attention (:423-430); coords as validated by
+ * Trellis2SlatDit::prepare (runtime/trellis2_dit.rs:511-544).              */
+int lux3d_qk_l2norm_rope3d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_gamma,
+                           const lux3d_tensor_t *k, const lux3d_tensor_t *k_gamma,
+                           const lux3d_tensor_t *cos, const lux3d_tensor_t *sin,
+                           const lux3d_tensor_t *coords, float base,
+                           const lux3d_tensor_t *q_out, const lux3d_tensor_t *k_out,
+                           lux3d_stream_t stream);
+
+/* Trellis2Rope3d::cos_sin (runtime/trellis2_blocks.rs:106-134) on the
+ * device: coords int32 [L, 3] -> cos, sin contiguous [L, head_dim/2] f32.   */
+int lux3d_rope3d_tables(const lux3d_tensor_t *coords, int64_t head_dim, float base,
+                        const lux3d_tensor_t *cos, const lux3d_tensor_t *sin,
+                        lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * DINOv3 2D RoPE (R3) on Q and K [B, H, S, D] views: tokens s < num_prefix
+ * pass through unchanged, token s >= num_prefix uses table row
+ * s - num_prefix of cos/sin [S - num_prefix, D]:
+ *   out = x*cos + rotate_half(x)*sin,  rotate_half(x) = cat(-x2, x1).
+ * Replaces apply_rotary_to_patches + rotate_half
+ * (runtime/trellis2_dino.rs:406-445); tables from
+ * Trellis2DinoConfig::rope_cos_sin (:140-187). k may be NULL.               */
+int lux3d_dinov3_rope(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
+                      const lux3d_tensor_t *cos, const lux3d_tensor_t *sin,
+                      int64_t num_prefix, const lux3d_tensor_t *q_out,
+                      const lux3d_tensor_t *k_out, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Activations on contiguous tensors (y may alias x):
+ *   gelu_erf  = 0.5*x*(1 + erf(x/sqrt(2)))       Tensor::gelu_erf
+ *     (runtime/nn_blocks.rs:233,252; vggt.rs:412; triposg_dit.rs:298,380;
+ *      trellis2_dino.rs:353; triposg_dino.rs:225)
+ *   gelu_tanh = 0.5*x*(1 + tanh(sqrt(2/pi)*x*(1 + 0.044715*x^2)))
+ *     Tensor::gelu (runtime/trellis2_blocks.rs:558-561)
+ *   silu      = x / (1 + exp(-x))                Tensor::silu
+ *     (runtime/trellis2_blocks.rs:236,257; vggt.rs:393)                     */
+int lux3d_gelu_erf(const lux3d_tensor_t *x, const lux3d_tensor_t *y, lux3d_stream_t stream);
+int lux3d_gelu_tanh(const lux3d_tensor_t *x, const lux3d_tensor_t *y, lux3d_stream_t stream);
+int lux3d_silu(const lux3d_tensor_t *x, const lux3d_tensor_t *y, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Sinusoidal timestep embedding, t: f32 [n] (device), out: f32 [n, dim]:
+ *   f_i = exp(-ln(10000) * i / half), arg = t*f_i, half = dim/2
+ *   cos_first = 1: [cos(arg), sin(arg)] (+ a zero for odd dim)
+ *     timestep_embedding (runtime/trellis2_blocks.rs:184-204), dim 256
+ *   cos_first = 0: [sin(arg), cos(arg)]
+ *     TripoSgDiT::timestep_embedding (runtime/triposg_dit.rs:280-297),
+ *     dim = width; dim must be even.
+ * freqs: optional f32 [dim/2] device vector of the f_i. The reference builds
+ * them on the host with libm expf (trellis2_blocks.rs:191-194,
+ * triposg_dit.rs:289-291) and uploads them; passing those exact values makes
+ * every argument t*f_i bit-identical to the reference. NULL computes f_i on
+ * the device (f64 exp rounded once to f32, which can differ from a libm
+ * expf result by 1 ulp).                                                    */
+int lux3d_timestep_embedding(const lux3d_tensor_t *t, const lux3d_tensor_t *freqs,
+                             int64_t dim, int32_t cos_first,
+                             const lux3d_tensor_t *out, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * GGML Q8_0 dequantisation: blocks u8 [nblocks*34] of {f16 d (LE); int8
+ * qs[32]} -> y [nblocks*32] (f32, bf16 or f16, contiguous), y = f32(d)*qs
+ * (exact in f32) rounded once to y's dtype: bit-exact.
+ * Replaces QTensor::dequantize for Q8_0 weights (runtime/nn_blocks.rs:140,
+ * examples/quant_probe.rs:84-89); the Q8_0 selection rule is
+ * weights/quantize.rs:319-338 (rank 2, row length % 32 == 0).              */
+int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y,
+                       lux3d_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LUX3D_FUSED_H */

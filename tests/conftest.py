@@ -1,0 +1,102 @@
+"""Shared test setup: import paths, the `gpu` marker and comparison helpers.
+
+Tolerances: bit-exact for dequant and index math; bf16 within
+2 ulp of the oracle; f32 within 1e-5 relative to the output's scale (the
+per-tensor RMS, so that values near zero are not judged on a relative error
+that the reference's own f32 arithmetic cannot meet).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for sub in ("candle-3d_amd", "oracle"):
+    p = os.path.join(ROOT, sub)
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (ROCm device); run with -m gpu")
+
+
+BF16_ULP_TOL = 2
+BF16_ATOL_REL = 2.0 ** -17
+F32_REL_TOL = 1e-5
+
+
+def bf16_ordered(bits: np.ndarray) -> np.ndarray:
+    """Map bf16 (or f16) bit patterns to integers whose difference is the ulp distance."""
+    b = bits.astype(np.int64)
+    mag = b & 0x7FFF
+    return np.where(b & 0x8000, -mag, mag)
+
+
+def ulp_distance16(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    a = np.asarray(a_bits, dtype=np.uint16)
+    b = np.asarray(b_bits, dtype=np.uint16)
+    return np.abs(bf16_ordered(a) - bf16_ordered(b))
+
+
+def assert_bf16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL, f16=False):
+    """bf16/f16 parity: every element within `tol` ulp of the oracle, except
+    where the oracle's value is far below bf16's resolution at the tensor's
+    scale. There (outputs produced by cancellation, e.g. n*w + b ~ 0 or a
+    rotation's re*c - im*s ~ 0, or the GELU tails that the reference's own f32
+    formula rounds to zero) the ulp count of a value near 0 measures only the
+    f32 rounding of the intermediate terms, and the element is instead held to
+    an absolute error <= atol_rel * RMS(oracle output) (2^-17 of the scale:
+    a few f32 roundings of terms of the tensor's magnitude, 2^-9 of one bf16
+    ulp at that magnitude)."""
+    got = np.asarray(got_bits, dtype=np.uint16).reshape(-1)
+    want = np.asarray(want_bits, dtype=np.uint16).reshape(-1)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    nan_lim = 0x7C00 if f16 else 0x7F80
+    nan_g = (got & 0x7FFF) > nan_lim
+    nan_w = (want & 0x7FFF) > nan_lim
+    assert np.array_equal(nan_g, nan_w), f"{what}: NaN positions differ"
+    g, w = got[~nan_g], want[~nan_w]
+    d = ulp_distance16(g, w)
+    worst = int(d.max()) if d.size else 0
+    if worst <= tol:
+        return worst
+    bad = d > tol
+    gf = _bits_to_f32(g[bad], f16)
+    wf = _bits_to_f32(w[bad], f16)
+    wall = _bits_to_f32(w, f16)
+    finite = np.isfinite(wall)
+    rms = float(np.sqrt(np.mean(wall[finite].astype(np.float64) ** 2))) if finite.any() else 1.0
+    err = np.abs(gf.astype(np.float64) - wf.astype(np.float64))
+    assert np.all(err <= atol_rel * rms), (
+        f"{what}: {int(bad.sum())} of {d.size} elements beyond {tol} ulp (max {worst}); "
+        f"max |err| {err.max():.3e} = {err.max() / rms:.3e} x RMS (limit {atol_rel:.3e} x RMS) "
+        f"at oracle value {wf[np.argmax(err)]:.6e}, got {gf[np.argmax(err)]:.6e}")
+    return worst
+
+
+def _bits_to_f32(b, f16=False):
+    b = np.asarray(b, dtype=np.uint16)
+    if f16:
+        return b.view(np.float16).astype(np.float32)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_f16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL):
+    return assert_bf16_close(got_bits, want_bits, tol, what, atol_rel, f16=True)
+
+
+def assert_f32_close(got, want, rel=F32_REL_TOL, what=""):
+    got = np.asarray(got, dtype=np.float32).reshape(-1)
+    want = np.asarray(want, dtype=np.float32).reshape(-1)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"{what}: NaN positions differ"
+    ok = ~np.isnan(want)
+    scale = float(np.sqrt(np.mean(want[ok].astype(np.float64) ** 2))) if ok.any() else 1.0
+    scale = max(scale, 1e-30)
+    err = np.abs(got[ok].astype(np.float64) - want[ok].astype(np.float64))
+    bound = rel * np.maximum(np.abs(want[ok].astype(np.float64)), scale)
+    worst = float((err / np.maximum(np.abs(want[ok]), scale)).max()) if err.size else 0.0
+    assert np.all(err <= bound), f"{what}: max relative error {worst:.3e} > {rel:g}"
+    return worst

@@ -1,0 +1,479 @@
+"""Pins the CPU oracle (oracle/lux3d_oracle.c) before it is trusted as the
+parity reference. Every function is checked against something other than a
+retyping of its own formula:
+  - the reference's own known-answer tests (file:line cited per test),
+  - an independent implementation (torch in float64),
+  - closed forms, special cases and invariants of the mathematics
+    (identity rotations, norm preservation, RoPE's relative-position
+    property, exact products for Q8_0).
+Each check is chosen so that a plausible slip (wrong sign, swapped halves,
+wrong axis, dropped term, eps in the wrong place) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import lux3d_oracle as orc
+from lux3d_fused import synth
+
+from conftest import assert_bf16_close, assert_f32_close
+
+orc.set_threads(4)
+
+
+def f64(a):
+    return torch.from_numpy(np.asarray(a, dtype=np.float64))
+
+
+def to_bf16_bits(a64: np.ndarray) -> np.ndarray:
+    """float64 -> f32 -> bf16 bits (torch RNE), for expected values."""
+    t = torch.from_numpy(np.asarray(a64, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# conversions
+# ---------------------------------------------------------------------------
+
+def test_bf16_rounding_matches_torch_and_half_nan_rule():
+    x = np.concatenate([synth.normal(1, 100000) * np.float32(1e3),
+                        np.array([0.0, -0.0, 1.0, np.inf, -np.inf, 3.3895314e38, 1e-40], dtype=np.float32)])
+    # ties: exact halfway patterns (low 16 bits 0x8000) with even and odd lsb
+    ties = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7F8000], dtype=np.uint32).view(np.float32)
+    x = np.concatenate([x, ties])
+    got = orc.bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    # half 2.x: NaN keeps sign + top payload and is made quiet (| 0x40)
+    nans = np.array([0x7F800001, 0xFF812345, 0x7FC00000], dtype=np.uint32)
+    got = orc.bf16_bits(nans.view(np.float32))
+    assert list(got) == [0x7F80 | 0x40, 0xFF81 | 0x40, 0x7FC0 | 0x40]
+
+
+def test_f16_conversions_match_numpy():
+    bits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    vals = bits.view(np.float16)
+    finite = np.isfinite(vals)
+    out = np.array([orc.LIB.or_f16_to_f32(int(b)) for b in bits[::7]], dtype=np.float32)
+    assert np.array_equal(out[finite[::7]], vals[::7][finite[::7]].astype(np.float32))
+    x = np.concatenate([synth.normal(3, 50000) * np.float32(3e3), synth.normal(4, 50000) * np.float32(1e-5)])
+    got = np.array([orc.LIB.or_f32_to_f16(float(v)) for v in x[::5]], dtype=np.uint16)
+    assert np.array_equal(got, x[::5].astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm family
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("slow", [False, True])
+def test_layer_norm_matches_torch_f64(slow):
+    x = synth.normal(10, 64 * 1024).reshape(64, 1024) * np.float32(2.0) + np.float32(0.5)
+    w = synth.normal(11, 1024, 1.0, 0.02)
+    b = synth.normal(12, 1024, 0.0, 0.02)
+    y = orc.layer_norm(x, w, b, 1e-5, slow=slow)
+    ref = F.layer_norm(f64(x), (1024,), f64(w), f64(b), eps=1e-5).numpy()
+    assert_f32_close(y, ref, what="L1/L2 vs torch")
+
+
+def test_layer_norm_bf16_single_rounding():
+    x32 = synth.normal(13, 16 * 2048).reshape(16, 2048)
+    xb = orc.bf16_bits(x32)
+    y = orc.layer_norm(xb, None, None, 1e-6, dt=orc.BF16)
+    ref = F.layer_norm(f64(orc.bf16_to_f32(xb)), (2048,), eps=1e-6).numpy()
+    assert_bf16_close(y, to_bf16_bits(ref), tol=1, what="bf16 LN")
+
+
+def test_layer_norm_invariants():
+    x = synth.normal(14, 8 * 512).reshape(8, 512)
+    y = orc.layer_norm(x, None, None, 1e-12)
+    assert np.allclose(y.mean(axis=1), 0.0, atol=1e-6)
+    assert np.allclose((y.astype(np.float64) ** 2).mean(axis=1), 1.0, atol=1e-5)
+    # shift invariance. candle's fast path uses var = E[x^2] - mean^2 (one
+    # pass), which cancels for offset rows; the composed (two-pass) path does not.
+    y2 = orc.layer_norm(x + np.float32(0.5), None, None, 1e-12)
+    assert np.max(np.abs(y2 - y)) < 5e-5
+    ys = orc.layer_norm(x, None, None, 1e-12, slow=True)
+    ys2 = orc.layer_norm(x + np.float32(7.0), None, None, 1e-12, slow=True)
+    assert np.max(np.abs(ys2 - ys)) < 5e-6
+    # constant rows: (x - mean) == 0 exactly, so the output is the bias exactly
+    c = np.full((3, 256), 1.25, dtype=np.float32)
+    b = synth.normal(15, 256)
+    for fn in (lambda: orc.layer_norm(c, np.ones(256, np.float32), b, 1e-5),
+               lambda: orc.layer_norm(c, np.ones(256, np.float32), b, 1e-5, slow=True)):
+        assert np.array_equal(fn(), np.broadcast_to(b, c.shape))
+    # eps inside the sqrt: var = 0 rows of L3 give 0 / sqrt(eps) = 0
+    assert np.array_equal(orc.layer_norm_no_affine(c, 1e-6), np.zeros_like(c))
+
+
+def test_layer_norm_no_affine_matches_torch():
+    x = synth.normal(16, 32 * 1536).reshape(32, 1536)
+    y = orc.layer_norm_no_affine(x, 1e-6)
+    assert_f32_close(y, F.layer_norm(f64(x), (1536,), eps=1e-6).numpy(), what="L3")
+
+
+def test_residual_layer_norm_reductions():
+    x = synth.normal(17, 16 * 1024).reshape(16, 1024)
+    a = synth.normal(18, 16 * 1024).reshape(16, 1024)
+    w = synth.normal(19, 1024, 1.0, 0.02)
+    b = synth.normal(20, 1024, 0.0, 0.02)
+    # gamma = 0: h == x exactly, y == L1(x)
+    h, y = orc.residual_layer_norm(x, a, np.zeros(1024, np.float32), w, b, 1e-5)
+    assert np.array_equal(h, x)
+    assert np.array_equal(y, orc.layer_norm(x, w, b, 1e-5))
+    # gamma absent (F3): h == x + a
+    h, y = orc.residual_layer_norm(x, a, None, w, b, 1e-5)
+    assert np.array_equal(h, (x + a).astype(np.float32))
+    # LayerScale gamma ~ N(1e-5, 1e-6): y vs torch on the f64 sum
+    g = synth.normal(21, 1024, 1e-5, 1e-6)
+    h, y = orc.residual_layer_norm(x, a, g, w, b, 1e-5)
+    ref_h = f64(x) + f64(a) * f64(g)
+    assert np.max(np.abs(h - ref_h.numpy())) < 1e-6
+    assert_f32_close(y, F.layer_norm(ref_h, (1024,), f64(w), f64(b), eps=1e-5).numpy(), what="F1")
+    # bf16: the norm reads the stored (rounded) residual stream
+    xb, ab = orc.bf16_bits(x), orc.bf16_bits(a)
+    hb, yb = orc.residual_layer_norm(xb, ab, g, w, b, 1e-5, dt=orc.BF16)
+    assert np.array_equal(yb, orc.layer_norm(hb, w, b, 1e-5, dt=orc.BF16))
+
+
+# ---------------------------------------------------------------------------
+# AdaLN modulate / gate / MV
+# ---------------------------------------------------------------------------
+
+def test_chunk_modulation_order_kat():
+    """tests/trellis2_blocks.rs:205-225: chunk(6) of [1..12] with C = 2."""
+    from lux3d_fused.ops import chunk_modulation
+    mod = torch.arange(1, 13, dtype=torch.float32).reshape(1, 12)
+    chunks = chunk_modulation(mod)
+    want = [[1, 2], [3, 4], [5, 6], [7, 8], [9, 10], [11, 12]]
+    for c, w in zip(chunks, want):
+        assert tuple(c.shape) == (1, 1, 2)
+        assert c.flatten().tolist() == w
+
+
+def test_adaln_modulate_against_torch_and_reductions():
+    rows, C = 40, 256
+    x = synth.normal(30, rows * C).reshape(rows, C)
+    offs = np.array([0, 15, 40], dtype=np.int64)
+    t_emb = synth.normal(31, 2 * 6 * C, 0.0, 0.1).reshape(2, 6 * C)
+    modulation = synth.normal(32, 6 * C, 0.0, 0.1)
+    piece = lambda k: np.ascontiguousarray(t_emb[:, k * C:(k + 1) * C])  # noqa: E731
+    base = lambda k: modulation[k * C:(k + 1) * C]  # noqa: E731
+    y = orc.adaln_modulate(x, offs, piece(0), piece(1), None, base(0), base(1), None, eps=1e-6)
+    n = F.layer_norm(f64(x), (C,), eps=1e-6)
+    ref = torch.empty_like(n)
+    for s in range(2):
+        r0, r1 = offs[s], offs[s + 1]
+        mv = f64(modulation) + f64(t_emb[s])       # mod_vec = modulation + t_emb
+        sh, sc = mv[0:C], mv[C:2 * C]              # chunk order: shift_msa, scale_msa, ...
+        ref[r0:r1] = n[r0:r1] * (1.0 + sc) + sh
+    assert_f32_close(y, ref.numpy(), what="M1 ragged")
+    # scale = shift = 0 reduces to L3 exactly
+    z = np.zeros((2, C), np.float32)
+    assert np.array_equal(orc.adaln_modulate(x, offs, z, z, eps=1e-6), orc.layer_norm_no_affine(x, 1e-6))
+    # gate variant (vggt.rs:399-405): gate = 0 gives x back exactly
+    yg = orc.adaln_modulate(x, offs, piece(0), piece(1), z, eps=1e-6)
+    assert np.array_equal(yg, x)
+    # gate = 1 gives modulated + x
+    yg1 = orc.adaln_modulate(x, offs, piece(0), piece(1), np.ones((2, C), np.float32), eps=1e-6)
+    y0 = orc.adaln_modulate(x, offs, piece(0), piece(1), eps=1e-6)
+    assert np.array_equal(yg1, (y0 + x).astype(np.float32))
+
+
+def test_gated_residual():
+    rows, C = 30, 128
+    x = synth.normal(33, rows * C).reshape(rows, C)
+    h = synth.normal(34, rows * C).reshape(rows, C)
+    offs = np.array([0, 10, 30], dtype=np.int64)
+    g = synth.normal(35, 2 * C, 0.0, 0.1).reshape(2, C)
+    out = orc.gated_residual(x, h, offs, g)
+    ref = f64(x).clone()
+    ref[:10] += f64(h[:10]) * f64(g[0])
+    ref[10:] += f64(h[10:]) * f64(g[1])
+    assert np.max(np.abs(out - ref.numpy())) < 1e-6
+    assert np.array_equal(orc.gated_residual(x, h, offs, np.zeros((2, C), np.float32)), x)
+
+
+# ---------------------------------------------------------------------------
+# Head norms
+# ---------------------------------------------------------------------------
+
+def test_rms_norm_heads_matches_torch():
+    x = synth.normal(40, 2 * 4 * 16 * 128).reshape(2, 4, 16, 128)
+    w = synth.normal(41, 128, 1.0, 0.02)
+    y = orc.rms_norm_heads(x, w, 1e-6)
+    xd = f64(x)
+    ref = xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + 1e-6) * f64(w)
+    assert_f32_close(y, ref.numpy(), what="N1")
+    # scale invariance for norms far above eps
+    y2 = orc.rms_norm_heads(x * np.float32(64.0), w, 1e-6)
+    assert np.max(np.abs(y2 - y)) < 1e-5
+
+
+def test_qk_l2norm_kat():
+    """tests/trellis2_blocks.rs:126-153: [3, 4, 0, 0], gamma 1 -> [1.2, 1.6, 0, 0];
+    gamma 2 -> [2.4, 3.2, 0, 0] (F.normalize * gamma * sqrt(4))."""
+    x = np.array([[[3.0, 4.0, 0.0, 0.0]]], dtype=np.float32)
+    y = orc.qk_l2norm(x, np.ones((1, 4), np.float32))
+    assert np.allclose(y.reshape(-1), [1.2, 1.6, 0.0, 0.0], atol=1e-6)
+    y = orc.qk_l2norm(x, np.full((1, 4), 2.0, np.float32))
+    assert np.allclose(y.reshape(-1), [2.4, 3.2, 0.0, 0.0], atol=1e-6)
+    # zero vector: clamp(0, 1e-12) keeps it zero (no NaN)
+    assert np.array_equal(orc.qk_l2norm(np.zeros((1, 2, 4), np.float32), np.ones((2, 4), np.float32)),
+                          np.zeros((1, 2, 4), np.float32))
+    # per-head gamma is indexed by head
+    xs = synth.normal(42, 5 * 3 * 64).reshape(5, 3, 64)
+    g = synth.normal(43, 3 * 64, 1.0, 0.1).reshape(3, 64)
+    y = orc.qk_l2norm(xs, g)
+    ref = F.normalize(f64(xs), dim=-1) * f64(g) * 8.0
+    assert_f32_close(y, ref.numpy(), what="N2")
+
+
+# ---------------------------------------------------------------------------
+# R1: VGGT 2D RoPE
+# ---------------------------------------------------------------------------
+
+def _rope2d_rotate(t, pos, d=64, base=100.0):
+    c, s = orc.rope2d_tables(pos, d, base)
+    return orc.rope2d_apply(t, c, s), c, s
+
+
+def test_rope2d_specials_are_identity_and_tables_closed_form():
+    pos = synth.vggt_positions(1, 3, 4)           # 5 specials at (0, 0)
+    c, s = orc.rope2d_tables(pos, 64, 100.0)
+    assert np.all(c[0, :5] == 1.0) and np.all(s[0, :5] == 0.0)
+    # frequency index 0 has inv_freq exactly 1: angle == position. y-half (dims
+    # 0..31) follows pos_y, x-half (32..63) pos_x; sin_alt negates the first
+    # quarter of each half.
+    tok = 5 + 2 * 4 + 3                            # patch (y=2, x=3) -> pos (3, 4)
+    assert tuple(pos[0, tok]) == (3, 4)
+    assert c[0, tok, 0] == np.float32(math.cos(3.0)) and c[0, tok, 16] == np.float32(math.cos(3.0))
+    assert c[0, tok, 32] == np.float32(math.cos(4.0))
+    assert s[0, tok, 0] == -np.float32(math.sin(3.0)) and s[0, tok, 16] == np.float32(math.sin(3.0))
+    assert s[0, tok, 48] == np.float32(math.sin(4.0))
+    # the k-th frequency is 100^(-2k/32), checked in f64
+    for k in (1, 7, 15):
+        ang = 3.0 * 100.0 ** (-2.0 * k / 32.0)
+        assert abs(c[0, tok, k] - math.cos(ang)) < 2e-7
+
+
+def test_rope2d_rotation_properties():
+    n = 40
+    pos = np.stack([synth.uniform(50, n, 0, 37).astype(np.int32),
+                    synth.uniform(51, n, 0, 37).astype(np.int32)], axis=1)[None]
+    q = synth.normal(52, 1 * 2 * n * 64).reshape(1, 2, n, 64)
+    k = synth.normal(53, 1 * 2 * n * 64).reshape(1, 2, n, 64)
+    rq, _, _ = _rope2d_rotate(q, pos)
+    # norm preservation on each rotated pair (j, j^16)
+    e_in = q[..., :16] ** 2 + q[..., 16:32] ** 2
+    e_out = rq[..., :16] ** 2 + rq[..., 16:32] ** 2
+    assert np.max(np.abs(e_in - e_out)) < 1e-4
+    # relative-position property: <R(p)q, R(p')k> depends only on p - p'
+    shift = np.array([[[7, 11]]], dtype=np.int32)
+    rk, _, _ = _rope2d_rotate(k, pos)
+    rq2, _, _ = _rope2d_rotate(q, pos + shift)
+    rk2, _, _ = _rope2d_rotate(k, pos + shift)
+    d1 = np.einsum("bhnd,bhnd->bhn", rq.astype(np.float64), rk.astype(np.float64))
+    d2 = np.einsum("bhnd,bhnd->bhn", rq2.astype(np.float64), rk2.astype(np.float64))
+    assert np.max(np.abs(d1 - d2)) < 2e-4
+    # as a complex rotation: (t[j] + i t[j+16]) * e^{i*angle} per y/x half
+    c, s = orc.rope2d_tables(pos, 64, 100.0)
+    zq = q[..., 0:16].astype(np.float64) + 1j * q[..., 16:32]
+    ang = np.arctan2(-s[:, None, :, 0:16].astype(np.float64), c[:, None, :, 0:16])
+    want = zq * np.exp(1j * ang)
+    assert np.max(np.abs(rq[..., 0:16] - want.real)) < 2e-5
+    assert np.max(np.abs(rq[..., 16:32] - want.imag)) < 2e-5
+
+
+def test_layernorm_rope2d_is_ln_then_rope():
+    pos = synth.vggt_positions(1, 5, 6)
+    n = pos.shape[1]
+    q = synth.normal(54, 2 * n * 64).reshape(1, 2, n, 64)
+    w, b = synth.normal(55, 64, 1.0, 0.05), synth.normal(56, 64, 0.0, 0.05)
+    c, s = orc.rope2d_tables(pos, 64, 100.0)
+    fused = orc.layernorm_rope2d(q, w, b, 1e-5, c, s)
+    ln = F.layer_norm(f64(q), (64,), f64(w), f64(b), eps=1e-5).numpy().astype(np.float32)
+    assert_f32_close(fused, orc.rope2d_apply(ln, c, s), what="L2+R1")
+
+
+# ---------------------------------------------------------------------------
+# R2: TRELLIS.2 3D RoPE
+# ---------------------------------------------------------------------------
+
+def test_rope3d_tables_kat():
+    """tests/trellis2_blocks.rs:43-73 (head_dim 12: freq_dim 2, freqs [1, 1e4^-0.5])."""
+    coords = np.array([[1, 0, 0], [0, 1, 0]], dtype=np.int32)
+    c, s = orc.rope3d_tables(coords, 12)
+    assert c.shape == (2, 6)
+    freq2 = 1.0 / 10000.0 ** 0.5
+    for tok, co in enumerate(coords):
+        angles = [co[0] * 1.0, co[0] * freq2, co[1] * 1.0, co[1] * freq2, co[2] * 1.0, co[2] * freq2]
+        for j, a in enumerate(angles):
+            assert abs(c[tok, j] - math.cos(a)) < 1e-6
+            assert abs(s[tok, j] - math.sin(a)) < 1e-6
+
+
+def test_rope3d_apply_kat():
+    """tests/trellis2_blocks.rs:78-111: complex product per interleaved pair,
+    the zero-angle pairs are the identity, energy is preserved."""
+    coords = np.array([[1, 0, 0]], dtype=np.int32)
+    c, s = orc.rope3d_tables(coords, 12)
+    x = np.array([1.0, 0.0, 2.0, 3.0, 5.0, 0.0, 7.0, 1.0, 0.0, 2.0, 4.0, 4.0], dtype=np.float32)
+    out = orc.rope3d_apply(x.reshape(1, 1, 1, 12), c, s).reshape(-1)
+    freq2 = 1.0 / 10000.0 ** 0.5
+    phases = [(1.0, 1.0), (freq2, freq2), (0.0, 0.0)]
+    for pair in range(6):
+        ac, as_ = (math.cos(phases[pair][0]), math.sin(phases[pair][1])) if pair < 2 else (1.0, 0.0)
+        re, im = x[2 * pair], x[2 * pair + 1]
+        assert abs(out[2 * pair] - (re * ac - im * as_)) < 1e-5
+        assert abs(out[2 * pair + 1] - (re * as_ + im * ac)) < 1e-5
+    e_in = float((x.reshape(-1, 2) ** 2).sum())
+    e_out = float((out.reshape(-1, 2) ** 2).sum())
+    assert abs(e_in - e_out) < 1e-4
+
+
+def test_rope3d_head128_layout_and_pad_pair():
+    """head_dim 128: 21 freqs per axis, axis-major (x, y, z), pair 63 is pad."""
+    coords = np.array([[5, 9, 13]], dtype=np.int32)
+    c, s = orc.rope3d_tables(coords, 128)
+    assert c.shape == (1, 64)
+    assert c[0, 63] == 1.0 and s[0, 63] == 0.0
+    for axis, val in enumerate((5, 9, 13)):
+        for i in (0, 1, 20):
+            ang = val * 10000.0 ** (-i / 21.0)
+            assert abs(c[0, axis * 21 + i] - math.cos(ang)) < 2e-6
+    x = synth.normal(60, 3 * 2 * 128).reshape(1, 3, 2, 128)
+    coords3 = np.array([[5, 9, 13], [0, 0, 0], [63, 1, 2]], dtype=np.int32)
+    c3, s3 = orc.rope3d_tables(coords3, 128)
+    y = orc.rope3d_apply(x, c3, s3)
+    assert np.array_equal(y[0, 1], x[0, 1])                    # coord (0,0,0): identity
+    assert np.array_equal(y[..., 126:], x[..., 126:])          # pad pair untouched
+    g = np.ones((2, 128), np.float32)
+    fused = orc.qk_l2norm_rope3d(x.reshape(3, 2, 128), g, c3, s3)
+    two = orc.rope3d_apply(orc.qk_l2norm(x.reshape(3, 2, 128), g).reshape(1, 3, 2, 128), c3, s3)
+    assert_f32_close(fused.reshape(-1), two.reshape(-1), what="N2+R2 fused vs composed")
+
+
+# ---------------------------------------------------------------------------
+# R3: DINOv3 RoPE
+# ---------------------------------------------------------------------------
+
+def test_dinov3_tables_kat():
+    """runtime/trellis2_dino.rs:516-569 (head_dim 8, 2x2 grid, inv_freq [1, 0.1])."""
+    c, s = orc.dinov3_rope_tables(2, 2, 8, 100.0)
+    inv = [1.0, 1.0 / 100.0 ** 0.5]
+    two_pi = 2.0 * math.pi
+    for y in range(2):
+        cy = 2.0 * ((y + 0.5) / 2) - 1.0
+        for x in range(2):
+            cx = 2.0 * ((x + 0.5) / 2) - 1.0
+            half = [two_pi * cy * f for f in inv] + [two_pi * cx * f for f in inv]
+            row = half + half
+            for j, a in enumerate(row):
+                assert abs(c[y * 2 + x, j] - math.cos(a)) < 1e-6
+                assert abs(s[y * 2 + x, j] - math.sin(a)) < 1e-6
+
+
+def test_dinov3_rotate_half_and_prefix_kat():
+    """runtime/trellis2_dino.rs:571-644: rotate_half([1..8]) = [-5..-8, 1..4];
+    prefix tokens pass through; patches get q*c + rotate_half(q)*s."""
+    x = np.arange(1, 9, dtype=np.float32).reshape(1, 1, 1, 8)
+    rh = orc.dinov3_rope_apply(x, 0, np.zeros((1, 8), np.float32), np.ones((1, 8), np.float32))
+    assert rh.reshape(-1).tolist() == [-5.0, -6.0, -7.0, -8.0, 1.0, 2.0, 3.0, 4.0]
+    npfx, patches, hd = 3, 2, 8
+    q = (0.1 * (np.arange((npfx + patches) * hd, dtype=np.float32) + 1.0)).reshape(1, 1, npfx + patches, hd)
+    cval, sval = 0.5, math.sqrt(0.5)
+    out = orc.dinov3_rope_apply(q, npfx, np.full((patches, hd), cval, np.float32),
+                                np.full((patches, hd), sval, np.float32))
+    assert np.array_equal(out[0, 0, :npfx], q[0, 0, :npfx])
+    qp = q[0, 0, npfx]
+    for d in range(hd):
+        partner = -qp[d + hd // 2] if d < hd // 2 else qp[d - hd // 2]
+        assert abs(out[0, 0, npfx, d] - (qp[d] * cval + partner * sval)) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Activations
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("act", ["gelu_erf", "gelu_tanh", "silu"])
+def test_activations_match_torch_f64(act):
+    x = np.concatenate([synth.normal(70, 200000) * np.float32(4.0),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 30.0, -30.0, 10.0, -10.0], np.float32)])
+    fn = {"gelu_erf": orc.gelu_erf, "gelu_tanh": orc.gelu_tanh, "silu": orc.silu}[act]
+    tf = {"gelu_erf": lambda t: F.gelu(t), "gelu_tanh": lambda t: F.gelu(t, approximate="tanh"),
+          "silu": F.silu}[act]
+    ref = tf(f64(x)).numpy()
+    assert_f32_close(fn(x), ref, what=act)
+    xb = orc.bf16_bits(x)
+    refb = tf(f64(orc.bf16_to_f32(xb))).numpy()
+    assert_bf16_close(fn(xb, dt=orc.BF16), to_bf16_bits(refb), tol=1, what=act + " bf16")
+
+
+# ---------------------------------------------------------------------------
+# Timestep embeddings
+# ---------------------------------------------------------------------------
+
+def test_timestep_embedding_kat_and_conventions():
+    """tests/trellis2_blocks.rs:157-171 (t = 500, dim 4, cos first)."""
+    emb = orc.timestep_embedding(np.array([500.0], np.float32), 4, cos_first=True).reshape(-1)
+    f1 = math.exp(-math.log(10000.0) / 2.0)
+    want = [math.cos(500.0), math.cos(500.0 * f1), math.sin(500.0), math.sin(500.0 * f1)]
+    assert np.allclose(emb, want, atol=1e-5)
+    # TripoSG is the same table with the halves swapped (sin first, dim = width)
+    t = synth.uniform(71, 5, 0.0, 1000.0)
+    a = orc.timestep_embedding(t, 2048, cos_first=True)
+    b = orc.timestep_embedding(t, 2048, cos_first=False)
+    assert np.array_equal(a[:, :1024], b[:, 1024:]) and np.array_equal(a[:, 1024:], b[:, :1024])
+    # odd dim: zero pad at the end
+    odd = orc.timestep_embedding(t, 7, cos_first=True)
+    assert np.all(odd[:, 6] == 0.0)
+    # frequencies follow 10000^(-i/half) (f64 check, small t keeps the arguments exact-ish)
+    small = orc.timestep_embedding(np.array([1.0], np.float32), 256, cos_first=True).reshape(-1)
+    i = np.arange(128)
+    assert np.max(np.abs(small[:128] - np.cos(10000.0 ** (-i / 128.0)))) < 2e-7
+
+
+# ---------------------------------------------------------------------------
+# Q8_0
+# ---------------------------------------------------------------------------
+
+def test_q8_0_dequant_brute_force():
+    scales = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0xBC00, 0x7BFF, 0xFBFF,
+                       0x1234, 0x2E66, 0x7C00, 0xFC00, 0x7E00], dtype=np.uint16)
+    qs = np.arange(-128, 128, dtype=np.int16).astype(np.int8).reshape(8, 32)
+    blocks = np.empty((len(scales) * 8, 34), dtype=np.uint8)
+    for si, sc in enumerate(scales):
+        for r in range(8):
+            blocks[si * 8 + r, 0] = sc & 0xFF          # little-endian f16 scale
+            blocks[si * 8 + r, 1] = sc >> 8
+            blocks[si * 8 + r, 2:] = qs[r].view(np.uint8)
+    d = np.repeat(scales.view(np.float16).astype(np.float32), 8 * 32)
+    q = np.tile(qs.reshape(-1).astype(np.float32), len(scales))
+    with np.errstate(invalid="ignore"):
+        exact = (q * d).astype(np.float32)                 # exact: <= 7 x 11 significant bits
+    got32 = orc.dequant_q8_0(blocks, orc.F32)
+    assert np.array_equal(np.isnan(got32), np.isnan(exact))
+    fin = ~np.isnan(exact)
+    assert np.array_equal(got32[fin].view(np.uint32), exact[fin].view(np.uint32))
+    got_b = orc.dequant_q8_0(blocks, orc.BF16)
+    want_b = torch.from_numpy(exact).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got_b[fin], want_b[fin])
+    assert np.all((got_b[~fin] & 0x7FFF) > 0x7F80)
+    got_h = orc.dequant_q8_0(blocks, orc.F16)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want_h = exact.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got_h[fin], want_h[fin])
+
+
+def test_threads_do_not_change_results():
+    x = synth.normal(80, 300 * 1024).reshape(300, 1024)
+    w = synth.normal(81, 1024, 1.0, 0.02)
+    orc.set_threads(1)
+    a = orc.layer_norm(x, w, None, 1e-5)
+    orc.set_threads(7)
+    b = orc.layer_norm(x, w, None, 1e-5)
+    orc.set_threads(4)
+    assert np.array_equal(a, b)
