@@ -53,6 +53,39 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t v) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-byte streaming accesses. Activations are touched exactly once per op, so
+// they are loaded and stored non-temporally (the "nt" cache policy: streamed
+// through L2 / the Infinity Cache without displacing reused data such as the
+// per-channel parameters). LUX3D_NT_STREAMS=0 selects plain accesses (used to
+// measure the difference).
+// ---------------------------------------------------------------------------
+#ifndef LUX3D_NT_STREAMS
+#define LUX3D_NT_STREAMS 1
+#endif
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <bool NT = (LUX3D_NT_STREAMS != 0)>
+__device__ __forceinline__ uint4 ld16(const void *p) {
+  if constexpr (NT) {
+    u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+
+template <bool NT = (LUX3D_NT_STREAMS != 0)>
+__device__ __forceinline__ void st16(void *p, uint4 v) {
+  if constexpr (NT) {
+    u32x4_t t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t *>(p));
+  } else {
+    *reinterpret_cast<uint4 *>(p) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // dtype tags and 8-element chunk I/O
 // ---------------------------------------------------------------------------
 
@@ -63,8 +96,9 @@ struct F16 { static constexpr int code = LUX3D_F16; static constexpr int bytes =
 template <typename T> struct Chunk;
 
 template <> struct Chunk<BF16> {
+  template <bool NT = (LUX3D_NT_STREAMS != 0)>
   __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
-    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint4 u = ld16<NT>(p);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -78,7 +112,7 @@ template <> struct Chunk<BF16> {
     u.y = pack_bf16x2(v[2], v[3]);
     u.z = pack_bf16x2(v[4], v[5]);
     u.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4 *>(p) = u;
+    st16(p, u);
   }
   // value as it reads back after a store (for outputs that are re-read)
   __device__ __forceinline__ static float round_trip(float f) {
@@ -87,8 +121,9 @@ template <> struct Chunk<BF16> {
 };
 
 template <> struct Chunk<F16> {
+  template <bool NT = (LUX3D_NT_STREAMS != 0)>
   __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
-    uint4 u = *reinterpret_cast<const uint4 *>(p);
+    uint4 u = ld16<NT>(p);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -102,7 +137,7 @@ template <> struct Chunk<F16> {
     u.y = pack_f16x2(v[2], v[3]);
     u.z = pack_f16x2(v[4], v[5]);
     u.w = pack_f16x2(v[6], v[7]);
-    *reinterpret_cast<uint4 *>(p) = u;
+    st16(p, u);
   }
   __device__ __forceinline__ static float round_trip(float f) {
     return f16_bits_to_f32(pack_f16x2(f, 0.f) & 0xFFFFu);
@@ -110,16 +145,17 @@ template <> struct Chunk<F16> {
 };
 
 template <> struct Chunk<F32> {
+  template <bool NT = (LUX3D_NT_STREAMS != 0)>
   __device__ __forceinline__ static void load(const void *p, float (&v)[8]) {
-    const float4 *q = reinterpret_cast<const float4 *>(p);
-    float4 a = q[0], b = q[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    const char *c = reinterpret_cast<const char *>(p);
+    uint4 a = ld16<NT>(c), b = ld16<NT>(c + 16);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
   }
   __device__ __forceinline__ static void store(void *p, const float (&v)[8]) {
-    float4 *q = reinterpret_cast<float4 *>(p);
-    q[0] = make_float4(v[0], v[1], v[2], v[3]);
-    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+    char *c = reinterpret_cast<char *>(p);
+    st16(c, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])));
+    st16(c + 16, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])));
   }
   __device__ __forceinline__ static float round_trip(float f) { return f; }
 };
@@ -158,12 +194,13 @@ __device__ __forceinline__ float param1(const void *p, int dt, int64_t i, float 
 // 8 consecutive parameters starting at element i (i a multiple of 8 and the
 // base 16-byte aligned: checked on the host before a vector kernel is chosen).
 __device__ __forceinline__ void param8(const void *p, int dt, int64_t i, float dflt, float (&v)[8]) {
+  // parameters are re-read by every row: plain (cached) loads
   if (dt == LUX3D_F32) {
-    Chunk<F32>::load(reinterpret_cast<const float *>(p) + i, v);
+    Chunk<F32>::load<false>(reinterpret_cast<const float *>(p) + i, v);
   } else if (dt == LUX3D_BF16) {
-    Chunk<BF16>::load(reinterpret_cast<const uint16_t *>(p) + i, v);
+    Chunk<BF16>::load<false>(reinterpret_cast<const uint16_t *>(p) + i, v);
   } else if (dt == LUX3D_F16) {
-    Chunk<F16>::load(reinterpret_cast<const uint16_t *>(p) + i, v);
+    Chunk<F16>::load<false>(reinterpret_cast<const uint16_t *>(p) + i, v);
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = dflt;

@@ -208,15 +208,22 @@ template <typename T, int MODE>
 hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   if (p.rows <= 0) return hipSuccess;
   const int64_t chunks = p.d / 8;
-  // Rows per wavefront-group: one wave per row when there are enough rows to
-  // fill 256 CUs several times over, otherwise split each row over 2 or 4
-  // waves so short jobs (DINOv3's 1029 tokens) still occupy the chip.
+  // Threads per row (TPR). Short jobs (DINOv2/DINOv3's ~1k tokens) split each
+  // row over 2 or 4 wavefronts so the chip is still occupied. For long jobs
+  // the layout is the one measured fastest on MI355X at the configs shapes:
+  // the fused residual + LayerNorm (two input streams) and the gated residual
+  // run a row on 2 wavefronts with one chunk per lane (configs[1] F1: 18.4 us
+  // vs 20.0 us on one wavefront), the single-stream LayerNorm / modulate on
+  // one wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs
+  // 9.4 us on 2 wavefronts).
   int tpr = 0, nc = 0;
   if (vec) {
-    const int prefs[3] = {p.rows >= 4096 ? 64 : (p.rows >= 2048 ? 128 : 256),
-                          p.rows >= 2048 ? 128 : 64, 64};
-    const int order[3][3] = {{64, 128, 256}, {128, 64, 256}, {256, 128, 64}};
-    const int *ord = prefs[0] == 64 ? order[0] : (prefs[0] == 128 ? order[1] : order[2]);
+    int ord[3] = {64, 128, 256};
+    if (p.rows < 2048) {
+      ord[0] = 256; ord[1] = 128; ord[2] = 64;
+    } else if (MODE == ROW_RESID_LN || MODE == ROW_GATE) {
+      if (chunks % 128 == 0 && chunks / 128 <= 2) { ord[0] = 128; ord[1] = 64; }
+    }
     for (int i = 0; i < 3 && !tpr; ++i) {
       const int cand = ord[i];
       if (chunks % cand) continue;

@@ -2,11 +2,12 @@
 // sinusoidal timestep embeddings and the bit-exact GGML Q8_0 dequant.
 //
 // Activations are pure HBM streams (one read, one write per element). Each
-// thread moves kUnroll chunks of 8 elements; the loads of all chunks are
-// issued before any arithmetic, and consecutive lanes touch consecutive
-// 16-byte chunks, so each wavefront keeps 4 KiB (bf16) in flight. The
-// transcendental work is kept to one exp2 + one reciprocal per element for
-// the tanh GELU and SiLU (hardware v_exp_f32 / v_rcp_f32).
+// thread moves one 16-byte chunk of 8 elements (measured on MI355X: one chunk
+// per thread streams at 6.0 TB/s for configs[2], 2 and 4 chunks per thread at
+// 5.8 / 5.5 TB/s), consecutive lanes touch consecutive chunks, and the
+// activations are loaded and stored non-temporally. The transcendental work is
+// one exp2 + one reciprocal per element for the tanh GELU and SiLU (hardware
+// v_exp_f32 / v_rcp_f32).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -15,7 +16,7 @@ namespace lux3d {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
@@ -39,18 +40,18 @@ template <int ACT> __device__ __forceinline__ float act(float x) {
   }
 }
 
-template <typename T, int ACT>
+template <typename T, int ACT, int U = kUnroll>
 __global__ __launch_bounds__(kBlock) void act_kernel(const void *x, void *y, int64_t nchunks) {
   constexpr int EB = T::bytes;
-  const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
-  float v[kUnroll][8];
+  const int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
+  float v[U][8];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t c = base + u * kBlock;
     if (c < nchunks) Chunk<T>::load(reinterpret_cast<const char *>(x) + c * 8 * EB, v[u]);
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int64_t c = base + u * kBlock;
     if (c < nchunks) {
 #pragma unroll

@@ -31,159 +31,218 @@ __device__ __forceinline__ int64_t load_index(const void *p, int dt, int64_t i) 
                          : (int64_t)reinterpret_cast<const int32_t *>(p)[i];
 }
 
-// Phase (C[j], S[j]) of element j for token (b, n): out[j] = y[j]*C[j] +
-// y[j ^ M]*S[j]. (DINOv3 prefix tokens never reach this: they are not rotated.)
+// Stage the rotation of the tile's tokens into LDS: Cs[t*D + j], Ss[t*D + j]
+// for tile token t and element j, so that out[j] = y[j]*C[j] + y[j^M]*S[j].
+// Angle-based sources compute each distinct angle once (D/2 per token) and
+// write the two elements that share it.
 template <int ROT, int D>
-__device__ __forceinline__ void phase(const HeadParams &p, int64_t b, int64_t n, int j, float &C,
-                                      float &S) {
-  if constexpr (ROT == HR_R1_TAB) {
-    const int64_t off = b * p.tab_sB + n * p.tab_sN + j;
-    C = param1(p.tab_c, p.tab_dt, off, 1.f);
-    S = param1(p.tab_s, p.tab_dt, off, 0.f);
-  } else if constexpr (ROT == HR_R1_POS) {
-    // Rope2d: half = D/2 per axis (y then x), table row [f, f] of D/4 freqs,
-    // sin negated on the first quarter of each half (sin_alt).
-    constexpr int half = D / 2, quarter = D / 4;
-    const int axis = j / half, jj = j % half;
-    const uint32_t pv = (uint32_t)load_index(p.pos, p.pos_dt, b * p.pos_sB + n * p.pos_sN + axis * p.pos_sC);
-    const float ang = (float)pv * p.freq[jj % quarter];
-    float sv, cv;
-    sincosf(ang, &sv, &cv);
-    C = cv;
-    S = jj < quarter ? -sv : sv;
-  } else if constexpr (ROT == HR_R2_TAB || ROT == HR_R2_COORD) {
-    const int i = j >> 1;
-    float cv, sv;
-    if constexpr (ROT == HR_R2_TAB) {
-      const int64_t off = n * p.tab_sN + i;
-      cv = param1(p.tab_c, p.tab_dt, off, 1.f);
-      sv = param1(p.tab_s, p.tab_dt, off, 0.f);
-    } else {
-      float ang = 0.f;
-      if (i < 3 * p.nfreq) {
-        const int axis = i / p.nfreq;
-        const int32_t cval = reinterpret_cast<const int32_t *>(p.pos)[n * p.pos_sN + axis * p.pos_sC];
-        ang = (float)cval * p.freq[i % p.nfreq];
+__device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0, int tb, uint32_t ntok,
+                                             uint32_t N, float *Cs, float *Ss) {
+  constexpr int half = D / 2, quarter = D / 4;
+  if constexpr (ROT == HR_R1_TAB || ROT == HR_R3_TAB) {
+    for (int e = threadIdx.x; e < tb * D; e += blockDim.x) {
+      const int t = e / D, j = e % D;
+      uint32_t tok = tok0 + t;
+      tok = tok < ntok ? tok : ntok - 1;
+      const uint32_t b = tok / N, n = tok % N;
+      float C = 1.f, S = 0.f;
+      if constexpr (ROT == HR_R1_TAB) {
+        const int64_t off = (int64_t)b * p.tab_sB + (int64_t)n * p.tab_sN + j;
+        C = param1(p.tab_c, p.tab_dt, off, 1.f);
+        S = param1(p.tab_s, p.tab_dt, off, 0.f);
+      } else if (n >= p.prefix) {
+        const int64_t off = (int64_t)(n - p.prefix) * p.tab_sN + j;
+        C = param1(p.tab_c, p.tab_dt, off, 1.f);
+        const float sv = param1(p.tab_s, p.tab_dt, off, 0.f);
+        S = j < half ? -sv : sv;  // rotate_half = cat(-x2, x1)
       }
-      sincosf(ang, &sv, &cv);
+      Cs[e] = C;
+      Ss[e] = S;
     }
-    C = cv;
-    S = (j & 1) ? sv : -sv;
-  } else if constexpr (ROT == HR_R3_TAB) {
-    const int64_t off = (n - p.prefix) * p.tab_sN + j;
-    C = param1(p.tab_c, p.tab_dt, off, 1.f);
-    const float sv = param1(p.tab_s, p.tab_dt, off, 0.f);
-    S = j < D / 2 ? -sv : sv;
   } else {
-    C = 1.f;
-    S = 0.f;
+    for (int e = threadIdx.x; e < tb * half; e += blockDim.x) {
+      const int t = e / half, a = e % half;
+      uint32_t tok = tok0 + t;
+      tok = tok < ntok ? tok : ntok - 1;
+      const uint32_t b = tok / N, n = tok % N;
+      float cv, sv;
+      int j0, j1;
+      if constexpr (ROT == HR_R1_POS) {
+        // Rope2d: angle a = (axis, k); elements axis*half + k (sin negated:
+        // the sin_alt quarter) and axis*half + quarter + k share it.
+        const int axis = a / quarter, k = a % quarter;
+        const uint32_t pv = (uint32_t)load_index(
+            p.pos, p.pos_dt, (int64_t)b * p.pos_sB + (int64_t)n * p.pos_sN + axis * p.pos_sC);
+        sincosf((float)pv * p.freq[k], &sv, &cv);
+        j0 = axis * half + k;
+        j1 = j0 + quarter;
+      } else {
+        // TRELLIS.2: pair a = (re, im) = elements (2a, 2a+1); angle axis-major,
+        // the trailing pad pairs have angle 0.
+        if constexpr (ROT == HR_R2_TAB) {
+          const int64_t off = (int64_t)n * p.tab_sN + a;
+          cv = param1(p.tab_c, p.tab_dt, off, 1.f);
+          sv = param1(p.tab_s, p.tab_dt, off, 0.f);
+        } else {
+          float ang = 0.f;
+          if (a < 3 * p.nfreq) {
+            const int axis = a / p.nfreq;
+            const int32_t cval = reinterpret_cast<const int32_t *>(p.pos)[(int64_t)n * p.pos_sN + axis * p.pos_sC];
+            ang = (float)cval * p.freq[a % p.nfreq];
+          }
+          sincosf(ang, &sv, &cv);
+        }
+        j0 = 2 * a;
+        j1 = 2 * a + 1;
+      }
+      Cs[t * D + j0] = cv;
+      Ss[t * D + j0] = -sv;
+      Cs[t * D + j1] = cv;
+      Ss[t * D + j1] = sv;
+    }
   }
 }
 
-template <typename T, int D, int NORM, int ROT>
-__global__ __launch_bounds__(512) void head_kernel(HeadParams p) {
+// Workgroup barrier for LDS only: waits for this wave's LDS writes, then
+// s_barrier. Unlike __syncthreads() it does not drain the wave's outstanding
+// global loads, so the row data requested before the phase staging stays in
+// flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt left at their maximum
+  __builtin_amdgcn_s_barrier();
+}
+
+// Grid: x = tiles of `tb` consecutive tokens, y = tensor (q, k). Work items
+// are (token, head) rows of LPR lanes; each thread owns R of the tile's rows.
+// Order of work per workgroup: issue every row load (and the per-channel
+// parameters), then stage the tile's rotation phases in LDS while those loads
+// are in flight, one LDS barrier, then normalise / rotate / store. Each
+// workgroup therefore waits on one HBM round trip. Rows of one head are
+// adjacent in the [B, H, N, D] output across the tile's tokens, so a head's
+// stores form contiguous runs of tb*D elements.
+template <typename T, int D, int NORM, int ROT, int R>
+__global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   constexpr int LPR = D / 8;
   constexpr int M = RotPartner<ROT, D>::M;
   constexpr int EB = T::bytes;
-  __shared__ float Cs[D], Ss[D];
+  extern __shared__ float lds[];
+  float *Cs = lds, *Ss = lds + tb * D;
 
-  const int64_t tok = blockIdx.x;
-  const int64_t b = tok / p.N, n = tok % p.N;
-  bool rotate = ROT != HR_NONE;
-  if constexpr (ROT == HR_R3_TAB) rotate = n >= p.prefix;
+  const HeadIO io = p.io[blockIdx.y];
+  const uint32_t N = (uint32_t)p.N, H = (uint32_t)p.H;
+  const uint32_t ntok = (uint32_t)(p.B * p.N);
+  const uint32_t tok0 = blockIdx.x * (uint32_t)tb;
+  const int lane = threadIdx.x % LPR;
+  const int ipp = blockDim.x / LPR;
+  const uint32_t items = (uint32_t)tb * H;
+
+  float v[R][8];
+  uint32_t tt[R], hh[R], nn[R], bb[R];
+  bool live[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t it = (uint32_t)(r * ipp) + threadIdx.x / LPR;
+    uint32_t t = it / H, h = it % H;
+    uint32_t tok = tok0 + t;
+    live[r] = it < items && tok < ntok;
+    if (!live[r]) { t = 0; h = 0; tok = tok0; }
+    const uint32_t b = tok / N, n = tok % N;
+    tt[r] = t; hh[r] = h; nn[r] = n; bb[r] = b;
+    const char *xp = reinterpret_cast<const char *>(io.x) +
+                     ((int64_t)b * io.sB + (int64_t)h * io.sH + (int64_t)n * io.sN + lane * 8) * EB;
+    Chunk<T>::load(xp, v[r]);
+  }
+  float w[8], bias[8];
+  if constexpr (NORM == HN_LN || NORM == HN_RMS) param8(io.p0, io.p0_dt, lane * 8, 1.f, w);
+  if constexpr (NORM == HN_LN) param8(io.p1, io.p1_dt, lane * 8, 0.f, bias);
+
   if constexpr (ROT != HR_NONE) {
-    if (rotate) {
-      for (int j = threadIdx.x; j < D; j += blockDim.x) phase<ROT, D>(p, b, n, j, Cs[j], Ss[j]);
-    }
-    __syncthreads();
+    stage_phases<ROT, D>(p, tok0, tb, ntok, N, Cs, Ss);
+    lds_barrier();
   }
 
-  const int lane = threadIdx.x % LPR;
-  const int rows_per_pass = blockDim.x / LPR;
-  const int64_t nrows = (int64_t)p.ntens * p.H;
-  for (int64_t slot = threadIdx.x / LPR; slot < nrows; slot += rows_per_pass) {
-    const int ti = slot >= p.H ? 1 : 0;
-    const int64_t h = slot - (int64_t)ti * p.H;
-    const HeadIO &io = ti ? p.io[1] : p.io[0];
-    float v[8];
-    const char *xp = reinterpret_cast<const char *>(io.x) +
-                     (b * io.sB + h * io.sH + n * io.sN + lane * 8) * EB;
-    Chunk<T>::load(xp, v);
-
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
     if constexpr (NORM == HN_LN) {
       float s = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) s += v[k];
+      for (int k = 0; k < 8; ++k) s += v[r][k];
       const float mean = group_sum<LPR>(s) * (1.0f / D);
       float s2 = 0.f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        v[k] -= mean;
-        s2 += v[k] * v[k];
+        v[r][k] -= mean;
+        s2 += v[r][k] * v[r][k];
       }
       const float rstd = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
-      float w[8], bb[8];
-      param8(io.p0, io.p0_dt, lane * 8, 1.f, w);
-      param8(io.p1, io.p1_dt, lane * 8, 0.f, bb);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = v[k] * rstd * w[k] + bb[k];
+      for (int k = 0; k < 8; ++k) v[r][k] = v[r][k] * rstd * w[k] + bias[k];
     } else if constexpr (NORM == HN_RMS) {
       float s2 = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) s2 += v[k] * v[k];
-      const float r = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
-      float w[8];
-      param8(io.p0, io.p0_dt, lane * 8, 1.f, w);
+      for (int k = 0; k < 8; ++k) s2 += v[r][k] * v[r][k];
+      const float rr = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = (v[k] * r) * w[k];
+      for (int k = 0; k < 8; ++k) v[r][k] = (v[r][k] * rr) * w[k];
     } else if constexpr (NORM == HN_L2) {
       float s2 = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) s2 += v[k] * v[k];
+      for (int k = 0; k < 8; ++k) s2 += v[r][k] * v[r][k];
       const float nrm = fminf(fmaxf(sqrtf(group_sum<LPR>(s2)), 1e-12f), 1.0e30f);
-      const float r = 1.0f / nrm;
+      const float rr = 1.0f / nrm;
       const float scale = sqrtf((float)D);
       float g[8];
-      param8(io.p0, io.p0_dt, h * D + lane * 8, 1.f, g);
+      param8(io.p0, io.p0_dt, (int64_t)hh[r] * D + lane * 8, 1.f, g);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = ((v[k] * r) * g[k]) * scale;
+      for (int k = 0; k < 8; ++k) v[r][k] = ((v[r][k] * rr) * g[k]) * scale;
     }
-
     if constexpr (ROT != HR_NONE) {
+      bool rotate = true;
+      if constexpr (ROT == HR_R3_TAB) rotate = nn[r] >= (uint32_t)p.prefix;  // prefix tokens pass through
       if (rotate) {
         float pv[8];
         if constexpr (M < 8) {
 #pragma unroll
-          for (int k = 0; k < 8; ++k) pv[k] = v[k ^ M];
+          for (int k = 0; k < 8; ++k) pv[k] = v[r][k ^ M];
         } else {
 #pragma unroll
-          for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 8>(v[k]);
+          for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 8>(v[r][k]);
         }
-        const int j0 = lane * 8;
+        const float *C = Cs + tt[r] * D + lane * 8;
+        const float *S = Ss + tt[r] * D + lane * 8;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = __fadd_rn(__fmul_rn(v[k], Cs[j0 + k]), __fmul_rn(pv[k], Ss[j0 + k]));
+        for (int k = 0; k < 8; ++k) v[r][k] = __fadd_rn(__fmul_rn(v[r][k], C[k]), __fmul_rn(pv[k], S[k]));
       }
     }
-
-    char *yp = reinterpret_cast<char *>(io.y) + (b * io.oB + h * io.oH + n * io.oN + lane * 8) * EB;
-    Chunk<T>::store(yp, v);
+    if (live[r]) {
+      char *yp = reinterpret_cast<char *>(io.y) +
+                 ((int64_t)bb[r] * io.oB + (int64_t)hh[r] * io.oH + (int64_t)nn[r] * io.oN + lane * 8) * EB;
+      Chunk<T>::store(yp, v[r]);
+    }
   }
 }
 
 template <typename T, int D>
 hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
   const int64_t tokens = p.B * p.N;
-  if (tokens <= 0) return hipSuccess;
+  if (tokens <= 0 || p.H <= 0) return hipSuccess;
+  if (tokens > INT32_MAX || p.H > 4096) return hipErrorInvalidValue;
   constexpr int LPR = D / 8;
-  int64_t threads = (int64_t)p.ntens * p.H * LPR;
-  if (threads <= 0) return hipSuccess;  // no heads: nothing to do
-  threads = ((threads + 63) / 64) * 64;
-  if (threads > 512) threads = 512;
-  const dim3 grid((unsigned)tokens), block((unsigned)threads);
-#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                  \
-  if (norm == NORM_ && rot == ROT_) {                                                 \
-    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_>), grid, block, 0, s, p);       \
-    return hipGetLastError();                                                         \
+  constexpr int R = T::bytes == 4 ? 1 : 2;
+  // Whole heads per pass: threads = k*H*LPR rounded to wavefronts, <= 256.
+  const int64_t hl = p.H * LPR;
+  int64_t k = hl >= 256 ? 1 : 256 / hl;
+  int64_t threads = ((k * hl + 63) / 64) * 64;
+  if (threads > 256) threads = 256;
+  const int64_t ipp = threads / LPR;
+  int64_t tb = (R * ipp) / p.H;
+  if (tb < 1) return hipErrorInvalidValue;  // more heads than one pass holds (H*D > 2048)
+  const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
+  const dim3 grid((unsigned)((tokens + tb - 1) / tb), (unsigned)p.ntens), block((unsigned)threads);
+#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                              \
+  if (norm == NORM_ && rot == ROT_) {                                                             \
+    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R>), grid, block, lds, s, p, (int)tb);     \
+    return hipGetLastError();                                                                     \
   }
   LUX3D_HEAD_CASE(HN_LN, HR_R1_TAB) LUX3D_HEAD_CASE(HN_LN, HR_R1_POS)
   LUX3D_HEAD_CASE(HN_NONE, HR_R1_TAB) LUX3D_HEAD_CASE(HN_NONE, HR_R1_POS)

@@ -74,6 +74,12 @@ class Lux3dError(RuntimeError):
 
 
 def _load() -> ctypes.CDLL:
+    # PyTorch-ROCm ships its own libamdhip64.so / libhsa-runtime64.so. Import
+    # it first so that liblux3d_fused.so's libamdhip64.so.7 dependency
+    # resolves (by soname) to the runtime torch already loaded: two HIP
+    # runtimes in one process each open the device and the second one reports
+    # "no ROCm-capable device".
+    import torch  # noqa: F401
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is not built; run `make -C candle-3d_amd` (or __graft_entry__.build())"

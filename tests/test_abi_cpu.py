@@ -1,0 +1,180 @@
+"""The C ABI without a GPU: liblux3d_fused.so loads, exports every entry
+point that include/lux3d_fused.h declares (and nothing is missing from the
+ctypes binding), and invalid arguments are rejected on the host with the
+documented status codes and a message, before any HIP call is made. The
+descriptors here point at fake addresses that are never dereferenced: every
+call below must fail validation."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from lux3d_fused import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lux3d_fused.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lux3d_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = header_functions()
+    assert "lux3d_layer_norm" in names and "lux3d_dequant_q8_0" in names
+    assert len(names) == len(_lib.SIGNATURES) + 2  # + abi_version, last_error
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (lux3d_[a-z0-9_]+)", out))
+    missing = [n for n in header_functions() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for n in header_functions():
+        assert hasattr(_lib.LIB, n)
+    assert set(_lib.SIGNATURES) <= exported
+
+
+def test_abi_version():
+    assert _lib.LIB.lux3d_abi_version() == 1
+    assert _lib.ABI_VERSION == 1
+
+
+FAKE = 0x100000  # 16-byte aligned fake device address; never dereferenced
+
+
+def T(shape, dtype=_lib.BF16, strides=None, data=FAKE):
+    if strides is None:
+        strides, acc = [], 1
+        for n in reversed(shape):
+            strides.insert(0, acc)
+            acc *= n
+    return ctypes.pointer(_lib.descriptor(data, dtype, shape, strides))
+
+
+def status(name, *args):
+    rc, msg = _lib.call_status(name, *args)
+    return rc, msg
+
+
+def test_layer_norm_argument_errors():
+    x = T([4, 64])
+    rc, msg = status("lux3d_layer_norm", None, None, None, 1e-5, x, None)
+    assert rc == _lib.ERR_NULL and "`x` is NULL" in msg
+    rc, msg = status("lux3d_layer_norm", x, T([32], _lib.F32), None, 1e-5, x, None)
+    assert rc == _lib.ERR_SHAPE and "`w`" in msg
+    rc, msg = status("lux3d_layer_norm", x, None, None, 1e-5, T([4, 64], _lib.F32), None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_layer_norm", x, None, None, 1e-5, T([4, 32]), None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_layer_norm", T([4, 64], strides=[64, 2]), None, None, 1e-5, x, None)
+    assert rc == _lib.ERR_LAYOUT
+    rc, msg = status("lux3d_layer_norm", T([4, 64], _lib.I32), None, None, 1e-5, x, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_layer_norm", x, None, None, -1.0, x, None)
+    assert rc == _lib.ERR_VALUE
+    bad_rank = _lib.descriptor(FAKE, _lib.BF16, [4], [1])
+    bad_rank.rank = 0
+    rc, msg = status("lux3d_layer_norm", ctypes.pointer(bad_rank), None, None, 1e-5, x, None)
+    assert rc == _lib.ERR_SHAPE
+    # leading dims that do not form a uniform row stride
+    rc, msg = status("lux3d_layer_norm", T([2, 3, 64], strides=[1000, 64, 1]), None, None, 1e-5, T([2, 3, 64]),
+                     None)
+    assert rc == _lib.ERR_LAYOUT
+
+
+def test_residual_and_modulate_errors():
+    x = T([8, 128])
+    rc, msg = status("lux3d_residual_layer_norm", x, T([8, 64]), None, None, None, 1e-5, x, x, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_adaln_modulate", x, None, None, None, T([2, 128], _lib.F32), None, None, None, 1e-6, x,
+                     None)
+    assert rc == _lib.ERR_NULL
+    # 8 rows do not split into 3 equal segments without offsets
+    sh = T([3, 128], _lib.F32)
+    rc, msg = status("lux3d_adaln_modulate", x, None, sh, None, sh, None, None, None, 1e-6, x, None)
+    assert rc == _lib.ERR_SHAPE and "seg_offsets" in msg
+    # offsets must be int64 [S+1]
+    rc, msg = status("lux3d_adaln_modulate", x, T([4], _lib.I32), sh, None, sh, None, None, None, 1e-6, x, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_adaln_modulate", x, T([3], _lib.I64), sh, None, sh, None, None, None, 1e-6, x, None)
+    assert rc == _lib.ERR_SHAPE
+    # base without piece
+    rc, msg = status("lux3d_gated_residual", x, x, None, None, T([128], _lib.F32), x, None)
+    assert rc == _lib.ERR_NULL
+
+
+def test_head_op_errors():
+    q = T([2, 16, 10, 64], strides=[10 * 3 * 16 * 64, 64, 3 * 16 * 64, 1])
+    out = T([2, 16, 10, 64])
+    tab = T([2, 10, 64], _lib.F32)
+    # head dim 32 unsupported
+    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 32]), None, None, None, None, None, 1e-5, tab, tab,
+                     T([2, 16, 10, 32]), None, None)
+    assert rc == _lib.ERR_SHAPE and "head dim" in msg
+    # wrong table shape
+    rc, msg = status("lux3d_qk_layernorm_rope2d", q, None, None, None, None, None, 1e-5, T([2, 11, 64], _lib.F32),
+                     tab, out, None, None)
+    assert rc == _lib.ERR_SHAPE
+    # LayerNorm needs both w and b
+    rc, msg = status("lux3d_qk_layernorm_rope2d", q, T([64], _lib.F32), None, None, None, None, 1e-5, tab, tab, out,
+                     None, None)
+    assert rc == _lib.ERR_NULL
+    # misaligned head rows
+    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 64], data=FAKE + 2), None, None, None, None, None,
+                     1e-5, tab, tab, out, None, None)
+    assert rc == _lib.ERR_LAYOUT
+    # positions must be [B, N, 2] int
+    rc, msg = status("lux3d_qk_layernorm_rope2d_pos", q, None, None, None, None, None, 1e-5,
+                     T([2, 10, 2], _lib.F32), 100.0, out, None, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_qk_layernorm_rope2d_pos", q, None, None, None, None, None, 1e-5,
+                     T([2, 10, 2], _lib.I32), -1.0, out, None, None)
+    assert rc == _lib.ERR_VALUE
+    # rope3d: tables and coords together are ambiguous
+    x = T([1, 10, 12, 128])
+    rc, msg = status("lux3d_qk_l2norm_rope3d", x, None, None, None, T([10, 64], _lib.F32), T([10, 64], _lib.F32),
+                     T([10, 3], _lib.I32), 10000.0, x, None, None)
+    assert rc == _lib.ERR_VALUE
+    rc, msg = status("lux3d_qk_l2norm_rope3d", x, T([12, 64], _lib.F32), None, None, None, None, None, 10000.0, x,
+                     None, None)
+    assert rc == _lib.ERR_SHAPE   # gamma must be [H, D] = 12*128 elements
+    # dinov3: prefix larger than the sequence
+    y = T([1, 16, 9, 64])
+    rc, msg = status("lux3d_dinov3_rope", y, None, T([4, 64], _lib.F32), T([4, 64], _lib.F32), 10, y, None, None)
+    assert rc == _lib.ERR_VALUE
+
+
+def test_pointwise_errors():
+    x = T([100])
+    rc, msg = status("lux3d_gelu_tanh", x, T([99]), None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_silu", x, T([100], _lib.F32), None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_gelu_erf", T([10, 10], strides=[20, 1]), T([10, 10]), None)
+    assert rc == _lib.ERR_LAYOUT
+    rc, msg = status("lux3d_timestep_embedding", T([2], _lib.F32), None, 255, 0, T([2, 255], _lib.F32), None)
+    assert rc == _lib.ERR_VALUE     # sin-first needs an even dim
+    rc, msg = status("lux3d_timestep_embedding", T([2], _lib.F32), T([100], _lib.F32), 256, 1,
+                     T([2, 256], _lib.F32), None)
+    assert rc == _lib.ERR_SHAPE     # freqs must hold dim/2 values
+    rc, msg = status("lux3d_dequant_q8_0", T([35], _lib.U8), T([32]), None)
+    assert rc == _lib.ERR_SHAPE and "34-byte" in msg
+    rc, msg = status("lux3d_dequant_q8_0", T([68], _lib.U8), T([32]), None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_dequant_q8_0", T([34], _lib.U8, data=FAKE + 1), T([32]), None)
+    assert rc == _lib.ERR_LAYOUT
+    rc, msg = status("lux3d_dequant_q8_0", T([34], _lib.F32), T([32]), None)
+    assert rc == _lib.ERR_DTYPE
+
+
+def test_python_mirror_raises_lux3d_error():
+    from lux3d_fused import Lux3dError
+    with pytest.raises(Lux3dError) as e:
+        _lib.call("lux3d_layer_norm", None, None, None, 1e-5, None, None)
+    assert e.value.code == _lib.ERR_NULL
