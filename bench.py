@@ -85,6 +85,21 @@ def time_graph(torch, launches, per_graph, replays=5):
     return us
 
 
+def committed_traffic(tag):
+    """HBM bytes per launch of op `tag` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary profiles/traffic_<tag>.md (calibrated against a copy of
+    known size), or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{tag}.md")
+    if not os.path.exists(path):
+        return None
+    text = open(path).read()
+    try:
+        blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+        return max(v["hbm_bytes"] for v in blob["kernels"].values())
+    except (IndexError, ValueError, KeyError):
+        return None
+
+
 def all_workloads():
     from lux3d_fused import workloads as W
     return [(f, True) for f in W.TARGETS] + [(f, False) for f in W.EXTRAS]
@@ -155,6 +170,17 @@ def main():
     dev = torch.device("cuda:0")
     from lux3d_fused import workloads as W
 
+    if args.profile == "copy_1gib":
+        # calibration kernel of known traffic for the FETCH_SIZE / WRITE_SIZE
+        # counters: 1 GiB read + 1 GiB written per launch
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        print(f"[profile] copy_1gib iters={args.iters}", flush=True)
+        for _ in range(args.iters):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"op": "copy_1gib", "bytes_read": 1 << 30, "bytes_written": 1 << 30}), flush=True)
+        return
     if args.profile:
         for f, _ in all_workloads():
             wl = f(dev)
@@ -200,13 +226,7 @@ def main():
     us_qk = time_graph(torch, qk.launch, n_k)
     dom, us_dom = (qk, us_qk) if us_qk >= us_f1 else (f1, us_f1)
     achieved = dom.bytes / us_dom / 1e3
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        try:
-            traffic = json.load(open(tpath)).get(f"cfg{dom.config}_{dom.name}")
-        except Exception:
-            traffic = None
+    traffic = committed_traffic(f"cfg{dom.config}_{dom.name}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                 "kernel": dom.kernel, "op": f"cfg{dom.config}_{dom.name}", "us": round(us_dom, 3),
