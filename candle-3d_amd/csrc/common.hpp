@@ -261,6 +261,16 @@ template <int M> __device__ __forceinline__ float lane_xor(float v) {
   else return __shfl_xor(v, M, 64);
 }
 
+// Workgroup barrier that orders LDS only: the fences are scoped to the
+// local (LDS) address space, so the wave waits for its own LDS accesses
+// (lgkmcnt) but not for outstanding global loads or stores, which stay in
+// flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int64_t uniform(int64_t v) {
   uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
   uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));

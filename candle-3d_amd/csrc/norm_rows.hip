@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
-template <int TPR>
+template <int TPR, int BLOCK = kBlock>
 __device__ __forceinline__ float row_total(float s, float *red) {
   s = wave_sum(s);
   if constexpr (TPR == 64) {
@@ -28,7 +28,7 @@ __device__ __forceinline__ float row_total(float s, float *red) {
     constexpr int WPR = TPR / 64;
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[w] = s;
-    __syncthreads();
+    lds_barrier();  // the row's stores (e.g. the residual stream h) stay in flight
     const int w0 = (w / WPR) * WPR;
     float tot = red[w0];
 #pragma unroll
@@ -48,11 +48,12 @@ __device__ __forceinline__ void mod8(const ModPiece &m, int64_t seg, int64_t idx
   }
 }
 
-template <typename T, int TPR, int NC, int MODE>
-__global__ __launch_bounds__(kBlock) void row_kernel(RowParams p) {
-  constexpr int RPB = kBlock / TPR;
+template <typename T, int TPR, int NC, int MODE, int BLOCK = kBlock>
+__global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
+  static_assert(BLOCK % TPR == 0, "a block holds whole rows");
+  constexpr int RPB = BLOCK / TPR;
   constexpr int EB = T::bytes;
-  __shared__ float red_a[kBlock / 64], red_b[kBlock / 64];
+  __shared__ float red_a[BLOCK / 64], red_b[BLOCK / 64];
 
   const int t = threadIdx.x % TPR;
   int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kBlock) void row_kernel(RowParams p) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) s += v[c][k];
   const float inv_d = 1.0f / (float)p.d;
-  const float mean = row_total<TPR>(s, red_a) * inv_d;
+  const float mean = row_total<TPR, BLOCK>(s, red_a) * inv_d;
   float s2 = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(kBlock) void row_kernel(RowParams p) {
       const float dv = v[c][k] - mean;
       s2 += dv * dv;
     }
-  const float var = row_total<TPR>(s2, red_b) * inv_d;
+  const float var = row_total<TPR, BLOCK>(s2, red_b) * inv_d;
   const float rstd = 1.0f / sqrtf(var + p.eps);
 
   char *yr = reinterpret_cast<char *>(p.y) + row * p.y_rs * EB;
@@ -208,46 +209,53 @@ template <typename T, int MODE>
 hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   if (p.rows <= 0) return hipSuccess;
   const int64_t chunks = p.d / 8;
-  // Threads per row (TPR). Short jobs (DINOv2/DINOv3's ~1k tokens) split each
-  // row over 2 or 4 wavefronts so the chip is still occupied. For long jobs
-  // the layout is the one measured fastest on MI355X at the configs shapes:
-  // the fused residual + LayerNorm (two input streams) and the gated residual
-  // run a row on 2 wavefronts with one chunk per lane (configs[1] F1: 18.4 us
-  // vs 20.0 us on one wavefront), the single-stream LayerNorm / modulate on
-  // one wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs
-  // 9.4 us on 2 wavefronts).
+  // Layout: threads per row (TPR), chunks per lane (NC) and workgroup size.
+  // Short jobs (DINOv2/DINOv3's ~1k tokens) split each row over 2-4
+  // wavefronts, one row per workgroup, so the chip is still occupied. For
+  // long jobs the layout is the one measured fastest on MI355X at the configs
+  // shapes: the fused residual + LayerNorm runs a row on 2 wavefronts with one
+  // chunk per lane (configs[1] F1: 18.0 us vs 20.4 us on one wavefront), the
+  // gated residual on 4 wavefronts when a row is 256 chunks (configs[2]:
+  // 9.9 us vs 10.8 us), the single-stream LayerNorm / modulate on one
+  // wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs 9.4 us).
   int tpr = 0, nc = 0;
+  bool row_per_block = false;
   if (vec) {
     int ord[3] = {64, 128, 256};
     if (p.rows < 2048) {
       ord[0] = 256; ord[1] = 128; ord[2] = 64;
-    } else if (MODE == ROW_RESID_LN || MODE == ROW_GATE) {
+      row_per_block = true;
+    } else if (MODE == ROW_RESID_LN) {
       if (chunks % 128 == 0 && chunks / 128 <= 2) { ord[0] = 128; ord[1] = 64; }
+    } else if (MODE == ROW_GATE) {
+      if (chunks == 256) { ord[0] = 256; ord[1] = 128; ord[2] = 64; }
+      else if (chunks % 128 == 0 && chunks / 128 <= 2) { ord[0] = 128; ord[1] = 64; }
     }
     for (int i = 0; i < 3 && !tpr; ++i) {
       const int cand = ord[i];
       if (chunks % cand) continue;
       const int64_t n = chunks / cand;
-      if (n == 1 || n == 2 || n == 3 || n == 4 || n == 8) { tpr = cand; nc = (int)n; }
+      if (n == 1 || n == 2 || n == 3 || n == 4 || (n == 8 && cand == 64)) { tpr = cand; nc = (int)n; }
     }
+    if (tpr == 64) row_per_block = false;
   }
-  if (!tpr) {
+  if (!tpr) {  // any width / alignment: one 256-thread block per row
     hipLaunchKernelGGL((row_kernel_any<T, MODE>), dim3((unsigned)p.rows), dim3(kBlock), 0, s, p);
     return hipGetLastError();
   }
-  const int64_t rpb = kBlock / tpr;
+  const int block = row_per_block ? tpr : kBlock;
+  const int64_t rpb = block / tpr;
   const dim3 grid((unsigned)((p.rows + rpb - 1) / rpb));
-#define LUX3D_ROW_CASE(TPR_, NC_)                                                   \
-  if (tpr == TPR_ && nc == NC_) {                                                   \
-    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE>), grid, dim3(kBlock), 0, s, p); \
-    return hipGetLastError();                                                       \
+#define LUX3D_ROW_CASE(TPR_, NC_, BLK_)                                                      \
+  if (tpr == TPR_ && nc == NC_ && block == BLK_) {                                           \
+    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_>), grid, dim3(BLK_), 0, s, p);   \
+    return hipGetLastError();                                                                \
   }
-  LUX3D_ROW_CASE(64, 1) LUX3D_ROW_CASE(64, 2) LUX3D_ROW_CASE(64, 3) LUX3D_ROW_CASE(64, 4)
-  LUX3D_ROW_CASE(64, 8)
-  LUX3D_ROW_CASE(128, 1) LUX3D_ROW_CASE(128, 2) LUX3D_ROW_CASE(128, 3) LUX3D_ROW_CASE(128, 4)
-  LUX3D_ROW_CASE(128, 8)
-  LUX3D_ROW_CASE(256, 1) LUX3D_ROW_CASE(256, 2) LUX3D_ROW_CASE(256, 3) LUX3D_ROW_CASE(256, 4)
-  LUX3D_ROW_CASE(256, 8)
+  LUX3D_ROW_CASE(64, 1, 256) LUX3D_ROW_CASE(64, 2, 256) LUX3D_ROW_CASE(64, 3, 256)
+  LUX3D_ROW_CASE(64, 4, 256) LUX3D_ROW_CASE(64, 8, 256)
+  LUX3D_ROW_CASE(128, 1, 256) LUX3D_ROW_CASE(128, 2, 256) LUX3D_ROW_CASE(128, 3, 256) LUX3D_ROW_CASE(128, 4, 256)
+  LUX3D_ROW_CASE(128, 1, 128) LUX3D_ROW_CASE(128, 2, 128) LUX3D_ROW_CASE(128, 3, 128) LUX3D_ROW_CASE(128, 4, 128)
+  LUX3D_ROW_CASE(256, 1, 256) LUX3D_ROW_CASE(256, 2, 256) LUX3D_ROW_CASE(256, 3, 256) LUX3D_ROW_CASE(256, 4, 256)
 #undef LUX3D_ROW_CASE
   return hipErrorInvalidValue;
 }

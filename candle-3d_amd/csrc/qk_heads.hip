@@ -103,15 +103,6 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
   }
 }
 
-// Workgroup barrier for LDS only: waits for this wave's LDS writes, then
-// s_barrier. Unlike __syncthreads() it does not drain the wave's outstanding
-// global loads, so the row data requested before the phase staging stays in
-// flight across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt / expcnt left at their maximum
-  __builtin_amdgcn_s_barrier();
-}
-
 // Grid: x = tiles of `tb` consecutive tokens, y = tensor (q, k). Work items
 // are (token, head) rows of LPR lanes; each thread owns R of the tile's rows.
 // Order of work per workgroup: issue every row load (and the per-channel
