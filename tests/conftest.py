@@ -100,3 +100,36 @@ def assert_f32_close(got, want, rel=F32_REL_TOL, what=""):
     worst = float((err / np.maximum(np.abs(want[ok]), scale)).max()) if err.size else 0.0
     assert np.all(err <= bound), f"{what}: max relative error {worst:.3e} > {rel:g}"
     return worst
+
+
+def bf16_bits_from_f64(want) -> np.ndarray:
+    """float64 values -> bf16 bits, rounded to nearest even through f32 (the
+    double rounding can move a value by 1 ulp, inside every tolerance here)."""
+    f = np.ascontiguousarray(want, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(f), ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def assert_vs_f64(got, want64, dt: str, what="", rel=F32_REL_TOL):
+    """Output against a float64 expectation from the golden fixtures: f32
+    within `rel` of max(|want|, RMS(want)); bf16 (uint16 bits) within 2 ulp of
+    the expectation's bf16 rounding, with the absolute floor of
+    assert_bf16_close; f16 likewise."""
+    want64 = np.asarray(want64, dtype=np.float64)
+    if dt == "f32":
+        got = np.asarray(got, dtype=np.float32).reshape(-1).astype(np.float64)
+        w = want64.reshape(-1)
+        assert got.shape == w.shape, f"{what}: shape {got.shape} vs {w.shape}"
+        scale = max(float(np.sqrt(np.mean(w ** 2))) if w.size else 1.0, 1e-30)
+        bound = rel * np.maximum(np.abs(w), scale)
+        err = np.abs(got - w)
+        assert np.all(err <= bound), (
+            f"{what}: max error {float((err / np.maximum(np.abs(w), scale)).max()):.3e} > {rel:g} (relative)")
+        return
+    if dt == "bf16":
+        return assert_bf16_close(got, bf16_bits_from_f64(want64), what=what)
+    if dt == "f16":
+        want_bits = np.asarray(want64, dtype=np.float16).view(np.uint16)
+        return assert_f16_close(got, want_bits, what=what)
+    raise ValueError(dt)
