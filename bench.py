@@ -85,6 +85,23 @@ def time_graph(torch, launches, per_graph, replays=5):
     return us
 
 
+def copy_ceiling_us(torch, dev, nbytes, n=50):
+    """Average us of the runtime's device-to-device copy (hipMemcpyAsync via
+    torch's copy_) moving the same bytes as an op (nbytes/2 read + nbytes/2
+    written per launch), graph-timed like the ops, rotating over buffer pairs
+    that together exceed the 256 MB Infinity Cache. A reference point for what
+    a plain streaming kernel of the runtime gets at this transfer size; it is
+    not an upper bound (the fused kernels beat it at most sizes)."""
+    half = max(256, (nbytes // 2 + 255) // 256 * 256)
+    sets = max(3, -(-(768 << 20) // (2 * half)))
+    bufs = [(torch.ones(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
+            for _ in range(sets)]
+    us = time_graph(torch, lambda i: bufs[i % sets][1].copy_(bufs[i % sets][0]), n)
+    del bufs
+    torch.cuda.empty_cache()
+    return us
+
+
 def committed_traffic(tag):
     """HBM bytes per launch of op `tag` from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary profiles/traffic_<tag>.md (calibrated against a copy of
@@ -232,8 +249,13 @@ def main():
                 "kernel": dom.kernel, "op": f"cfg{dom.config}_{dom.name}", "us": round(us_dom, 3),
                 "algorithmic_bytes": dom.bytes}
     step_ops = {f"cfg1_{f1.name}": us_f1, f"cfg1_{qk.name}": us_qk}
-    del f1, qk
+    dom_bytes = dom.bytes
+    del f1, qk, dom
     torch.cuda.empty_cache()
+    copy_us = copy_ceiling_us(torch, dev, dom_bytes)
+    roofline["runtime_copy"] = {"us": round(copy_us, 3), "gbs": round(dom_bytes / copy_us / 1e3, 1),
+                                "speed_vs_runtime_copy": round(copy_us / us_dom, 4),
+                                "what": "hipMemcpyAsync D2D of the same bytes (half read, half written)"}
 
     # ---- every op at its config shape ----------------------------------------------
     table = []
@@ -243,18 +265,22 @@ def main():
         if args.only and tag not in args.only and wl.name not in args.only:
             del wl
             continue
+        cfg, dtype, shape, sets, note = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note
         us = step_ops.get(tag)
         if us is None:
             n = 200 if wl.bytes < 64 << 20 else 50
             us = time_graph(torch, wl.launch, n)
         gbs = wl.bytes / us / 1e3
-        table.append({"op": tag, "config": wl.config, "dtype": wl.dtype, "shape": wl.shape,
-                      "bytes": wl.bytes, "us": round(us, 3), "gbs": round(gbs, 1),
-                      "frac_peak": round(gbs / PEAK_GBS, 4), "target_70pct": bool(target),
-                      "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
-                      "rotation_sets": wl.sets, **({"note": wl.ideal_note} if wl.ideal_note else {})})
+        nbytes = wl.bytes
         del wl
         torch.cuda.empty_cache()
+        cus = copy_ceiling_us(torch, dev, nbytes, 200 if nbytes < 64 << 20 else 50)
+        table.append({"op": tag, "config": cfg, "dtype": dtype, "shape": shape,
+                      "bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
+                      "frac_peak": round(gbs / PEAK_GBS, 4), "runtime_copy_us": round(cus, 3),
+                      "speed_vs_runtime_copy": round(cus / us, 4), "target_70pct": bool(target),
+                      "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
+                      "rotation_sets": sets, **({"note": note} if note else {})})
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -103,15 +103,17 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
   }
 }
 
-// Grid: x = tiles of `tb` consecutive tokens, y = tensor (q, k). Work items
-// are (token, head) rows of LPR lanes; each thread owns R of the tile's rows.
-// Order of work per workgroup: issue every row load (and the per-channel
-// parameters), then stage the tile's rotation phases in LDS while those loads
-// are in flight, one LDS barrier, then normalise / rotate / store. Each
-// workgroup therefore waits on one HBM round trip. Rows of one head are
-// adjacent in the [B, H, N, D] output across the tile's tokens, so a head's
-// stores form contiguous runs of tb*D elements.
-template <typename T, int D, int NORM, int ROT, int R>
+// Grid: x = tiles of `tb` consecutive tokens; y = tensor (q, k) when NTB = 1,
+// or 1 when NTB = 2 (each workgroup then handles q and k of its tokens, whose
+// rows lie side by side in a packed qkv buffer, and stages the phases once).
+// Work items are (token, head) rows of LPR lanes; each thread owns R of the
+// tile's rows per tensor. Order of work per workgroup: issue every row load
+// (and the per-channel parameters), then stage the tile's rotation phases in
+// LDS while those loads are in flight, one LDS barrier, then normalise /
+// rotate / store. Each workgroup therefore waits on one HBM round trip. Rows
+// of one head are adjacent in the [B, H, N, D] output across the tile's
+// tokens, so a head's stores form contiguous runs of tb*D elements.
+template <typename T, int D, int NORM, int ROT, int R, int NTB>
 __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   constexpr int LPR = D / 8;
   constexpr int M = RotPartner<ROT, D>::M;
@@ -119,7 +121,6 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   extern __shared__ float lds[];
   float *Cs = lds, *Ss = lds + tb * D;
 
-  const HeadIO io = p.io[blockIdx.y];
   const uint32_t N = (uint32_t)p.N, H = (uint32_t)p.H;
   const uint32_t ntok = (uint32_t)(p.B * p.N);
   const uint32_t tok0 = blockIdx.x * (uint32_t)tb;
@@ -127,7 +128,6 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   const int ipp = blockDim.x / LPR;
   const uint32_t items = (uint32_t)tb * H;
 
-  float v[R][8];
   uint32_t tt[R], hh[R], nn[R], bb[R];
   bool live[R];
 #pragma unroll
@@ -137,15 +137,22 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
     uint32_t tok = tok0 + t;
     live[r] = it < items && tok < ntok;
     if (!live[r]) { t = 0; h = 0; tok = tok0; }
-    const uint32_t b = tok / N, n = tok % N;
-    tt[r] = t; hh[r] = h; nn[r] = n; bb[r] = b;
-    const char *xp = reinterpret_cast<const char *>(io.x) +
-                     ((int64_t)b * io.sB + (int64_t)h * io.sH + (int64_t)n * io.sN + lane * 8) * EB;
-    Chunk<T>::load(xp, v[r]);
+    tt[r] = t; hh[r] = h; nn[r] = tok % N; bb[r] = tok / N;
   }
-  float w[8], bias[8];
-  if constexpr (NORM == HN_LN || NORM == HN_RMS) param8(io.p0, io.p0_dt, lane * 8, 1.f, w);
-  if constexpr (NORM == HN_LN) param8(io.p1, io.p1_dt, lane * 8, 0.f, bias);
+  float v[NTB][R][8];
+  float w[NTB][8], bias[NTB][8];
+#pragma unroll
+  for (int q = 0; q < NTB; ++q) {
+    const HeadIO &io = p.io[NTB == 1 ? blockIdx.y : q];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const char *xp = reinterpret_cast<const char *>(io.x) +
+                       ((int64_t)bb[r] * io.sB + (int64_t)hh[r] * io.sH + (int64_t)nn[r] * io.sN + lane * 8) * EB;
+      Chunk<T>::load(xp, v[q][r]);
+    }
+    if constexpr (NORM == HN_LN || NORM == HN_RMS) param8(io.p0, io.p0_dt, lane * 8, 1.f, w[q]);
+    if constexpr (NORM == HN_LN) param8(io.p1, io.p1_dt, lane * 8, 0.f, bias[q]);
+  }
 
   if constexpr (ROT != HR_NONE) {
     stage_phases<ROT, D>(p, tok0, tb, ntok, N, Cs, Ss);
@@ -153,71 +160,74 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   }
 
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if constexpr (NORM == HN_LN) {
-      float s = 0.f;
+  for (int q = 0; q < NTB; ++q) {
+    const HeadIO &io = p.io[NTB == 1 ? blockIdx.y : q];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) s += v[r][k];
-      const float mean = group_sum<LPR>(s) * (1.0f / D);
-      float s2 = 0.f;
+    for (int r = 0; r < R; ++r) {
+      float (&x)[8] = v[q][r];
+      if constexpr (NORM == HN_LN) {
+        float s = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        v[r][k] -= mean;
-        s2 += v[r][k] * v[r][k];
-      }
-      const float rstd = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
+        for (int k = 0; k < 8; ++k) s += x[k];
+        const float mean = group_sum<LPR>(s) * (1.0f / D);
+        float s2 = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[r][k] = v[r][k] * rstd * w[k] + bias[k];
-    } else if constexpr (NORM == HN_RMS) {
-      float s2 = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s2 += v[r][k] * v[r][k];
-      const float rr = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[r][k] = (v[r][k] * rr) * w[k];
-    } else if constexpr (NORM == HN_L2) {
-      float s2 = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s2 += v[r][k] * v[r][k];
-      const float nrm = fminf(fmaxf(sqrtf(group_sum<LPR>(s2)), 1e-12f), 1.0e30f);
-      const float rr = 1.0f / nrm;
-      const float scale = sqrtf((float)D);
-      float g[8];
-      param8(io.p0, io.p0_dt, (int64_t)hh[r] * D + lane * 8, 1.f, g);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[r][k] = ((v[r][k] * rr) * g[k]) * scale;
-    }
-    if constexpr (ROT != HR_NONE) {
-      bool rotate = true;
-      if constexpr (ROT == HR_R3_TAB) rotate = nn[r] >= (uint32_t)p.prefix;  // prefix tokens pass through
-      if (rotate) {
-        float pv[8];
-        if constexpr (M < 8) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) pv[k] = v[r][k ^ M];
-        } else {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 8>(v[r][k]);
+        for (int k = 0; k < 8; ++k) {
+          x[k] -= mean;
+          s2 += x[k] * x[k];
         }
-        const float *C = Cs + tt[r] * D + lane * 8;
-        const float *S = Ss + tt[r] * D + lane * 8;
+        const float rstd = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[r][k] = __fadd_rn(__fmul_rn(v[r][k], C[k]), __fmul_rn(pv[k], S[k]));
+        for (int k = 0; k < 8; ++k) x[k] = x[k] * rstd * w[q][k] + bias[q][k];
+      } else if constexpr (NORM == HN_RMS) {
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
+        const float rr = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = (x[k] * rr) * w[q][k];
+      } else if constexpr (NORM == HN_L2) {
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
+        const float nrm = fminf(fmaxf(sqrtf(group_sum<LPR>(s2)), 1e-12f), 1.0e30f);
+        const float rr = 1.0f / nrm;
+        const float scale = sqrtf((float)D);
+        float g[8];
+        param8(io.p0, io.p0_dt, (int64_t)hh[r] * D + lane * 8, 1.f, g);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = ((x[k] * rr) * g[k]) * scale;
       }
-    }
-    if (live[r]) {
-      char *yp = reinterpret_cast<char *>(io.y) +
-                 ((int64_t)bb[r] * io.oB + (int64_t)hh[r] * io.oH + (int64_t)nn[r] * io.oN + lane * 8) * EB;
-      Chunk<T>::store(yp, v[r]);
+      if constexpr (ROT != HR_NONE) {
+        bool rotate = true;
+        if constexpr (ROT == HR_R3_TAB) rotate = nn[r] >= (uint32_t)p.prefix;  // prefix tokens pass through
+        if (rotate) {
+          float pv[8];
+          if constexpr (M < 8) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) pv[k] = x[k ^ M];
+          } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 8>(x[k]);
+          }
+          const float *C = Cs + tt[r] * D + lane * 8;
+          const float *S = Ss + tt[r] * D + lane * 8;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) x[k] = __fadd_rn(__fmul_rn(x[k], C[k]), __fmul_rn(pv[k], S[k]));
+        }
+      }
+      if (live[r]) {
+        char *yp = reinterpret_cast<char *>(io.y) +
+                   ((int64_t)bb[r] * io.oB + (int64_t)hh[r] * io.oH + (int64_t)nn[r] * io.oN + lane * 8) * EB;
+        Chunk<T>::store(yp, v[q][r]);
+      }
     }
   }
 }
 
-template <typename T, int D>
-hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
+template <typename T, int D, int NTB>
+hipError_t launch_dn(int norm, int rot, const HeadParams &p, hipStream_t s) {
   const int64_t tokens = p.B * p.N;
-  if (tokens <= 0 || p.H <= 0) return hipSuccess;
-  if (tokens > INT32_MAX || p.H > 4096) return hipErrorInvalidValue;
   constexpr int LPR = D / 8;
   constexpr int R = T::bytes == 4 ? 1 : 2;
   // Whole heads per pass: threads = k*H*LPR rounded to wavefronts, <= 256.
@@ -229,11 +239,11 @@ hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
   int64_t tb = (R * ipp) / p.H;
   if (tb < 1) return hipErrorInvalidValue;  // more heads than one pass holds (H*D > 2048)
   const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
-  const dim3 grid((unsigned)((tokens + tb - 1) / tb), (unsigned)p.ntens), block((unsigned)threads);
-#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                              \
-  if (norm == NORM_ && rot == ROT_) {                                                             \
-    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R>), grid, block, lds, s, p, (int)tb);     \
-    return hipGetLastError();                                                                     \
+  const dim3 grid((unsigned)((tokens + tb - 1) / tb), NTB == 2 ? 1u : (unsigned)p.ntens), block((unsigned)threads);
+#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                                 \
+  if (norm == NORM_ && rot == ROT_) {                                                                \
+    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R, NTB>), grid, block, lds, s, p, (int)tb);   \
+    return hipGetLastError();                                                                        \
   }
   LUX3D_HEAD_CASE(HN_LN, HR_R1_TAB) LUX3D_HEAD_CASE(HN_LN, HR_R1_POS)
   LUX3D_HEAD_CASE(HN_NONE, HR_R1_TAB) LUX3D_HEAD_CASE(HN_NONE, HR_R1_POS)
@@ -245,6 +255,18 @@ hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
   LUX3D_HEAD_CASE(HN_NONE, HR_NONE)
 #undef LUX3D_HEAD_CASE
   return hipErrorInvalidValue;
+}
+
+// q and k share a workgroup for D = 128 (measured: configs[2] RMS and
+// configs[3] L2+RoPE gain 7-9%); for D = 64 one tensor per workgroup is
+// faster.
+template <typename T, int D>
+hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
+  const int64_t tokens = p.B * p.N;
+  if (tokens <= 0 || p.H <= 0) return hipSuccess;
+  if (tokens > INT32_MAX || p.H > 4096) return hipErrorInvalidValue;
+  if (D == 128 && p.ntens == 2) return launch_dn<T, D, 2>(norm, rot, p, s);
+  return launch_dn<T, D, 1>(norm, rot, p, s);
 }
 
 template <typename T>
