@@ -48,15 +48,66 @@ __device__ __forceinline__ void mod8(const ModPiece &m, int64_t seg, int64_t idx
   }
 }
 
-template <typename T, int TPR, int NC, int MODE, int BLOCK = kBlock>
+// Per-segment pieces (AdaLN shift / scale / gate, each optionally plus its
+// base vector) are the same for every row of a segment. With STAGE, a
+// workgroup whose rows all lie in one segment sums each piece once into LDS
+// (dynamic shared memory, npieces * d floats) and every row reads it from
+// there: re-reading the f32 pieces per row from the vector cache moved 2-4x
+// the row's own bytes through it (configs[3] ragged modulate with base
+// vectors: 92.6 us direct, 68.3 us staged). A workgroup that straddles a
+// segment boundary reads them per row from global memory.
+struct Staged {
+  float *shift, *scale1, *gate;  // scale1 = scale + 1
+};
+
+template <int MODE, int BLOCK>
+__device__ __forceinline__ void stage_pieces(const RowParams &p, int64_t seg, float *lds, Staged &st) {
+  const int64_t d = p.d;
+  const bool has_gate = MODE == ROW_GATE || p.gate.dt >= 0;
+  float *q = lds;
+  if constexpr (MODE == ROW_MODULATE) {
+    st.shift = q; q += d;
+    st.scale1 = q; q += d;
+  }
+  st.gate = has_gate ? q : nullptr;
+  for (int64_t e = threadIdx.x; e < d / 8; e += BLOCK) {
+    float a[8];
+    if constexpr (MODE == ROW_MODULATE) {
+      mod8(p.shift, seg, e * 8, 0.f, a);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) st.shift[e * 8 + k] = a[k];
+      mod8(p.scale, seg, e * 8, 0.f, a);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) st.scale1[e * 8 + k] = a[k] + 1.0f;
+    }
+    if (has_gate) {
+      mod8(p.gate, seg, e * 8, 1.f, a);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) st.gate[e * 8 + k] = a[k];
+    }
+  }
+  lds_barrier();
+}
+
+__device__ __forceinline__ void lds8(const float *src, int64_t idx, float (&v)[8]) {
+  const float4 a = *reinterpret_cast<const float4 *>(src + idx);
+  const float4 b = *reinterpret_cast<const float4 *>(src + idx + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <typename T, int TPR, int NC, int MODE, int BLOCK = kBlock, bool STAGE = false>
 __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   static_assert(BLOCK % TPR == 0, "a block holds whole rows");
+  static_assert(!STAGE || MODE == ROW_MODULATE || MODE == ROW_GATE, "only segment pieces are staged");
   constexpr int RPB = BLOCK / TPR;
   constexpr int EB = T::bytes;
   __shared__ float red_a[BLOCK / 64], red_b[BLOCK / 64];
+  extern __shared__ __align__(16) float lds_pieces[];  // 16-byte aligned: read as float4
 
   const int t = threadIdx.x % TPR;
-  int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const int64_t row0 = (int64_t)blockIdx.x * RPB;
+  int64_t row = row0 + threadIdx.x / TPR;
   const bool live = row < p.rows;
   row = uniform(live ? row : p.rows - 1);
 
@@ -65,8 +116,24 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) Chunk<T>::load(xr + (int64_t)(c * TPR + t) * 8 * EB, v[c]);
 
+  // segment of this row; with STAGE, whether the workgroup shares one
+  bool staged = false;
+  Staged st{};
+  int64_t seg = 0;
+  if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE) {
+    if constexpr (STAGE) {
+      const int64_t last = row0 + RPB - 1 < p.rows ? row0 + RPB - 1 : p.rows - 1;
+      const int64_t seg0 = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row0);
+      staged = segment_of(p.seg_off, p.nseg, p.rows_per_seg, last) == seg0;  // uniform over the workgroup
+      seg = seg0;
+      if (staged) stage_pieces<MODE, BLOCK>(p, seg0, lds_pieces, st);
+      else seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
+    } else {
+      seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
+    }
+  }
+
   if constexpr (MODE == ROW_GATE) {
-    const int64_t seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
     const char *ar = reinterpret_cast<const char *>(p.a) + row * p.a_rs * EB;
     char *yr = reinterpret_cast<char *>(p.y) + row * p.y_rs * EB;
 #pragma unroll
@@ -74,7 +141,8 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       const int64_t idx = (int64_t)(c * TPR + t) * 8;
       float hv[8], g[8];
       Chunk<T>::load(ar + idx * EB, hv);
-      mod8(p.gate, seg, idx, 1.f, g);
+      if (staged) lds8(st.gate, idx, g);
+      else mod8(p.gate, seg, idx, 1.f, g);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[c][k] = __fadd_rn(v[c][k], __fmul_rn(hv[k], g[k]));
       if (live) Chunk<T>::store(yr + idx * EB, v[c]);
@@ -123,18 +191,25 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
 
   char *yr = reinterpret_cast<char *>(p.y) + row * p.y_rs * EB;
   if constexpr (MODE == ROW_MODULATE) {
-    const int64_t seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t idx = (int64_t)(c * TPR + t) * 8;
-      float sh[8], sc[8], out[8];
-      mod8(p.shift, seg, idx, 0.f, sh);
-      mod8(p.scale, seg, idx, 0.f, sc);
+      float sh[8], sc1[8], out[8];
+      if (staged) {
+        lds8(st.shift, idx, sh);
+        lds8(st.scale1, idx, sc1);
+      } else {
+        mod8(p.shift, seg, idx, 0.f, sh);
+        mod8(p.scale, seg, idx, 0.f, sc1);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * (sc[k] + 1.0f) + sh[k];
+        for (int k = 0; k < 8; ++k) sc1[k] = sc1[k] + 1.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * sc1[k] + sh[k];
       if (p.gate.dt >= 0) {
         float g[8];
-        mod8(p.gate, seg, idx, 1.f, g);
+        if (staged) lds8(st.gate, idx, g);
+        else mod8(p.gate, seg, idx, 1.f, g);
 #pragma unroll
         for (int k = 0; k < 8; ++k) out[k] = g[k] * out[k] + v[c][k];
       }
@@ -213,11 +288,13 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   // Short jobs (DINOv2/DINOv3's ~1k tokens) split each row over 2-4
   // wavefronts, one row per workgroup, so the chip is still occupied. For
   // long jobs the layout is the one measured fastest on MI355X at the configs
-  // shapes: the fused residual + LayerNorm runs a row on 2 wavefronts with one
-  // chunk per lane (configs[1] F1: 18.0 us vs 20.4 us on one wavefront), the
-  // gated residual on 4 wavefronts when a row is 256 chunks (configs[2]:
-  // 9.9 us vs 10.8 us), the single-stream LayerNorm / modulate on one
+  // shapes: the fused residual + LayerNorm and the gated residual run a row on
+  // 2 wavefronts with one or two chunks per lane (configs[1] F1: 18.0 us vs
+  // 20.4 us on one wavefront; the gate without a base vector on 4 wavefronts
+  // when a row is 256 chunks), the single-stream LayerNorm / modulate on one
   // wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs 9.4 us).
+  // 256-thread workgroups of several rows let modulate / gate share the
+  // staged segment pieces.
   int tpr = 0, nc = 0;
   bool row_per_block = false;
   if (vec) {
@@ -228,7 +305,10 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
     } else if (MODE == ROW_RESID_LN) {
       if (chunks % 128 == 0 && chunks / 128 <= 2) { ord[0] = 128; ord[1] = 64; }
     } else if (MODE == ROW_GATE) {
-      if (chunks == 256) { ord[0] = 256; ord[1] = 128; ord[2] = 64; }
+      // one gate vector per row read straight from the cache is cheapest on
+      // 4 wavefronts (configs[2]: 9.7 us vs 10.3 us staged); gate + base
+      // is cheaper staged on 2-row workgroups (10.9 us vs 11.3 us)
+      if (chunks == 256 && p.gate.base_dt < 0) { ord[0] = 256; ord[1] = 128; ord[2] = 64; }
       else if (chunks % 128 == 0 && chunks / 128 <= 2) { ord[0] = 128; ord[1] = 64; }
     }
     for (int i = 0; i < 3 && !tpr; ++i) {
@@ -246,10 +326,20 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   const int block = row_per_block ? tpr : kBlock;
   const int64_t rpb = block / tpr;
   const dim3 grid((unsigned)((p.rows + rpb - 1) / rpb));
-#define LUX3D_ROW_CASE(TPR_, NC_, BLK_)                                                      \
-  if (tpr == TPR_ && nc == NC_ && block == BLK_) {                                           \
-    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_>), grid, dim3(BLK_), 0, s, p);   \
-    return hipGetLastError();                                                                \
+  // Stage the segment pieces in LDS when a workgroup holds several rows.
+  const int npieces = MODE == ROW_MODULATE ? 2 + (p.gate.dt >= 0 ? 1 : 0) : (MODE == ROW_GATE ? 1 : 0);
+  const size_t lds = (size_t)npieces * (size_t)p.d * sizeof(float);
+  const bool stage = npieces > 0 && rpb > 1 && lds <= 64 * 1024;
+#define LUX3D_ROW_CASE(TPR_, NC_, BLK_)                                                                 \
+  if (tpr == TPR_ && nc == NC_ && block == BLK_) {                                                      \
+    if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE) {                                           \
+      if (stage && BLK_ > TPR_) {                                                                       \
+        hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_, (BLK_ > TPR_)>), grid, dim3(BLK_), lds, s, p); \
+        return hipGetLastError();                                                                       \
+      }                                                                                                 \
+    }                                                                                                   \
+    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_>), grid, dim3(BLK_), 0, s, p);              \
+    return hipGetLastError();                                                                           \
   }
   LUX3D_ROW_CASE(64, 1, 256) LUX3D_ROW_CASE(64, 2, 256) LUX3D_ROW_CASE(64, 3, 256)
   LUX3D_ROW_CASE(64, 4, 256) LUX3D_ROW_CASE(64, 8, 256)

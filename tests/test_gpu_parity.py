@@ -237,6 +237,67 @@ def test_gated_residual(dev, ops, orc, synth, ragged):
     check(out, want, "bf16", "gated_residual")
 
 
+# Segment boundaries that fall inside a workgroup of several rows: those
+# workgroups read the segment pieces per row, the others share them in LDS.
+STRADDLE = [((2049, 1, 1027, 2000), 1536), ((1031, 1031, 1031), 2048)]
+
+
+@pytest.mark.parametrize("sizes,C", STRADDLE)
+@pytest.mark.parametrize("with_gate", [False, True])
+def test_adaln_modulate_straddling_segments(dev, ops, orc, synth, sizes, C, with_gate):
+    print(f"\n[case] adaln_modulate segments {sizes} C={C} gate={with_gate}", flush=True)
+    S, n = len(sizes), sum(sizes)
+    x = synth.normal(91, n * C).reshape(n, C)
+    t_emb = synth.normal(92, S * 6 * C, 0.0, 0.1).reshape(S, 6 * C)
+    modulation = synth.normal(93, 6 * C, 0.0, 0.1)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    xd = dev_tensor(x, "bf16", dev)
+    pieces = ops.chunk_modulation(torch.from_numpy(t_emb).to(dev))
+    base = torch.from_numpy(modulation).to(dev).chunk(6)
+    y = ops.adaln_modulate(xd, pieces[0], pieces[1], pieces[2] if with_gate else None,
+                           shift_base=base[0], scale_base=base[1], gate_base=base[2] if with_gate else None,
+                           seg_offsets=torch.from_numpy(offs).to(dev), eps=1e-6)
+    sync()
+    sl = lambda k: np.ascontiguousarray(t_emb[:, k * C:(k + 1) * C])  # noqa: E731
+    bl = lambda k: modulation[k * C:(k + 1) * C]  # noqa: E731
+    want = orc.adaln_modulate(host_view(xd, "bf16"), offs, sl(0), sl(1), sl(2) if with_gate else None,
+                              bl(0), bl(1), bl(2) if with_gate else None, eps=1e-6, dt=orc.BF16)
+    check(y, want, "bf16", "adaln straddling segments")
+
+
+@pytest.mark.parametrize("sizes,C", STRADDLE)
+def test_gated_residual_straddling_segments(dev, ops, orc, synth, sizes, C):
+    print(f"\n[case] gated_residual segments {sizes} C={C}", flush=True)
+    S, n = len(sizes), sum(sizes)
+    x = synth.normal(94, n * C).reshape(n, C)
+    h = synth.normal(95, n * C).reshape(n, C)
+    gate_seg = synth.normal(96, S * C, 0.0, 0.1).reshape(S, C)
+    gate_base = synth.normal(97, C, 0.0, 0.1)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    xd, hd = dev_tensor(x, "bf16", dev), dev_tensor(h, "bf16", dev)
+    out = ops.gated_residual(xd, hd, torch.from_numpy(gate_seg).to(dev), gate_base=torch.from_numpy(gate_base).to(dev),
+                             seg_offsets=torch.from_numpy(offs).to(dev))
+    sync()
+    want = orc.gated_residual(host_view(xd, "bf16"), host_view(hd, "bf16"), offs, gate_seg, gate_base, dt=orc.BF16)
+    check(out, want, "bf16", "gated_residual straddling segments")
+
+
+def test_adaln_modulate_dense_uneven_segments(dev, ops, orc, synth):
+    """Equal segments without offsets ([B, L, C] with L not a multiple of the
+    rows per workgroup)."""
+    print("\n[case] adaln_modulate dense B=3 L=1031", flush=True)
+    B, L, C = 3, 1031, 2048
+    x = synth.normal(98, B * L * C).reshape(B, L, C)
+    shift = synth.normal(99, B * C, 0.0, 0.1).reshape(B, C)
+    scale = synth.normal(100, B * C, 0.0, 0.1).reshape(B, C)
+    xd = dev_tensor(x, "bf16", dev)
+    y = ops.adaln_modulate(xd, torch.from_numpy(shift).to(dev), torch.from_numpy(scale).to(dev), eps=1e-6)
+    sync()
+    want = orc.adaln_modulate(host_view(xd, "bf16"), np.array([0, L, 2 * L, 3 * L]), shift, scale, eps=1e-6,
+                              dt=orc.BF16)
+    check(y, want, "bf16", "adaln dense uneven")
+
+
 # ---------------------------------------------------------------------------
 # VGGT: QK LayerNorm + 2D RoPE
 # ---------------------------------------------------------------------------
