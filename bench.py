@@ -93,7 +93,7 @@ def copy_ceiling_us(torch, dev, nbytes, n=50):
     a plain streaming kernel of the runtime gets at this transfer size; it is
     not an upper bound (the fused kernels beat it at most sizes)."""
     half = max(256, (nbytes // 2 + 255) // 256 * 256)
-    sets = max(3, -(-(768 << 20) // (2 * half)))
+    sets = min(64, max(3, -(-(768 << 20) // (2 * half))))
     bufs = [(torch.ones(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
             for _ in range(sets)]
     us = time_graph(torch, lambda i: bufs[i % sets][1].copy_(bufs[i % sets][0]), n)
