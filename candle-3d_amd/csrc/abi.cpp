@@ -246,6 +246,7 @@ int segments(const lux3d_tensor_t *seg_offsets, int64_t rows, int64_t piece_segs
 struct HeadView {
   const void *p;
   int64_t B, H, N, D, sB, sH, sN;
+  bool vec;  // D is 64 or 128 and the rows (and parameters) are 16-byte aligned
 };
 
 int head_tensor(const lux3d_tensor_t *t, const char *fn, const char *name, int ib, int ih, int in,
@@ -262,12 +263,14 @@ int head_tensor(const lux3d_tensor_t *t, const char *fn, const char *name, int i
   v.sB = t->stride[ib];
   v.sH = t->stride[ih];
   v.sN = t->stride[in];
-  if (t->stride[3] != 1) return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must have a unit innermost stride", fn, name);
-  if (v.D != 64 && v.D != 128) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld unsupported (64 or 128)", fn, (long long)v.D);
+  if (t->stride[3] != 1 && v.D > 1)
+    return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must have a unit innermost stride", fn, name);
+  if (v.D < 1 || v.D > 8192) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld out of range [1, 8192]", fn, (long long)v.D);
   const int64_t e = elem_bytes(t->dtype);
   const bool al = aligned16(v.p) && ((v.sB * e) % 16 == 0 || v.B == 1) && ((v.sH * e) % 16 == 0 || v.H == 1) &&
                   ((v.sN * e) % 16 == 0 || v.N == 1);
-  if (!al) return fail(LUX3D_ERR_LAYOUT, "%s: `%s` head rows must be 16-byte aligned", fn, name);
+  // other head dims and unaligned views take the generic kernel
+  v.vec = (v.D == 64 || v.D == 128) && al;
   return LUX3D_OK;
 }
 
@@ -277,10 +280,7 @@ int same_heads(const HeadView &a, const HeadView &b, const char *fn, const char 
   return LUX3D_OK;
 }
 
-int param_aligned(const void *p, int dt, const char *fn, const char *name) {
-  if (dt >= 0 && !aligned16(p)) return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must be 16-byte aligned", fn, name);
-  return LUX3D_OK;
-}
+bool param_aligned(const void *p, int dt) { return dt < 0 || aligned16(p); }
 
 // One q/k side: input view, output view and up to two parameter vectors.
 int head_side(const lux3d_tensor_t *x, const lux3d_tensor_t *y, const lux3d_tensor_t *p0, int64_t p0_len,
@@ -299,8 +299,7 @@ int head_side(const lux3d_tensor_t *x, const lux3d_tensor_t *y, const lux3d_tens
   io.oB = yv.sB; io.oH = yv.sH; io.oN = yv.sN;
   if ((r = param_vec(p0, p0_len, fn, p0n, io.p0, io.p0_dt))) return r;
   if ((r = param_vec(p1, xv.D, fn, p1n, io.p1, io.p1_dt))) return r;
-  if ((r = param_aligned(io.p0, io.p0_dt, fn, p0n))) return r;
-  if ((r = param_aligned(io.p1, io.p1_dt, fn, p1n))) return r;
+  xv.vec = xv.vec && yv.vec && param_aligned(io.p0, io.p0_dt) && param_aligned(io.p1, io.p1_dt);
   return LUX3D_OK;
 }
 
@@ -473,6 +472,9 @@ int qk_rope2d_common(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor
   if (qn && !(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
   norm = qn ? HN_LN : HN_NONE;
   p.B = qv.B; p.H = qv.H; p.N = qv.N; p.D = qv.D; p.eps = eps;
+  p.vec = qv.vec && (p.ntens == 1 || kv.vec);
+  // Rope2d rotates the quarters of each half (attention_math.rs:28-30)
+  if (p.D % 4) return fail(LUX3D_ERR_SHAPE, "%s: rope token_dim must be divisible by 4, got %lld", fn, (long long)p.D);
   return LUX3D_OK;
 }
 
@@ -525,6 +527,7 @@ int lux3d_qk_layernorm_rope2d_pos(const lux3d_tensor_t *q, const lux3d_tensor_t 
   if ((r = qk_rope2d_common(fn, q, q_w, q_b, k, k_w, k_b, eps, q_out, k_out, p, norm))) return r;
   if ((r = index_tensor(positions, fn, "positions", p.B, p.N, 2, true))) return r;
   if (!(base > 0.f) || !std::isfinite(base)) return fail(LUX3D_ERR_VALUE, "%s: base must be a positive number", fn);
+  if (p.D / 4 > 64) return fail(LUX3D_ERR_SHAPE, "%s: token_dim %lld above 256 (use the tables entry)", fn, (long long)p.D);
   p.pos = positions->data; p.pos_dt = positions->dtype;
   p.pos_sB = positions->stride[0]; p.pos_sN = positions->stride[1]; p.pos_sC = positions->stride[2];
   rope2d_inv_freq(base, p.D, p.freq);
@@ -577,6 +580,7 @@ int lux3d_rms_norm_heads(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w, con
   }
   if (!(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
   p.B = qv.B; p.H = qv.H; p.N = qv.N; p.D = qv.D; p.eps = eps;
+  p.vec = qv.vec && (p.ntens == 1 || kv.vec);
   return hip_status(launch_heads(HN_RMS, HR_NONE, q->dtype, p, stream_of(stream)), fn);
 }
 
@@ -604,8 +608,11 @@ int lux3d_qk_l2norm_rope3d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_gamm
     p.ntens = 2;
   }
   p.B = qv.B; p.H = qv.H; p.N = qv.N; p.D = qv.D;
+  p.vec = qv.vec && (p.ntens == 1 || kv.vec);
   const int norm = q_gamma ? HN_L2 : HN_NONE;
   int rot = HR_NONE;
+  if ((cos || sin || coords) && p.D % 2)
+    return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld must be even to rotate (re, im) pairs", fn, (long long)p.D);
   if (cos || sin) {
     if (!cos || !sin) return fail(LUX3D_ERR_NULL, "%s: pass both cos and sin tables", fn);
     if (coords) return fail(LUX3D_ERR_VALUE, "%s: pass tables or coords, not both", fn);
@@ -623,6 +630,9 @@ int lux3d_qk_l2norm_rope3d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_gamm
   } else if (coords) {
     if ((r = index_tensor(coords, fn, "coords", 0, p.N, 3, false))) return r;
     if (!(base > 0.f) || !std::isfinite(base)) return fail(LUX3D_ERR_VALUE, "%s: base must be a positive number", fn);
+    if (p.D / 2 / 3 < 1 || p.D / 2 / 3 > 64)
+      return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld gives %lld frequencies per axis (1..64)", fn, (long long)p.D,
+                  (long long)(p.D / 2 / 3));
     p.pos = coords->data; p.pos_dt = LUX3D_I32; p.pos_sN = coords->stride[0]; p.pos_sC = coords->stride[1];
     p.nfreq = (int)rope3d_freq(base, p.D, p.freq);
     rot = HR_R2_COORD;
@@ -672,6 +682,8 @@ int lux3d_dinov3_rope(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lu
     p.ntens = 2;
   }
   p.B = qv.B; p.H = qv.H; p.N = qv.N; p.D = qv.D;
+  p.vec = qv.vec && (p.ntens == 1 || kv.vec);
+  if (p.D % 2) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld must be even (rotate_half)", fn, (long long)p.D);
   if (num_prefix < 0 || num_prefix > p.N) return fail(LUX3D_ERR_VALUE, "%s: num_prefix out of range", fn);
   if ((r = check_desc(cos, fn, "cos")) || (r = check_desc(sin, fn, "sin"))) return r;
   for (const lux3d_tensor_t *t : {cos, sin}) {

@@ -71,6 +71,9 @@ struct HeadParams {
   float freq[64] = {};
   int nfreq = 0;
   int64_t prefix = 0;
+  // Vector path allowed: D is 64 or 128 and every head row and per-channel
+  // parameter vector is 16-byte aligned. Otherwise the generic kernel runs.
+  bool vec = true;
 };
 
 hipError_t launch_heads(int norm, int rot, int dt, const HeadParams &p, hipStream_t s);

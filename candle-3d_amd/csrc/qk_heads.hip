@@ -225,6 +225,148 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   }
 }
 
+// Generic path for any head dim and any alignment (the reference's own
+// tests use head dims 4, 6 and 12): one wavefront per (tensor, b, h, n) row,
+// lanes striding over the D elements, element loads re-read from the cache
+// instead of held in registers, and each element's phase evaluated where it
+// is used. Same arithmetic as head_kernel, element for element.
+template <int ROT>
+__device__ __forceinline__ void phase_any(const HeadParams &p, int64_t b, int64_t n, int64_t j, float &C,
+                                          float &S, int64_t &partner) {
+  const int64_t D = p.D, half = D / 2, quarter = D / 4;
+  C = 1.f;
+  S = 0.f;
+  partner = j;
+  if constexpr (ROT == HR_R1_TAB || ROT == HR_R1_POS) {
+    const int64_t jj = j % half;
+    partner = j - jj + (jj < quarter ? jj + quarter : jj - quarter);
+    if constexpr (ROT == HR_R1_TAB) {
+      const int64_t off = b * p.tab_sB + n * p.tab_sN + j;
+      C = param1(p.tab_c, p.tab_dt, off, 1.f);
+      S = param1(p.tab_s, p.tab_dt, off, 0.f);
+    } else {
+      const int64_t axis = j / half;
+      const uint32_t pv = (uint32_t)load_index(p.pos, p.pos_dt, b * p.pos_sB + n * p.pos_sN + axis * p.pos_sC);
+      float sv, cv;
+      sincosf((float)pv * p.freq[jj % quarter], &sv, &cv);
+      C = cv;
+      S = jj < quarter ? -sv : sv;
+    }
+  } else if constexpr (ROT == HR_R2_TAB || ROT == HR_R2_COORD) {
+    const int64_t a = j / 2;
+    partner = j ^ 1;
+    float sv, cv;
+    if constexpr (ROT == HR_R2_TAB) {
+      cv = param1(p.tab_c, p.tab_dt, n * p.tab_sN + a, 1.f);
+      sv = param1(p.tab_s, p.tab_dt, n * p.tab_sN + a, 0.f);
+    } else {
+      float ang = 0.f;
+      if (a < 3 * p.nfreq) {
+        const int32_t cval = reinterpret_cast<const int32_t *>(p.pos)[n * p.pos_sN + (a / p.nfreq) * p.pos_sC];
+        ang = (float)cval * p.freq[a % p.nfreq];
+      }
+      sincosf(ang, &sv, &cv);
+    }
+    C = cv;
+    S = (j & 1) ? sv : -sv;
+  } else if constexpr (ROT == HR_R3_TAB) {
+    partner = j < half ? j + half : j - half;
+    if (n >= p.prefix) {
+      const int64_t off = (n - p.prefix) * p.tab_sN + j;
+      C = param1(p.tab_c, p.tab_dt, off, 1.f);
+      const float sv = param1(p.tab_s, p.tab_dt, off, 0.f);
+      S = j < half ? -sv : sv;
+    } else {
+      partner = j;  // prefix tokens pass through
+    }
+  }
+}
+
+template <typename T, int NORM, int ROT>
+__global__ __launch_bounds__(256) void head_kernel_any(HeadParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t per = p.B * p.H * p.N;
+  const int64_t row = uniform((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (row >= per * p.ntens) return;  // wave-uniform
+  const int q = (int)(row / per);
+  int64_t r = row % per;
+  const int64_t n = r % p.N;
+  r /= p.N;
+  const int64_t h = r % p.H, b = r / p.H;
+  const HeadIO &io = p.io[q];
+  const int64_t D = p.D;
+  const int64_t xo = b * io.sB + h * io.sH + n * io.sN;
+  const int64_t yo = b * io.oB + h * io.oH + n * io.oN;
+
+  float mean = 0.f, rs = 1.f;
+  if constexpr (NORM == HN_LN) {
+    float s = 0.f;
+    for (int64_t j = lane; j < D; j += 64) s += load1<T>(io.x, xo + j);
+    mean = wave_sum(s) * (1.0f / (float)D);
+    float s2 = 0.f;
+    for (int64_t j = lane; j < D; j += 64) {
+      const float c = load1<T>(io.x, xo + j) - mean;
+      s2 += c * c;
+    }
+    rs = 1.0f / sqrtf(wave_sum(s2) * (1.0f / (float)D) + p.eps);
+  } else if constexpr (NORM == HN_RMS || NORM == HN_L2) {
+    float s2 = 0.f;
+    for (int64_t j = lane; j < D; j += 64) {
+      const float v = load1<T>(io.x, xo + j);
+      s2 += v * v;
+    }
+    if constexpr (NORM == HN_RMS) {
+      rs = 1.0f / sqrtf(wave_sum(s2) * (1.0f / (float)D) + p.eps);
+    } else {
+      rs = 1.0f / fminf(fmaxf(sqrtf(wave_sum(s2)), 1e-12f), 1.0e30f);
+    }
+  }
+  auto normed = [&](int64_t j) -> float {
+    const float v = load1<T>(io.x, xo + j);
+    if constexpr (NORM == HN_LN) {
+      return (v - mean) * rs * param1(io.p0, io.p0_dt, j, 1.f) + param1(io.p1, io.p1_dt, j, 0.f);
+    } else if constexpr (NORM == HN_RMS) {
+      return (v * rs) * param1(io.p0, io.p0_dt, j, 1.f);
+    } else if constexpr (NORM == HN_L2) {
+      return ((v * rs) * param1(io.p0, io.p0_dt, h * D + j, 1.f)) * sqrtf((float)D);
+    } else {
+      return v;
+    }
+  };
+  for (int64_t j = lane; j < D; j += 64) {
+    float out = normed(j);
+    if constexpr (ROT != HR_NONE) {
+      float C, S;
+      int64_t pj;
+      phase_any<ROT>(p, b, n, j, C, S, pj);
+      if (pj != j) out = __fadd_rn(__fmul_rn(out, C), __fmul_rn(normed(pj), S));
+    }
+    store1<T>(io.y, yo + j, out);
+  }
+}
+
+template <typename T>
+hipError_t launch_any(int norm, int rot, const HeadParams &p, hipStream_t s) {
+  const int64_t rows = p.B * p.H * p.N * p.ntens;
+  if (rows <= 0 || p.D <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define LUX3D_ANY_CASE(NORM_, ROT_)                                                 \
+  if (norm == NORM_ && rot == ROT_) {                                               \
+    hipLaunchKernelGGL((head_kernel_any<T, NORM_, ROT_>), grid, block, 0, s, p);    \
+    return hipGetLastError();                                                       \
+  }
+  LUX3D_ANY_CASE(HN_LN, HR_R1_TAB) LUX3D_ANY_CASE(HN_LN, HR_R1_POS)
+  LUX3D_ANY_CASE(HN_NONE, HR_R1_TAB) LUX3D_ANY_CASE(HN_NONE, HR_R1_POS)
+  LUX3D_ANY_CASE(HN_LN, HR_NONE)
+  LUX3D_ANY_CASE(HN_RMS, HR_NONE)
+  LUX3D_ANY_CASE(HN_L2, HR_NONE) LUX3D_ANY_CASE(HN_L2, HR_R2_TAB) LUX3D_ANY_CASE(HN_L2, HR_R2_COORD)
+  LUX3D_ANY_CASE(HN_NONE, HR_R2_TAB) LUX3D_ANY_CASE(HN_NONE, HR_R2_COORD)
+  LUX3D_ANY_CASE(HN_NONE, HR_R3_TAB)
+  LUX3D_ANY_CASE(HN_NONE, HR_NONE)
+#undef LUX3D_ANY_CASE
+  return hipErrorInvalidValue;
+}
+
 template <typename T, int D, int NTB>
 hipError_t launch_dn(int norm, int rot, const HeadParams &p, hipStream_t s) {
   const int64_t tokens = p.B * p.N;
@@ -271,9 +413,10 @@ hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
 
 template <typename T>
 hipError_t launch_t(int norm, int rot, const HeadParams &p, hipStream_t s) {
-  if (p.D == 64) return launch_d<T, 64>(norm, rot, p, s);
-  if (p.D == 128) return launch_d<T, 128>(norm, rot, p, s);
-  return hipErrorInvalidValue;
+  if (p.vec && p.D == 64) return launch_d<T, 64>(norm, rot, p, s);
+  if (p.vec && p.D == 128) return launch_d<T, 128>(norm, rot, p, s);
+  if (p.B * p.H * p.N > INT32_MAX / 2) return hipErrorInvalidValue;
+  return launch_any<T>(norm, rot, p, s);
 }
 
 // ---- table builders ---------------------------------------------------------

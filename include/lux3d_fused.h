@@ -139,7 +139,9 @@ int lux3d_gated_residual(const lux3d_tensor_t *x, const lux3d_tensor_t *h,
  * VGGT/Pi3 2D RoPE (R1) on Q and K head views, optionally after a per-head
  * affine LayerNorm (the q_norm/k_norm of the attention).
  *   q, k: [B, H, N, D] views with any outer strides (e.g. the permuted
- *     [B, N, 3, H, D] qkv buffer), D = 64 or 128; k may be NULL.
+ *     [B, N, 3, H, D] qkv buffer), D a multiple of 4 (as Rope2d requires);
+ *     k may be NULL. D = 64 or 128 with 16-byte aligned rows takes the
+ *     vectorised kernel, other head dims and alignments a generic one.
  *   q_w/q_b (k_w/k_b): [D] LayerNorm affine, or all NULL for RoPE only.
  *   cos_full, sin_alt_full: [B, N, D] or [B, 1, N, D] f32 tables as built by
  *     Rope2d::embeddings (sin table with the rotate-half negation folded in).
@@ -192,7 +194,7 @@ int lux3d_rms_norm_heads(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w,
 
 /* --------------------------------------------------------------------------
  * TRELLIS.2 q/k L2 "RMS" norm (N2) and/or 3D RoPE (R2) on [B, L, H, D] head
- * views (any outer strides; D = 64 or 128), q and k in one launch:
+ * views (any outer strides; any D, even when rotating), q and k in one launch:
  *   N2 (gamma [H, D] given): y = x / clamp(||x||, 1e-12, 1e30) * gamma * sqrt(D)
  *   R2 (phases given): pairs (y[2i], y[2i+1]) rotated by phase i of token l,
  *     from tables cos/sin [L, D/2] (Trellis2Rope3d::cos_sin layout) or

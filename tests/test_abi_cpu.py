@@ -113,10 +113,11 @@ def test_head_op_errors():
     q = T([2, 16, 10, 64], strides=[10 * 3 * 16 * 64, 64, 3 * 16 * 64, 1])
     out = T([2, 16, 10, 64])
     tab = T([2, 10, 64], _lib.F32)
-    # head dim 32 unsupported
-    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 32]), None, None, None, None, None, 1e-5, tab, tab,
-                     T([2, 16, 10, 32]), None, None)
-    assert rc == _lib.ERR_SHAPE and "head dim" in msg
+    # Rope2d needs a token_dim divisible by 4 (the reference's own check)
+    tab30 = T([2, 10, 30], _lib.F32)
+    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 30]), None, None, None, None, None, 1e-5, tab30,
+                     tab30, T([2, 16, 10, 30]), None, None)
+    assert rc == _lib.ERR_SHAPE and "divisible by 4" in msg
     # wrong table shape
     rc, msg = status("lux3d_qk_layernorm_rope2d", q, None, None, None, None, None, 1e-5, T([2, 11, 64], _lib.F32),
                      tab, out, None, None)
@@ -125,10 +126,15 @@ def test_head_op_errors():
     rc, msg = status("lux3d_qk_layernorm_rope2d", q, T([64], _lib.F32), None, None, None, None, 1e-5, tab, tab, out,
                      None, None)
     assert rc == _lib.ERR_NULL
-    # misaligned head rows
-    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 64], data=FAKE + 2), None, None, None, None, None,
-                     1e-5, tab, tab, out, None, None)
+    # a non-unit innermost stride
+    rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 64], strides=[20480, 1280, 128, 2]), None, None,
+                     None, None, None, 1e-5, tab, tab, out, None, None)
     assert rc == _lib.ERR_LAYOUT
+    # positions-based rotation holds at most 64 frequencies per axis half
+    big = T([2, 16, 10, 512])
+    rc, msg = status("lux3d_qk_layernorm_rope2d_pos", big, None, None, None, None, None, 1e-5,
+                     T([2, 10, 2], _lib.I32), 100.0, big, None, None)
+    assert rc == _lib.ERR_SHAPE
     # positions must be [B, N, 2] int
     rc, msg = status("lux3d_qk_layernorm_rope2d_pos", q, None, None, None, None, None, 1e-5,
                      T([2, 10, 2], _lib.F32), 100.0, out, None, None)
@@ -144,6 +150,15 @@ def test_head_op_errors():
     rc, msg = status("lux3d_qk_l2norm_rope3d", x, T([12, 64], _lib.F32), None, None, None, None, None, 10000.0, x,
                      None, None)
     assert rc == _lib.ERR_SHAPE   # gamma must be [H, D] = 12*128 elements
+    # rotating (re, im) pairs needs an even head dim; coords give 1..64 frequencies per axis
+    odd = T([1, 10, 2, 7])
+    rc, msg = status("lux3d_qk_l2norm_rope3d", odd, None, None, None, None, None, T([10, 3], _lib.I32), 10000.0,
+                     odd, None, None)
+    assert rc == _lib.ERR_SHAPE and "even" in msg
+    wide = T([1, 10, 2, 1024])
+    rc, msg = status("lux3d_qk_l2norm_rope3d", wide, None, None, None, None, None, T([10, 3], _lib.I32), 10000.0,
+                     wide, None, None)
+    assert rc == _lib.ERR_SHAPE and "frequencies" in msg
     # dinov3: prefix larger than the sequence
     y = T([1, 16, 9, 64])
     rc, msg = status("lux3d_dinov3_rope", y, None, T([4, 64], _lib.F32), T([4, 64], _lib.F32), 10, y, None, None)
