@@ -1,0 +1,274 @@
+// lux3d_candle.hpp -- C++ mirror of candle-3d's Tensor-level interface for
+// the fused transformer-layer path, built on the liblux3d_fused C ABI
+// (lux3d_fused.h).
+//
+// The reference is Rust (crates/lux3d-core over a candle fork). This header
+// keeps its names, argument meaning and error behaviour:
+//   * a Tensor is device storage shared between views plus a layout (shape,
+//     element strides, start offset), like candle's Arc<Storage> + Layout;
+//     views (narrow / transpose / permute / get / chunk / unsqueeze) copy
+//     nothing;
+//   * ops allocate their outputs, as a candle CustomOp does, and enqueue one
+//     kernel on the tensor's device stream; only the host transfers
+//     (from_* / to_vec_*) synchronise;
+//   * every failure the reference reports through `candle_core::Result` /
+//     `bail!` is thrown here as lux3d::candle::Error, with the C ABI's status
+//     and message (or the reference's own message where the check is the
+//     reference's).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <array>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "lux3d_fused.h"
+
+namespace lux3d::candle {
+
+enum class DType : int32_t {
+  F32 = LUX3D_F32,
+  BF16 = LUX3D_BF16,
+  F16 = LUX3D_F16,
+  I32 = LUX3D_I32,
+  I64 = LUX3D_I64,
+  U8 = LUX3D_U8,
+};
+size_t dtype_size(DType dt);
+
+// candle_core::Error: status is a lux3d_status (LUX3D_ERR_*).
+class Error : public std::runtime_error {
+ public:
+  Error(int status, const std::string &msg) : std::runtime_error(msg), status_(status) {}
+  int status() const { return status_; }
+
+ private:
+  int status_;
+};
+
+// A HIP device and the stream every op on it is enqueued on (the null
+// stream unless with_stream() names another).
+class Device {
+ public:
+  static Device hip(int ordinal = 0);
+  Device with_stream(hipStream_t s) const;
+  int ordinal() const { return ordinal_; }
+  hipStream_t stream() const { return stream_; }
+  void synchronize() const;
+
+ private:
+  int ordinal_ = 0;
+  hipStream_t stream_ = nullptr;
+};
+
+using Shape = std::vector<int64_t>;
+
+class Tensor {
+ public:
+  Tensor() = default;
+  // Device allocations (contents undefined / zero) and host uploads. f32
+  // values are rounded to nearest even for bf16 / f16 (half-crate rules).
+  static Tensor empty(const Shape &shape, DType dt, const Device &dev);
+  static Tensor zeros(const Shape &shape, DType dt, const Device &dev);
+  static Tensor from_f32(const std::vector<float> &v, const Shape &shape, DType dt, const Device &dev);
+  static Tensor from_i32(const std::vector<int32_t> &v, const Shape &shape, const Device &dev);
+  static Tensor from_i64(const std::vector<int64_t> &v, const Shape &shape, const Device &dev);
+  static Tensor from_u8(const std::vector<uint8_t> &v, const Shape &shape, const Device &dev);
+
+  const Shape &dims() const { return shape_; }
+  int64_t dim(int i) const;
+  size_t rank() const { return shape_.size(); }
+  int64_t elem_count() const;
+  const Shape &stride() const { return stride_; }
+  DType dtype() const { return dtype_; }
+  const Device &device() const { return device_; }
+  bool is_contiguous() const;
+
+  // Views (no copies).
+  Tensor narrow(int dim, int64_t start, int64_t len) const;
+  Tensor transpose(int d0, int d1) const;
+  Tensor permute(const std::vector<int> &order) const;
+  Tensor get(int64_t index) const;  // Tensor::i(index) on dim 0
+  Tensor unsqueeze(int dim) const;
+  Tensor reshape(const Shape &shape) const;  // contiguous tensors only
+  std::vector<Tensor> chunk(int64_t n, int dim) const;
+
+  // Device -> host in logical (row-major) order; synchronises the stream.
+  std::vector<float> to_vec_f32() const;
+  std::vector<uint16_t> to_vec_u16() const;  // raw bf16 / f16 bits
+
+  // The C ABI descriptor of this view.
+  lux3d_tensor_t desc() const;
+
+ private:
+  struct Storage;
+  std::shared_ptr<Storage> storage_;
+  int64_t offset_ = 0;  // elements
+  Shape shape_, stride_;
+  DType dtype_ = DType::F32;
+  Device device_;
+  static Tensor alloc(const Shape &shape, DType dt, const Device &dev);
+  std::vector<uint8_t> gather_bytes() const;
+};
+
+// ---- LayerNorm family -----------------------------------------------------
+
+// candle_nn::ops::layer_norm(x, alpha, beta, eps) over the last dim.
+Tensor layer_norm(const Tensor &x, const Tensor &alpha, const Tensor &beta, float eps);
+
+// candle_nn::LayerNorm as built by `layer_norm(dim, eps, vb)` (the affine
+// LayerNorm of runtime/vggt.rs:104, runtime/pi3_encoder.rs:67, ...).
+class LayerNorm {
+ public:
+  LayerNorm(Tensor weight, std::optional<Tensor> bias, double eps);
+  Tensor forward(const Tensor &xs) const;
+  const Tensor &weight() const { return weight_; }
+  const std::optional<Tensor> &bias() const { return bias_; }
+  double eps() const { return eps_; }
+
+ private:
+  Tensor weight_;
+  std::optional<Tensor> bias_;
+  double eps_;
+};
+
+// layer_norm_no_affine (runtime/trellis2_blocks.rs:280-286).
+Tensor layer_norm_no_affine(const Tensor &xs, double eps);
+
+// LayerScale (runtime/nn_blocks.rs:210-214): xs * gamma.
+class LayerScale {
+ public:
+  explicit LayerScale(Tensor gamma) : gamma_(std::move(gamma)) {}
+  const Tensor &gamma() const { return gamma_; }
+
+ private:
+  Tensor gamma_;
+};
+
+// `h = x + ls(a)` then `norm(h)` (VggtBlock::forward, runtime/vggt.rs:113-124;
+// ls may be null for the plain residual of runtime/triposg_dit.rs:364-379).
+// Returns (h, norm(h)).
+std::pair<Tensor, Tensor> residual_layer_norm(const Tensor &x, const Tensor &a, const LayerScale *ls,
+                                              const LayerNorm &norm);
+
+// ---- AdaLN (TRELLIS.2) ----------------------------------------------------
+
+// chunk_modulation (runtime/trellis2_blocks.rs:264-277): the six [B, 1, C]
+// views (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp).
+std::array<Tensor, 6> chunk_modulation(const Tensor &mod_vec);
+
+// `layer_norm_no_affine(x) * (1 + scale) + shift` (and `gate * (...) + x`
+// when gate is given) with shift / scale / gate per batch element or per
+// ragged segment (seg_offsets int64 [S+1]); `*_base` is the block's
+// `modulation` vector added to each piece (runtime/trellis2_blocks.rs:617-630,
+// 693-706; runtime/vggt.rs:399-405).
+struct Modulation {
+  Tensor shift, scale;
+  std::optional<Tensor> gate, shift_base, scale_base, gate_base;
+};
+Tensor adaln_modulate(const Tensor &x, const Modulation &m, double eps,
+                      const std::optional<Tensor> &seg_offsets = std::nullopt);
+
+// `xs + h * gate` (runtime/trellis2_blocks.rs:632-633).
+Tensor gated_residual(const Tensor &x, const Tensor &h, const Tensor &gate,
+                      const std::optional<Tensor> &gate_base = std::nullopt,
+                      const std::optional<Tensor> &seg_offsets = std::nullopt);
+
+// ---- VGGT / Pi3 2D RoPE (runtime/attention_math.rs) -------------------------
+
+struct RopeEmbeddings {
+  Tensor cos_full, sin_alt_full;  // [b, 1, n, token_dim] f32
+};
+
+class Rope2d {
+ public:
+  explicit Rope2d(float base) : base_(base) {}
+  // positions: int32 / int64 [b, n, 2] on the device.
+  RopeEmbeddings embeddings(const Tensor &positions, size_t token_dim) const;
+  float base() const { return base_; }
+
+ private:
+  float base_;
+};
+
+// apply_layernorm_rope (runtime/attention_math.rs:127-150) and apply_rope
+// (:155-165) on [b, h, n, d] views (strided allowed, unit inner stride).
+Tensor apply_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeEmbeddings &embeddings);
+Tensor apply_rope(const Tensor &tokens, const RopeEmbeddings &embeddings);
+
+// Both calls of VggtAttention::forward (runtime/vggt.rs:170-181) in one
+// launch, the rotation computed from the positions in-kernel.
+std::pair<Tensor, Tensor> qk_layernorm_rope2d(const Tensor &q, const Tensor &k, const LayerNorm &q_norm,
+                                              const LayerNorm &k_norm, const Tensor &positions, float base);
+
+// ---- TripoSG --------------------------------------------------------------
+
+// RmsNormHeads::rms_norm_heads (runtime/triposg_dit.rs:509-522), eps 1e-6.
+Tensor rms_norm_heads(const Tensor &x, const Tensor &weight);
+
+// TripoSgDiT::timestep_embedding (runtime/triposg_dit.rs:280-297):
+// [sin(t*f), cos(t*f)] for t [n] -> [n, dim].
+Tensor triposg_timestep_embedding(const Tensor &t, size_t dim);
+
+// ---- TRELLIS.2 ------------------------------------------------------------
+
+// Trellis2QkRmsNorm (runtime/trellis2_blocks.rs:288-320), gamma [heads, head_dim].
+class Trellis2QkRmsNorm {
+ public:
+  explicit Trellis2QkRmsNorm(Tensor gamma) : gamma_(std::move(gamma)) {}
+  Tensor forward(const Tensor &xs) const;  // xs [B, L, H, D]
+
+ private:
+  Tensor gamma_;
+};
+
+// Trellis2Rope3d (runtime/trellis2_blocks.rs:84-161).
+class Trellis2Rope3d {
+ public:
+  explicit Trellis2Rope3d(size_t head_dim, float rope_base = 10000.0f) : head_dim_(head_dim), rope_base_(rope_base) {}
+  size_t head_dim() const { return head_dim_; }
+  // coords: [L, 3] flattened (x, y, z). Returns (cos, sin) [L, head_dim/2] f32.
+  std::pair<Tensor, Tensor> cos_sin(const std::vector<int64_t> &coords, const Device &dev) const;
+  // x [B, L, H, head_dim]
+  Tensor apply(const Tensor &x, const Tensor &cos, const Tensor &sin) const;
+
+ private:
+  size_t head_dim_;
+  float rope_base_;
+};
+
+// Both tensors' N2 then R2 (Trellis2SelfAttention::attention,
+// runtime/trellis2_blocks.rs:423-430) in one launch from voxel coords.
+std::pair<Tensor, Tensor> qk_l2norm_rope3d(const Tensor &q, const Tensor &k, const Tensor &q_gamma,
+                                           const Tensor &k_gamma, const Tensor &coords, float rope_base = 10000.0f);
+
+// timestep_embedding (runtime/trellis2_blocks.rs:184-204): [cos, sin], [dim].
+Tensor timestep_embedding(float t, size_t dim, const Device &dev);
+
+// Trellis2DinoConfig::rope_cos_sin (runtime/trellis2_dino.rs:140-187):
+// (cos, sin) [grid_h * grid_w, head_dim], built on the host as the
+// reference does.
+std::pair<Tensor, Tensor> dinov3_rope_cos_sin(size_t head_dim, float rope_theta, size_t grid_h, size_t grid_w,
+                                              const Device &dev);
+
+// apply_rotary_to_patches (runtime/trellis2_dino.rs:406-436).
+std::pair<Tensor, Tensor> apply_rotary_to_patches(const Tensor &q, const Tensor &k, const Tensor &cos,
+                                                  const Tensor &sin, size_t num_prefix);
+
+// ---- elementwise / quantised weights -----------------------------------------
+
+Tensor gelu(const Tensor &x);      // Tensor::gelu (tanh approximation)
+Tensor gelu_erf(const Tensor &x);  // Tensor::gelu_erf
+Tensor silu(const Tensor &x);      // Tensor::silu
+
+// QTensor::dequantize for GGML Q8_0 (runtime/nn_blocks.rs:140): `blocks`
+// holds elem_count(shape)/32 records of 34 bytes; out dtype F32, BF16 or F16.
+Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out);
+
+}  // namespace lux3d::candle

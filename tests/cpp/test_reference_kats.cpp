@@ -1,0 +1,345 @@
+// The reference's own known-answer tests for this path, restated against the
+// C++ mirror (candle-3d_amd/host/lux3d_candle.hpp) and run on the GPU:
+//   tests/trellis2_blocks.rs:43-171, 205-225   (crates/lux3d-core)
+//   src/runtime/trellis2_dino.rs:516-644        (DINOv3 RoPE unit tests)
+// plus the reference's error behaviour for the same functions and a few
+// closed-form checks of the other mirrored ops.
+//
+// Usage: test_reference_kats [--cpu]
+//   --cpu runs only the checks that fail before any device work (argument
+//   validation), for a machine without a GPU. Exit status 0 when all pass.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "lux3d_candle.hpp"
+
+using namespace lux3d::candle;
+
+namespace {
+
+int g_failures = 0;
+
+#define CHECK(cond)                                                                    \
+  do {                                                                                 \
+    if (!(cond)) {                                                                     \
+      std::printf("    CHECK failed at %s:%d: %s\n", __FILE__, __LINE__, #cond);       \
+      ++g_failures;                                                                    \
+      return;                                                                          \
+    }                                                                                  \
+  } while (0)
+
+#define CHECK_NEAR(a, b, tol)                                                          \
+  do {                                                                                 \
+    const double a_ = (a), b_ = (b);                                                   \
+    if (!(std::fabs(a_ - b_) < (tol))) {                                               \
+      std::printf("    CHECK_NEAR failed at %s:%d: %s = %.9g, %s = %.9g (tol %g)\n",   \
+                  __FILE__, __LINE__, #a, a_, #b, b_, (double)(tol));                 \
+      ++g_failures;                                                                    \
+      return;                                                                          \
+    }                                                                                  \
+  } while (0)
+
+// The reference bails with these messages; the mirror throws Error with them.
+template <typename F>
+bool throws_with(F &&f, const char *needle) {
+  try {
+    f();
+  } catch (const Error &e) {
+    if (std::strstr(e.what(), needle)) return true;
+    std::printf("    threw a different message: %s\n", e.what());
+    return false;
+  }
+  return false;
+}
+
+std::vector<float> iota_f(size_t n, float start, float step) {
+  std::vector<float> v(n);
+  for (size_t i = 0; i < n; ++i) v[i] = start + step * (float)i;
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// tests/trellis2_blocks.rs
+// ---------------------------------------------------------------------------
+
+// rope_tables_match_reference_formula (:43-74): head_dim 12 -> freq_dim 2 per
+// axis, freqs = [1, 10000^-0.5], axis-major angles, pad pair at angle 0.
+void rope_tables_match_reference_formula(const Device &dev) {
+  Trellis2Rope3d rope(12);
+  const std::vector<int64_t> coords{1, 0, 0, 0, 1, 0};
+  auto [cos, sin] = rope.cos_sin(coords, dev);
+  CHECK((cos.dims() == Shape{2, 6}));
+  const std::vector<float> c = cos.to_vec_f32(), s = sin.to_vec_f32();
+  const float freq2 = 1.0f / std::pow(10000.0f, 0.5f);
+  for (int token = 0; token < 2; ++token) {
+    const int64_t *cd = &coords[token * 3];
+    const float angles[6] = {(float)cd[0] * 1.0f, (float)cd[0] * freq2, (float)cd[1] * 1.0f,
+                             (float)cd[1] * freq2, (float)cd[2] * 1.0f, (float)cd[2] * freq2};
+    for (int j = 0; j < 6; ++j) {
+      CHECK_NEAR(c[token * 6 + j], std::cos(angles[j]), 1e-6);
+      CHECK_NEAR(s[token * 6 + j], std::sin(angles[j]), 1e-6);
+    }
+  }
+}
+
+// rope_apply_matches_complex_product_and_preserves_norm (:79-111).
+void rope_apply_matches_complex_product_and_preserves_norm(const Device &dev) {
+  Trellis2Rope3d rope(12);
+  auto [cos, sin] = rope.cos_sin({1, 0, 0}, dev);
+  const std::vector<float> x{1.0f, 0.0f, 2.0f, 3.0f, 5.0f, 0.0f, 7.0f, 1.0f, 0.0f, 2.0f, 4.0f, 4.0f};
+  const Tensor xs = Tensor::from_f32(x, {1, 1, 1, 12}, DType::F32, dev);
+  const Tensor out_t = rope.apply(xs, cos, sin);
+  CHECK((out_t.dims() == Shape{1, 1, 1, 12}));
+  const std::vector<float> out = out_t.to_vec_f32();
+  const float freq2 = 1.0f / std::pow(10000.0f, 0.5f);
+  const float phases[3][2] = {{1.0f, 1.0f}, {freq2, freq2}, {0.0f, 0.0f}};
+  for (int pair = 0; pair < 6; ++pair) {
+    float ac = 1.0f, as = 0.0f;  // z coordinate zero + pad pair: angle 0
+    if (pair < 2) {
+      ac = std::cos(phases[pair][0]);
+      as = std::sin(phases[pair][1]);
+    }
+    const float re = x[2 * pair], im = x[2 * pair + 1];
+    CHECK_NEAR(out[2 * pair], re * ac - im * as, 1e-5);
+    CHECK_NEAR(out[2 * pair + 1], re * as + im * ac, 1e-5);
+  }
+  float e_in = 0.f, e_out = 0.f;
+  for (int i = 0; i < 12; ++i) {
+    e_in += x[i] * x[i];
+    e_out += out[i] * out[i];
+  }
+  CHECK_NEAR(e_in, e_out, 1e-4);
+}
+
+// qk_rms_norm_matches_reference (:126-153).
+void qk_rms_norm_matches_reference(const Device &dev) {
+  const Tensor xs = Tensor::from_f32({3.0f, 4.0f, 0.0f, 0.0f}, {1, 1, 1, 4}, DType::F32, dev);
+  const float gammas[2] = {1.0f, 2.0f};
+  const float want[2][4] = {{0.6f * 2.0f, 0.8f * 2.0f, 0.0f, 0.0f}, {2.4f, 3.2f, 0.0f, 0.0f}};
+  for (int g = 0; g < 2; ++g) {
+    Trellis2QkRmsNorm norm(Tensor::from_f32(std::vector<float>(4, gammas[g]), {1, 4}, DType::F32, dev));
+    const std::vector<float> out = norm.forward(xs).to_vec_f32();
+    for (int i = 0; i < 4; ++i) CHECK_NEAR(out[i], want[g][i], 1e-6);
+  }
+}
+
+// timestep_embedding_matches_reference (:157-171).
+void timestep_embedding_matches_reference(const Device &dev) {
+  const Tensor emb = timestep_embedding(500.0f, 4, dev);
+  CHECK((emb.dims() == Shape{4}));
+  const std::vector<float> v = emb.to_vec_f32();
+  const float freq1 = (float)std::exp(-std::log(10000.0) / 2.0);
+  const float expected[4] = {std::cos(500.0f), std::cos(500.0f * freq1), std::sin(500.0f), std::sin(500.0f * freq1)};
+  for (int i = 0; i < 4; ++i) CHECK_NEAR(v[i], expected[i], 1e-5);
+}
+
+// ada_ln_modulation_chunks_in_reference_order (:205-225).
+void ada_ln_modulation_chunks_in_reference_order(const Device &dev) {
+  const Tensor mod_vec = Tensor::from_f32(iota_f(12, 1.0f, 1.0f), {1, 12}, DType::F32, dev);
+  const std::array<Tensor, 6> chunks = chunk_modulation(mod_vec);
+  for (int i = 0; i < 6; ++i) {
+    CHECK((chunks[i].dims() == Shape{1, 1, 2}));
+    const std::vector<float> v = chunks[i].to_vec_f32();
+    CHECK(v[0] == (float)(2 * i + 1) && v[1] == (float)(2 * i + 2));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// src/runtime/trellis2_dino.rs tests
+// ---------------------------------------------------------------------------
+
+// rope_tables_match_hand_computed_cos_sin (:516-565): head_dim 8, theta 100,
+// 2x2 grid -> inv_freq [1, 0.1], [y freqs, x freqs] tiled twice.
+void dinov3_rope_tables_match_hand_computed_cos_sin(const Device &dev) {
+  const size_t grid = 2;
+  auto [cos, sin] = dinov3_rope_cos_sin(8, 100.0f, grid, grid, dev);
+  CHECK((cos.dims() == Shape{4, 8}) && (sin.dims() == Shape{4, 8}));
+  const std::vector<float> c = cos.to_vec_f32(), s = sin.to_vec_f32();
+  const float inv_freq[2] = {1.0f, 1.0f / std::pow(100.0f, 0.5f)};
+  const float two_pi = (float)(M_PI * 2.0);
+  int row = 0;
+  for (size_t y = 0; y < grid; ++y) {
+    const float cy = 2.0f * (((float)y + 0.5f) / (float)grid) - 1.0f;
+    for (size_t x = 0; x < grid; ++x, ++row) {
+      const float cx = 2.0f * (((float)x + 0.5f) / (float)grid) - 1.0f;
+      std::vector<float> half;
+      for (float coord : {cy, cx})
+        for (float f : inv_freq) half.push_back(two_pi * coord * f);
+      for (int j = 0; j < 8; ++j) {
+        const float want = half[j % 4];
+        CHECK_NEAR(c[row * 8 + j], std::cos(want), 1e-6);
+        CHECK_NEAR(s[row * 8 + j], std::sin(want), 1e-6);
+      }
+    }
+  }
+}
+
+// rope_applies_to_patches_only_and_prefix_tokens_pass_through (:583-643).
+void dinov3_rope_applies_to_patches_only(const Device &dev) {
+  const size_t head_dim = 8, num_prefix = 3, patches = 2, seq = num_prefix + patches;
+  std::vector<float> qv(seq * head_dim);
+  for (size_t i = 0; i < qv.size(); ++i) qv[i] = 0.1f * ((float)i + 1.0f);
+  const Tensor q = Tensor::from_f32(qv, {1, 1, (int64_t)seq, (int64_t)head_dim}, DType::F32, dev);
+  const Tensor k = Tensor::from_f32(qv, {1, 1, (int64_t)seq, (int64_t)head_dim}, DType::F32, dev);
+  const float c = 0.5f, s = std::sqrt(0.5f);
+  const Tensor cos = Tensor::from_f32(std::vector<float>(patches * head_dim, c),
+                                      {(int64_t)patches, (int64_t)head_dim}, DType::F32, dev);
+  const Tensor sin = Tensor::from_f32(std::vector<float>(patches * head_dim, s),
+                                      {(int64_t)patches, (int64_t)head_dim}, DType::F32, dev);
+  auto [q_rot, k_rot] = apply_rotary_to_patches(q, k, cos, sin, num_prefix);
+  const std::vector<float> r = q_rot.to_vec_f32();
+  for (size_t token = 0; token < num_prefix; ++token)
+    for (size_t d = 0; d < head_dim; ++d) CHECK_NEAR(r[token * head_dim + d], 0.1f * ((float)(token * head_dim + d) + 1.0f), 1e-6);
+  const float base = 0.1f * (float)(num_prefix * head_dim + 1);
+  std::vector<float> qp(head_dim);
+  for (size_t i = 0; i < head_dim; ++i) qp[i] = base + 0.1f * (float)i;
+  for (size_t d = 0; d < head_dim; ++d) {
+    const float partner = d < head_dim / 2 ? -qp[d + head_dim / 2] : qp[d - head_dim / 2];
+    CHECK_NEAR(r[num_prefix * head_dim + d], qp[d] * c + partner * s, 1e-5);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Closed-form checks of the other mirrored ops (small hand-checkable inputs)
+// ---------------------------------------------------------------------------
+
+// VGGT block residual: h = x + a*gamma exactly (f32, one rounding each), y = LN(h).
+void residual_layer_norm_closed_form(const Device &dev) {
+  const int64_t d = 8;
+  const std::vector<float> x = iota_f(d, -1.0f, 0.25f), a = iota_f(d, 2.0f, -0.5f), g(d, 0.5f);
+  const LayerNorm norm(Tensor::from_f32(std::vector<float>(d, 1.0f), {d}, DType::F32, dev),
+                       Tensor::from_f32(std::vector<float>(d, 0.0f), {d}, DType::F32, dev), 1e-5);
+  const LayerScale ls(Tensor::from_f32(g, {d}, DType::F32, dev));
+  auto [h, y] = residual_layer_norm(Tensor::from_f32(x, {1, d}, DType::F32, dev),
+                                    Tensor::from_f32(a, {1, d}, DType::F32, dev), &ls, norm);
+  const std::vector<float> hv = h.to_vec_f32(), yv = y.to_vec_f32();
+  double mean = 0, var = 0;
+  for (int64_t i = 0; i < d; ++i) {
+    CHECK(hv[i] == x[i] + a[i] * 0.5f);
+    mean += hv[i];
+  }
+  mean /= d;
+  for (int64_t i = 0; i < d; ++i) var += (hv[i] - mean) * (hv[i] - mean);
+  var /= d;
+  for (int64_t i = 0; i < d; ++i) CHECK_NEAR(yv[i], (hv[i] - mean) / std::sqrt(var + 1e-5), 1e-5);
+}
+
+// VGGT QK LN + 2D RoPE on a strided qkv view: position (0, 0) is the
+// identity rotation, so the special tokens equal the plain LayerNorm.
+void vggt_qk_layernorm_rope_specials_are_plain_layernorm(const Device &dev) {
+  const int64_t B = 1, N = 3, H = 2, D = 8;
+  std::vector<float> qkv((size_t)(B * N * 3 * H * D));
+  for (size_t i = 0; i < qkv.size(); ++i) qkv[i] = std::sin(0.37f * (float)i) * 2.0f;
+  const Tensor t = Tensor::from_f32(qkv, {B, N, 3, H, D}, DType::F32, dev);
+  const Tensor perm = t.permute({2, 0, 3, 1, 4});  // [3, B, H, N, D]
+  const Tensor q = perm.get(0), k = perm.get(1);
+  const LayerNorm ln(Tensor::from_f32(std::vector<float>(D, 1.0f), {D}, DType::F32, dev),
+                     Tensor::from_f32(std::vector<float>(D, 0.0f), {D}, DType::F32, dev), 1e-5);
+  const Tensor pos = Tensor::from_i32({0, 0, 1, 2, 2, 1}, {B, N, 2}, dev);
+  auto [qo, ko] = qk_layernorm_rope2d(q, k, ln, ln, pos, 100.0f);
+  const RopeEmbeddings emb = Rope2d(100.0f).embeddings(pos, (size_t)D);
+  const Tensor q_tab = apply_layernorm_rope(q, ln, emb);
+  const std::vector<float> a = qo.to_vec_f32(), b = q_tab.to_vec_f32();
+  CHECK(ko.dims() == qo.dims());
+  // positions and tables paths agree
+  for (size_t i = 0; i < a.size(); ++i) CHECK_NEAR(a[i], b[i], 1e-5);
+  // token 0 of every head is the plain LayerNorm of its row
+  const std::vector<float> qin = q.to_vec_f32();
+  for (int64_t h = 0; h < H; ++h) {
+    const float *row = &qin[(size_t)((h * N + 0) * D)];
+    double mean = 0, var = 0;
+    for (int64_t j = 0; j < D; ++j) mean += row[j];
+    mean /= D;
+    for (int64_t j = 0; j < D; ++j) var += (row[j] - mean) * (row[j] - mean);
+    var /= D;
+    for (int64_t j = 0; j < D; ++j) CHECK_NEAR(a[(size_t)((h * N) * D + j)], (row[j] - mean) / std::sqrt(var + 1e-5), 1e-5);
+  }
+}
+
+// Q8_0: w = f16(d) * int8(q), exact.
+void dequantize_q8_0_exact(const Device &dev) {
+  std::vector<uint8_t> blk(34);
+  const uint16_t d_half = 0x3800;  // 0.5
+  std::memcpy(blk.data(), &d_half, 2);
+  for (int i = 0; i < 32; ++i) blk[2 + i] = (uint8_t)(int8_t)(i - 16);
+  const Tensor w = dequantize_q8_0(Tensor::from_u8(blk, {34}, dev), {32}, DType::F32);
+  const std::vector<float> v = w.to_vec_f32();
+  for (int i = 0; i < 32; ++i) CHECK(v[i] == 0.5f * (float)(i - 16));
+}
+
+// ---------------------------------------------------------------------------
+// Error behaviour (the reference's bail! messages)
+// ---------------------------------------------------------------------------
+
+void errors_on_host(const Device &dev) {
+  CHECK(throws_with([&] { Trellis2Rope3d(12).cos_sin({1, 2, 3, 4}, dev); },
+                    "TRELLIS.2 RoPE coords must be [L, 3] flattened"));
+  CHECK(throws_with([&] { Trellis2Rope3d(4).cos_sin({1, 2, 3}, dev); }, "is too small for 3-axis RoPE"));
+  CHECK(throws_with([&] { Trellis2Rope3d(13).cos_sin({1, 2, 3}, dev); }, "must be divisible by 2"));
+  CHECK(throws_with([&] { dinov3_rope_cos_sin(10, 100.0f, 2, 2, dev); }, "is not divisible by 4"));
+}
+
+void errors_on_device(const Device &dev) {
+  const Tensor pos = Tensor::from_i32({0, 0, 1, 1}, {1, 2, 2}, dev);
+  CHECK(throws_with([&] { Rope2d(100.0f).embeddings(pos, 6); }, "rope token_dim must be divisible by 4"));
+  Trellis2Rope3d rope(12);
+  auto [cos, sin] = rope.cos_sin({1, 0, 0}, dev);
+  const Tensor x2 = Tensor::zeros({1, 2, 1, 12}, DType::F32, dev);
+  CHECK(throws_with([&] { rope.apply(x2, cos, sin); }, "RoPE tables must be [2, 6]"));
+  // a C ABI check surfaces as Error with the library's status and message
+  try {
+    layer_norm(Tensor::zeros({4, 8}, DType::BF16, dev), Tensor::zeros({7}, DType::F32, dev),
+               Tensor::zeros({8}, DType::F32, dev), 1e-5f);
+    CHECK(false);
+  } catch (const Error &e) {
+    CHECK(e.status() == LUX3D_ERR_SHAPE);
+  }
+}
+
+struct Case {
+  const char *name;
+  std::function<void(const Device &)> fn;
+  bool needs_gpu;
+};
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+  const std::vector<Case> cases = {
+      {"errors_on_host", errors_on_host, false},
+      {"rope_tables_match_reference_formula", rope_tables_match_reference_formula, true},
+      {"rope_apply_matches_complex_product_and_preserves_norm", rope_apply_matches_complex_product_and_preserves_norm, true},
+      {"qk_rms_norm_matches_reference", qk_rms_norm_matches_reference, true},
+      {"timestep_embedding_matches_reference", timestep_embedding_matches_reference, true},
+      {"ada_ln_modulation_chunks_in_reference_order", ada_ln_modulation_chunks_in_reference_order, true},
+      {"dinov3_rope_tables_match_hand_computed_cos_sin", dinov3_rope_tables_match_hand_computed_cos_sin, true},
+      {"dinov3_rope_applies_to_patches_only", dinov3_rope_applies_to_patches_only, true},
+      {"residual_layer_norm_closed_form", residual_layer_norm_closed_form, true},
+      {"vggt_qk_layernorm_rope_specials_are_plain_layernorm", vggt_qk_layernorm_rope_specials_are_plain_layernorm, true},
+      {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
+      {"errors_on_device", errors_on_device, true},
+  };
+  Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed
+  if (!cpu_only) dev = Device::hip(0);
+  int run = 0;
+  for (const Case &c : cases) {
+    if (cpu_only && c.needs_gpu) continue;
+    const int before = g_failures;
+    try {
+      c.fn(dev);
+    } catch (const std::exception &e) {
+      std::printf("    unexpected exception: %s\n", e.what());
+      ++g_failures;
+    }
+    std::printf("%s %s\n", g_failures == before ? "PASS" : "FAIL", c.name);
+    std::fflush(stdout);
+    ++run;
+  }
+  std::printf("%d cases, %d failures\n", run, g_failures);
+  return g_failures == 0 ? 0 : 1;
+}
