@@ -556,3 +556,14 @@ def test_dequant_q8_0(dev, ops, orc, synth, out, which):
     got2 = host_view(buf[1:], out).reshape(-1)
     assert np.array_equal(got2.view(np.uint32 if out == "f32" else np.uint16),
                           want.view(np.uint32 if out == "f32" else np.uint16))
+    # blocks that are only 2-byte aligned (direct kernel) and a block count
+    # that leaves a ragged last workgroup (staged kernel's tail)
+    raw = torch.empty(blocks.size + 2, dtype=torch.uint8, device=dev)
+    raw[2:] = bd
+    y3 = ops.dequantize_q8_0(raw[2:], shape, TDT[out])
+    nb = blocks.size // 34 - 5
+    y4 = ops.dequantize_q8_0(bd[:nb * 34], (nb * 32,), TDT[out])
+    sync()
+    u = np.uint32 if out == "f32" else np.uint16
+    assert np.array_equal(host_view(y3, out).reshape(-1).view(u), want.view(u)), "2-byte aligned blocks"
+    assert np.array_equal(host_view(y4, out).reshape(-1).view(u), want[:nb * 32].view(u)), "ragged block count"
