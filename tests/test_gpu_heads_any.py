@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 
 pytestmark = pytest.mark.gpu
 
-from conftest import assert_bf16_close, assert_f32_close  # noqa: E402
+from conftest import assert_bf16_close, assert_f16_close, assert_f32_close  # noqa: E402
 
 
 @pytest.fixture(scope="module")
@@ -43,7 +43,7 @@ def synth():
     return s
 
 
-TDT = {"f32": torch.float32, "bf16": torch.bfloat16}
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def to_dev(a, dev, dt="f32"):
@@ -51,20 +51,25 @@ def to_dev(a, dev, dt="f32"):
 
 
 def host(t, dt):
+    """f32 -> numpy f32; bf16 -> uint16 bits; f16 -> numpy float16 (the oracle's encodings)."""
     t = t.detach().contiguous().cpu()
-    return t.numpy() if dt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+    if dt == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
 
 
 def check(got, want, dt, what):
     g = host(got, dt)
     if dt == "f32":
         assert_f32_close(g, want, what=what)
-    else:
+    elif dt == "bf16":
         assert_bf16_close(g, want, what=what)
+    else:
+        assert_f16_close(g.view(np.uint16), np.asarray(want).view(np.uint16), what=what)
 
 
 def odt(orc, dt):
-    return orc.F32 if dt == "f32" else orc.BF16
+    return {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}[dt]
 
 
 def misaligned(t):
@@ -77,7 +82,8 @@ def misaligned(t):
 
 
 @pytest.mark.parametrize("dt,D,source", [("bf16", 12, "tables"), ("bf16", 12, "positions"), ("f32", 32, "tables"),
-                                         ("bf16", 96, "positions"), ("f32", 96, "positions")])
+                                         ("bf16", 96, "positions"), ("f32", 96, "positions"),
+                                         ("f16", 64, "positions"), ("f16", 64, "tables"), ("f16", 12, "positions")])
 def test_qk_layernorm_rope2d_any_dim(dev, ops, orc, synth, dt, D, source):
     print(f"\n[case] qk_layernorm_rope2d D={D} dt={dt} source={source}", flush=True)
     B, H, ph, pw = 2, 3, 4, 5
@@ -132,26 +138,27 @@ def test_head_kernels_on_unaligned_views(dev, ops, orc, synth, dt):
     check(ro, orc.rms_norm_heads(np.ascontiguousarray(host(r, dt)), rw, 1e-6, dt=odt(orc, dt)), dt, "unaligned RMS")
 
 
-@pytest.mark.parametrize("D", [4, 96, 130])
-def test_rms_norm_heads_any_dim(dev, ops, orc, synth, D):
-    print(f"\n[case] rms_norm_heads D={D}", flush=True)
+@pytest.mark.parametrize("dt,D", [("bf16", 4), ("bf16", 96), ("bf16", 130), ("f16", 128), ("f16", 96)])
+def test_rms_norm_heads_any_dim(dev, ops, orc, synth, dt, D):
+    print(f"\n[case] rms_norm_heads D={D} dt={dt}", flush=True)
     B, L, H = 2, 33, 5
-    qkv = to_dev(synth.normal(221, B * L * H * 3 * D).reshape(B, L, H, 3 * D), dev, "bf16")
+    qkv = to_dev(synth.normal(221, B * L * H * 3 * D).reshape(B, L, H, 3 * D), dev, dt)
     q, k = qkv[..., :D].transpose(1, 2), qkv[..., D:2 * D].transpose(1, 2)
     wq, wk = synth.normal(222, D, 1.0, 0.05), synth.normal(223, D, 1.0, 0.05)
     T = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
     qo, ko = ops.rms_norm_heads(q, T(wq), 1e-6, k=k, k_weight=T(wk))
     torch.cuda.synchronize()
-    check(qo, orc.rms_norm_heads(np.ascontiguousarray(host(q, "bf16")), wq, 1e-6, dt=orc.BF16), "bf16", "q")
-    check(ko, orc.rms_norm_heads(np.ascontiguousarray(host(k, "bf16")), wk, 1e-6, dt=orc.BF16), "bf16", "k")
+    check(qo, orc.rms_norm_heads(np.ascontiguousarray(host(q, dt)), wq, 1e-6, dt=odt(orc, dt)), dt, "q")
+    check(ko, orc.rms_norm_heads(np.ascontiguousarray(host(k, dt)), wk, 1e-6, dt=odt(orc, dt)), dt, "k")
 
 
-@pytest.mark.parametrize("D,source", [(6, "coords"), (12, "coords"), (12, "tables"), (36, "coords")])
-def test_qk_l2norm_rope3d_any_dim(dev, ops, orc, synth, D, source):
-    print(f"\n[case] qk_l2norm_rope3d D={D} source={source}", flush=True)
+@pytest.mark.parametrize("dt,D,source", [("f32", 6, "coords"), ("f32", 12, "coords"), ("f32", 12, "tables"),
+                                         ("f32", 36, "coords"), ("f16", 128, "coords"), ("f16", 12, "tables")])
+def test_qk_l2norm_rope3d_any_dim(dev, ops, orc, synth, dt, D, source):
+    print(f"\n[case] qk_l2norm_rope3d D={D} dt={dt} source={source}", flush=True)
     L, H = 40, 2
     coords = synth.unique_voxels(231, L, 64)
-    qkv = to_dev(synth.normal(232, L * 3 * H * D).reshape(1, L, 3, H, D), dev, "f32")
+    qkv = to_dev(synth.normal(232, L * 3 * H * D).reshape(1, L, 3, H, D), dev, dt)
     q, k = qkv[:, :, 0], qkv[:, :, 1]
     gq = synth.normal(233, H * D, 1.0, 0.05).reshape(H, D)
     T = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
@@ -162,21 +169,21 @@ def test_qk_l2norm_rope3d_any_dim(dev, ops, orc, synth, D, source):
         qo, ko = ops.qk_l2norm_rope3d(q, k, T(gq), T(gq), cos=T(cos), sin=T(sin))
     torch.cuda.synchronize()
     for got, src, what in ((qo, q, "q"), (ko, k, "k")):
-        want = orc.qk_l2norm_rope3d(np.ascontiguousarray(host(src, "f32")).reshape(L, H, D), gq, cos, sin)
-        check(got, want.reshape(1, L, H, D), "f32", what)
+        want = orc.qk_l2norm_rope3d(np.ascontiguousarray(host(src, dt)).reshape(L, H, D), gq, cos, sin, dt=odt(orc, dt))
+        check(got, want.reshape(1, L, H, D), dt, what)
 
 
-@pytest.mark.parametrize("D", [32, 48])
-def test_dinov3_rope_any_dim(dev, ops, orc, synth, D):
-    print(f"\n[case] dinov3 rope D={D}", flush=True)
+@pytest.mark.parametrize("dt,D", [("f32", 32), ("f32", 48), ("f16", 64), ("f16", 32)])
+def test_dinov3_rope_any_dim(dev, ops, orc, synth, dt, D):
+    print(f"\n[case] dinov3 rope D={D} dt={dt}", flush=True)
     B, H, grid = 1, 3, 4
     S = 5 + grid * grid
     cos, sin = orc.dinov3_rope_tables(grid, grid, D)
-    x = to_dev(synth.normal(241, B * H * S * D).reshape(B, H, S, D), dev, "f32")
+    x = to_dev(synth.normal(241, B * H * S * D).reshape(B, H, S, D), dev, dt)
     T = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
     qo, _ = ops.apply_rotary_to_patches(x, x, T(cos), T(sin), 5)
     torch.cuda.synchronize()
-    check(qo, orc.dinov3_rope_apply(np.ascontiguousarray(host(x, "f32")), 5, cos, sin), "f32", "q")
+    check(qo, orc.dinov3_rope_apply(np.ascontiguousarray(host(x, dt)), 5, cos, sin, dt=odt(orc, dt)), dt, "q")
 
 
 # ---------------------------------------------------------------------------
