@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "candle-3d_amd"))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, TFLOP/s
 METRIC = "fused-op achieved HBM GB/s (% of MI355X peak) + µs/op at VGGT/DiT shapes"
 
 
@@ -265,7 +266,7 @@ def main():
         if args.only and tag not in args.only and wl.name not in args.only:
             del wl
             continue
-        cfg, dtype, shape, sets, note = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note
+        cfg, dtype, shape, sets, note, flops = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note, wl.flops
         us = step_ops.get(tag)
         if us is None:
             n = 200 if wl.bytes < 64 << 20 else 50
@@ -280,7 +281,9 @@ def main():
                       "frac_peak": round(gbs / PEAK_GBS, 4), "runtime_copy_us": round(cus, 3),
                       "speed_vs_runtime_copy": round(cus / us, 4), "target_70pct": bool(target),
                       "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
-                      "rotation_sets": sets, **({"note": note} if note else {})})
+                      "rotation_sets": sets, **({"note": note} if note else {}),
+                      **({"bound": "mfma", "tflops": round(flops / us / 1e6, 1),
+                          "frac_mfma_peak": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4)} if flops else {})})
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -47,7 +47,7 @@ int elem_bytes(int dt) {
     case LUX3D_F32: case LUX3D_I32: return 4;
     case LUX3D_BF16: case LUX3D_F16: return 2;
     case LUX3D_I64: return 8;
-    case LUX3D_U8: return 1;
+    case LUX3D_U8: case LUX3D_I8: return 1;
   }
   return 0;
 }
@@ -771,6 +771,73 @@ int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y, lu
   return hip_status(launch_dequant_q8_0(reinterpret_cast<const uint8_t *>(blocks->data), nblocks, y->dtype, y->data,
                                         vec, stream_of(stream)),
                     fn);
+}
+
+int lux3d_q8_0_repack(const lux3d_tensor_t *blocks, int64_t n, int64_t k, const lux3d_tensor_t *qs,
+                      const lux3d_tensor_t *scales, lux3d_stream_t stream) {
+  const char *fn = "lux3d_q8_0_repack";
+  int r;
+  if ((r = check_desc(blocks, fn, "blocks")) || (r = check_desc(qs, fn, "qs")) ||
+      (r = check_desc(scales, fn, "scales")))
+    return r;
+  if (n < 0 || k < 0 || k % 32) return fail(LUX3D_ERR_SHAPE, "%s: weight [%lld, %lld] needs k %% 32 == 0", fn,
+                                           (long long)n, (long long)k);
+  if (blocks->dtype != LUX3D_U8) return fail(LUX3D_ERR_DTYPE, "%s: blocks must be u8", fn);
+  if (qs->dtype != LUX3D_I8) return fail(LUX3D_ERR_DTYPE, "%s: qs must be int8", fn);
+  if (scales->dtype != LUX3D_F32) return fail(LUX3D_ERR_DTYPE, "%s: scales must be f32", fn);
+  if (!is_contiguous(blocks) || !is_contiguous(qs) || !is_contiguous(scales))
+    return fail(LUX3D_ERR_LAYOUT, "%s: tensors must be contiguous", fn);
+  const int64_t nblocks = n * (k / 32);
+  if (numel(blocks) != nblocks * 34)
+    return fail(LUX3D_ERR_SHAPE, "%s: %lld bytes of blocks for a [%lld, %lld] weight (expected %lld)", fn,
+                (long long)numel(blocks), (long long)n, (long long)k, (long long)(nblocks * 34));
+  if (numel(qs) != n * k || numel(scales) != nblocks)
+    return fail(LUX3D_ERR_SHAPE, "%s: qs must hold n*k values and scales n*k/32", fn);
+  if (reinterpret_cast<uintptr_t>(blocks->data) & 1u)
+    return fail(LUX3D_ERR_LAYOUT, "%s: blocks must be 2-byte aligned", fn);
+  if (!aligned16(qs->data) || !aligned16(scales->data))
+    return fail(LUX3D_ERR_LAYOUT, "%s: qs and scales must be 16-byte aligned", fn);
+  return hip_status(launch_q8_0_repack(reinterpret_cast<const uint8_t *>(blocks->data), nblocks,
+                                       reinterpret_cast<int8_t *>(qs->data), reinterpret_cast<float *>(scales->data),
+                                       stream_of(stream)),
+                    fn);
+}
+
+int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const lux3d_tensor_t *scales,
+                      const lux3d_tensor_t *bias, const lux3d_tensor_t *y, lux3d_stream_t stream) {
+  const char *fn = "lux3d_q8_0_linear";
+  int r;
+  RowView xv, yv;
+  if ((r = row_tensor(x, fn, "x", LUX3D_BF16, xv))) return r;
+  if ((r = row_tensor(y, fn, "y", -1, yv))) return r;
+  if ((r = check_desc(qs, fn, "qs")) || (r = check_desc(scales, fn, "scales"))) return r;
+  if (qs->dtype != LUX3D_I8 || qs->rank != 2 || !is_contiguous(qs))
+    return fail(LUX3D_ERR_SHAPE, "%s: qs must be a contiguous int8 [n, k] (from lux3d_q8_0_repack)", fn);
+  const int64_t n = qs->shape[0], k = qs->shape[1];
+  if (k != xv.d) return fail(LUX3D_ERR_SHAPE, "%s: x has %lld features, the weight %lld", fn, (long long)xv.d,
+                             (long long)k);
+  if (k % 32 || k == 0) return fail(LUX3D_ERR_SHAPE, "%s: k must be a positive multiple of 32", fn);
+  if (scales->dtype != LUX3D_F32 || !is_contiguous(scales) || numel(scales) != n * (k / 32))
+    return fail(LUX3D_ERR_SHAPE, "%s: scales must be a contiguous f32 [n, k/32]", fn);
+  if (yv.d != n || yv.rows != xv.rows)
+    return fail(LUX3D_ERR_SHAPE, "%s: y must be [%lld, %lld]", fn, (long long)xv.rows, (long long)n);
+  const float *bp = nullptr;
+  if (bias) {
+    if ((r = check_desc(bias, fn, "bias"))) return r;
+    if (bias->dtype != LUX3D_F32 || !is_contiguous(bias) || numel(bias) != n)
+      return fail(LUX3D_ERR_SHAPE, "%s: bias must be a contiguous f32 [n]", fn);
+    bp = reinterpret_cast<const float *>(bias->data);
+  }
+  if (!aligned16(x->data) || (xv.rows > 1 && (xv.rs * 2) % 16) || !aligned16(qs->data))
+    return fail(LUX3D_ERR_LAYOUT, "%s: x rows and qs must be 16-byte aligned", fn);
+  Q8GemmParams p;
+  p.x = xv.p; p.ldx = xv.rs;
+  p.qs = reinterpret_cast<const int8_t *>(qs->data);
+  p.scales = reinterpret_cast<const float *>(scales->data);
+  p.bias = bp;
+  p.y = const_cast<void *>(yv.p); p.ldy = yv.rs;
+  p.M = xv.rows; p.N = n; p.K = k;
+  return hip_status(launch_q8_0_gemm(y->dtype, p, stream_of(stream)), fn);
 }
 
 }  // extern "C"

@@ -97,4 +97,17 @@ hipError_t launch_timestep(const float *t, int64_t n, const float *freqs, int64_
 hipError_t launch_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *y,
                                bool vec, hipStream_t s);
 
+// ---- Q8_0 quantized linear ---------------------------------------------------
+// y[m, n] = sum_k x[m, k] * bf16(q[n, k] * scale[n, k / 32]) (+ bias[n]).
+struct Q8GemmParams {
+  const void *x = nullptr; int64_t ldx = 0;   // bf16 [M, K] rows, 16-byte aligned
+  const int8_t *qs = nullptr;                 // [N, K] contiguous, 16-byte aligned
+  const float *scales = nullptr;              // [N, K / 32] contiguous
+  const float *bias = nullptr;                // [N] or null
+  void *y = nullptr; int64_t ldy = 0;         // [M, N] rows
+  int64_t M = 0, N = 0, K = 0;
+};
+hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs, float *scales, hipStream_t s);
+hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s);
+
 }  // namespace lux3d

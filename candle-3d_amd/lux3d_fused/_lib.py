@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 
 MAX_RANK = 5
 
-F32, BF16, F16, I32, I64, U8 = 0, 1, 2, 3, 4, 5
+F32, BF16, F16, I32, I64, U8, I8 = 0, 1, 2, 3, 4, 5, 6
 
 OK = 0
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_LAYOUT, ERR_HIP, ERR_VALUE = -1, -2, -3, -4, -5, -6
@@ -61,6 +61,8 @@ SIGNATURES = {
     "lux3d_silu": [TP, TP, S],
     "lux3d_timestep_embedding": [TP, TP, ctypes.c_int64, ctypes.c_int32, TP, S],
     "lux3d_dequant_q8_0": [TP, TP, S],
+    "lux3d_q8_0_repack": [TP, ctypes.c_int64, ctypes.c_int64, TP, TP, S],
+    "lux3d_q8_0_linear": [TP, TP, TP, TP, TP, S],
 }
 
 

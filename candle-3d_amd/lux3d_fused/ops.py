@@ -20,7 +20,7 @@ import torch
 from . import _lib
 
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16,
-       torch.int32: _lib.I32, torch.int64: _lib.I64, torch.uint8: _lib.U8}
+       torch.int32: _lib.I32, torch.int64: _lib.I64, torch.uint8: _lib.U8, torch.int8: _lib.I8}
 
 
 def desc(t: Optional[torch.Tensor]):
@@ -334,3 +334,43 @@ def dequantize_q8_0(blocks: torch.Tensor, shape, dtype=torch.bfloat16) -> torch.
     y = torch.empty(tuple(shape), dtype=dtype, device=blocks.device)
     _lib.call("lux3d_dequant_q8_0", desc(blocks.reshape(-1)), desc(y), _stream(y))
     return y
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 quantized linear
+# ---------------------------------------------------------------------------
+
+def q8_0_repack(blocks: torch.Tensor, n: int, k: int):
+    """The load-time step of a Q8_0 quantized linear (QMatMul::from_qtensor,
+    runtime/nn_blocks.rs:145-150): GGML blocks of the weight [n, k] ->
+    (qs int8 [n, k], scales f32 [n, k/32]), exact."""
+    qs = torch.empty((n, k), dtype=torch.int8, device=blocks.device)
+    scales = torch.empty((n, k // 32), dtype=torch.float32, device=blocks.device)
+    _lib.call("lux3d_q8_0_repack", desc(blocks.reshape(-1)), int(n), int(k), desc(qs), desc(scales),
+              _stream(blocks))
+    return qs, scales
+
+
+def q8_0_linear(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                out_dtype=torch.bfloat16) -> torch.Tensor:
+    """`Linear::forward` for a Q8_0 weight (runtime/nn_blocks.rs:83-93):
+    y = x @ dequant(W)^T (+ bias), x bf16 [..., k] -> y [..., n]."""
+    n = qs.shape[0]
+    y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=out_dtype, device=x.device)
+    _lib.call("lux3d_q8_0_linear", desc(x), desc(qs), desc(scales), desc(bias), desc(y), _stream(x))
+    return y
+
+
+class QMatMul:
+    """QMatMul over a Q8_0 weight [n, k] (the reference keeps the packed
+    QTensor; here the blocks are repacked once to int8 + f32 scales)."""
+
+    def __init__(self, qs: torch.Tensor, scales: torch.Tensor):
+        self.qs, self.scales = qs, scales
+
+    @classmethod
+    def from_q8_0(cls, blocks: torch.Tensor, n: int, k: int) -> "QMatMul":
+        return cls(*q8_0_repack(blocks, n, k))
+
+    def forward(self, xs: torch.Tensor, bias: Optional[torch.Tensor] = None, out_dtype=torch.bfloat16):
+        return q8_0_linear(xs, self.qs, self.scales, bias, out_dtype)

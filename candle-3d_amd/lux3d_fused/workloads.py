@@ -34,6 +34,7 @@ class Workload:
     launch: Callable[[int], object] = field(repr=False)
     sets: int = 1
     ideal_note: str = ""
+    flops: int = 0       # matrix-core work per launch (GEMMs); 0 for streaming ops
 
 
 def _cur() -> int:
@@ -373,6 +374,44 @@ def cfg4_dinov3_rope(dev) -> Workload:
 
 
 # The configs[1..4] ops BASELINE.md names (the >=70%-of-peak targets), then extras.
+def _q8_linear(dev, cfg, m, k, n, what) -> Workload:
+    """Q8_0 quantized linear y = x @ dequant(W)^T + bias at a model's shape.
+    The weight is repacked once (load time, outside the timed launch); x
+    rotates over sets that exceed the Infinity Cache, the weight stays one
+    tensor, as a layer's weight does across the tokens of a step."""
+    from . import _lib
+    s = synth.config_seed(cfg) + 500
+    x0 = _normal(s, (m, k), dev, torch.bfloat16)
+    blocks = _t(synth.q8_0_blocks(s + 1, n * k // 32), dev)
+    qs, scales = ops.q8_0_repack(blocks, n, k)
+    bias = _normal(s + 2, (n,), dev, torch.float32, 0.0, 0.5)
+    nbytes = m * k * 2 + n * k + n * (k // 32) * 4 + n * 4 + m * n * 2
+    n_sets = _n_sets(m * k * 2 + m * n * 2)
+    xs = [_fill_like(x0, j) for j in range(n_sets)]
+    ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+    dx = [ops.desc(v) for v in xs]
+    dy = [ops.desc(v) for v in ys]
+    dq, dsc, db = ops.desc(qs), ops.desc(scales), ops.desc(bias)
+
+    def launch(i):
+        j = i % n_sets
+        _lib.call("lux3d_q8_0_linear", dx[j], dq, dsc, db, dy[j], _cur())
+    wl = Workload("q8_0_linear", cfg, "q8_0_gemm_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
+                  f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
+    wl._keep = (xs, ys, qs, scales, bias, blocks, dx, dy, dq, dsc, db)
+    return wl
+
+
+def cfg4_q8_0_linear(dev) -> Workload:
+    # the configs[4] weight W [4096, 1024] applied to the 1029 DINOv3 tokens
+    return _q8_linear(dev, 4, 1029, 1024, 4096, "configs[4] weight, 1029 tokens")
+
+
+def cfg2_q8_0_linear(dev) -> Workload:
+    # TripoSG width 2048 -> 4x feed-forward, both CFG halves (2 x 2048 tokens)
+    return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection")
+
+
 TARGETS: List[Callable] = [
     cfg1_residual_layer_norm,
     cfg1_qk_layernorm_rope2d,
@@ -393,4 +432,6 @@ EXTRAS: List[Callable] = [
     cfg2_silu,
     cfg3_gated_residual_ragged,
     cfg4_dinov3_rope,
+    cfg4_q8_0_linear,
+    cfg2_q8_0_linear,
 ]

@@ -42,7 +42,8 @@ typedef enum {
   LUX3D_F16 = 2,
   LUX3D_I32 = 3,
   LUX3D_I64 = 4,
-  LUX3D_U8 = 5
+  LUX3D_U8 = 5,
+  LUX3D_I8 = 6
 } lux3d_dtype;
 
 typedef enum {
@@ -270,6 +271,37 @@ int lux3d_timestep_embedding(const lux3d_tensor_t *t, const lux3d_tensor_t *freq
  * weights/quantize.rs:319-338 (rank 2, row length % 32 == 0).              */
 int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y,
                        lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Q8_0 quantized linear (the "next" row of the path: the consumer of the
+ * dequant above).
+ *
+ * lux3d_q8_0_repack: one-time, at weight load. A Q8_0 weight [n, k] stored
+ * as GGML blocks (u8 [n*k/32*34], row-major over (n, k/32); k % 32 == 0) is
+ * rewritten as qs int8 (LUX3D_I8) [n, k] and scales f32 [n, k/32], both
+ * contiguous and 16-byte aligned, so the GEMM streams it with 16-byte loads.
+ * Exact (the values and scales are copied / widened, not rounded).
+ * The reference's load-time step for a quantized linear is
+ * QMatMul::from_qtensor (runtime/nn_blocks.rs:145-150).
+ *
+ * lux3d_q8_0_linear: y = x * W^T (+ bias) for the LinearInner::Quant branch
+ * of Linear::forward (runtime/nn_blocks.rs:83-93, QMatMul::forward then
+ * broadcast_add(bias)).
+ *   x: bf16 [..., k] rows with a unit inner stride, 16-byte aligned rows;
+ *   qs, scales: from lux3d_q8_0_repack for the weight [n, k];
+ *   bias: f32 [n] or NULL;
+ *   y: [..., n] rows, bf16 / f16 / f32.
+ * Each weight is dequantized exactly as lux3d_dequant_q8_0 does to bf16
+ * (RNE of the exact product), products accumulate in f32 (MFMA), the bias
+ * is added in f32 and y is rounded once. This is the dequantize-then-matmul
+ * path of candle's GPU backends with a bf16 dequant target; candle's CPU
+ * path instead quantizes x to Q8_0 blocks and takes integer dot products.   */
+int lux3d_q8_0_repack(const lux3d_tensor_t *blocks, int64_t n, int64_t k,
+                      const lux3d_tensor_t *qs, const lux3d_tensor_t *scales,
+                      lux3d_stream_t stream);
+int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
+                      const lux3d_tensor_t *scales, const lux3d_tensor_t *bias,
+                      const lux3d_tensor_t *y, lux3d_stream_t stream);
 
 #ifdef __cplusplus
 }

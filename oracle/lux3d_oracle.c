@@ -26,6 +26,8 @@
  *   or_gelu_*, or_silu       torch F.gelu / F.silu (f64)
  *   or_timestep_embedding_*  KAT tests/trellis2_blocks.rs:157-171 + f64 form
  *   or_dequant_q8_0          brute force over all int8 x f16 scale sweep
+ *   or_q8_0_linear           numpy f64 matmul of the dequantized weight; identity
+ *                            weight; tiny brute force (tests/test_oracle_pins.py)
  */
 #include "lux3d_oracle.h"
 
@@ -814,4 +816,55 @@ static void q8_rows(const void *p, int64_t r0, int64_t r1) {
 void or_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *out) {
   q8_ctx c = {blocks, out_dt, out};
   parallel_rows(nblocks, q8_rows, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Quantized linear: LinearInner::Quant forward (nn_blocks.rs:83-93) as     */
+/* QMatMul::forward with the weight dequantized to bf16, then the bias add. */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  const float *x, *w, *bias;
+  int64_t K, N;
+  int dt;
+  void *y;
+  float *abs_sum;
+} ql_ctx;
+
+static void ql_rows(const void *p, int64_t r0, int64_t r1) {
+  const ql_ctx *c = (const ql_ctx *)p;
+  for (int64_t m = r0; m < r1; ++m) {
+    const float *xr = c->x + m * c->K;
+    for (int64_t n = 0; n < c->N; ++n) {
+      const float *wr = c->w + n * c->K;
+      double acc = 0.0, aacc = 0.0;
+      for (int64_t k = 0; k < c->K; ++k) {
+        const double pr = (double)xr[k] * (double)wr[k];
+        acc += pr;
+        aacc += fabs(pr);
+      }
+      if (c->bias) acc += (double)c->bias[n];
+      const int64_t o = m * c->N + n;
+      if (c->dt == OR_BF16) ((uint16_t *)c->y)[o] = f64_to_bf16(acc);
+      else st(c->dt, c->y, o, (float)acc);
+      if (c->abs_sum) c->abs_sum[o] = (float)aacc;
+    }
+  }
+}
+
+void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
+                    const float *bias, int out_dt, void *y, float *abs_sum) {
+  float *xf = (float *)malloc(sizeof(float) * (size_t)(M * K));
+  float *wf = (float *)malloc(sizeof(float) * (size_t)(N * K));
+  uint16_t *wb = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(N * K));
+  if (!xf || !wf || !wb) {
+    free(xf); free(wf); free(wb);
+    return;
+  }
+  for (int64_t i = 0; i < M * K; ++i) xf[i] = or_bf16_to_f32(x[i]);
+  or_dequant_q8_0(blocks, N * (K / 32), OR_BF16, wb);
+  for (int64_t i = 0; i < N * K; ++i) wf[i] = or_bf16_to_f32(wb[i]);
+  ql_ctx c = {xf, wf, bias, K, N, out_dt, y, abs_sum};
+  parallel_rows(M, ql_rows, &c);
+  free(xf); free(wf); free(wb);
 }

@@ -126,6 +126,15 @@ void or_timestep_embedding_cos_first(const float *t, int64_t n, int64_t dim, flo
 /* GGML block_q8_0 = {f16 d; int8 qs[32]} (34 bytes); w = f32(d)*qs. */
 void or_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *out);
 
+/* ---- Q8_0 quantized linear (dequantize-then-matmul semantics) ------------- */
+/* y[m][n] = sum_k x[m][k] * w[n][k] (+ bias[n]) in double, rounded once to
+ * out_dt, with w = bf16(f32(q) * d) (the Q8_0 -> bf16 dequant above) and x
+ * bf16 bits [M, K]; blocks hold the weight [N, K] row-major over (n, k/32).
+ * abs_sum (optional, f32 [M, N]) receives sum_k |x * w|, the scale of the
+ * f32 accumulation error. */
+void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
+                    const float *bias, int out_dt, void *y, float *abs_sum);
+
 #ifdef __cplusplus
 }
 #endif

@@ -193,3 +193,32 @@ def test_python_mirror_raises_lux3d_error():
     with pytest.raises(Lux3dError) as e:
         _lib.call("lux3d_layer_norm", None, None, None, 1e-5, None, None)
     assert e.value.code == _lib.ERR_NULL
+
+
+def test_q8_0_linear_argument_errors():
+    n, k = 64, 96
+    blocks = T([n * k // 32 * 34], _lib.U8)
+    qs, scales = T([n, k], _lib.I8), T([n, k // 32], _lib.F32)
+    # repack: k must be a multiple of 32, the byte count must match, qs int8
+    rc, msg = status("lux3d_q8_0_repack", blocks, n, 100, qs, scales, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_q8_0_repack", T([n * k // 32 * 34 - 34], _lib.U8), n, k, qs, scales, None)
+    assert rc == _lib.ERR_SHAPE and "bytes of blocks" in msg
+    rc, msg = status("lux3d_q8_0_repack", blocks, n, k, T([n, k], _lib.U8), scales, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_q8_0_repack", blocks, n, k, T([n, k], _lib.I8, data=FAKE + 8), scales, None)
+    assert rc == _lib.ERR_LAYOUT
+    # linear: x bf16 with k features, rows 16-byte aligned; y [rows, n]
+    x, y = T([10, k]), T([10, n])
+    rc, msg = status("lux3d_q8_0_linear", T([10, k], _lib.F32), qs, scales, None, y, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_q8_0_linear", T([10, k + 32]), qs, scales, None, y, None)
+    assert rc == _lib.ERR_SHAPE and "features" in msg
+    rc, msg = status("lux3d_q8_0_linear", x, qs, scales, None, T([10, n + 1]), None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_q8_0_linear", x, qs, T([n, k // 32 + 1], _lib.F32), None, y, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_q8_0_linear", x, qs, scales, T([n + 1], _lib.F32), y, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_q8_0_linear", T([10, k], data=FAKE + 2), qs, scales, None, y, None)
+    assert rc == _lib.ERR_LAYOUT

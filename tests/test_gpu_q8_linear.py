@@ -1,0 +1,130 @@
+"""GPU parity of the Q8_0 quantized linear (lux3d_q8_0_repack +
+lux3d_q8_0_linear) against the oracle's dequantize-then-matmul
+(or_q8_0_linear, pinned in tests/test_oracle_pins.py).
+
+Tolerance: the GPU accumulates the K products in f32 on the matrix cores and
+the oracle in f64, so an output may differ by the f32 accumulation error
+(held to 2^-16 of sum_k |x*w|, the scale of that error) plus one unit of
+the output dtype's last place.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops(dev):
+    from lux3d_fused import ops as _ops
+    return _ops
+
+
+@pytest.fixture(scope="module")
+def orc():
+    import lux3d_oracle as o
+    o.set_threads(16)
+    return o
+
+
+@pytest.fixture(scope="module")
+def synth():
+    from lux3d_fused import synth as s
+    return s
+
+
+def to_f64(a, dt):
+    if dt == "bf16":
+        return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    if dt == "f16":
+        return np.asarray(a, dtype=np.uint16).view(np.float16).astype(np.float64)
+    return np.asarray(a, dtype=np.float32).astype(np.float64)
+
+
+def host(t, dt):
+    t = t.detach().contiguous().cpu()
+    return t.numpy() if dt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_gemm_close(got, want, abs_sum, dt, what):
+    g, w = to_f64(got, dt), to_f64(want, dt)
+    ulp = {"bf16": 2.0 ** -7, "f16": 2.0 ** -10, "f32": 2.0 ** -23}[dt]
+    bound = ulp * np.abs(w) + 2.0 ** -16 * abs_sum.astype(np.float64) + 1e-30
+    err = np.abs(g - w)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outputs out of tolerance; worst err "
+                           f"{err.max():.3e} (bound there {bound.reshape(-1)[np.argmax(err)]:.3e})")
+
+
+def make_problem(synth, orc, dev, m, k, n, seed, bias=True):
+    x = synth.normal(seed, m * k).reshape(m, k)
+    xd = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    blocks = synth.q8_0_blocks(seed + 1, n * k // 32)
+    b = synth.normal(seed + 2, n, 0.0, 0.5) if bias else None
+    return xd, blocks, b
+
+
+@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136)])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_q8_0_linear_matches_oracle(dev, ops, orc, synth, m, k, n, out):
+    print(f"\n[case] q8_0_linear m={m} k={k} n={n} out={out}", flush=True)
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 300 + m)
+    bd = torch.from_numpy(blocks).to(dev)
+    mm = ops.QMatMul.from_q8_0(bd, n, k)
+    y = mm.forward(xd, torch.from_numpy(b).to(dev), TDT[out])
+    torch.cuda.synchronize()
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, b, orc.F32 if out == "f32" else orc.BF16,
+                                    with_abs=True)
+    assert_gemm_close(host(y, out), want, abs_sum, out, f"q8_0_linear {m}x{k}x{n}")
+
+
+def test_q8_0_repack_is_exact(dev, ops, synth):
+    n, k = 96, 160
+    blocks = synth.q8_0_blocks(321, n * k // 32)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    torch.cuda.synchronize()
+    b = blocks.reshape(n * k // 32, 34)
+    assert np.array_equal(qs.cpu().numpy().reshape(-1), b[:, 2:].view(np.int8).reshape(-1))
+    assert np.array_equal(scales.cpu().numpy().reshape(-1),
+                          b[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1))
+
+
+def test_q8_0_linear_no_bias_f16_out_and_strided_rows(dev, ops, orc, synth):
+    """No bias, f16 output, x and y as row-strided views of wider buffers."""
+    m, k, n = 200, 512, 384
+    xd, blocks, _ = make_problem(synth, orc, dev, m, k, n, 700, bias=False)
+    xwide = torch.zeros((m, k + 64), dtype=torch.bfloat16, device=dev)
+    xwide[:, :k] = xd
+    ywide = torch.zeros((m, n + 32), dtype=torch.float16, device=dev)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    from lux3d_fused import _lib
+    _lib.call("lux3d_q8_0_linear", ops.desc(xwide[:, :k]), ops.desc(qs), ops.desc(scales), None,
+              ops.desc(ywide[:, :n]), None)
+    torch.cuda.synchronize()
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, None, orc.F16, with_abs=True)
+    assert_gemm_close(host(ywide[:, :n], "f16"), want, abs_sum, "f16", "f16 out, strided rows")
+    assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
+
+
+def test_q8_0_linear_large_sampled_rows(dev, ops, orc, synth):
+    """A TripoSG-sized projection (x [4096, 2048] -> [4096, 8192]); the oracle
+    checks a sample of 96 rows."""
+    m, k, n = 4096, 2048, 8192
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 900)
+    mm = ops.QMatMul.from_q8_0(torch.from_numpy(blocks).to(dev), n, k)
+    y = mm.forward(xd, torch.from_numpy(b).to(dev))
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(5).choice(m, 96, replace=False))
+    xs = host(xd, "bf16")[rows]
+    want, abs_sum = orc.q8_0_linear(xs, blocks, n, b, orc.BF16, with_abs=True)
+    assert_gemm_close(host(y, "bf16")[rows], want, abs_sum, "bf16", "sampled rows")

@@ -477,3 +477,56 @@ def test_threads_do_not_change_results():
     b = orc.layer_norm(x, w, None, 1e-5)
     orc.set_threads(4)
     assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 quantized linear (dequantize-then-matmul)
+# ---------------------------------------------------------------------------
+
+def _dequant_bf16_numpy(blocks, n, k):
+    """The bf16 weight the linear uses, decoded with numpy alone: f16 scale,
+    int8 values, exact product, RNE to bf16 (torch)."""
+    b = np.asarray(blocks, dtype=np.uint8).reshape(n * (k // 32), 34)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)          # [blocks, 1]
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    w = (q * d).reshape(n, k)
+    return torch.from_numpy(w).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def test_q8_0_linear_matches_numpy_f64_matmul():
+    m, k, n = 37, 256, 45
+    x = orc.bf16_bits(synth.normal(90, m * k).reshape(m, k))
+    blocks = synth.q8_0_blocks(91, n * k // 32)
+    bias = synth.normal(92, n, 0.0, 0.5)
+    y = orc.q8_0_linear(x, blocks, n, bias, orc.F32)
+    want = orc.bf16_to_f32(x).astype(np.float64) @ _dequant_bf16_numpy(blocks, n, k).T + bias.astype(np.float64)
+    # f64 sums in a different order, then one rounding to f32
+    assert np.all(np.abs(y - want) <= 2.0 ** -23 * np.abs(want) + 1e-30)
+    yb = orc.q8_0_linear(x, blocks, n, bias, orc.BF16)
+    assert np.array_equal(yb, to_bf16_bits(want))
+
+
+def test_q8_0_linear_identity_weight_and_brute_force():
+    # identity weight (d = 1.0, q = 1 on the diagonal) returns x exactly
+    k = 64
+    blocks = np.zeros((k, k // 32, 34), dtype=np.uint8)
+    blocks[:, :, 0], blocks[:, :, 1] = 0x00, 0x3C                    # f16 1.0, little-endian
+    for i in range(k):
+        blocks[i, i // 32, 2 + i % 32] = 1
+    x = orc.bf16_bits(synth.normal(93, 5 * k).reshape(5, k))
+    assert np.array_equal(orc.q8_0_linear(x, blocks.reshape(-1), k, None, orc.BF16), x)
+    # pure-Python brute force on a tiny case, decoding the bytes by hand
+    m, k, n = 2, 32, 3
+    x = orc.bf16_bits(synth.normal(94, m * k).reshape(m, k))
+    raw = synth.q8_0_blocks(95, n).reshape(n, 34)
+    xf = orc.bf16_to_f32(x)
+    got = orc.q8_0_linear(x, raw.reshape(-1), n, None, orc.F32)
+    for i in range(m):
+        for j in range(n):
+            d = float(np.frombuffer(bytes(raw[j, 0:2]), dtype="<f2")[0])
+            acc = 0.0
+            for t in range(k):
+                qv = int(raw[j, 2 + t]) - 256 * (raw[j, 2 + t] > 127)
+                w = float(torch.tensor(qv * d, dtype=torch.float32).to(torch.bfloat16).item())
+                acc += float(xf[i, t]) * w
+            assert abs(got[i, j] - acc) <= 2.0 ** -23 * abs(acc) + 1e-30, (i, j)
