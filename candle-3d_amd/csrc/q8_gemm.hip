@@ -13,11 +13,11 @@
 // are only 2-byte aligned, into int8 [N, K] row-major plus f32 scales
 // [N, K/32], so the GEMM streams them with 16-byte loads.
 //
-// GEMM tiling: a 256-thread workgroup computes a 128 x 128 tile of y; its
-// four wavefronts each own 64 x 64 (2 x 2 MFMA tiles of 32 x 32, 64 f32
-// accumulators per lane). Per k-step of 32 (one Q8_0 block) the workgroup
-// stages x[128 x 32] and the dequantised W[128 x 32] as bf16 in LDS
-// (double-buffered, rows padded to 80 bytes against bank conflicts); the
+// GEMM tiling: a 256-thread workgroup computes a BM x BN tile of y; its four
+// wavefronts each own (BM/2) x (BN/2) as 32 x 32 MFMA tiles with f32
+// accumulators. Per k-step of BK (two Q8_0 blocks where k allows) the
+// workgroup stages x[BM x BK] and the dequantised W[BN x BK] as bf16 in LDS
+// (double-buffered, rows padded by 16 bytes against bank conflicts); the
 // next k-step's global loads are issued before the current step's MFMAs, so
 // one barrier per k-step suffices.
 #include "common.hpp"
@@ -30,8 +30,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kLdsRow = kBK + 8;          // bf16 elements per LDS row (80 bytes)
+constexpr int kBK = 32;                   // the k granularity (one Q8_0 block)
 constexpr int kGemmThreads = 256;
 
 // ---- repack: GGML blocks -> int8 [N, K] + f32 scales [N, K/32] -------------
@@ -53,69 +52,91 @@ __global__ __launch_bounds__(256) void q8_0_repack_kernel(const uint8_t *blocks,
 
 // ---- GEMM -------------------------------------------------------------------
 
-template <typename OUT>
-__global__ __launch_bounds__(kGemmThreads) void q8_0_gemm_kernel(Q8GemmParams p) {
-  __shared__ __align__(16) __bf16 As[2][kBM * kLdsRow];
-  __shared__ __align__(16) __bf16 Bs[2][kBN * kLdsRow];
+// Block tile BM x BN, k-step BK (one or two Q8_0 blocks); the four
+// wavefronts form a 2 x 2 grid, each owning (BM/2) x (BN/2) = TM x TN MFMA
+// tiles of 32 x 32. MINW is the minimum number of wavefronts per SIMD the
+// register allocation must allow.
+template <typename OUT, int BM, int BN, int BK, int MINW>
+__global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmParams p) {
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int LDS_ROW = BK + 8;                    // bf16 per LDS row (odd multiple of 16 bytes)
+  constexpr int A_CPR = BK / 8;                      // 16-byte chunks per x row per k-step
+  constexpr int A_CHUNKS = BM * A_CPR / kGemmThreads;
+  constexpr int B_CPR = BK / 16;                     // 16-int8 chunks per weight row per k-step
+  constexpr int B_CHUNKS = BN * B_CPR / kGemmThreads;
+  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
+  static_assert(BK % 32 == 0, "k-steps are whole Q8_0 blocks");
+  __shared__ __align__(16) __bf16 As[2][BM * LDS_ROW];
+  __shared__ __align__(16) __bf16 Bs[2][BN * LDS_ROW];
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * kBM, n0 = (int64_t)blockIdx.x * kBN;
-  const int64_t nk = p.K / kBK;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int64_t nblk = p.K / 32;  // Q8_0 blocks per weight row
+  const int64_t nk = p.K / BK;
 
-  // global -> register staging assignments
-  // A: 128 rows x 64 bytes = 512 chunks of 16 B; thread t takes chunks t, t + 256
-  int64_t a_row[2];
-  int a_part[2];
+  // global -> register staging: x row chunks and weight row chunks. Rows past
+  // M (N) are clamped to M - 1 (N - 1): loaded, computed, never stored.
+  int64_t a_off[A_CHUNKS];
+  int a_lds[A_CHUNKS];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = t + i * kGemmThreads;
-    const int64_t r = m0 + (c >> 2);
-    a_row[i] = r < p.M ? r : p.M - 1;  // clamped rows are loaded and never stored
-    a_part[i] = c & 3;
+  for (int i = 0; i < A_CHUNKS; ++i) {
+    const int c = t + i * kGemmThreads, r = c / A_CPR, part = c % A_CPR;
+    const int64_t gr = m0 + r < p.M ? m0 + r : p.M - 1;
+    a_off[i] = (gr * p.ldx + part * 8) * 2;
+    a_lds[i] = r * LDS_ROW + part * 8;
   }
-  // B: 128 rows x 32 int8 = 256 chunks of 16 B; thread t takes chunk t
-  const int b_r = t >> 1, b_part = t & 1;
-  const int64_t b_row = n0 + b_r < p.N ? n0 + b_r : p.N - 1;
+  int64_t b_row[B_CHUNKS];
+  int b_part[B_CHUNKS], b_lds[B_CHUNKS];
+#pragma unroll
+  for (int i = 0; i < B_CHUNKS; ++i) {
+    const int c = t + i * kGemmThreads, r = c / B_CPR;
+    b_part[i] = c % B_CPR;
+    b_row[i] = n0 + r < p.N ? n0 + r : p.N - 1;
+    b_lds[i] = r * LDS_ROW + b_part[i] * 16;
+  }
 
   const char *xbase = reinterpret_cast<const char *>(p.x);
-  uint4 ra[2], rb;
-  float rd;
+  uint4 ra[A_CHUNKS], rb[B_CHUNKS];
+  float rd[B_CHUNKS];
   auto load_step = [&](int64_t kt) {
-    const int64_t k0 = kt * kBK;
+    const int64_t k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ra[i] = ld16(xbase + (a_row[i] * p.ldx + k0 + a_part[i] * 8) * 2);
-    rb = ld16(p.qs + b_row * p.K + k0 + b_part * 16);
-    rd = p.scales[b_row * nk + kt];
+    for (int i = 0; i < A_CHUNKS; ++i) ra[i] = ld16(xbase + a_off[i] + k0 * 2);
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      rb[i] = ld16(p.qs + b_row[i] * p.K + k0 + b_part[i] * 16);
+      rd[i] = p.scales[b_row[i] * nblk + k0 / 32 + b_part[i] / 2];
+    }
   };
   auto store_step = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = t + i * kGemmThreads;
-      *reinterpret_cast<uint4 *>(&As[buf][(c >> 2) * kLdsRow + a_part[i] * 8]) = ra[i];
-    }
-    // dequant: 16 int8 -> bf16(f32(q) * d), RNE (q * d is exact in f32)
-    const uint32_t w4[4] = {rb.x, rb.y, rb.z, rb.w};
-    uint32_t pk[8];
+    for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4 *>(&As[buf][a_lds[i]]) = ra[i];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t v = w4[j];
-      const float f0 = (float)(int8_t)(v & 0xFFu) * rd, f1 = (float)(int8_t)((v >> 8) & 0xFFu) * rd;
-      const float f2 = (float)(int8_t)((v >> 16) & 0xFFu) * rd, f3 = (float)(int8_t)(v >> 24) * rd;
-      pk[2 * j] = pack_bf16x2(f0, f1);
-      pk[2 * j + 1] = pack_bf16x2(f2, f3);
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      // dequant: 16 int8 -> bf16(f32(q) * d), RNE (q * d is exact in f32)
+      const uint32_t w4[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+      uint32_t pk[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = w4[j];
+        const float f0 = (float)(int8_t)(v & 0xFFu) * rd[i], f1 = (float)(int8_t)((v >> 8) & 0xFFu) * rd[i];
+        const float f2 = (float)(int8_t)((v >> 16) & 0xFFu) * rd[i], f3 = (float)(int8_t)(v >> 24) * rd[i];
+        pk[2 * j] = pack_bf16x2(f0, f1);
+        pk[2 * j + 1] = pack_bf16x2(f2, f3);
+      }
+      uint4 *dst = reinterpret_cast<uint4 *>(&Bs[buf][b_lds[i]]);
+      dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(&Bs[buf][b_r * kLdsRow + b_part * 16]);
-    dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
   };
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
 
   load_step(0);
   store_step(0);
@@ -126,18 +147,18 @@ __global__ __launch_bounds__(kGemmThreads) void q8_0_gemm_kernel(Q8GemmParams p)
     const int buf = (int)(kt & 1);
     if (kt + 1 < nk) load_step(kt + 1);
 #pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      bf16x8_t a[2], b[2];
+    for (int s = 0; s < BK / 16; ++s) {
+      bf16x8_t a[TM], b[TN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(wm * 64 + i * 32 + lrow) * kLdsRow + s * 16 + lk]);
+      for (int i = 0; i < TM; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(wm * (BM / 2) + i * 32 + lrow) * LDS_ROW + s * 16 + lk]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t *>(&Bs[buf][(wn * 64 + j * 32 + lrow) * kLdsRow + s * 16 + lk]);
+      for (int j = 0; j < TN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8_t *>(&Bs[buf][(wn * (BN / 2) + j * 32 + lrow) * LDS_ROW + s * 16 + lk]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) store_step(buf ^ 1);
     lds_barrier();
@@ -146,15 +167,15 @@ __global__ __launch_bounds__(kGemmThreads) void q8_0_gemm_kernel(Q8GemmParams p)
   // epilogue: lane holds C[8*(e/4) + 4*(lane/32) + e%4][lane%32] of each tile
   char *ybase = reinterpret_cast<char *>(p.y);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
     if (col >= p.N) continue;
     const float bias = p.bias ? p.bias[col] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         if (row >= p.M) continue;
         const float v = acc[i][j][e] + bias;
         if constexpr (OUT::code == LUX3D_F32) {
@@ -164,6 +185,28 @@ __global__ __launch_bounds__(kGemmThreads) void q8_0_gemm_kernel(Q8GemmParams p)
         }
       }
   }
+}
+
+// Tile choice (measured on MI355X, TFLOP/s at 1029x1024x4096 /
+// 4096x2048x8192): 256x128 with k-step 64 is fastest once there are >= 512
+// workgroups (529 at the larger shape; 128 x 128: 510); below that
+// 128x128 with k-step 64 (312 at the configs[4] shape; 64 x 128: 247).
+template <typename OUT>
+hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
+  auto groups = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+  const dim3 block(kGemmThreads);
+#define LUX3D_GEMM_TILE(BM_, BN_, BK_, W_)                                                              \
+  {                                                                                                     \
+    const dim3 grid((unsigned)((p.N + BN_ - 1) / BN_), (unsigned)((p.M + BM_ - 1) / BM_));              \
+    hipLaunchKernelGGL((q8_0_gemm_kernel<OUT, BM_, BN_, BK_, W_>), grid, block, 0, s, p);              \
+    return hipGetLastError();                                                                           \
+  }
+  if (p.K % 64 == 0) {
+    if (groups(256, 128) >= 512) LUX3D_GEMM_TILE(256, 128, 64, 1)
+    LUX3D_GEMM_TILE(128, 128, 64, 1)
+  }
+  LUX3D_GEMM_TILE(128, 128, 32, 1)
+#undef LUX3D_GEMM_TILE
 }
 
 }  // namespace
@@ -179,16 +222,13 @@ hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs
 hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
   if (p.K <= 0 || p.K % kBK) return hipErrorInvalidValue;
-  const int64_t gx = (p.N + kBN - 1) / kBN, gy = (p.M + kBM - 1) / kBM;
-  if (gx > INT32_MAX || gy > 65535) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)gx, (unsigned)gy), block(kGemmThreads);
+  if ((p.N + 127) / 128 > INT32_MAX || (p.M + 127) / 128 > 65535) return hipErrorInvalidValue;
   switch (out_dt) {
-    case LUX3D_BF16: hipLaunchKernelGGL(q8_0_gemm_kernel<BF16>, grid, block, 0, s, p); break;
-    case LUX3D_F16: hipLaunchKernelGGL(q8_0_gemm_kernel<F16>, grid, block, 0, s, p); break;
-    case LUX3D_F32: hipLaunchKernelGGL(q8_0_gemm_kernel<F32>, grid, block, 0, s, p); break;
-    default: return hipErrorInvalidValue;
+    case LUX3D_BF16: return launch_tiles<BF16>(p, s);
+    case LUX3D_F16: return launch_tiles<F16>(p, s);
+    case LUX3D_F32: return launch_tiles<F32>(p, s);
   }
-  return hipGetLastError();
+  return hipErrorInvalidValue;
 }
 
 }  // namespace lux3d

@@ -74,7 +74,7 @@ def make_problem(synth, orc, dev, m, k, n, seed, bias=True):
     return xd, blocks, b
 
 
-@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136)])
+@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136), (77, 96, 100)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_q8_0_linear_matches_oracle(dev, ops, orc, synth, m, k, n, out):
     print(f"\n[case] q8_0_linear m={m} k={k} n={n} out={out}", flush=True)
