@@ -131,7 +131,7 @@ size_t dtype_size(DType dt) {
     case DType::F32: case DType::I32: return 4;
     case DType::BF16: case DType::F16: return 2;
     case DType::I64: return 8;
-    case DType::U8: return 1;
+    case DType::U8: case DType::I8: return 1;
   }
   return 0;
 }
@@ -380,6 +380,7 @@ std::vector<float> Tensor::to_vec_f32() const {
       case DType::I32: { int32_t q; std::memcpy(&q, &b[i * 4], 4); v[i] = (float)q; break; }
       case DType::I64: { int64_t q; std::memcpy(&q, &b[i * 8], 8); v[i] = (float)q; break; }
       case DType::U8: v[i] = (float)b[i]; break;
+      case DType::I8: v[i] = (float)(int8_t)b[i]; break;
     }
   }
   return v;
@@ -658,6 +659,26 @@ Tensor silu(const Tensor &x) { return unary<lux3d_silu>(x); }
 Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out) {
   Tensor y = Tensor::empty(shape, out, blocks.device());
   abi_check(lux3d_dequant_q8_0(Desc(blocks).p(), Desc(y).p(), blocks.device().stream()));
+  return y;
+}
+
+QMatMul QMatMul::from_q8_0(const Tensor &blocks, int64_t n, int64_t k) {
+  if (n < 0 || k <= 0 || k % 32)
+    fail(LUX3D_ERR_SHAPE, "Q8_0 weight [" + std::to_string(n) + ", " + std::to_string(k) + "] needs k % 32 == 0");
+  QMatMul m;
+  m.qs_ = Tensor::empty({n, k}, DType::I8, blocks.device());
+  m.scales_ = Tensor::empty({n, k / 32}, DType::F32, blocks.device());
+  abi_check(lux3d_q8_0_repack(Desc(blocks).p(), n, k, Desc(m.qs_).p(), Desc(m.scales_).p(), blocks.device().stream()));
+  return m;
+}
+
+Tensor QMatMul::forward(const Tensor &xs, const std::optional<Tensor> &bias, DType out) const {
+  Shape shape = xs.dims();
+  if (shape.empty()) fail(LUX3D_ERR_SHAPE, "QMatMul::forward: scalar input");
+  shape.back() = out_dim();
+  Tensor y = Tensor::empty(shape, out, xs.device());
+  abi_check(lux3d_q8_0_linear(Desc(xs).p(), Desc(qs_).p(), Desc(scales_).p(), Desc(bias).p(), Desc(y).p(),
+                              xs.device().stream()));
   return y;
 }
 

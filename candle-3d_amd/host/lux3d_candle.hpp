@@ -39,6 +39,7 @@ enum class DType : int32_t {
   I32 = LUX3D_I32,
   I64 = LUX3D_I64,
   U8 = LUX3D_U8,
+  I8 = LUX3D_I8,
 };
 size_t dtype_size(DType dt);
 
@@ -270,5 +271,19 @@ Tensor silu(const Tensor &x);      // Tensor::silu
 // QTensor::dequantize for GGML Q8_0 (runtime/nn_blocks.rs:140): `blocks`
 // holds elem_count(shape)/32 records of 34 bytes; out dtype F32, BF16 or F16.
 Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out);
+
+// QMatMul over a Q8_0 weight [n, k] (QMatMul::from_qtensor and forward,
+// runtime/nn_blocks.rs:83-93, 145-150). from_q8_0 repacks the GGML blocks
+// once; forward(xs [..., k] bf16) = xs @ dequant(W)^T in f32 accumulation.
+class QMatMul {
+ public:
+  static QMatMul from_q8_0(const Tensor &blocks, int64_t n, int64_t k);
+  Tensor forward(const Tensor &xs, const std::optional<Tensor> &bias = std::nullopt, DType out = DType::BF16) const;
+  int64_t out_dim() const { return qs_.dim(0); }
+  int64_t in_dim() const { return qs_.dim(1); }
+
+ private:
+  Tensor qs_, scales_;
+};
 
 }  // namespace lux3d::candle

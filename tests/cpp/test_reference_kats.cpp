@@ -271,6 +271,34 @@ void dequantize_q8_0_exact(const Device &dev) {
   for (int i = 0; i < 32; ++i) CHECK(v[i] == 0.5f * (float)(i - 16));
 }
 
+// Quantized linear: W = d * q with d = 0.5 (f16 0x3800) and q[n][k] = (n + k) % 7 - 3;
+// y = x @ W^T + bias, checked against a double-precision host sum (every
+// product here is exact in bf16 x bf16 and the sums are small integers / 2).
+void q8_0_linear_closed_form(const Device &dev) {
+  const int64_t m = 3, k = 64, n = 5;
+  std::vector<uint8_t> blocks;
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t b = 0; b < k / 32; ++b) {
+      blocks.push_back(0x00);
+      blocks.push_back(0x38);
+      for (int j = 0; j < 32; ++j) blocks.push_back((uint8_t)(int8_t)((r + b * 32 + j) % 7 - 3));
+    }
+  const QMatMul mm = QMatMul::from_q8_0(Tensor::from_u8(blocks, {(int64_t)blocks.size()}, dev), n, k);
+  std::vector<float> x(m * k), bias(n);
+  for (int64_t i = 0; i < m * k; ++i) x[i] = (float)((i * 5) % 9 - 4);
+  for (int64_t j = 0; j < n; ++j) bias[j] = 0.25f * (float)j;
+  const Tensor y = mm.forward(Tensor::from_f32(x, {m, k}, DType::BF16, dev),
+                              Tensor::from_f32(bias, {n}, DType::F32, dev), DType::F32);
+  CHECK((y.dims() == Shape{m, n}));
+  const std::vector<float> v = y.to_vec_f32();
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      double acc = bias[j];
+      for (int64_t t = 0; t < k; ++t) acc += (double)x[i * k + t] * 0.5 * (double)((j + t) % 7 - 3);
+      CHECK(v[i * n + j] == (float)acc);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Error behaviour (the reference's bail! messages)
 // ---------------------------------------------------------------------------
@@ -281,6 +309,7 @@ void errors_on_host(const Device &dev) {
   CHECK(throws_with([&] { Trellis2Rope3d(4).cos_sin({1, 2, 3}, dev); }, "is too small for 3-axis RoPE"));
   CHECK(throws_with([&] { Trellis2Rope3d(13).cos_sin({1, 2, 3}, dev); }, "must be divisible by 2"));
   CHECK(throws_with([&] { dinov3_rope_cos_sin(10, 100.0f, 2, 2, dev); }, "is not divisible by 4"));
+  CHECK(throws_with([&] { QMatMul::from_q8_0(Tensor(), 4, 48); }, "needs k % 32 == 0"));
 }
 
 void errors_on_device(const Device &dev) {
@@ -322,6 +351,7 @@ int main(int argc, char **argv) {
       {"residual_layer_norm_closed_form", residual_layer_norm_closed_form, true},
       {"vggt_qk_layernorm_rope_specials_are_plain_layernorm", vggt_qk_layernorm_rope_specials_are_plain_layernorm, true},
       {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
+      {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
       {"errors_on_device", errors_on_device, true},
   };
   Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed
