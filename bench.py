@@ -269,7 +269,7 @@ def main():
         cfg, dtype, shape, sets, note, flops = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note, wl.flops
         us = step_ops.get(tag)
         if us is None:
-            n = 200 if wl.bytes < 64 << 20 else 50
+            n = wl.reps or (200 if wl.bytes < 64 << 20 else 50)
             us = time_graph(torch, wl.launch, n)
         gbs = wl.bytes / us / 1e3
         nbytes = wl.bytes

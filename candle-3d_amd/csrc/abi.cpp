@@ -840,4 +840,51 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
   return hip_status(launch_q8_0_gemm(y->dtype, p, stream_of(stream)), fn);
 }
 
+int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+               const lux3d_tensor_t *out, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa";
+  int r;
+  const lux3d_tensor_t *ts[4] = {q, k, v, out};
+  const char *names[4] = {"q", "k", "v", "out"};
+  for (int i = 0; i < 4; ++i) {
+    if ((r = check_desc(ts[i], fn, names[i]))) return r;
+    if (ts[i]->rank != 4)
+      return fail(LUX3D_ERR_SHAPE, "%s: `%s` must be [B, H, L, D] (rank %d given)", fn, names[i], ts[i]->rank);
+    if (ts[i]->dtype != q->dtype) return fail(LUX3D_ERR_DTYPE, "%s: q, k, v and out must share one dtype", fn);
+    if (ts[i]->shape[3] > 1 && ts[i]->stride[3] != 1)
+      return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must have a unit innermost stride", fn, names[i]);
+  }
+  if (!is_float(q->dtype)) return fail(LUX3D_ERR_DTYPE, "%s: dtype must be f32, bf16 or f16", fn);
+  const int64_t B = q->shape[0], H = q->shape[1], Lq = q->shape[2], D = q->shape[3], Lk = k->shape[2];
+  if (k->shape[0] != B || k->shape[1] != H || k->shape[3] != D)
+    return fail(LUX3D_ERR_SHAPE, "%s: k must be [%lld, %lld, Lk, %lld]", fn, (long long)B, (long long)H, (long long)D);
+  for (int i = 0; i < 4; ++i)
+    if (ts[i]->shape[3] != D) return fail(LUX3D_ERR_SHAPE, "%s: head dims differ", fn);
+  if (v->shape[0] != B || v->shape[1] != H || v->shape[2] != Lk)
+    return fail(LUX3D_ERR_SHAPE, "%s: v must have the shape of k", fn);
+  if (out->shape[0] != B || out->shape[1] != H || out->shape[2] != Lq)
+    return fail(LUX3D_ERR_SHAPE, "%s: out must have the shape of q", fn);
+  if (B * H * Lq > 0 && Lk == 0) return fail(LUX3D_ERR_SHAPE, "%s: k and v have no tokens", fn);
+  if (D > 512 || D < 1) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld outside 1..512", fn, (long long)D);
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(LUX3D_ERR_VALUE, "%s: scale must be finite and > 0", fn);
+  AttnParams p;
+  p.q = q->data; p.k = k->data; p.v = v->data; p.o = out->data;
+  p.B = B; p.H = H; p.Lq = Lq; p.Lk = Lk; p.D = D;
+  p.q_sb = q->stride[0]; p.q_sh = q->stride[1]; p.q_st = q->stride[2];
+  p.k_sb = k->stride[0]; p.k_sh = k->stride[1]; p.k_st = k->stride[2];
+  p.v_sb = v->stride[0]; p.v_sh = v->stride[1]; p.v_st = v->stride[2];
+  p.o_sb = out->stride[0]; p.o_sh = out->stride[1]; p.o_st = out->stride[2];
+  p.scale = scale;
+  // matrix cores: 2-byte types, D 64 / 128, every row start 16-byte aligned
+  bool mfma = q->dtype != LUX3D_F32 && (D == 64 || D == 128);
+  for (int i = 0; i < 4 && mfma; ++i) {
+    const lux3d_tensor_t *t = ts[i];
+    mfma = aligned16(t->data);
+    for (int a = 0; a < 3 && mfma; ++a)
+      if (t->shape[a] > 1 && t->stride[a] % 8) mfma = false;
+  }
+  p.mfma = mfma;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
 }  // extern "C"

@@ -1,0 +1,420 @@
+// attention.hip -- scaled dot-product attention for gfx950:
+// out = softmax(q k^T * scale) v over [B, H, L, D] views, one launch, no
+// scores buffer in HBM.
+//
+// Semantics: scores are exact f32 sums of the input products (matrix cores
+// accumulate bf16 x bf16 / f16 x f16 products in f32), the softmax runs in
+// f32 with a running maximum (exp2 of the log2e-scaled scores), the
+// probabilities are rounded to the input type for the P v product, which
+// again accumulates in f32, and the output is divided by the f32 row sum and
+// rounded once. That is the arithmetic of exact_sdpa_heads (f32 throughout)
+// up to the rounding of the probabilities; exact_query_chunked_sdpa on bf16
+// additionally rounds q * scale, the scores and the probabilities to bf16,
+// which this kernel does not.
+//
+// Matrix-core kernel (attn_mfma_kernel). A workgroup of 4 wavefronts owns
+// BQ = 128 * QT queries of one (batch, head); each wavefront keeps QT tiles
+// of 32 queries. Per block of BKV keys:
+//   S^T = K Q^T    A operand: K rows from LDS, B operand: Q held in registers.
+//                  The 32 x 32 result leaves every lane with ONE query
+//                  (lane % 32) and 16 keys, so the row max needs a single
+//                  exchange with lane ^ 32 and no other cross-lane traffic.
+//   O^T += V^T P^T A operand: V^T from LDS (V is transposed while staged),
+//                  B operand: the probabilities exactly where the S^T
+//                  accumulator left them (the key order inside a 16-key
+//                  k-step is permuted identically on both operands, which a
+//                  sum over keys does not see). O^T again gives each lane its
+//                  own query, so the rescale by exp2(m_old - m_new) and the
+//                  final 1/l are per-lane multiplies.
+// K and V^T blocks are double-buffered in LDS; the next block's global loads
+// are issued before the current block's math, one LDS barrier per block.
+// Workgroups are numbered so that the query blocks of one head run on one
+// XCD (hardware places workgroup i on XCD i % 8) and share its L2 copy of K
+// and V.
+//
+// Generic kernel (attn_generic_kernel): one wavefront per query row, f32
+// arithmetic throughout (lanes over keys for the scores, over head dims for
+// the output); any float dtype, any alignment, D <= 512.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lux3d {
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T> struct Mma;
+template <> struct Mma<BF16> {
+  typedef bf16x8_t op_t;
+  __device__ __forceinline__ static f32x16_t run(op_t a, op_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+};
+template <> struct Mma<F16> {
+  typedef f16x8_t op_t;
+  __device__ __forceinline__ static f32x16_t run(op_t a, op_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+};
+
+// The value the partner lane (lane ^ 32) holds, paired with this lane's own:
+// v_permlane32_swap exchanges the two 32-lane halves.
+__device__ __forceinline__ float half_swap_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Logical workgroup id for physical id `pid` of `n`: XCD x (pid % 8) gets the
+// contiguous logical range [start_x, start_x + count_x).
+__device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
+  const int64_t per = n / 8, rem = n % 8, xcd = pid % 8, idx = pid / 8;
+  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
+}
+
+template <typename T, int D, int QT, int BKV>
+__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+  using M = Mma<T>;
+  using op_t = typename M::op_t;
+  constexpr int BQ = 4 * 32 * QT;
+  constexpr int KROW = D + 8;              // 2-byte elements per K row in LDS (16-byte pad)
+  constexpr int VROW = BKV + 4;            // per V^T row (8-byte pad)
+  constexpr int KCH = BKV * D / 8 / 256;   // 16-byte K chunks per thread per block
+  constexpr int VGR = BKV * D / 16 / 256;  // 4 keys x 4 dims V groups per thread per block
+  constexpr int NKT = BKV / 32;            // 32-key tiles per block
+  constexpr int NDT = D / 32;              // 32-dim output tiles
+  static_assert(KCH >= 1 && VGR >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
+  __shared__ __align__(16) uint16_t Ks[2][BKV * KROW];
+  __shared__ __align__(16) uint16_t Vt[2][D * VROW];
+
+  const int64_t lid = xcd_logical_id(blockIdx.x, nwg);
+  const int64_t bh = lid / nqb, qb = lid % nqb;
+  const int64_t bi = bh / p.H, hi = bh % p.H;
+  const char *qbase = reinterpret_cast<const char *>(p.q) + (bi * p.q_sb + hi * p.q_sh) * 2;
+  const char *kbase = reinterpret_cast<const char *>(p.k) + (bi * p.k_sb + hi * p.k_sh) * 2;
+  const char *vbase = reinterpret_cast<const char *>(p.v) + (bi * p.v_sb + hi * p.v_sh) * 2;
+  char *obase = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh) * 2;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int64_t Lq = p.Lq, Lk = p.Lk;
+
+  // Q as the B operand: lane holds Q[query l32][c * 16 + 8 * hh + e].
+  op_t qf[QT][D / 16];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
+    qr = qr < Lq ? qr : Lq - 1;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qf[qt][c] = *reinterpret_cast<const op_t *>(qbase + (qr * p.q_st + c * 16 + 8 * hh) * 2);
+  }
+
+  // Staging: K rows as 16-byte chunks; V as 4 keys x 4 dims, transposed in
+  // registers and written as 4 rows of V^T. Keys past Lk are clamped to
+  // Lk - 1 (finite data; their scores are masked).
+  int k_row[KCH], k_part[KCH], v_dg[VGR], v_kg[VGR];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = t + i * 256;
+    k_row[i] = c / (D / 8);
+    k_part[i] = c % (D / 8);
+  }
+#pragma unroll
+  for (int i = 0; i < VGR; ++i) {
+    const int g = t + i * 256;
+    v_dg[i] = g % (D / 4);
+    v_kg[i] = g / (D / 4);
+  }
+  uint4 rk[KCH];
+  uint2 rv[VGR][4];
+  auto load_kv = [&](int64_t j) {
+    const int64_t key0 = j * BKV;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      int64_t key = key0 + k_row[i];
+      key = key < Lk ? key : Lk - 1;
+      rk[i] = ld16<false>(kbase + (key * p.k_st + k_part[i] * 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < VGR; ++i)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        int64_t key = key0 + v_kg[i] * 4 + kk;
+        key = key < Lk ? key : Lk - 1;
+        rv[i][kk] = *reinterpret_cast<const uint2 *>(vbase + (key * p.v_st + v_dg[i] * 4) * 2);
+      }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) *reinterpret_cast<uint4 *>(&Ks[buf][k_row[i] * KROW + k_part[i] * 8]) = rk[i];
+#pragma unroll
+    for (int i = 0; i < VGR; ++i) {
+      // rv[kk] = {dims 0,1 | dims 2,3} of key kk -> row dd = {keys 0,1 | keys 2,3}
+      const uint2 a = rv[i][0], b = rv[i][1], c = rv[i][2], d = rv[i][3];
+      const uint2 r0 = make_uint2((a.x & 0xFFFFu) | (b.x << 16), (c.x & 0xFFFFu) | (d.x << 16));
+      const uint2 r1 = make_uint2((a.x >> 16) | (b.x & 0xFFFF0000u), (c.x >> 16) | (d.x & 0xFFFF0000u));
+      const uint2 r2 = make_uint2((a.y & 0xFFFFu) | (b.y << 16), (c.y & 0xFFFFu) | (d.y << 16));
+      const uint2 r3 = make_uint2((a.y >> 16) | (b.y & 0xFFFF0000u), (c.y >> 16) | (d.y & 0xFFFF0000u));
+      uint16_t *dst = &Vt[buf][(v_dg[i] * 4) * VROW + v_kg[i] * 4];
+      *reinterpret_cast<uint2 *>(dst) = r0;
+      *reinterpret_cast<uint2 *>(dst + VROW) = r1;
+      *reinterpret_cast<uint2 *>(dst + 2 * VROW) = r2;
+      *reinterpret_cast<uint2 *>(dst + 3 * VROW) = r3;
+    }
+  };
+
+  f32x16_t o[QT][NDT];
+  float m[QT], l[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = f32x16_t{};
+  }
+  const float c2 = p.scale * kLog2e;
+  const int64_t nkv = (Lk + BKV - 1) / BKV;
+
+  load_kv(0);
+  store_kv(0);
+  lds_barrier();
+
+  for (int64_t j = 0; j < nkv; ++j) {
+    const int buf = (int)(j & 1);
+    if (j + 1 < nkv) load_kv(j + 1);
+
+    // S^T = K Q^T: lane holds key 8 * (i / 4) + 4 * hh + i % 4 of each 32-key tile, query l32.
+    f32x16_t s[QT][NKT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) s[qt][kt] = f32x16_t{};
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const op_t a = *reinterpret_cast<const op_t *>(&Ks[buf][(kt * 32 + l32) * KROW + c * 16 + 8 * hh]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) s[qt][kt] = M::run(a, qf[qt][c], s[qt][kt]);
+      }
+    if ((j + 1) * BKV > Lk) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t key = j * BKV + kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (key >= Lk) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) s[qt][kt][i] = -INFINITY;
+          }
+        }
+    }
+
+    // online softmax; P packed as the B operand of O^T += V^T P^T
+    op_t pf[QT][NKT * 2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
+      mx = half_swap_max(mx);
+      const float mn = fmaxf(m[qt], mx * c2);
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+      m[qt] = mn;
+      float ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          u32x4_t pk;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][8 * jj + 2 * e], c2, -mn));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][8 * jj + 2 * e + 1], c2, -mn));
+            ls += p0 + p1;
+            pk[e] = M::pack(p0, p1);
+          }
+          pf[qt][kt * 2 + jj] = __builtin_bit_cast(op_t, pk);
+        }
+      l[qt] = l[qt] * alpha + ls;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+    }
+
+    // O^T += V^T P^T: A = V^T[dim l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of tile kt
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const uint16_t *vr = &Vt[buf][(dt * 32 + l32) * VROW + kt * 32 + 16 * jj + 4 * hh];
+          const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
+          const op_t a = __builtin_bit_cast(op_t, u32x4_t{lo.x, lo.y, hi2.x, hi2.y});
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) o[qt][dt] = M::run(a, pf[qt][kt * 2 + jj], o[qt][dt]);
+        }
+
+    if (j + 1 < nkv) store_kv(buf ^ 1);
+    lds_barrier();
+  }
+
+  // out[query][dim]: lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
+    const float inv = 1.f / half_swap_sum(l[qt]);
+    if (qr >= Lq) continue;
+    char *orow = obase + qr * p.o_st * 2;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint2 w = make_uint2(M::pack(o[qt][dt][4 * g] * inv, o[qt][dt][4 * g + 1] * inv),
+                                   M::pack(o[qt][dt][4 * g + 2] * inv, o[qt][dt][4 * g + 3] * inv));
+        *reinterpret_cast<uint2 *>(orow + (dt * 32 + 8 * g + 4 * hh) * 2) = w;
+      }
+  }
+}
+
+// ---- generic kernel ----------------------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// DPL = head dims per lane (D <= 64 * DPL).
+template <typename T, int DPL>
+__global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // whole wavefronts leave; no barrier below
+  const int64_t bh = r / p.Lq, qi = r % p.Lq;
+  const int64_t bi = bh / p.H, hi = bh % p.H;
+  constexpr int EB = T::bytes;
+  const char *qrow = reinterpret_cast<const char *>(p.q) + (bi * p.q_sb + hi * p.q_sh + qi * p.q_st) * EB;
+  const char *kbase = reinterpret_cast<const char *>(p.k) + (bi * p.k_sb + hi * p.k_sh) * EB;
+  const char *vbase = reinterpret_cast<const char *>(p.v) + (bi * p.v_sb + hi * p.v_sh) * EB;
+  char *orow = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh + qi * p.o_st) * EB;
+  const int64_t D = p.D, Lk = p.Lk;
+
+  float qv[DPL], o[DPL];
+#pragma unroll
+  for (int u = 0; u < DPL; ++u) {
+    const int64_t d = lane + 64 * u;
+    qv[u] = d < D ? load1<T>(qrow, d) : 0.f;
+    o[u] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int64_t j0 = 0; j0 < Lk; j0 += 64) {
+    const int64_t key = j0 + lane;
+    const bool valid = key < Lk;
+    const char *kr = kbase + (valid ? key : Lk - 1) * p.k_st * EB;
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < DPL; ++u)
+      for (int e = 0; e < 64; ++e) {
+        const int64_t d = 64 * u + e;
+        if (d >= D) break;
+        s += bcast(qv[u], e) * load1<T>(kr, d);
+      }
+    s = valid ? s * p.scale : -INFINITY;
+    const float mn = fmaxf(m, wave_max(s));
+    const float alpha = __expf(m - mn);
+    const float pj = valid ? __expf(s - mn) : 0.f;
+    l = l * alpha + wave_sum_xor(pj);
+    m = mn;
+#pragma unroll
+    for (int u = 0; u < DPL; ++u) o[u] *= alpha;
+    const int64_t nk = Lk - j0 < 64 ? Lk - j0 : 64;
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pk = bcast(pj, kk);
+      const char *vr = vbase + (j0 + kk) * p.v_st * EB;
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) {
+        const int64_t d = lane + 64 * u;
+        if (d < D) o[u] += pk * load1<T>(vr, d);
+      }
+    }
+  }
+  const float inv = 1.f / l;
+#pragma unroll
+  for (int u = 0; u < DPL; ++u) {
+    const int64_t d = lane + 64 * u;
+    if (d < D) store1<T>(orow, d, o[u] * inv);
+  }
+}
+
+template <typename T, int D, int QT, int BKV>
+hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
+  constexpr int BQ = 4 * 32 * QT;
+  const int64_t nqb = (p.Lq + BQ - 1) / BQ;
+  const int64_t nwg = p.B * p.H * nqb;
+  if (nwg > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_generic(const AttnParams &p, hipStream_t s) {
+  const int64_t rows = p.B * p.H * p.Lq;
+  const int64_t groups = (rows + 3) / 4;
+  if (groups > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)groups), block(256);
+  if (p.D <= 64) hipLaunchKernelGGL((attn_generic_kernel<T, 1>), grid, block, 0, s, p, rows);
+  else if (p.D <= 128) hipLaunchKernelGGL((attn_generic_kernel<T, 2>), grid, block, 0, s, p, rows);
+  else if (p.D <= 256) hipLaunchKernelGGL((attn_generic_kernel<T, 4>), grid, block, 0, s, p, rows);
+  else if (p.D <= 512) hipLaunchKernelGGL((attn_generic_kernel<T, 8>), grid, block, 0, s, p, rows);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const AttnParams &p, hipStream_t s) {
+  if constexpr (T::code != LUX3D_F32) {
+    if (p.mfma) {
+      if (p.D == 64) return launch_mfma<T, 64, 2, 64>(p, s);
+      if (p.D == 128) return launch_mfma<T, 128, 1, 64>(p, s);
+    }
+  }
+  return launch_generic<T>(p, s);
+}
+
+}  // namespace
+
+hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s) {
+  if (p.B <= 0 || p.H <= 0 || p.Lq <= 0) return hipSuccess;
+  if (p.Lk <= 0 || p.D <= 0) return hipErrorInvalidValue;
+  switch (dt) {
+    case LUX3D_BF16: return launch_t<BF16>(p, s);
+    case LUX3D_F16: return launch_t<F16>(p, s);
+    case LUX3D_F32: return launch_t<F32>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lux3d

@@ -110,4 +110,21 @@ struct Q8GemmParams {
 hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs, float *scales, hipStream_t s);
 hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s);
 
+// Scaled dot-product attention over [B, H, L, D] views (element strides per
+// batch, head and token; unit inner stride). out = softmax(q k^T * scale) v.
+// `mfma` selects the matrix-core kernel (bf16 / f16, D 64 or 128, every row
+// 16-byte aligned); otherwise the generic kernel (any float dtype, D <= 512).
+struct AttnParams {
+  const void *q = nullptr, *k = nullptr, *v = nullptr;
+  void *o = nullptr;
+  int64_t B = 0, H = 0, Lq = 0, Lk = 0, D = 0;
+  int64_t q_sb = 0, q_sh = 0, q_st = 0;
+  int64_t k_sb = 0, k_sh = 0, k_st = 0;
+  int64_t v_sb = 0, v_sh = 0, v_st = 0;
+  int64_t o_sb = 0, o_sh = 0, o_st = 0;
+  float scale = 0.f;
+  bool mfma = false;
+};
+hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
+
 }  // namespace lux3d

@@ -63,6 +63,7 @@ SIGNATURES = {
     "lux3d_dequant_q8_0": [TP, TP, S],
     "lux3d_q8_0_repack": [TP, ctypes.c_int64, ctypes.c_int64, TP, TP, S],
     "lux3d_q8_0_linear": [TP, TP, TP, TP, TP, S],
+    "lux3d_sdpa": [TP, TP, TP, ctypes.c_float, TP, S],
 }
 
 

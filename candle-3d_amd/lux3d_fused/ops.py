@@ -374,3 +374,26 @@ class QMatMul:
 
     def forward(self, xs: torch.Tensor, bias: Optional[torch.Tensor] = None, out_dtype=torch.bfloat16):
         return q8_0_linear(xs, self.qs, self.scales, bias, out_dtype)
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(q k^T * scale) v over [B, H, L, D] views, one kernel, no scores
+    buffer (attention_math.rs:199-259). `out` (default: a new contiguous
+    [B, H, Lq, D]) may be any view with a unit inner stride, e.g. the
+    [B, Lq, H, D] layout the caller transposes to next."""
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _lib.call("lux3d_sdpa", desc(q), desc(k), desc(v), float(scale), desc(out), _stream(q))
+    return out
+
+
+def exact_query_chunked_sdpa(q, k, v, scale: float, chunk_size: int = 0) -> torch.Tensor:
+    """attention_math.rs:199-241. chunk_size only bounded the reference's
+    scores buffer; this kernel keeps no such buffer, so it is ignored."""
+    return sdpa(q, k, v, scale)
+
+
+def exact_sdpa_heads(q, k, v, scale: float) -> torch.Tensor:
+    """attention_math.rs:244-259 (f32 arithmetic, output in q's dtype)."""
+    return sdpa(q, k, v, scale)

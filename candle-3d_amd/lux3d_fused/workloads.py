@@ -35,6 +35,7 @@ class Workload:
     sets: int = 1
     ideal_note: str = ""
     flops: int = 0       # matrix-core work per launch (GEMMs); 0 for streaming ops
+    reps: int = 0        # launches per timing graph (0: chosen from the byte count)
 
 
 def _cur() -> int:
@@ -412,6 +413,48 @@ def cfg2_q8_0_linear(dev) -> Workload:
     return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection")
 
 
+def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50) -> Workload:
+    """Attention over q, k, v taken as the permuted views of a fused
+    [B, N, 3, H, D] qkv buffer (vggt.rs:161-168), output [B, H, N, D]."""
+    from . import _lib
+    s = synth.config_seed(cfg) + 700
+    qkv0 = _normal(s, (b, n, 3, h, d), dev, torch.bfloat16)
+    n_sets = max(2, _n_sets(qkv0.numel() * 2 + b * h * n * d * 2))
+    qkvs = [_fill_like(qkv0, j) for j in range(n_sets)]
+    outs = [torch.empty((b, h, n, d), dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+    descs = []
+    for qkv, o in zip(qkvs, outs):
+        v = qkv.permute(2, 0, 3, 1, 4)
+        descs.append((ops.desc(v[0]), ops.desc(v[1]), ops.desc(v[2]), ops.desc(o)))
+    scale = 1.0 / float(d) ** 0.5
+
+    def launch(i):
+        dq, dk, dv, do = descs[i % n_sets]
+        _lib.call("lux3d_sdpa", dq, dk, dv, scale, do, _cur())
+    nbytes = 4 * b * h * n * d * 2
+    wl = Workload(name, cfg, f"attn_mfma_kernel<BF16,{d}>", "bf16 -> f32 acc", nbytes,
+                  f"q,k,v [{b},{h},{n},{d}] from qkv [{b},{n},3,{h},{d}] ({what})", launch, n_sets,
+                  flops=4 * b * h * n * n * d, reps=reps)
+    wl._keep = (qkvs, outs, descs)
+    return wl
+
+
+def cfg1_sdpa_frame(dev) -> Workload:
+    return _sdpa(dev, "sdpa_frame", 1, 8, 1374, 16, 64, "VGGT frame attention")
+
+
+def cfg1_sdpa_global(dev) -> Workload:
+    return _sdpa(dev, "sdpa_global", 1, 1, 8 * 1374, 16, 64, "VGGT global attention", reps=20)
+
+
+def cfg2_sdpa(dev) -> Workload:
+    return _sdpa(dev, "sdpa", 2, 2, 2048, 16, 128, "TripoSG DiT self-attention, CFG pair")
+
+
+def cfg3_sdpa(dev) -> Workload:
+    return _sdpa(dev, "sdpa", 3, 1, 40000, 12, 128, "TRELLIS.2 SLAT, the 40k-voxel batch element", reps=5)
+
+
 TARGETS: List[Callable] = [
     cfg1_residual_layer_norm,
     cfg1_qk_layernorm_rope2d,
@@ -434,4 +477,8 @@ EXTRAS: List[Callable] = [
     cfg4_dinov3_rope,
     cfg4_q8_0_linear,
     cfg2_q8_0_linear,
+    cfg1_sdpa_frame,
+    cfg1_sdpa_global,
+    cfg2_sdpa,
+    cfg3_sdpa,
 ]

@@ -303,6 +303,24 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
                       const lux3d_tensor_t *scales, const lux3d_tensor_t *bias,
                       const lux3d_tensor_t *y, lux3d_stream_t stream);
 
+/* ---- attention ------------------------------------------------------------
+ * lux3d_sdpa: out = softmax(q k^T * scale) v, replacing
+ * exact_query_chunked_sdpa (runtime/attention_math.rs:199-241; its
+ * chunk_size only bounds the scores buffer, which this kernel never
+ * materialises) and exact_sdpa_heads (attention_math.rs:244-259).
+ *   q: [B, H, Lq, D]; k, v: [B, H, Lk, D]; out: [B, H, Lq, D];
+ *   one dtype for all four (f32, bf16 or f16); any batch / head / token
+ *   strides (the permuted views of a fused qkv buffer pass as they are),
+ *   unit innermost stride; Lk >= 1; D <= 512; scale finite and > 0.
+ * bf16 / f16 with D = 64 or 128 and every row 16-byte aligned run on the
+ * matrix cores: f32 scores, f32 softmax, the probabilities rounded to the
+ * input type for P v (f32 accumulation), one rounding of the output. Other
+ * cases run a generic kernel in f32 throughout, the arithmetic of
+ * exact_sdpa_heads. out must not overlap q, k or v.                          */
+int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
+               const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
+               lux3d_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

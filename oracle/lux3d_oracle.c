@@ -28,6 +28,10 @@
  *   or_dequant_q8_0          brute force over all int8 x f16 scale sweep
  *   or_q8_0_linear           numpy f64 matmul of the dequantized weight; identity
  *                            weight; tiny brute force (tests/test_oracle_pins.py)
+ *   or_sdpa                  scipy softmax + numpy f64 matmuls; closed forms
+ *                            (identical keys -> mean of v, one key -> v, a
+ *                            dominant key -> its v row); key-permutation
+ *                            invariance (tests/test_oracle_pins.py)
  */
 #include "lux3d_oracle.h"
 
@@ -867,4 +871,66 @@ void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *bloc
   ql_ctx c = {xf, wf, bias, K, N, out_dt, y, abs_sum};
   parallel_rows(M, ql_rows, &c);
   free(xf); free(wf); free(wb);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Attention: exact_sdpa_heads (attention_math.rs:244-259) -- widen q, k, v  */
+/* to float, scores = q k^T * scale, softmax over the keys, attn v, one       */
+/* rounding to the output dtype. exact_query_chunked_sdpa                     */
+/* (attention_math.rs:199-241) computes the same function (its query chunks   */
+/* only bound the scores buffer). Sums here run in double.                    */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  int in_dt, out_dt;
+  const void *q, *k, *v;
+  int64_t Lq, Lk, D;
+  double scale;
+  void *out;
+  float *wabs;
+} sdpa_ctx;
+
+static void sdpa_rows(const void *p, int64_t r0, int64_t r1) {
+  const sdpa_ctx *c = (const sdpa_ctx *)p;
+  const int64_t Lk = c->Lk, D = c->D;
+  double *s = (double *)malloc(sizeof(double) * (size_t)(Lk + 2 * D));
+  if (!s) return;
+  double *acc = s + Lk, *aacc = acc + D;
+  for (int64_t r = r0; r < r1; ++r) {  /* r = bh * Lq + i */
+    const int64_t bh = r / c->Lq;
+    const int64_t qo = r * D, ko = bh * Lk * D;
+    double mx = -INFINITY;
+    for (int64_t j = 0; j < Lk; ++j) {
+      double dot = 0.0;
+      for (int64_t d = 0; d < D; ++d)
+        dot += (double)ld(c->in_dt, c->q, qo + d) * (double)ld(c->in_dt, c->k, ko + j * D + d);
+      s[j] = dot * c->scale;
+      if (s[j] > mx) mx = s[j];
+    }
+    double l = 0.0;
+    for (int64_t j = 0; j < Lk; ++j) {
+      s[j] = exp(s[j] - mx);
+      l += s[j];
+    }
+    for (int64_t d = 0; d < D; ++d) acc[d] = aacc[d] = 0.0;
+    for (int64_t j = 0; j < Lk; ++j)
+      for (int64_t d = 0; d < D; ++d) {
+        const double pv = s[j] * (double)ld(c->in_dt, c->v, ko + j * D + d);
+        acc[d] += pv;
+        aacc[d] += fabs(pv);
+      }
+    for (int64_t d = 0; d < D; ++d) {
+      const double o = acc[d] / l;
+      if (c->out_dt == OR_BF16) ((uint16_t *)c->out)[qo + d] = f64_to_bf16(o);
+      else st(c->out_dt, c->out, qo + d, (float)o);
+      if (c->wabs) c->wabs[qo + d] = (float)(aacc[d] / l);
+    }
+  }
+  free(s);
+}
+
+void or_sdpa(int in_dt, const void *q, const void *k, const void *v, int64_t BH, int64_t Lq, int64_t Lk,
+             int64_t D, double scale, int out_dt, void *out, float *wabs) {
+  sdpa_ctx c = {in_dt, out_dt, q, k, v, Lq, Lk, D, scale, out, wabs};
+  parallel_rows(BH * Lq, sdpa_rows, &c);
 }

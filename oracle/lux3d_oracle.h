@@ -135,6 +135,14 @@ void or_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *o
 void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
                     const float *bias, int out_dt, void *y, float *abs_sum);
 
+/* Scaled dot-product attention, exact_sdpa_heads (attention_math.rs:244-259):
+ * q [BH, Lq, D], k and v [BH, Lk, D] contiguous in in_dt; out [BH, Lq, D] in
+ * out_dt = softmax(q k^T * scale) v, summed in double and rounded once.
+ * wabs (optional, f32 [BH, Lq, D]) receives sum_j p_j |v_j| / sum_j p_j, the
+ * scale of the error of rounding the probabilities. */
+void or_sdpa(int in_dt, const void *q, const void *k, const void *v, int64_t BH, int64_t Lq, int64_t Lk,
+             int64_t D, double scale, int out_dt, void *out, float *wabs);
+
 #ifdef __cplusplus
 }
 #endif

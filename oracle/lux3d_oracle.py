@@ -51,6 +51,7 @@ _SIG = {
     "or_timestep_embedding_cos_first": ([_P, _I, _I, _P], None),
     "or_dequant_q8_0": ([_P, _I, ctypes.c_int, _P], None),
     "or_q8_0_linear": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
+    "or_sdpa": ([ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, ctypes.c_int, _P, _P], None),
 }
 
 
@@ -315,3 +316,21 @@ def q8_0_linear(x_bits, blocks, n, bias=None, out_dt=BF16, with_abs=False):
     a = np.empty((m, n), dtype=np.float32) if with_abs else None
     LIB.or_q8_0_linear(_ptr(x_bits), m, k, _ptr(blocks), n, _ptr(_f32(bias)), out_dt, _ptr(y), _ptr(a))
     return (y, a) if with_abs else y
+
+
+def sdpa(q, k, v, scale, dt=None, out_dt=None, with_abs=False):
+    """Attention over q [..., Lq, D], k and v [..., Lk, D] (same leading dims;
+    f32, f16, or bf16 bits as uint16 with dt=BF16). Returns softmax(q k^T *
+    scale) v as [..., Lq, D] in out_dt (default: the input dtype) and, with
+    with_abs, sum_j p_j |v_j| / sum_j p_j as f32."""
+    dt = dt_of(q, dt)
+    out_dt = dt if out_dt is None else out_dt
+    q, k, v = (np.ascontiguousarray(a) for a in (q, k, v))
+    *lead, lq, d = q.shape
+    lk = k.shape[-2]
+    assert k.shape == v.shape and k.shape[-1] == d and tuple(k.shape[:-2]) == tuple(lead)
+    bh = int(np.prod(lead)) if lead else 1
+    out = np.empty(q.shape, dtype=np.float32 if out_dt == F32 else (np.float16 if out_dt == F16 else np.uint16))
+    a = np.empty(q.shape, dtype=np.float32) if with_abs else None
+    LIB.or_sdpa(dt, _ptr(q), _ptr(k), _ptr(v), bh, lq, lk, d, float(scale), out_dt, _ptr(out), _ptr(a))
+    return (out, a) if with_abs else out

@@ -222,3 +222,31 @@ def test_q8_0_linear_argument_errors():
     assert rc == _lib.ERR_SHAPE
     rc, msg = status("lux3d_q8_0_linear", T([10, k], data=FAKE + 2), qs, scales, None, y, None)
     assert rc == _lib.ERR_LAYOUT
+
+
+def test_sdpa_argument_errors():
+    q, k, v, o = T([2, 4, 33, 64]), T([2, 4, 50, 64]), T([2, 4, 50, 64]), T([2, 4, 33, 64])
+    rc, msg = status("lux3d_sdpa", T([8, 33, 64]), k, v, 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE and "[B, H, L, D]" in msg
+    rc, msg = status("lux3d_sdpa", q, T([2, 4, 50, 64], _lib.F32), v, 0.125, o, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_sdpa", q, T([2, 3, 50, 64]), v, 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_sdpa", q, k, T([2, 4, 49, 64]), 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE and "shape of k" in msg
+    rc, msg = status("lux3d_sdpa", q, k, v, 0.125, T([2, 4, 32, 64]), None)
+    assert rc == _lib.ERR_SHAPE and "shape of q" in msg
+    rc, msg = status("lux3d_sdpa", q, T([2, 4, 0, 64]), T([2, 4, 0, 64]), 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE and "no tokens" in msg
+    rc, msg = status("lux3d_sdpa", q, k, v, 0.0, o, None)
+    assert rc == _lib.ERR_VALUE
+    rc, msg = status("lux3d_sdpa", q, k, v, float("nan"), o, None)
+    assert rc == _lib.ERR_VALUE
+    big = [1, 1, 4, 1024]
+    rc, msg = status("lux3d_sdpa", T(big), T(big), T(big), 0.1, T(big), None)
+    assert rc == _lib.ERR_SHAPE and "head dim" in msg
+    strided = T([2, 4, 33, 64], strides=[4 * 33 * 128, 33 * 128, 128, 2])
+    rc, msg = status("lux3d_sdpa", strided, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_LAYOUT
+    rc, msg = status("lux3d_sdpa", None, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_NULL

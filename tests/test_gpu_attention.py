@@ -1,0 +1,210 @@
+"""GPU parity of lux3d_sdpa (exact_query_chunked_sdpa / exact_sdpa_heads,
+attention_math.rs:199-259) against the oracle's double-precision attention
+(or_sdpa, pinned in tests/test_oracle_pins.py).
+
+Tolerances, per output element, with want = the oracle's value and
+wabs = sum_j p_j |v_j| / sum_j p_j (the oracle reports it):
+- matrix-core path (bf16 / f16, D 64 / 128): the probabilities are rounded
+  to the input type before the P v product, an error of at most one half
+  unit in their last place relative to each p_j, so
+  |err| <= ulp * |want| + ulp * wabs (+ 1e-6 * wabs for the f32 sums), with
+  ulp = 2^-7 (bf16) or 2^-10 (f16);
+- generic path: f32 throughout, |err| <= 1e-5 * wabs + ulp(out) * |want|.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+ULP = {"bf16": 2.0 ** -7, "f16": 2.0 ** -10, "f32": 2.0 ** -23}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops(dev):
+    from lux3d_fused import ops as _ops
+    return _ops
+
+
+@pytest.fixture(scope="module")
+def orc():
+    import lux3d_oracle as o
+    o.set_threads(16)
+    return o
+
+
+def host(t, dt):
+    """[..., L, D] device tensor -> contiguous numpy (bf16 as uint16 bits)."""
+    t = t.detach().contiguous().cpu()
+    if dt == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def to_f64(a, dt):
+    if dt == "bf16":
+        return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return np.asarray(a).astype(np.float64)
+
+
+def oracle(orc, q, k, v, scale, dt):
+    code = {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}[dt]
+    return orc.sdpa(host(q, dt), host(k, dt), host(v, dt), scale, dt=code, with_abs=True)
+
+
+def assert_attn_close(got, want, wabs, dt, mfma, what):
+    g, w = to_f64(host(got, dt), dt), to_f64(want, dt)
+    a = wabs.astype(np.float64)
+    if mfma:
+        bound = ULP[dt] * np.abs(w) + (ULP[dt] + 1e-6) * a
+    else:
+        bound = 1e-5 * a + ULP[dt] * np.abs(w)
+    err = np.abs(g - w)
+    bad = err > bound + 1e-30
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outputs out of tolerance; worst err "
+                           f"{err.max():.3e} (bound there {bound.reshape(-1)[np.argmax(err)]:.3e})")
+
+
+def qkv_views(dev, b, n, h, d, dt, seed, kscale=1.0, rising=False):
+    """q, k, v as the permuted views of a fused [B, N, 3, H, D] qkv buffer,
+    the way vggt.rs:161-168 takes them."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((b, n, 3, h, d), generator=g, dtype=torch.float32)
+    x[:, :, 1] *= kscale
+    if rising:  # later keys score higher: the running maximum keeps moving
+        x[:, :, 1] *= torch.linspace(0.5, 3.0, n).view(1, n, 1, 1)
+    qkv = x.to(dev).to(TDT[dt]).permute(2, 0, 3, 1, 4)
+    return qkv[0], qkv[1], qkv[2]
+
+
+def _print_case(**kw):
+    print("\n[case] sdpa " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+@pytest.mark.parametrize("b,n,h,d,dt,kscale,rising", [
+    (2, 1374, 4, 64, "bf16", 1.0, False),     # VGGT frame-attention tokens (37 x 37 + 5)
+    (1, 517, 3, 128, "bf16", 2.0, True),     # TRELLIS.2 head dim, peaky and moving maxima
+    (2, 300, 2, 64, "f16", 3.0, True),
+    (1, 129, 2, 128, "f16", 1.0, False),
+    (1, 65, 1, 64, "bf16", 1.0, False),
+    (1, 63, 1, 64, "bf16", 4.0, False),
+])
+def test_sdpa_self_attention_mfma(dev, ops, orc, b, n, h, d, dt, kscale, rising):
+    _print_case(b=b, n=n, h=h, d=d, dt=dt)
+    q, k, v = qkv_views(dev, b, n, h, d, dt, 10 + n + d, kscale, rising)
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, dt)
+    assert_attn_close(out, want, wabs, dt, True, f"self {b}x{h}x{n}x{d} {dt}")
+
+
+@pytest.mark.parametrize("lq,lk,d", [(300, 517, 128), (1, 1, 64), (5, 1, 64), (1, 200, 128), (257, 64, 64)])
+def test_sdpa_cross_attention_and_edges(dev, ops, orc, lq, lk, d):
+    _print_case(lq=lq, lk=lk, d=d)
+    g = torch.Generator(device="cpu").manual_seed(lq * 7 + lk)
+    q = torch.randn((2, 3, lq, d), generator=g).to(dev).to(torch.bfloat16)
+    k = (2 * torch.randn((2, 3, lk, d), generator=g)).to(dev).to(torch.bfloat16)
+    v = torch.randn((2, 3, lk, d), generator=g).to(dev).to(torch.bfloat16)
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, "bf16")
+    assert_attn_close(out, want, wabs, "bf16", True, f"cross {lq}x{lk}x{d}")
+
+
+def test_sdpa_output_view_in_token_major_layout(dev, ops, orc):
+    """out written straight into [B, L, H, D] (the layout the reference
+    transposes to next, vggt.rs:184) through a permuted view."""
+    b, n, h, d = 2, 200, 4, 64
+    q, k, v = qkv_views(dev, b, n, h, d, "bf16", 77)
+    buf = torch.full((b, n, h, d), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.sdpa(q, k, v, 0.125, out=buf.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, 0.125, "bf16")
+    assert_attn_close(buf.permute(0, 2, 1, 3), want, wabs, "bf16", True, "token-major out")
+
+
+def _pattern_f32(index):
+    return ((np.asarray(index) % 23).astype(np.float32) - np.float32(11.0)) * np.float32(0.1)
+
+
+@pytest.mark.parametrize("t,tkv,seeds", [(17, 17, (1, 2, 3)), (9, 7, (4, 5, 6))])
+def test_sdpa_reference_kat_f32(dev, ops, orc, t, tkv, seeds):
+    """The reference's sparse self / cross attention tests
+    (tests/trellis2_sparse.rs:521-623): H=2, head_dim 8, pattern_f32 inputs,
+    scale 1/sqrt(8), max |diff| < 1e-5 against naive attention; here against
+    the oracle, on the generic f32 kernel."""
+    h, hd = 2, 8
+    arrs = [_pattern_f32(np.arange(h * n * hd) * 7 + s * 3).reshape(1, h, n, hd)
+            for n, s in ((t, seeds[0]), (tkv, seeds[1]), (tkv, seeds[2]))]
+    q, k, v = (torch.from_numpy(a).to(dev) for a in arrs)
+    scale = float(np.float32(1.0 / np.sqrt(np.float32(hd))))
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, "f32")
+    got = out.cpu().numpy()
+    assert np.abs(got - want).max() < 1e-5
+    assert_attn_close(out, want, wabs, "f32", False, f"kat {t}x{tkv}")
+
+
+@pytest.mark.parametrize("case", ["f32_d64", "bf16_d80", "bf16_unaligned", "f16_d32", "bf16_d256"])
+def test_sdpa_generic_kernel(dev, ops, orc, case):
+    _print_case(case=case)
+    dt = case.split("_")[0]
+    d = {"f32_d64": 64, "bf16_d80": 80, "bf16_unaligned": 64, "f16_d32": 32, "bf16_d256": 256}[case]
+    g = torch.Generator(device="cpu").manual_seed(len(case) * 31 + d)
+    lq, lk = 77, 130
+    if case == "bf16_unaligned":
+        # rows start 2 bytes past a 16-byte boundary: the generic kernel takes it
+        qb = torch.randn((1, 2, lq, d + 1), generator=g).to(dev).to(TDT[dt])
+        q = qb[..., 1:]
+    else:
+        q = torch.randn((1, 2, lq, d), generator=g).to(dev).to(TDT[dt])
+    k = torch.randn((1, 2, lk, d), generator=g).to(dev).to(TDT[dt])
+    v = torch.randn((1, 2, lk, d), generator=g).to(dev).to(TDT[dt])
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, dt)
+    assert_attn_close(out, want, wabs, dt, False, case)
+
+
+def test_sdpa_vggt_global_attention_sampled(dev, ops, orc):
+    """VGGT global attention (8 frames x 1374 tokens = 10992 per head, 16
+    heads, D 64); the oracle checks 64 sampled queries of every head."""
+    b, n, h, d = 1, 8 * 1374, 16, 64
+    q, k, v = qkv_views(dev, b, n, h, d, "bf16", 5)
+    out = ops.sdpa(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(3).choice(n, 64, replace=False))
+    qs = np.ascontiguousarray(host(q, "bf16")[:, :, rows])
+    want, wabs = orc.sdpa(qs, host(k, "bf16"), host(v, "bf16"), 0.125, dt=orc.BF16, with_abs=True)
+    got = out[:, :, torch.from_numpy(rows).to(dev)]
+    assert_attn_close(got, want, wabs, "bf16", True, "global sampled")
+
+
+def test_sdpa_graph_replay_matches_eager(dev, ops):
+    q, k, v = qkv_views(dev, 2, 500, 4, 128, "bf16", 9)
+    eager = ops.sdpa(q, k, v, 0.088)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ops.sdpa(q, k, v, 0.088, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

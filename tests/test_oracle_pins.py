@@ -530,3 +530,66 @@ def test_q8_0_linear_identity_weight_and_brute_force():
                 w = float(torch.tensor(qv * d, dtype=torch.float32).to(torch.bfloat16).item())
                 acc += float(xf[i, t]) * w
             assert abs(got[i, j] - acc) <= 2.0 ** -23 * abs(acc) + 1e-30, (i, j)
+
+
+def _pattern_f32(index):
+    """The reference's sparse-attention test inputs (tests/trellis2_sparse.rs:23-25)."""
+    return ((np.asarray(index) % 23).astype(np.float32) - np.float32(11.0)) * np.float32(0.1)
+
+
+def test_sdpa_matches_scipy_softmax_on_reference_test_inputs():
+    """The shapes of the reference's naive-attention tests
+    (tests/trellis2_sparse.rs:521-623: H=2, T=17 self and T=9 over Tkv=7
+    cross, head_dim 8, scale 1/sqrt(8)) with its pattern_f32 inputs, against
+    scipy.special.softmax and numpy matmuls in f64."""
+    from scipy.special import softmax
+    for t, tkv, seeds in [(17, 17, (1, 2, 3)), (9, 7, (4, 5, 6))]:
+        h, hd = 2, 8
+        q, k, v = (_pattern_f32(np.arange(h * n * hd) * 7 + s * 3).reshape(h, n, hd)
+                   for n, s in ((t, seeds[0]), (tkv, seeds[1]), (tkv, seeds[2])))
+        scale = 1.0 / np.sqrt(np.float32(hd))
+        got = orc.sdpa(q, k, v, float(np.float32(scale)))
+        q64, k64, v64 = (a.astype(np.float64) for a in (q, k, v))
+        want = softmax(q64 @ k64.transpose(0, 2, 1) * float(np.float32(scale)), axis=-1) @ v64
+        assert np.all(np.abs(got - want) <= 2.0 ** -23 * np.abs(want) + 1e-30)
+
+
+def test_sdpa_closed_forms_and_key_permutation():
+    rng = np.random.default_rng(11)
+    # identical keys: uniform weights, the output is the mean of the values
+    q = rng.standard_normal((3, 5, 16)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((3, 1, 16)).astype(np.float32), 9, axis=1)
+    v = rng.standard_normal((3, 9, 16)).astype(np.float32)
+    got = orc.sdpa(q, k, v, 0.25)
+    want = np.broadcast_to(v.astype(np.float64).mean(axis=1, keepdims=True), got.shape)
+    assert np.all(np.abs(got - want) <= 2.0 ** -22 * np.abs(want) + 1e-7)
+    # one key: the output is that value row for every query
+    got = orc.sdpa(q, k[:, :1], v[:, :1], 0.25)
+    assert np.array_equal(got, np.broadcast_to(v[:, :1], got.shape))
+    # a dominant key (score gap > 200 after scaling) takes all the weight
+    k2 = rng.standard_normal((1, 6, 4)).astype(np.float32)
+    k2[0, 4] = 100.0
+    q2 = np.ones((1, 2, 4), dtype=np.float32)
+    v2 = rng.standard_normal((1, 6, 4)).astype(np.float32)
+    assert np.array_equal(orc.sdpa(q2, k2, v2, 1.0), np.broadcast_to(v2[:, 4:5], (1, 2, 4)))
+    # permuting the (key, value) pairs leaves the output unchanged (up to the
+    # order of the f64 sums); a mixed-up transpose or index would not
+    perm = rng.permutation(9)
+    q3 = rng.standard_normal((2, 7, 16)).astype(np.float32)
+    k3 = rng.standard_normal((2, 9, 16)).astype(np.float32)
+    v3 = rng.standard_normal((2, 9, 16)).astype(np.float32)
+    a = orc.sdpa(q3, k3, v3, 0.3)
+    b = orc.sdpa(q3, k3[:, perm], v3[:, perm], 0.3)
+    assert np.all(np.abs(a - b) <= 2.0 ** -22 * np.abs(a) + 1e-7)
+
+
+def test_sdpa_bf16_inputs_round_once():
+    rng = np.random.default_rng(12)
+    q, k, v = (orc.bf16_bits(rng.standard_normal((2, n, 64))) for n in (33, 70, 70))
+    got, wabs = orc.sdpa(q, k, v, 0.125, dt=orc.BF16, with_abs=True)
+    from scipy.special import softmax
+    q64, k64, v64 = (orc.bf16_to_f32(a).astype(np.float64) for a in (q, k, v))
+    p = softmax(q64 @ k64.transpose(0, 2, 1) * 0.125, axis=-1)
+    want = p @ v64
+    assert np.array_equal(got, to_bf16_bits(want))
+    assert np.allclose(wabs, p @ np.abs(v64), rtol=1e-6)
