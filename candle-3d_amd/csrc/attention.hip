@@ -6,8 +6,8 @@
 // accumulate bf16 x bf16 / f16 x f16 products in f32), the softmax runs in
 // f32 with a running maximum (exp2 of the log2e-scaled scores), the
 // probabilities are rounded to the input type for the P v product, which
-// again accumulates in f32, and the output is divided by the f32 row sum and
-// rounded once. That is the arithmetic of exact_sdpa_heads (f32 throughout)
+// again accumulates in f32, and the output is divided by the f32 sum of those
+// same rounded probabilities and rounded once. That is the arithmetic of exact_sdpa_heads (f32 throughout)
 // up to the rounding of the probabilities; exact_query_chunked_sdpa on bf16
 // additionally rounds q * scale, the scores and the probabilities to bf16,
 // which this kernel does not.
@@ -35,6 +35,8 @@
 // Generic kernel (attn_generic_kernel): one wavefront per query row, f32
 // arithmetic throughout (lanes over keys for the scores, over head dims for
 // the output); any float dtype, any alignment, D <= 512.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -56,6 +58,11 @@ template <> struct Mma<BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  __device__ __forceinline__ static float sum2(uint32_t pair, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), one, acc, false);
+  }
 };
 template <> struct Mma<F16> {
   typedef f16x8_t op_t;
@@ -63,6 +70,11 @@ template <> struct Mma<F16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+  __device__ __forceinline__ static float sum2(uint32_t pair, float acc) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), one, acc, false);
+  }
 };
 
 // The value the partner lane (lane ^ 32) holds, paired with this lane's own:
@@ -83,8 +95,19 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
 }
 
-template <typename T, int D, int QT, int BKV>
-__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+// LAZY: the reference maximum m moves only when a block's maximum exceeds it
+// by more than 8 (log2 units), so probabilities exp2(s - m) stay <= 2^8 and
+// the O rescale (skipped by a wave-uniform test while every factor is 1) is
+// rare after the first blocks. The final O / l is the same function.
+// DOT: the row sum l adds the probabilities as rounded for the P v product
+// (v_dot2 of a packed pair with (1, 1)), one instruction per pair.
+// PHASED (QT == 2): P v of query tile 0 is issued before the softmax of
+// tile 1, so the matrix cores and the VALU overlap inside one wavefront.
+// Measured on MI355X (TFLOP/s, VGGT frame / global, D 64): LAZY + DOT +
+// PHASED 617 / 795 against 579 / 700 without; D 128 (TripoSG / TRELLIS.2
+// 16k) LAZY + DOT 718 / 877 against 679 / 827, PHASED by key tile no gain.
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED>
+__global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   using M = Mma<T>;
   using op_t = typename M::op_t;
   constexpr int BQ = 4 * 32 * QT;
@@ -137,9 +160,27 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t
     v_dg[i] = g % (D / 4);
     v_kg[i] = g / (D / 4);
   }
+  // byte offsets of this thread's rows relative to a block's first key
+  int64_t k_off[KCH], v_off[VGR];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) k_off[i] = ((int64_t)k_row[i] * p.k_st + k_part[i] * 8) * 2;
+#pragma unroll
+  for (int i = 0; i < VGR; ++i) v_off[i] = ((int64_t)v_kg[i] * 4 * p.v_st + v_dg[i] * 4) * 2;
+  const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2, vrow = p.v_st * 2;
   uint4 rk[KCH];
   uint2 rv[VGR][4];
-  auto load_kv = [&](int64_t j) {
+  // `clamp` (the tail block only): keys past Lk read row Lk - 1
+  auto load_kv = [&](int64_t j, bool clamp) {
+    if (!clamp) {
+      const char *kb = kbase + j * kstep, *vb = vbase + j * vstep;
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) rk[i] = ld16<false>(kb + k_off[i]);
+#pragma unroll
+      for (int i = 0; i < VGR; ++i)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) rv[i][kk] = *reinterpret_cast<const uint2 *>(vb + v_off[i] + kk * vrow);
+      return;
+    }
     const int64_t key0 = j * BKV;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
@@ -186,14 +227,17 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t
   }
   const float c2 = p.scale * kLog2e;
   const int64_t nkv = (Lk + BKV - 1) / BKV;
+  const bool tail = (Lk % BKV) != 0;
 
-  load_kv(0);
+  load_kv(0, nkv == 1 && tail);
   store_kv(0);
   lds_barrier();
 
-  for (int64_t j = 0; j < nkv; ++j) {
+  // one block of keys; MASK (the partial tail block) sets scores past Lk to -inf
+  auto step = [&](int64_t j, auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
     const int buf = (int)(j & 1);
-    if (j + 1 < nkv) load_kv(j + 1);
+    if (j + 1 < nkv) load_kv(j + 1, tail && j + 2 == nkv);
 
     // S^T = K Q^T: lane holds key 8 * (i / 4) + 4 * hh + i % 4 of each 32-key tile, query l32.
     f32x16_t s[QT][NKT];
@@ -209,35 +253,41 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) s[qt][kt] = M::run(a, qf[qt][c], s[qt][kt]);
       }
-    if ((j + 1) * BKV > Lk) {
+    if constexpr (MASK) {
+      const int lim = (int)(Lk - j * BKV) - 4 * hh;  // local key offsets >= lim + 4 hh are past Lk
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int64_t key = j * BKV + kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key >= Lk) {
+        for (int i = 0; i < 16; ++i)
+          if (kt * 32 + 8 * (i >> 2) + (i & 3) >= lim) {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) s[qt][kt][i] = -INFINITY;
           }
-        }
     }
 
-    // online softmax; P packed as the B operand of O^T += V^T P^T
+    // online softmax of query tile qt; P packed as the B operand of O^T += V^T P^T
     op_t pf[QT][NKT * 2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
+    float alpha_q[QT];
+    auto softmax = [&](int qt, int k0, int k1) {  // over key tiles [k0, k1)
       float mx = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
+      for (int kt = k0; kt < k1; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
-      mx = half_swap_max(mx);
-      const float mn = fmaxf(m[qt], mx * c2);
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mn);
+      const float cand = half_swap_max(mx) * c2;
+      // LAZY keeps the reference maximum until a score exceeds it by 2^8: the
+      // probabilities stay <= 256 and most blocks need no rescale at all
+      float mn = m[qt];
+      if constexpr (LAZY) {
+        if (cand > mn + 8.f) mn = cand;
+      } else {
+        mn = fmaxf(mn, cand);
+      }
+      alpha_q[qt] = __builtin_amdgcn_exp2f(m[qt] - mn);
       m[qt] = mn;
       float ls = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
+      for (int kt = k0; kt < k1; ++kt)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           u32x4_t pk;
@@ -245,33 +295,70 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnParams p, int64_t
           for (int e = 0; e < 4; ++e) {
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][8 * jj + 2 * e], c2, -mn));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][8 * jj + 2 * e + 1], c2, -mn));
-            ls += p0 + p1;
             pk[e] = M::pack(p0, p1);
+            // DOT: sum the rounded probabilities the P v product uses
+            if constexpr (DOT) ls = M::sum2(pk[e], ls);
+            else ls += p0 + p1;
           }
           pf[qt][kt * 2 + jj] = __builtin_bit_cast(op_t, pk);
         }
-      l[qt] = l[qt] * alpha + ls;
+      l[qt] = l[qt] * alpha_q[qt] + ls;
+    };
+    auto rescale = [&](int qt) {
+      if (!LAZY || __builtin_amdgcn_ballot_w64(alpha_q[qt] != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha;
+        for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha_q[qt];
+      }
+    };
+    // A = V^T[dim l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of tile kt
+    auto vfrag = [&](int dt, int kt, int jj) {
+      const uint16_t *vr = &Vt[buf][(dt * 32 + l32) * VROW + kt * 32 + 16 * jj + 4 * hh];
+      const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
+      return __builtin_bit_cast(op_t, u32x4_t{lo.x, lo.y, hi2.x, hi2.y});
+    };
+    if constexpr (PHASED && QT == 2) {
+      // P v of query tile 0 has no dependence on the softmax of tile 1:
+      // issued together, the matrix cores and the VALU overlap in one wavefront
+      softmax(0, 0, NKT);
+      rescale(0);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) o[0][dt] = M::run(vfrag(dt, kt, jj), pf[0][kt * 2 + jj], o[0][dt]);
+      softmax(1, 0, NKT);
+      rescale(1);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) o[1][dt] = M::run(vfrag(dt, kt, jj), pf[1][kt * 2 + jj], o[1][dt]);
+    } else {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        softmax(qt, 0, NKT);
+        rescale(qt);
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const op_t a = vfrag(dt, kt, jj);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = M::run(a, pf[qt][kt * 2 + jj], o[qt][dt]);
+          }
     }
-
-    // O^T += V^T P^T: A = V^T[dim l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of tile kt
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const uint16_t *vr = &Vt[buf][(dt * 32 + l32) * VROW + kt * 32 + 16 * jj + 4 * hh];
-          const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
-          const op_t a = __builtin_bit_cast(op_t, u32x4_t{lo.x, lo.y, hi2.x, hi2.y});
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) o[qt][dt] = M::run(a, pf[qt][kt * 2 + jj], o[qt][dt]);
-        }
 
     if (j + 1 < nkv) store_kv(buf ^ 1);
     lds_barrier();
-  }
+  };
+  const int64_t nfull = tail ? nkv - 1 : nkv;
+  for (int64_t j = 0; j < nfull; ++j) step(j, std::false_type{});
+  if (tail) step(nkv - 1, std::true_type{});
 
   // out[query][dim]: lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
 #pragma unroll
@@ -369,13 +456,14 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
   }
 }
 
-template <typename T, int D, int QT, int BKV>
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED>
 hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
   constexpr int BQ = 4 * 32 * QT;
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED>), dim3((unsigned)nwg), dim3(256), 0, s, p,
+                     nqb, nwg);
   return hipGetLastError();
 }
 
@@ -397,8 +485,8 @@ template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
-      if (p.D == 64) return launch_mfma<T, 64, 2, 64>(p, s);
-      if (p.D == 128) return launch_mfma<T, 128, 1, 64>(p, s);
+      if (p.D == 64) return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);
+      if (p.D == 128) return launch_mfma<T, 128, 1, 64, 2, true, true, false>(p, s);
     }
   }
   return launch_generic<T>(p, s);
