@@ -272,6 +272,15 @@ Tensor silu(const Tensor &x);      // Tensor::silu
 // holds elem_count(shape)/32 records of 34 bytes; out dtype F32, BF16 or F16.
 Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out);
 
+// Attention over [B, H, L, D] views: softmax(q k^T * scale) v, one kernel,
+// no scores buffer. exact_query_chunked_sdpa (attention_math.rs:199-241; the
+// chunk size only bounded the reference's scores buffer and is ignored) and
+// exact_sdpa_heads (attention_math.rs:244-259). Returns a contiguous
+// [B, H, Lq, D] tensor in q's dtype.
+Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale,
+                                size_t chunk_size = SIZE_MAX);
+Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float scale);
+
 // QMatMul over a Q8_0 weight [n, k] (QMatMul::from_qtensor and forward,
 // runtime/nn_blocks.rs:83-93, 145-150). from_q8_0 repacks the GGML blocks
 // once; forward(xs [..., k] bf16) = xs @ dequant(W)^T in f32 accumulation.

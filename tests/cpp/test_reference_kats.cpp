@@ -299,6 +299,59 @@ void q8_0_linear_closed_form(const Device &dev) {
     }
 }
 
+// tests/trellis2_sparse.rs:471-623: exact self / cross attention (H = 2,
+// head_dim 8, pattern_f32 inputs) against naive per-head softmax attention,
+// max |diff| < 1e-5.
+float pattern_f32(size_t index) { return ((float)(index % 23) - 11.0f) * 0.1f; }
+
+std::vector<float> naive_attention(const std::vector<float> &q, const std::vector<float> &k,
+                                   const std::vector<float> &v, size_t heads, size_t tokens, size_t kv_tokens,
+                                   size_t hd) {
+  const float scale = 1.0f / std::sqrt((float)hd);
+  std::vector<float> out(heads * tokens * hd, 0.0f);
+  for (size_t h = 0; h < heads; ++h)
+    for (size_t t = 0; t < tokens; ++t) {
+      std::vector<float> sc(kv_tokens);
+      float mx = -INFINITY;
+      for (size_t j = 0; j < kv_tokens; ++j) {
+        float dot = 0.0f;
+        for (size_t d = 0; d < hd; ++d) dot += q[(h * tokens + t) * hd + d] * k[(h * kv_tokens + j) * hd + d];
+        sc[j] = dot * scale;
+        mx = std::max(mx, sc[j]);
+      }
+      float sum = 0.0f;
+      for (float &x : sc) {
+        x = std::exp(x - mx);
+        sum += x;
+      }
+      for (size_t j = 0; j < kv_tokens; ++j)
+        for (size_t d = 0; d < hd; ++d) out[(h * tokens + t) * hd + d] += sc[j] / sum * v[(h * kv_tokens + j) * hd + d];
+    }
+  return out;
+}
+
+void sparse_attention_matches_naive(const Device &dev) {
+  const size_t H = 2, HD = 8;
+  const size_t cases[2][5] = {{17, 17, 1, 2, 3}, {9, 7, 4, 5, 6}};
+  for (const auto &c : cases) {
+    const size_t T = c[0], TKV = c[1];
+    auto pat = [&](size_t n, size_t seed) {
+      std::vector<float> x(H * n * HD);
+      for (size_t i = 0; i < x.size(); ++i) x[i] = pattern_f32(i * 7 + seed * 3);
+      return x;
+    };
+    const std::vector<float> q = pat(T, c[2]), k = pat(TKV, c[3]), v = pat(TKV, c[4]);
+    const Tensor out = exact_query_chunked_sdpa(Tensor::from_f32(q, {1, (int64_t)H, (int64_t)T, (int64_t)HD}, DType::F32, dev),
+                                                Tensor::from_f32(k, {1, (int64_t)H, (int64_t)TKV, (int64_t)HD}, DType::F32, dev),
+                                                Tensor::from_f32(v, {1, (int64_t)H, (int64_t)TKV, (int64_t)HD}, DType::F32, dev),
+                                                1.0f / std::sqrt((float)HD), 5);
+    const std::vector<float> got = out.to_vec_f32(), want = naive_attention(q, k, v, H, T, TKV, HD);
+    float md = 0.0f;
+    for (size_t i = 0; i < got.size(); ++i) md = std::max(md, std::fabs(got[i] - want[i]));
+    CHECK(md < 1e-5f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Error behaviour (the reference's bail! messages)
 // ---------------------------------------------------------------------------
@@ -352,6 +405,7 @@ int main(int argc, char **argv) {
       {"vggt_qk_layernorm_rope_specials_are_plain_layernorm", vggt_qk_layernorm_rope_specials_are_plain_layernorm, true},
       {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
       {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
+      {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
       {"errors_on_device", errors_on_device, true},
   };
   Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed
