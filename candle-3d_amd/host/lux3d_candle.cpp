@@ -3,6 +3,8 @@
 // memory through the HIP runtime, every op one C ABI call.
 #include "lux3d_candle.hpp"
 
+#include "lux3d_weights.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -691,6 +693,202 @@ Tensor QMatMul::forward(const Tensor &xs, const std::optional<Tensor> &bias, DTy
   abi_check(lux3d_q8_0_linear(Desc(xs).p(), Desc(qs_).p(), Desc(scales_).p(), Desc(bias).p(), Desc(y).p(),
                               xs.device().stream()));
   return y;
+}
+
+// ---------------------------------------------------------------------------
+// Weight files
+// ---------------------------------------------------------------------------
+
+namespace {
+
+WeightInfo to_info(const lux3d_weights_tensor_t &t) {
+  WeightInfo w;
+  w.name = t.name;
+  w.dtype = t.dtype;
+  w.shape.assign(t.shape, t.shape + t.rank);
+  w.nbytes = t.nbytes;
+  w.data = t.data;
+  return w;
+}
+
+void weights_check(bool ok) {
+  if (!ok) fail(LUX3D_ERR_VALUE, lux3d_weights_last_error());
+}
+
+float host_elem_f32(int src_dt, const uint8_t *b, size_t i) {
+  switch (src_dt) {
+    case LUX3D_F32: { float f; std::memcpy(&f, b + 4 * i, 4); return f; }
+    case LUX3D_BF16: { uint16_t h; std::memcpy(&h, b + 2 * i, 2); return bf16_to_f32(h); }
+    case LUX3D_F16: { uint16_t h; std::memcpy(&h, b + 2 * i, 2); return f16_to_f32(h); }
+  }
+  return 0.f;
+}
+
+// Host bytes of lux3d dtype `src_dt` -> a device tensor of dtype `dt`
+// (float types: widened exactly, rounded once; other types must match).
+Tensor upload_as(const void *src, int src_dt, uint64_t nbytes, const Shape &shape, DType dt, const Device &dev,
+                 const std::string &name) {
+  Tensor t = Tensor::empty(shape, dt, dev);
+  if (src_dt == (int)dt) {
+    if ((uint64_t)t.elem_count() * dtype_size(dt) != nbytes)
+      fail(LUX3D_ERR_SHAPE, "tensor `" + name + "`: byte count does not match its shape");
+    return upload(t, src, nbytes);
+  }
+  const bool fsrc = src_dt == LUX3D_F32 || src_dt == LUX3D_BF16 || src_dt == LUX3D_F16;
+  const bool fdst = dt == DType::F32 || dt == DType::BF16 || dt == DType::F16;
+  if (!fsrc || !fdst) fail(LUX3D_ERR_DTYPE, "tensor `" + name + "`: no conversion to the requested dtype");
+  const size_t n = (size_t)t.elem_count();
+  const uint8_t *b = static_cast<const uint8_t *>(src);
+  if (dt == DType::F32) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = host_elem_f32(src_dt, b, i);
+    return upload(t, v.data(), n * 4);
+  }
+  std::vector<uint16_t> v(n);
+  for (size_t i = 0; i < n; ++i) {
+    const float f = host_elem_f32(src_dt, b, i);
+    v[i] = dt == DType::BF16 ? f32_to_bf16(f) : f32_to_f16(f);
+  }
+  return upload(t, v.data(), n * 2);
+}
+
+void check_shape(const Shape &expected, const Shape &got, const std::string &name) {
+  if (expected != got)
+    fail(LUX3D_ERR_SHAPE, "shape mismatch for " + name + ", expected " + dims_str(expected) + ", got " + dims_str(got));
+}
+
+}  // namespace
+
+GgufFile GgufFile::open(const std::string &path) {
+  lux3d_gguf_t *g = lux3d_gguf_open(path.c_str());
+  weights_check(g != nullptr);
+  GgufFile f;
+  f.h_ = std::shared_ptr<lux3d_gguf_t>(g, lux3d_gguf_close);
+  return f;
+}
+
+uint32_t GgufFile::version() const { return lux3d_gguf_version(h_.get()); }
+
+std::vector<std::string> GgufFile::names() const {
+  std::vector<std::string> r;
+  lux3d_weights_tensor_t t;
+  for (int64_t i = 0; i < lux3d_gguf_tensor_count(h_.get()); ++i)
+    if (lux3d_gguf_tensor(h_.get(), i, &t) == LUX3D_OK) r.emplace_back(t.name);
+  return r;
+}
+
+bool GgufFile::contains(const std::string &name) const { return lux3d_gguf_find(h_.get(), name.c_str()) >= 0; }
+
+WeightInfo GgufFile::info(const std::string &name) const {
+  const int64_t i = lux3d_gguf_find(h_.get(), name.c_str());
+  if (i < 0) fail(LUX3D_ERR_VALUE, "cannot find tensor " + name);
+  lux3d_weights_tensor_t t;
+  weights_check(lux3d_gguf_tensor(h_.get(), i, &t) == LUX3D_OK);
+  return to_info(t);
+}
+
+std::optional<std::string> GgufFile::metadata_string(const std::string &key) const {
+  const int64_t i = lux3d_gguf_metadata_find(h_.get(), key.c_str());
+  if (i < 0) return std::nullopt;
+  int32_t type, et;
+  const void *v;
+  uint64_t n;
+  weights_check(lux3d_gguf_metadata(h_.get(), i, nullptr, &type, &et, &v, &n) == LUX3D_OK);
+  if (type != LUX3D_GGUF_STRING) return std::nullopt;
+  return std::string(static_cast<const char *>(v), (size_t)n);
+}
+
+std::optional<uint64_t> GgufFile::metadata_uint(const std::string &key) const {
+  const int64_t i = lux3d_gguf_metadata_find(h_.get(), key.c_str());
+  if (i < 0) return std::nullopt;
+  int32_t type, et;
+  const void *v;
+  uint64_t n;
+  weights_check(lux3d_gguf_metadata(h_.get(), i, nullptr, &type, &et, &v, &n) == LUX3D_OK);
+  const uint8_t *b = static_cast<const uint8_t *>(v);
+  switch (type) {
+    case LUX3D_GGUF_U8: return (uint64_t)b[0];
+    case LUX3D_GGUF_U16: { uint16_t x; std::memcpy(&x, b, 2); return x; }
+    case LUX3D_GGUF_U32: { uint32_t x; std::memcpy(&x, b, 4); return x; }
+    case LUX3D_GGUF_U64: { uint64_t x; std::memcpy(&x, b, 8); return x; }
+  }
+  return std::nullopt;
+}
+
+Tensor GgufFile::get(const std::string &name, DType dt, const Device &dev) const {
+  const WeightInfo w = info(name);
+  switch (w.dtype) {
+    case LUX3D_GGML_Q8_0: {
+      const Tensor blocks = upload(Tensor::empty({(int64_t)w.nbytes}, DType::U8, dev), w.data, w.nbytes);
+      return dequantize_q8_0(blocks, w.shape, dt);
+    }
+    case LUX3D_GGML_F32: return upload_as(w.data, LUX3D_F32, w.nbytes, w.shape, dt, dev, name);
+    case LUX3D_GGML_F16: return upload_as(w.data, LUX3D_F16, w.nbytes, w.shape, dt, dev, name);
+    case LUX3D_GGML_BF16: return upload_as(w.data, LUX3D_BF16, w.nbytes, w.shape, dt, dev, name);
+  }
+  fail(LUX3D_ERR_DTYPE, "tensor `" + name + "` has ggml type " + std::to_string(w.dtype) +
+                            " (F32, F16, BF16 and Q8_0 are supported)");
+}
+
+Tensor GgufFile::get(const Shape &expected, const std::string &name, DType dt, const Device &dev) const {
+  check_shape(expected, info(name).shape, name);
+  return get(name, dt, dev);
+}
+
+QMatMul GgufFile::get_qmatmul(const std::string &name, int64_t out_dim, int64_t in_dim, const Device &dev) const {
+  const WeightInfo w = info(name);
+  if (w.shape != Shape{out_dim, in_dim})
+    fail(LUX3D_ERR_SHAPE, "quantized linear weight shape " + dims_str(w.shape) + " does not match expected (" +
+                              std::to_string(out_dim) + ", " + std::to_string(in_dim) + ")");
+  if (w.dtype != LUX3D_GGML_Q8_0)
+    fail(LUX3D_ERR_DTYPE, "tensor `" + name + "` is not Q8_0 (ggml type " + std::to_string(w.dtype) + ")");
+  const Tensor blocks = upload(Tensor::empty({(int64_t)w.nbytes}, DType::U8, dev), w.data, w.nbytes);
+  return QMatMul::from_q8_0(blocks, out_dim, in_dim);
+}
+
+SafetensorsFile SafetensorsFile::open(const std::string &path) {
+  lux3d_safetensors_t *s = lux3d_safetensors_open(path.c_str());
+  weights_check(s != nullptr);
+  SafetensorsFile f;
+  f.h_ = std::shared_ptr<lux3d_safetensors_t>(s, lux3d_safetensors_close);
+  return f;
+}
+
+std::vector<std::string> SafetensorsFile::names() const {
+  std::vector<std::string> r;
+  lux3d_weights_tensor_t t;
+  for (int64_t i = 0; i < lux3d_safetensors_tensor_count(h_.get()); ++i)
+    if (lux3d_safetensors_tensor(h_.get(), i, &t) == LUX3D_OK) r.emplace_back(t.name);
+  return r;
+}
+
+bool SafetensorsFile::contains(const std::string &name) const {
+  return lux3d_safetensors_find(h_.get(), name.c_str()) >= 0;
+}
+
+WeightInfo SafetensorsFile::info(const std::string &name) const {
+  const int64_t i = lux3d_safetensors_find(h_.get(), name.c_str());
+  if (i < 0) fail(LUX3D_ERR_VALUE, "cannot find tensor " + name);
+  lux3d_weights_tensor_t t;
+  weights_check(lux3d_safetensors_tensor(h_.get(), i, &t) == LUX3D_OK);
+  return to_info(t);
+}
+
+std::optional<std::string> SafetensorsFile::metadata(const std::string &key) const {
+  const char *v = lux3d_safetensors_metadata(h_.get(), key.c_str());
+  if (!v) return std::nullopt;
+  return std::string(v);
+}
+
+Tensor SafetensorsFile::get(const std::string &name, DType dt, const Device &dev) const {
+  const WeightInfo w = info(name);
+  if (w.dtype < 0) fail(LUX3D_ERR_DTYPE, "tensor `" + name + "` has a dtype this reader does not convert");
+  return upload_as(w.data, w.dtype, w.nbytes, w.shape, dt, dev, name);
+}
+
+Tensor SafetensorsFile::get(const Shape &expected, const std::string &name, DType dt, const Device &dev) const {
+  check_shape(expected, info(name).shape, name);
+  return get(name, dt, dev);
 }
 
 }  // namespace lux3d::candle

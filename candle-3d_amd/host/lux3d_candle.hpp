@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "lux3d_fused.h"
+#include "lux3d_weights.h"
 
 namespace lux3d::candle {
 
@@ -284,6 +285,8 @@ Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float
 // QMatMul over a Q8_0 weight [n, k] (QMatMul::from_qtensor and forward,
 // runtime/nn_blocks.rs:83-93, 145-150). from_q8_0 repacks the GGML blocks
 // once; forward(xs [..., k] bf16) = xs @ dequant(W)^T in f32 accumulation.
+class GgufFile;
+
 class QMatMul {
  public:
   static QMatMul from_q8_0(const Tensor &blocks, int64_t n, int64_t k);
@@ -293,6 +296,61 @@ class QMatMul {
 
  private:
   Tensor qs_, scales_;
+};
+
+// ---------------------------------------------------------------------------
+// Weight files (lux3d_weights.h underneath): VarBuilder::from_gguf and
+// VarBuilder::from_mmaped_safetensors (weights/mod.rs:121-140). The files
+// stay mapped while the object lives; get() uploads and converts on the
+// device (Q8_0 through the dequant kernel).
+// ---------------------------------------------------------------------------
+
+struct WeightInfo {
+  std::string name;
+  int32_t dtype = 0;  // GGUF: ggml type id; safetensors: lux3d_dtype (-1: not one)
+  Shape shape;
+  uint64_t nbytes = 0;
+  const void *data = nullptr;  // host bytes in the mapping
+};
+
+class GgufFile {
+ public:
+  static GgufFile open(const std::string &path);
+  uint32_t version() const;
+  std::vector<std::string> names() const;
+  bool contains(const std::string &name) const;
+  WeightInfo info(const std::string &name) const;
+  // gguf_metadata_string (weights/mod.rs:656-661): a string value or nothing
+  std::optional<std::string> metadata_string(const std::string &key) const;
+  std::optional<uint64_t> metadata_uint(const std::string &key) const;
+  // VarBuilder::get on a GGUF: the tensor in dtype `dt` on `dev` (Q8_0 is
+  // dequantized exactly, F16 / BF16 / F32 converted with one RNE rounding)
+  Tensor get(const std::string &name, DType dt, const Device &dev) const;
+  // VarBuilder::get(shape, name): the same, with the reference's shape check
+  Tensor get(const Shape &expected, const std::string &name, DType dt, const Device &dev) const;
+  // VarBuilder::get_quantized + QMatMul::from_qtensor for a rank-2 Q8_0
+  // weight (nn_blocks.rs:107-150); quantized_linear's shape check against
+  // (out_dim, in_dim)
+  QMatMul get_qmatmul(const std::string &name, int64_t out_dim, int64_t in_dim, const Device &dev) const;
+
+ private:
+  std::shared_ptr<lux3d_gguf_t> h_;
+};
+
+class SafetensorsFile {
+ public:
+  static SafetensorsFile open(const std::string &path);
+  std::vector<std::string> names() const;
+  bool contains(const std::string &name) const;
+  WeightInfo info(const std::string &name) const;
+  std::optional<std::string> metadata(const std::string &key) const;
+  // VarBuilder::get: the tensor in `dt` on `dev` (float types converted with
+  // one RNE rounding; integer types must match `dt`)
+  Tensor get(const std::string &name, DType dt, const Device &dev) const;
+  Tensor get(const Shape &expected, const std::string &name, DType dt, const Device &dev) const;
+
+ private:
+  std::shared_ptr<lux3d_safetensors_t> h_;
 };
 
 }  // namespace lux3d::candle

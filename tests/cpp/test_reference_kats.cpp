@@ -352,6 +352,51 @@ void sparse_attention_matches_naive(const Device &dev) {
   }
 }
 
+// A GGUF container as the reference's quantizer lays it out
+// (tests/golden/tiny_q8.gguf, written by tests/golden/make_gguf.py): the Q8_0
+// weight becomes a QMatMul (VarBuilder::get_quantized + QMatMul::from_qtensor,
+// nn_blocks.rs:107-150), the F16 bias is read through VarBuilder::get, and
+// x @ W^T + b is exact for these small-integer values.
+std::string g_fixture_dir;
+
+void gguf_q8_linear_from_file(const Device &dev) {
+  const GgufFile f = GgufFile::open(g_fixture_dir + "/tiny_q8.gguf");
+  CHECK(f.metadata_string("lux3d.family") == std::optional<std::string>("trellis2"));
+  CHECK(f.metadata_uint("lux3d.tensor_count") == std::optional<uint64_t>(3));
+  CHECK(!f.metadata_string("lux3d.tensor_count"));
+  const std::string wn = "blocks.0.mlp.fc1.weight", bn = "blocks.0.mlp.fc1.bias";
+  const WeightInfo w = f.info(wn);
+  CHECK((w.shape == Shape{8, 64}) && w.dtype == LUX3D_GGML_Q8_0 && w.nbytes == 8 * 2 * 34);
+  // host decode of the blocks: d = f16 0.5, q int8
+  const uint8_t *bytes = static_cast<const uint8_t *>(w.data);
+  std::vector<double> wt(8 * 64);
+  for (int r = 0; r < 8; ++r)
+    for (int c = 0; c < 64; ++c) {
+      const uint8_t *blk = bytes + (r * 2 + c / 32) * 34;
+      CHECK(blk[0] == 0x00 && blk[1] == 0x38);
+      wt[r * 64 + c] = 0.5 * (double)(int8_t)blk[2 + c % 32];
+    }
+  const std::vector<float> deq = f.get(wn, DType::F32, dev).to_vec_f32();
+  for (int i = 0; i < 8 * 64; ++i) CHECK(deq[i] == (float)wt[i]);
+  const QMatMul mm = f.get_qmatmul(wn, 8, 64, dev);
+  const Tensor bias = f.get(bn, DType::F32, dev);
+  std::vector<float> x(3 * 64);
+  for (int i = 0; i < 3 * 64; ++i) x[i] = (float)((i * 11) % 7 - 3);
+  const std::vector<float> y = mm.forward(Tensor::from_f32(x, {3, 64}, DType::BF16, dev), bias, DType::F32).to_vec_f32();
+  for (int m = 0; m < 3; ++m)
+    for (int r = 0; r < 8; ++r) {
+      double acc = 0.25 * r - 1.0;
+      for (int c = 0; c < 64; ++c) acc += (double)x[m * 64 + c] * wt[r * 64 + c];
+      CHECK(y[m * 8 + r] == (float)acc);
+    }
+  const std::vector<float> nw = f.get(Shape{64}, "blocks.0.norm.weight", DType::F32, dev).to_vec_f32();
+  for (int c = 0; c < 64; ++c) CHECK(nw[c] == 1.0f + (float)c / 64.0f);
+  CHECK(throws_with([&] { f.get_qmatmul(wn, 64, 8, dev); }, "does not match expected (64, 8)"));
+  CHECK(throws_with([&] { f.get(Shape{65}, "blocks.0.norm.weight", DType::F32, dev); }, "shape mismatch"));
+  CHECK(throws_with([&] { f.get_qmatmul(bn, 8, 1, dev); }, "does not match expected"));
+  CHECK(throws_with([&] { f.info("nope"); }, "cannot find tensor nope"));
+}
+
 // ---------------------------------------------------------------------------
 // Error behaviour (the reference's bail! messages)
 // ---------------------------------------------------------------------------
@@ -363,6 +408,10 @@ void errors_on_host(const Device &dev) {
   CHECK(throws_with([&] { Trellis2Rope3d(13).cos_sin({1, 2, 3}, dev); }, "must be divisible by 2"));
   CHECK(throws_with([&] { dinov3_rope_cos_sin(10, 100.0f, 2, 2, dev); }, "is not divisible by 4"));
   CHECK(throws_with([&] { QMatMul::from_q8_0(Tensor(), 4, 48); }, "needs k % 32 == 0"));
+  CHECK(throws_with([&] { GgufFile::open(g_fixture_dir + "/missing.gguf"); }, "cannot open"));
+  CHECK(throws_with([&] { SafetensorsFile::open(g_fixture_dir + "/tiny_q8.gguf"); }, "safetensors"));
+  const GgufFile f = GgufFile::open(g_fixture_dir + "/tiny_q8.gguf");
+  CHECK(f.version() == 3 && f.names().size() == 3 && f.contains("blocks.0.norm.weight"));
 }
 
 void errors_on_device(const Device &dev) {
@@ -392,6 +441,11 @@ struct Case {
 
 int main(int argc, char **argv) {
   const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+  {  // fixtures live in tests/golden, beside this binary's tests/cpp
+    std::string self = argv[0];
+    const size_t slash = self.find_last_of('/');
+    g_fixture_dir = (slash == std::string::npos ? std::string(".") : self.substr(0, slash)) + "/../golden";
+  }
   const std::vector<Case> cases = {
       {"errors_on_host", errors_on_host, false},
       {"rope_tables_match_reference_formula", rope_tables_match_reference_formula, true},
@@ -406,6 +460,7 @@ int main(int argc, char **argv) {
       {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
       {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
       {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
+      {"gguf_q8_linear_from_file", gguf_q8_linear_from_file, true},
       {"errors_on_device", errors_on_device, true},
   };
   Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed
