@@ -72,6 +72,7 @@ int check_desc(const lux3d_tensor_t *t, const char *fn, const char *name) {
 }
 
 bool is_contiguous(const lux3d_tensor_t *t) {
+  if (numel(t) == 0) return true;  // no element to address: any strides will do
   int64_t expect = 1;
   for (int i = t->rank - 1; i >= 0; --i) {
     if (t->shape[i] != 1 && t->stride[i] != expect) return false;
@@ -885,6 +886,149 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_ten
   }
   p.mfma = mfma;
   return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+// ---- sparse ops --------------------------------------------------------------
+
+namespace {
+int contiguous_of(const lux3d_tensor_t *t, const char *fn, const char *name, int dtype, int rank) {
+  int r = check_desc(t, fn, name);
+  if (r) return r;
+  if (dtype >= 0 && t->dtype != dtype) return fail(LUX3D_ERR_DTYPE, "%s: `%s` has the wrong dtype", fn, name);
+  if (rank > 0 && t->rank != rank) return fail(LUX3D_ERR_SHAPE, "%s: `%s` must have rank %d", fn, name, rank);
+  if (!is_contiguous(t)) return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must be contiguous", fn, name);
+  return LUX3D_OK;
+}
+}  // namespace
+
+int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *keys, const lux3d_tensor_t *vals,
+                           const lux3d_tensor_t *nbr, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sparse_neighbors";
+  int r;
+  if ((r = contiguous_of(coords, fn, "coords", LUX3D_I32, 2)) || (r = contiguous_of(keys, fn, "keys", LUX3D_I64, -1)) ||
+      (r = contiguous_of(vals, fn, "vals", LUX3D_I32, -1)) || (r = contiguous_of(nbr, fn, "nbr", LUX3D_I32, 2)))
+    return r;
+  const int64_t n = coords->shape[0], cap = numel(keys);
+  if (coords->shape[1] != 3) return fail(LUX3D_ERR_SHAPE, "%s: coords must be [N, 3]", fn);
+  if (nbr->shape[0] != n || nbr->shape[1] != 27) return fail(LUX3D_ERR_SHAPE, "%s: nbr must be [%lld, 27]", fn,
+                                                              (long long)n);
+  if (numel(vals) != cap) return fail(LUX3D_ERR_SHAPE, "%s: keys and vals must have the same length", fn);
+  if (cap < 2 * n || cap <= 0 || (cap & (cap - 1)))
+    return fail(LUX3D_ERR_SHAPE, "%s: the table needs a power-of-two capacity >= 2 N = %lld (got %lld)", fn,
+                (long long)(2 * n), (long long)cap);
+  if (n > INT32_MAX / 27) return fail(LUX3D_ERR_SHAPE, "%s: too many voxels", fn);
+  return hip_status(launch_sparse_map(static_cast<const int32_t *>(coords->data), n,
+                                      static_cast<unsigned long long *>(keys->data), static_cast<int32_t *>(vals->data),
+                                      cap, static_cast<int32_t *>(nbr->data), stream_of(stream)),
+                    fn);
+}
+
+int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr, const lux3d_tensor_t *weight,
+                        const lux3d_tensor_t *bias, const lux3d_tensor_t *out, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sparse_conv3d";
+  int r;
+  if ((r = contiguous_of(x, fn, "x", LUX3D_F32, 2)) || (r = contiguous_of(nbr, fn, "nbr", LUX3D_I32, 2)) ||
+      (r = contiguous_of(weight, fn, "weight", LUX3D_F32, 3)) || (r = contiguous_of(out, fn, "out", LUX3D_F32, 2)))
+    return r;
+  const int64_t n = x->shape[0], cin = x->shape[1], cout = weight->shape[1];
+  if (nbr->shape[0] != n || nbr->shape[1] != 27) return fail(LUX3D_ERR_SHAPE, "%s: nbr must be [%lld, 27]", fn,
+                                                              (long long)n);
+  if (weight->shape[0] != 27 || weight->shape[2] != cin)
+    return fail(LUX3D_ERR_SHAPE, "SparseConv3d expects [N, %lld] with weight [27, Cout, %lld]", (long long)cin,
+                (long long)weight->shape[2]);
+  if (out->shape[0] != n || out->shape[1] != cout) return fail(LUX3D_ERR_SHAPE, "%s: out must be [%lld, %lld]", fn,
+                                                                (long long)n, (long long)cout);
+  const float *bp = nullptr;
+  if (bias) {
+    if ((r = contiguous_of(bias, fn, "bias", LUX3D_F32, -1))) return r;
+    if (numel(bias) != cout) return fail(LUX3D_ERR_SHAPE, "%s: bias must have %lld elements", fn, (long long)cout);
+    bp = static_cast<const float *>(bias->data);
+  }
+  SparseConvParams p;
+  p.x = static_cast<const float *>(x->data);
+  p.nbr = static_cast<const int32_t *>(nbr->data);
+  p.w = static_cast<const float *>(weight->data);
+  p.bias = bp;
+  p.out = static_cast<float *>(out->data);
+  p.n = n; p.cin = cin; p.cout = cout;
+  p.mfma = cin % 16 == 0 && cin > 0 && aligned16(x->data) && aligned16(weight->data);
+  return hip_status(launch_sparse_conv(p, stream_of(stream)), fn);
+}
+
+int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids, const lux3d_tensor_t *out,
+                            lux3d_stream_t stream) {
+  const char *fn = "lux3d_index_select_rows";
+  int r;
+  if ((r = contiguous_of(src, fn, "src", -1, -1)) || (r = contiguous_of(ids, fn, "ids", -1, 1)) ||
+      (r = contiguous_of(out, fn, "out", src->dtype, src->rank)))
+    return r;
+  if (ids->dtype != LUX3D_I32 && ids->dtype != LUX3D_I64)
+    return fail(LUX3D_ERR_DTYPE, "%s: ids must be int32 or int64", fn);
+  if (out->shape[0] != ids->shape[0]) return fail(LUX3D_ERR_SHAPE, "%s: out must have one row per id", fn);
+  int64_t row = 1;
+  for (int i = 1; i < src->rank; ++i) {
+    if (out->shape[i] != src->shape[i]) return fail(LUX3D_ERR_SHAPE, "%s: out rows must match src rows", fn);
+    row *= src->shape[i];
+  }
+  return hip_status(launch_gather_rows(src->data, src->shape[0], ids->data, ids->dtype == LUX3D_I64, ids->shape[0],
+                                       nullptr, out->data, row * elem_bytes(src->dtype), stream_of(stream)),
+                    fn);
+}
+
+int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t *feats, const lux3d_tensor_t *logits,
+                             const lux3d_tensor_t *workspace, const lux3d_tensor_t *out_coords,
+                             const lux3d_tensor_t *src_rows, const lux3d_tensor_t *out_feats,
+                             const lux3d_tensor_t *sub, const lux3d_tensor_t *count, lux3d_stream_t stream) {
+  const char *fn = "lux3d_channel_to_spatial";
+  int r;
+  if ((r = contiguous_of(coords, fn, "coords", LUX3D_I32, 2)) || (r = contiguous_of(feats, fn, "feats", -1, 2)) ||
+      (r = contiguous_of(logits, fn, "logits", -1, 2)) || (r = contiguous_of(workspace, fn, "workspace", LUX3D_I32, -1)) ||
+      (r = contiguous_of(out_coords, fn, "out_coords", LUX3D_I32, 2)) ||
+      (r = contiguous_of(src_rows, fn, "src_rows", LUX3D_I32, -1)) ||
+      (r = contiguous_of(out_feats, fn, "out_feats", feats->dtype, 2)) ||
+      (r = contiguous_of(count, fn, "count", LUX3D_I32, -1)))
+    return r;
+  const int64_t n = coords->shape[0], c = feats->shape[1];
+  if (coords->shape[1] != 3) return fail(LUX3D_ERR_SHAPE, "%s: coords must be [N, 3]", fn);
+  if (feats->shape[0] != n)
+    return fail(LUX3D_ERR_SHAPE, "channel_to_spatial coords/features mismatch: %lld coords vs %lld rows",
+                (long long)n, (long long)feats->shape[0]);
+  if (c % 8) return fail(LUX3D_ERR_SHAPE,
+                         "channel_to_spatial expects channels divisible by 8 (layout [child, channel]), got %lld",
+                         (long long)c);
+  if (!is_float(logits->dtype)) return fail(LUX3D_ERR_DTYPE, "%s: logits must be f32, bf16 or f16", fn);
+  if (logits->shape[0] != n || logits->shape[1] != 8)
+    return fail(LUX3D_ERR_SHAPE, "subdivision logits must be [%lld, 8], got [%lld, %lld]", (long long)n,
+                (long long)logits->shape[0], (long long)logits->shape[1]);
+  const int64_t nb = (n + 1023) / 1024;
+  if (numel(workspace) < n + nb)
+    return fail(LUX3D_ERR_SHAPE, "%s: workspace needs N + ceil(N / 1024) = %lld int32", fn, (long long)(n + nb));
+  if (out_coords->shape[0] != 8 * n || out_coords->shape[1] != 3 || numel(src_rows) != 8 * n ||
+      out_feats->shape[0] != 8 * n || out_feats->shape[1] != c / 8 || numel(count) != 1)
+    return fail(LUX3D_ERR_SHAPE, "%s: outputs must hold 8 N = %lld rows (out_feats [8 N, C / 8]) and count 1", fn,
+                (long long)(8 * n));
+  float *sp = nullptr;
+  if (sub) {
+    if ((r = contiguous_of(sub, fn, "sub", LUX3D_F32, -1))) return r;
+    if (numel(sub) != 8 * n) return fail(LUX3D_ERR_SHAPE, "%s: sub must be [N, 8]", fn);
+    sp = static_cast<float *>(sub->data);
+  }
+  if (n > INT32_MAX / 8) return fail(LUX3D_ERR_SHAPE, "%s: too many parents", fn);
+  C2SParams p;
+  p.coords = static_cast<const int32_t *>(coords->data);
+  p.feats = feats->data;
+  p.logits = logits->data;
+  p.logits_dt = logits->dtype;
+  p.n = n;
+  p.child_row_bytes = (c / 8) * elem_bytes(feats->dtype);
+  p.offs = static_cast<int32_t *>(workspace->data);
+  p.block_sums = p.offs + n;
+  p.out_coords = static_cast<int32_t *>(out_coords->data);
+  p.src_rows = static_cast<int32_t *>(src_rows->data);
+  p.count = static_cast<int32_t *>(count->data);
+  p.out_feats = out_feats->data;
+  p.sub = sp;
+  return hip_status(launch_c2s(p, stream_of(stream)), fn);
 }
 
 }  // extern "C"

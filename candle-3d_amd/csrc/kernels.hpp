@@ -127,4 +127,35 @@ struct AttnParams {
 };
 hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
 
+// TRELLIS.2 sparse voxel ops.
+// Coordinate hash (cap: a power of two >= 2n) and neighbour table nbr [n, 27].
+hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
+                             int32_t *nbr, hipStream_t s);
+struct SparseConvParams {
+  const float *x = nullptr;       // [n, cin]
+  const int32_t *nbr = nullptr;   // [n, 27]
+  const float *w = nullptr;       // [27, cout, cin]
+  const float *bias = nullptr;    // [cout] or null
+  float *out = nullptr;           // [n, cout]
+  int64_t n = 0, cin = 0, cout = 0;
+  bool mfma = false;              // cin % 16 == 0, 16-byte aligned x and w
+};
+hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s);
+// out[m] = src[ids[m]] for m < rows (and m < *count when count is given);
+// rows of row_bytes bytes; ids out of range give zero rows.
+hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bool ids64, int64_t rows,
+                              const int32_t *count, void *out, int64_t row_bytes, hipStream_t s);
+struct C2SParams {
+  const int32_t *coords = nullptr;  // [n, 3]
+  const void *feats = nullptr;      // [n, C], rows of 8 children x child_row_bytes
+  const void *logits = nullptr;     // [n, 8]
+  int logits_dt = 0;
+  int64_t n = 0, child_row_bytes = 0;
+  int32_t *offs = nullptr, *block_sums = nullptr;  // workspace [n], [ceil(n / 1024)]
+  int32_t *out_coords = nullptr, *src_rows = nullptr, *count = nullptr;  // [8n, 3], [8n], [1]
+  void *out_feats = nullptr;        // [8n, C / 8]
+  float *sub = nullptr;             // [n, 8] or null
+};
+hipError_t launch_c2s(const C2SParams &p, hipStream_t s);
+
 }  // namespace lux3d

@@ -1,0 +1,481 @@
+// sparse.hip -- TRELLIS.2 sparse voxel ops for gfx950 (runtime/trellis2_sparse.rs):
+// the coordinate map and neighbour table, the submanifold 3x3x3 sparse
+// convolution, row gathers and the channel-to-spatial (C2S) subdivision.
+//
+// Coordinate map: an open-addressing hash table in a caller workspace (keys
+// packed as 3 x 21-bit biased coordinates, linear probing, 64-bit
+// compare-and-swap inserts; a duplicate coordinate keeps the largest row,
+// which is the reference HashMap's "later insert overwrites"). The
+// neighbour table nbr[i][k] = row of coords[i] + delta(k) or -1, with
+// k = kd*9 + kh*3 + kw and delta = (kd-1, kh-1, kw-1).
+//
+// Sparse convolution, output-stationary: out[i, :] = bias + sum_k W_k
+// x[nbr[i][k], :] as ONE implicit GEMM [N, 27*Cin] x [27*Cin, Cout] whose A
+// rows are gathered through the neighbour table (missing neighbours load
+// zeros). The reference's 27 gather + GEMM + index_add passes become one
+// kernel, and every output element is written once: no scatter, no atomics,
+// a fixed summation order. f32 in, f32 accumulation on the matrix cores
+// (v_mfma_f32_32x32x2_f32), as the reference computes sparse features in F32.
+// Taps that no row of a tile uses are skipped.
+//
+// C2S: per parent the leaf mask (logits > 0) and its popcount, an exclusive
+// scan of the counts (block scans + one scan of the block totals), then one
+// thread per (parent, subidx) writes the child coordinate and source row in
+// the reference order (parent order, ascending subidx), and a row gather
+// copies the child features. The child count is written to device memory.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lux3d {
+
+namespace {
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr unsigned long long kEmptyKey = ~0ull;
+
+__device__ __forceinline__ unsigned long long pack_coord(int32_t x, int32_t y, int32_t z) {
+  return ((unsigned long long)(uint32_t)(x + (1 << 20)) << 42) | ((unsigned long long)(uint32_t)(y + (1 << 20)) << 21) |
+         (unsigned long long)(uint32_t)(z + (1 << 20));
+}
+__device__ __forceinline__ bool coord_ok(int32_t x, int32_t y, int32_t z) {
+  const int32_t lo = -(1 << 20), hi = (1 << 20) - 1;
+  return x >= lo && x < hi && y >= lo && y < hi && z >= lo && z < hi;
+}
+__device__ __forceinline__ uint64_t hash_key(unsigned long long k) {
+  uint64_t h = (uint64_t)k * 0x9E3779B97F4A7C15ull;
+  return h ^ (h >> 29);
+}
+
+__global__ __launch_bounds__(256) void map_clear_kernel(unsigned long long *keys, int32_t *vals, int64_t cap) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < cap) {
+    keys[i] = kEmptyKey;
+    vals[i] = -1;
+  }
+}
+
+__global__ __launch_bounds__(256) void map_insert_kernel(const int32_t *coords, int64_t n, unsigned long long *keys,
+                                                         int32_t *vals, int64_t cap) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
+  if (!coord_ok(x, y, z)) return;
+  const unsigned long long key = pack_coord(x, y, z);
+  uint64_t slot = hash_key(key) & (uint64_t)(cap - 1);
+  for (int64_t probe = 0; probe < cap; ++probe) {  // cap >= 2n: a free slot exists
+    const unsigned long long prev = atomicCAS(&keys[slot], kEmptyKey, key);
+    if (prev == kEmptyKey || prev == key) {
+      atomicMax(&vals[slot], (int32_t)i);
+      return;
+    }
+    slot = (slot + 1) & (uint64_t)(cap - 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void map_neighbors_kernel(const int32_t *coords, int64_t n,
+                                                            const unsigned long long *keys, const int32_t *vals,
+                                                            int64_t cap, int32_t *nbr) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n * 27) return;
+  const int64_t i = t / 27;
+  const int k = (int)(t % 27);
+  const int32_t x = coords[3 * i] + k / 9 - 1, y = coords[3 * i + 1] + (k % 9) / 3 - 1, z = coords[3 * i + 2] + k % 3 - 1;
+  int32_t found = -1;
+  if (coord_ok(x, y, z)) {
+    const unsigned long long key = pack_coord(x, y, z);
+    uint64_t slot = hash_key(key) & (uint64_t)(cap - 1);
+    for (int64_t probe = 0; probe < cap; ++probe) {
+      const unsigned long long kk = keys[slot];
+      if (kk == key) {
+        found = vals[slot];
+        break;
+      }
+      if (kk == kEmptyKey) break;
+      slot = (slot + 1) & (uint64_t)(cap - 1);
+    }
+  }
+  nbr[t] = found;
+}
+
+// ---- sparse convolution -------------------------------------------------------
+
+// A 256-thread workgroup computes BM rows x BN output channels; its 4
+// wavefronts (2 x 2) each own (BM/2) x (BN/2) as 32 x 32 f32 MFMA tiles. The
+// K loop runs over the used taps and Cin in steps of BK = 16.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams p) {
+  constexpr int BK = 16;
+  constexpr int ROW = BK + 1;  // floats per LDS row (odd: conflict-free column reads)
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int ACH = BM * BK / 4 / 256, BCH = BN * BK / 4 / 256;  // float4 per thread per step
+  static_assert(ACH >= 1 && BCH >= 1, "tile");
+  __shared__ float As[2][BM * ROW];
+  __shared__ float Bs[2][BN * ROW];
+  __shared__ int32_t nb[BM * 27];
+  __shared__ uint32_t tap_mask;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int64_t N = p.n, Cin = p.cin, Cout = p.cout;
+
+  if (t == 0) tap_mask = 0u;
+  __syncthreads();
+  uint32_t my_mask = 0;
+  for (int e = t; e < BM * 27; e += 256) {
+    const int r = e / 27, k = e % 27;
+    int32_t s = m0 + r < N ? p.nbr[(m0 + r) * 27 + k] : -1;
+    s = s < N ? s : -1;  // a table entry past the rows reads as a missing neighbour
+    nb[e] = s;
+    if (s >= 0) my_mask |= 1u << k;
+  }
+  if (my_mask) atomicOr(&tap_mask, my_mask);
+  __syncthreads();
+  const uint32_t mask = tap_mask;
+
+  // staging: A = gathered x rows, B = W[k] rows (output channels past Cout clamp)
+  int a_row[ACH], a_part[ACH], b_row[BCH], b_part[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = t + i * 256;
+    a_row[i] = c / (BK / 4);
+    a_part[i] = c % (BK / 4);
+  }
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int c = t + i * 256;
+    b_row[i] = c / (BK / 4);
+    b_part[i] = c % (BK / 4);
+  }
+  const int64_t csteps = Cin / BK;
+  float4 ra[ACH], rb[BCH];
+  auto load_step = [&](int k, int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int32_t s = nb[a_row[i] * 27 + k];
+      ra[i] = s >= 0 ? *reinterpret_cast<const float4 *>(p.x + (int64_t)s * Cin + c0 + a_part[i] * 4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      int64_t o = n0 + b_row[i];
+      o = o < Cout ? o : Cout - 1;
+      rb[i] = *reinterpret_cast<const float4 *>(p.w + ((int64_t)k * Cout + o) * Cin + c0 + b_part[i] * 4);
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      float *d = &As[buf][a_row[i] * ROW + a_part[i] * 4];
+      d[0] = ra[i].x; d[1] = ra[i].y; d[2] = ra[i].z; d[3] = ra[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      float *d = &Bs[buf][b_row[i] * ROW + b_part[i] * 4];
+      d[0] = rb[i].x; d[1] = rb[i].y; d[2] = rb[i].z; d[3] = rb[i].w;
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+
+  // the step sequence: used taps in order, Cin chunks inside each
+  const int ntaps = __builtin_popcount(mask);
+  const int64_t nsteps = (int64_t)ntaps * csteps;
+  auto step_at = [&](int64_t st, int &k, int64_t &c0) {
+    const int64_t ti = st / csteps;
+    c0 = (st % csteps) * BK;
+    uint32_t mm = mask;
+    for (int64_t q = 0; q < ti; ++q) mm &= mm - 1;  // drop the lowest ti set bits
+    k = __builtin_ctz(mm);
+  };
+  if (nsteps > 0) {
+    int k;
+    int64_t c0;
+    step_at(0, k, c0);
+    load_step(k, c0);
+    store_step(0);
+  }
+  lds_barrier();
+  const int lrow = lane & 31, lk = lane >> 5;
+  int cur_k;
+  int64_t cur_c0;
+  if (nsteps > 0) step_at(0, cur_k, cur_c0);
+  for (int64_t st = 0; st < nsteps; ++st) {
+    const int buf = (int)(st & 1);
+    int nk = cur_k;
+    int64_t nc0 = cur_c0 + BK;
+    if (nc0 >= Cin) {  // next used tap
+      nc0 = 0;
+      const uint32_t rest = mask & ~((2u << cur_k) - 1u);
+      nk = rest ? __builtin_ctz(rest) : cur_k;
+    }
+    if (st + 1 < nsteps) load_step(nk, nc0);
+#pragma unroll
+    for (int s2 = 0; s2 < BK / 2; ++s2) {
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = As[buf][(wm * (BM / 2) + i * 32 + lrow) * ROW + s2 * 2 + lk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = Bs[buf][(wn * (BN / 2) + j * 32 + lrow) * ROW + s2 * 2 + lk];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (st + 1 < nsteps) store_step(buf ^ 1);
+    lds_barrier();
+    cur_k = nk;
+    cur_c0 = nc0;
+  }
+
+  // C[8 * (e / 4) + 4 * (lane / 32) + e % 4][lane % 32]: rows are voxels, columns output channels
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+    if (col >= Cout) continue;
+    const float bias = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (row < N) p.out[row * Cout + col] = acc[i][j][e] + bias;
+      }
+  }
+}
+
+// Any Cin / Cout: one thread per output element, f32 sums in tap, channel order.
+__global__ __launch_bounds__(256) void sparse_conv_generic_kernel(SparseConvParams p) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= p.n * p.cout) return;
+  const int64_t i = t / p.cout, o = t % p.cout;
+  float acc = 0.f;
+  for (int k = 0; k < 27; ++k) {
+    const int32_t s = p.nbr[i * 27 + k];
+    if (s < 0 || s >= p.n) continue;
+    const float *xr = p.x + (int64_t)s * p.cin, *wr = p.w + ((int64_t)k * p.cout + o) * p.cin;
+    for (int64_t c = 0; c < p.cin; ++c) acc = __builtin_fmaf(wr[c], xr[c], acc);
+  }
+  p.out[t] = acc + (p.bias ? p.bias[o] : 0.f);
+}
+
+// ---- row gather -------------------------------------------------------------------
+
+// out[m, :] = src[ids[m], :] for m < rows (rows read from `count` when given);
+// ids out of range give zero rows. VEC: 16-byte aligned rows.
+template <typename IDX, bool VEC>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64_t nsrc, const IDX *ids, int64_t rows,
+                                                          const int32_t *count, char *out, int64_t row_bytes) {
+  const int64_t lim = count ? (int64_t)*count : rows;
+  const int64_t units = VEC ? row_bytes / 16 : row_bytes;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = t / units, u = t % units;
+  if (m >= lim || m >= rows) return;
+  const int64_t id = (int64_t)ids[m];
+  if (VEC) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (id >= 0 && id < nsrc) v = *reinterpret_cast<const uint4 *>(src + id * row_bytes + u * 16);
+    *reinterpret_cast<uint4 *>(out + m * row_bytes + u * 16) = v;
+  } else {
+    out[m * row_bytes + u] = (id >= 0 && id < nsrc) ? src[id * row_bytes + u] : 0;
+  }
+}
+
+// ---- C2S ----------------------------------------------------------------------------
+
+constexpr int kScanBlock = 1024;  // parents per scan block (256 threads x 4)
+
+template <typename T>
+__global__ __launch_bounds__(256) void c2s_count_kernel(const void *logits, int64_t n, float *sub, int32_t *offs,
+                                                        int32_t *block_sums) {
+  __shared__ int32_t wsum[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t p0 = (int64_t)blockIdx.x * kScanBlock + t * 4;
+  int32_t c[4];
+  int32_t tot = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t p = p0 + q;
+    int32_t cnt = 0;
+    if (p < n) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bool leaf = load1<T>(logits, p * 8 + s) > 0.f;
+        cnt += leaf;
+        if (sub) sub[p * 8 + s] = leaf ? 1.f : 0.f;
+      }
+    }
+    c[q] = cnt;
+    tot += cnt;
+  }
+  // exclusive scan of the thread totals inside the wave, then across waves
+  int32_t incl = tot;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  int32_t run = base + incl - tot;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (p0 + q < n) offs[p0 + q] = run;
+    run += c[q];
+  }
+  if (t == 255) block_sums[blockIdx.x] = base + incl;
+}
+
+// exclusive scan of the block totals in place (one workgroup); total -> count
+__global__ __launch_bounds__(256) void c2s_scan_kernel(int32_t *block_sums, int64_t nb, int32_t *count) {
+  __shared__ int32_t wsum[4];
+  __shared__ int32_t carry;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (t == 0) carry = 0;
+  __syncthreads();
+  for (int64_t b0 = 0; b0 < nb; b0 += 256) {
+    const int64_t b = b0 + t;
+    const int32_t v = b < nb ? block_sums[b] : 0;
+    int32_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t u = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += u;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int32_t base = carry;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    if (b < nb) block_sums[b] = base + incl - v;
+    __syncthreads();
+    if (t == 255) carry = base + incl;
+    __syncthreads();
+  }
+  if (t == 0) *count = carry;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void c2s_emit_kernel(const int32_t *coords, const void *logits, int64_t n,
+                                                       const int32_t *offs, const int32_t *block_sums,
+                                                       int32_t *out_coords, int32_t *src_rows) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n * 8) return;
+  const int64_t p = t / 8;
+  const int s = (int)(t % 8);
+  if (!(load1<T>(logits, t) > 0.f)) return;
+  int32_t before = 0;
+  for (int q = 0; q < s; ++q) before += load1<T>(logits, p * 8 + q) > 0.f;
+  const int64_t j = (int64_t)offs[p] + block_sums[p / kScanBlock] + before;
+  out_coords[3 * j] = coords[3 * p] * 2 + (s & 1);
+  out_coords[3 * j + 1] = coords[3 * p + 1] * 2 + ((s >> 1) & 1);
+  out_coords[3 * j + 2] = coords[3 * p + 2] * 2 + (s >> 2);
+  src_rows[j] = (int32_t)(p * 8 + s);
+}
+
+unsigned grid_of(int64_t threads) { return (unsigned)((threads + 255) / 256); }
+
+}  // namespace
+
+hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
+                             int32_t *nbr, hipStream_t s) {
+  if (cap <= 0 || (cap & (cap - 1)) || cap < 2 * n) return hipErrorInvalidValue;
+  if (grid_of(cap) == 0 || (cap + 255) / 256 > INT32_MAX || (n * 27 + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(map_clear_kernel, dim3(grid_of(cap)), dim3(256), 0, s, keys, vals, cap);
+  if (n == 0) return hipGetLastError();
+  hipLaunchKernelGGL(map_insert_kernel, dim3(grid_of(n)), dim3(256), 0, s, coords, n, keys, vals, cap);
+  hipLaunchKernelGGL(map_neighbors_kernel, dim3(grid_of(n * 27)), dim3(256), 0, s, coords, n, keys, vals, cap, nbr);
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s) {
+  if (p.n <= 0 || p.cout <= 0) return hipSuccess;
+  if (p.mfma) {
+    const int64_t gy = (p.n + 63) / 64;
+    if (gy > 65535) {
+      if ((p.n + 127) / 128 > 65535) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((sparse_conv_mfma_kernel<128, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)((p.n + 127) / 128)),
+                         dim3(256), 0, s, p);
+      return hipGetLastError();
+    }
+    hipLaunchKernelGGL((sparse_conv_mfma_kernel<64, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)gy), dim3(256), 0,
+                       s, p);
+    return hipGetLastError();
+  }
+  if ((p.n * p.cout + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sparse_conv_generic_kernel, dim3(grid_of(p.n * p.cout)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bool ids64, int64_t rows,
+                              const int32_t *count, void *out, int64_t row_bytes, hipStream_t s) {
+  if (rows <= 0 || row_bytes <= 0) return hipSuccess;
+  const bool vec = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const int64_t units = vec ? row_bytes / 16 : row_bytes;
+  if ((rows * units + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid(grid_of(rows * units)), block(256);
+  const char *sp = static_cast<const char *>(src);
+  char *op = static_cast<char *>(out);
+  if (ids64) {
+    if (vec) hipLaunchKernelGGL((gather_rows_kernel<int64_t, true>), grid, block, 0, s, sp, nsrc,
+                                static_cast<const int64_t *>(ids), rows, count, op, row_bytes);
+    else hipLaunchKernelGGL((gather_rows_kernel<int64_t, false>), grid, block, 0, s, sp, nsrc,
+                            static_cast<const int64_t *>(ids), rows, count, op, row_bytes);
+  } else {
+    if (vec) hipLaunchKernelGGL((gather_rows_kernel<int32_t, true>), grid, block, 0, s, sp, nsrc,
+                                static_cast<const int32_t *>(ids), rows, count, op, row_bytes);
+    else hipLaunchKernelGGL((gather_rows_kernel<int32_t, false>), grid, block, 0, s, sp, nsrc,
+                            static_cast<const int32_t *>(ids), rows, count, op, row_bytes);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_c2s(const C2SParams &p, hipStream_t s) {
+  const int64_t nb = (p.n + kScanBlock - 1) / kScanBlock;
+  if (p.n < 0 || (p.n * 8 + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  if (p.n == 0) {
+    hipLaunchKernelGGL(c2s_scan_kernel, dim3(1), dim3(256), 0, s, p.block_sums, (int64_t)0, p.count);
+    return hipGetLastError();
+  }
+  switch (p.logits_dt) {
+    case LUX3D_F32:
+      hipLaunchKernelGGL((c2s_count_kernel<F32>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
+                         p.block_sums);
+      break;
+    case LUX3D_BF16:
+      hipLaunchKernelGGL((c2s_count_kernel<BF16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
+                         p.block_sums);
+      break;
+    case LUX3D_F16:
+      hipLaunchKernelGGL((c2s_count_kernel<F16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
+                         p.block_sums);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(c2s_scan_kernel, dim3(1), dim3(256), 0, s, p.block_sums, nb, p.count);
+  switch (p.logits_dt) {
+    case LUX3D_F32:
+      hipLaunchKernelGGL((c2s_emit_kernel<F32>), dim3(grid_of(p.n * 8)), dim3(256), 0, s, p.coords, p.logits, p.n,
+                         p.offs, p.block_sums, p.out_coords, p.src_rows);
+      break;
+    case LUX3D_BF16:
+      hipLaunchKernelGGL((c2s_emit_kernel<BF16>), dim3(grid_of(p.n * 8)), dim3(256), 0, s, p.coords, p.logits, p.n,
+                         p.offs, p.block_sums, p.out_coords, p.src_rows);
+      break;
+    default:
+      hipLaunchKernelGGL((c2s_emit_kernel<F16>), dim3(grid_of(p.n * 8)), dim3(256), 0, s, p.coords, p.logits, p.n,
+                         p.offs, p.block_sums, p.out_coords, p.src_rows);
+      break;
+  }
+  // child features: rows src_rows[j] of feats viewed as [n * 8, C / 8]
+  return launch_gather_rows(p.feats, p.n * 8, p.src_rows, false, p.n * 8, p.count, p.out_feats, p.child_row_bytes, s);
+}
+
+}  // namespace lux3d

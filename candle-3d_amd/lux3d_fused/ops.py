@@ -397,3 +397,72 @@ def exact_query_chunked_sdpa(q, k, v, scale: float, chunk_size: int = 0) -> torc
 def exact_sdpa_heads(q, k, v, scale: float) -> torch.Tensor:
     """attention_math.rs:244-259 (f32 arithmetic, output in q's dtype)."""
     return sdpa(q, k, v, scale)
+
+
+# ---------------------------------------------------------------------------
+# TRELLIS.2 sparse voxel ops (runtime/trellis2_sparse.rs)
+# ---------------------------------------------------------------------------
+
+def kernel_offset_delta(k: int):
+    """trellis2_sparse.rs:83-91: k = kd*9 + kh*3 + kw -> (kd-1, kh-1, kw-1)."""
+    return (k // 9 - 1, (k % 9) // 3 - 1, k % 3 - 1)
+
+
+def sparse_neighbors(coords: torch.Tensor) -> torch.Tensor:
+    """CoordMap + per-offset lookups on the device: coords int32 [N, 3] ->
+    nbr int32 [N, 27] (-1: missing)."""
+    n = coords.shape[0]
+    cap = 16
+    while cap < 2 * n:
+        cap *= 2
+    keys = torch.empty(cap, dtype=torch.int64, device=coords.device)
+    vals = torch.empty(cap, dtype=torch.int32, device=coords.device)
+    nbr = torch.empty((n, 27), dtype=torch.int32, device=coords.device)
+    _lib.call("lux3d_sparse_neighbors", desc(coords), desc(keys), desc(vals), desc(nbr), _stream(coords))
+    return nbr
+
+
+class SparseConv3d:
+    """Submanifold 3x3x3 sparse convolution (trellis2_sparse.rs:135-243).
+    `weight` is the checkpoint's flex_gemm layout [Cout, 3, 3, 3, Cin] (or
+    its flattened GGUF form); it is transposed once to [27, Cout, Cin] f32."""
+
+    def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor], in_channels: int, out_channels: int):
+        w = weight.reshape(out_channels, 27, in_channels).to(torch.float32)
+        self.weight27 = w.permute(1, 0, 2).contiguous()
+        self.bias = None if bias is None else bias.to(torch.float32).contiguous()
+        self.in_channels, self.out_channels = in_channels, out_channels
+
+    def forward(self, coords_or_nbr: torch.Tensor, feats: torch.Tensor) -> torch.Tensor:
+        """coords int32 [N, 3] (the neighbour table is built) or a prebuilt
+        nbr int32 [N, 27]; feats f32 [N, Cin] -> [N, Cout] f32."""
+        nbr = coords_or_nbr if coords_or_nbr.shape[-1] == 27 else sparse_neighbors(coords_or_nbr)
+        out = torch.empty((feats.shape[0], self.out_channels), dtype=torch.float32, device=feats.device)
+        _lib.call("lux3d_sparse_conv3d", desc(feats), desc(nbr), desc(self.weight27), desc(self.bias), desc(out),
+                  _stream(feats))
+        return out
+
+
+def index_select_rows(feats: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """index_select_rows (trellis2_sparse.rs:117-131): feats[ids] along dim 0."""
+    out = torch.empty((ids.shape[0],) + tuple(feats.shape[1:]), dtype=feats.dtype, device=feats.device)
+    _lib.call("lux3d_index_select_rows", desc(feats), desc(ids), desc(out), _stream(feats))
+    return out
+
+
+def channel_to_spatial(coords: torch.Tensor, feats: torch.Tensor, subdiv_logits: torch.Tensor):
+    """channel_to_spatial (trellis2_sparse.rs:269-338) on the device. Returns
+    (child coords int32 [M, 3], child feats [M, C/8], sub_binary f32 [N, 8])
+    after one stream sync to read M."""
+    n, c = feats.shape
+    dev = feats.device
+    ws = torch.empty(n + (n + 1023) // 1024, dtype=torch.int32, device=dev)
+    oc = torch.empty((8 * n, 3), dtype=torch.int32, device=dev)
+    src = torch.empty(8 * n, dtype=torch.int32, device=dev)
+    of = torch.empty((8 * n, c // 8), dtype=feats.dtype, device=dev)
+    sub = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("lux3d_channel_to_spatial", desc(coords), desc(feats), desc(subdiv_logits), desc(ws), desc(oc),
+              desc(src), desc(of), desc(sub), desc(cnt), _stream(feats))
+    m = int(cnt.item())
+    return oc[:m], of[:m], sub

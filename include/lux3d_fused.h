@@ -303,6 +303,54 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
                       const lux3d_tensor_t *scales, const lux3d_tensor_t *bias,
                       const lux3d_tensor_t *y, lux3d_stream_t stream);
 
+/* ---- TRELLIS.2 sparse voxel ops (runtime/trellis2_sparse.rs) ----------------
+ * lux3d_sparse_neighbors: CoordMap::new + the per-offset lookups of
+ * SparseConv3d::forward (trellis2_sparse.rs:62-91, 205-222), on the device.
+ *   coords: int32 [N, 3] contiguous (x, y, z), each within (-2^20, 2^20 - 1);
+ *   keys: int64 [cap], vals: int32 [cap] -- a workspace, cap a power of two
+ *         >= 2 N (the hash table; cleared here);
+ *   nbr: int32 [N, 27] out: nbr[i][k] = row of coords[i] + (kd-1, kh-1, kw-1),
+ *        k = kd*9 + kh*3 + kw, or -1. A repeated coordinate maps to its last
+ *        row (HashMap::insert overwrites).
+ *
+ * lux3d_sparse_conv3d: SparseConv3d::forward (trellis2_sparse.rs:197-243),
+ * submanifold 3x3x3, output rows = input rows:
+ *   out[i, o] = bias[o] + sum_k sum_c W[k][o][c] * x[nbr[i][k], c]
+ *   x: f32 [N, Cin], nbr: int32 [N, 27] (from lux3d_sparse_neighbors),
+ *   weight: f32 [27, Cout, Cin] (the loader's transposed kernel, weight27),
+ *   bias: f32 [Cout] or NULL, out: f32 [N, Cout]; all contiguous.
+ * One output-stationary implicit GEMM on the matrix cores (f32 MFMA) when
+ * Cin % 16 == 0 and x, weight are 16-byte aligned; otherwise a generic
+ * kernel. f32 accumulation; no scatter.
+ *
+ * lux3d_index_select_rows: index_select_rows (trellis2_sparse.rs:117-131):
+ *   out[m, ...] = src[ids[m], ...]; src [R, ...] and out [M, ...] contiguous,
+ *   same dtype and row shape; ids int32 or int64 [M]. Ids outside [0, R)
+ *   give zero rows (no error: checking would need a device sync).
+ *
+ * lux3d_channel_to_spatial: channel_to_spatial (trellis2_sparse.rs:269-338):
+ *   coords int32 [N, 3]; feats [N, C] (any dtype, C % 8 == 0, contiguous);
+ *   logits [N, 8] (f32 / bf16 / f16, contiguous; leaf = logits > 0);
+ *   workspace int32 [N + ceil(N / 1024)];
+ *   out: out_coords int32 [8N, 3], src_rows int32 [8N], out_feats [8N, C/8]
+ *   (feats' dtype), sub f32 [N, 8] (1 / 0; may be NULL), count int32 [1].
+ *   The first M = *count rows of the outputs hold the children in the
+ *   reference order (parent order, ascending subidx = dx + 2 dy + 4 dz); the
+ *   count stays in device memory (read it after a stream sync).            */
+int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *keys,
+                           const lux3d_tensor_t *vals, const lux3d_tensor_t *nbr,
+                           lux3d_stream_t stream);
+int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
+                        const lux3d_tensor_t *weight, const lux3d_tensor_t *bias,
+                        const lux3d_tensor_t *out, lux3d_stream_t stream);
+int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids,
+                            const lux3d_tensor_t *out, lux3d_stream_t stream);
+int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t *feats,
+                             const lux3d_tensor_t *logits, const lux3d_tensor_t *workspace,
+                             const lux3d_tensor_t *out_coords, const lux3d_tensor_t *src_rows,
+                             const lux3d_tensor_t *out_feats, const lux3d_tensor_t *sub,
+                             const lux3d_tensor_t *count, lux3d_stream_t stream);
+
 /* ---- attention ------------------------------------------------------------
  * lux3d_sdpa: out = softmax(q k^T * scale) v, replacing
  * exact_query_chunked_sdpa (runtime/attention_math.rs:199-241; its

@@ -28,6 +28,13 @@
  *   or_dequant_q8_0          brute force over all int8 x f16 scale sweep
  *   or_q8_0_linear           numpy f64 matmul of the dequantized weight; identity
  *                            weight; tiny brute force (tests/test_oracle_pins.py)
+ *   or_sparse_neighbors      reference KATs (tests/trellis2_sparse.rs:67-93) + brute
+ *                            force over all pairs
+ *   or_sparse_conv3d         torch conv3d (f64) on the densified grid; the
+ *                            reference's identity / shift kernels
+ *                            (tests/trellis2_sparse.rs:164-237)
+ *   or_channel_to_spatial    reference KAT (tests/trellis2_sparse.rs:274-318) +
+ *                            S2C round trip
  *   or_sdpa                  scipy softmax + numpy f64 matmuls; closed forms
  *                            (identical keys -> mean of v, one key -> v, a
  *                            dominant key -> its v row); key-permutation
@@ -933,4 +940,129 @@ void or_sdpa(int in_dt, const void *q, const void *k, const void *v, int64_t BH,
              int64_t D, double scale, int out_dt, void *out, float *wabs) {
   sdpa_ctx c = {in_dt, out_dt, q, k, v, Lq, Lk, D, scale, out, wabs};
   parallel_rows(BH * Lq, sdpa_rows, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* TRELLIS.2 sparse ops (runtime/trellis2_sparse.rs)                        */
+/* ------------------------------------------------------------------------ */
+
+/* Open-addressing map (x, y, z) -> row; an insert of an existing key
+ * overwrites, as HashMap::insert in CoordMap::new (trellis2_sparse.rs:72-79). */
+typedef struct {
+  int64_t cap;
+  int64_t *keys;
+  int32_t *vals;
+} cmap_t;
+
+static int64_t cmap_key(int32_t x, int32_t y, int32_t z) {
+  return (((int64_t)x + (1 << 20)) << 42) | (((int64_t)y + (1 << 20)) << 21) | ((int64_t)z + (1 << 20));
+}
+static uint64_t cmap_hash(int64_t k) {
+  uint64_t h = (uint64_t)k * 0x9E3779B97F4A7C15ull;
+  return h ^ (h >> 29);
+}
+static int cmap_init(cmap_t *m, int64_t n) {
+  m->cap = 16;
+  while (m->cap < 2 * n) m->cap *= 2;
+  m->keys = (int64_t *)malloc(sizeof(int64_t) * (size_t)m->cap);
+  m->vals = (int32_t *)malloc(sizeof(int32_t) * (size_t)m->cap);
+  if (!m->keys || !m->vals) return 0;
+  for (int64_t i = 0; i < m->cap; ++i) m->keys[i] = -1;
+  return 1;
+}
+static void cmap_free(cmap_t *m) { free(m->keys); free(m->vals); }
+static void cmap_put(cmap_t *m, int64_t k, int32_t v) {
+  uint64_t s = cmap_hash(k) & (uint64_t)(m->cap - 1);
+  while (m->keys[s] != -1 && m->keys[s] != k) s = (s + 1) & (uint64_t)(m->cap - 1);
+  m->keys[s] = k;
+  m->vals[s] = v;
+}
+static int32_t cmap_get(const cmap_t *m, int64_t k) {
+  uint64_t s = cmap_hash(k) & (uint64_t)(m->cap - 1);
+  while (m->keys[s] != -1) {
+    if (m->keys[s] == k) return m->vals[s];
+    s = (s + 1) & (uint64_t)(m->cap - 1);
+  }
+  return -1;
+}
+
+/* kernel_offset_delta (trellis2_sparse.rs:83-91): k = kd*9 + kh*3 + kw. */
+static void offset_delta(int k, int32_t d[3]) {
+  d[0] = k / 9 - 1;
+  d[1] = (k % 9) / 3 - 1;
+  d[2] = k % 3 - 1;
+}
+
+void or_sparse_neighbors(const int32_t *coords, int64_t n, int32_t *nbr) {
+  cmap_t m;
+  if (!cmap_init(&m, n)) return;
+  for (int64_t i = 0; i < n; ++i) cmap_put(&m, cmap_key(coords[3 * i], coords[3 * i + 1], coords[3 * i + 2]), (int32_t)i);
+  for (int64_t i = 0; i < n; ++i)
+    for (int k = 0; k < 27; ++k) {
+      int32_t d[3];
+      offset_delta(k, d);
+      nbr[i * 27 + k] = cmap_get(&m, cmap_key(coords[3 * i] + d[0], coords[3 * i + 1] + d[1], coords[3 * i + 2] + d[2]));
+    }
+  cmap_free(&m);
+}
+
+/* SparseConv3d::forward (trellis2_sparse.rs:197-243): out[i, o] = bias[o] +
+ * sum_k sum_c W[k][o][c] * x[nbr[i][k], c], missing neighbours contribute
+ * zero; W is the [27, Cout, Cin] kernel. Sums in double, one rounding to f32;
+ * abs_sum (optional) receives sum |W x|. */
+typedef struct {
+  const float *x, *w, *bias;
+  const int32_t *nbr;
+  int64_t cin, cout;
+  float *out, *abs_sum;
+} conv_ctx;
+
+static void conv_rows(const void *p, int64_t r0, int64_t r1) {
+  const conv_ctx *c = (const conv_ctx *)p;
+  for (int64_t i = r0; i < r1; ++i)
+    for (int64_t o = 0; o < c->cout; ++o) {
+      double acc = c->bias ? (double)c->bias[o] : 0.0, aacc = 0.0;
+      for (int k = 0; k < 27; ++k) {
+        const int32_t s = c->nbr[i * 27 + k];
+        if (s < 0) continue;
+        const float *xr = c->x + (int64_t)s * c->cin, *wr = c->w + ((int64_t)k * c->cout + o) * c->cin;
+        for (int64_t ch = 0; ch < c->cin; ++ch) {
+          const double pr = (double)wr[ch] * (double)xr[ch];
+          acc += pr;
+          aacc += fabs(pr);
+        }
+      }
+      c->out[i * c->cout + o] = (float)acc;
+      if (c->abs_sum) c->abs_sum[i * c->cout + o] = (float)aacc;
+    }
+}
+
+void or_sparse_conv3d(const float *x, int64_t n, int64_t cin, const int32_t *nbr, const float *w, const float *bias,
+                      int64_t cout, float *out, float *abs_sum) {
+  conv_ctx c = {x, w, bias, nbr, cin, cout, out, abs_sum};
+  parallel_rows(n, conv_rows, &c);
+}
+
+/* channel_to_spatial (trellis2_sparse.rs:269-338): leaf = logits > 0 per
+ * parent; children in parent order, ascending subidx = dx + 2 dy + 4 dz; child
+ * coord = 2 parent + (dx, dy, dz); child features = row parent * 8 + subidx of
+ * feats viewed as [N * 8, C / 8]. Returns the child count M; out_coords
+ * [M, 3], out_feats [M, C / 8], src_rows [M] (optional), sub [N, 8] (1 / 0). */
+int64_t or_channel_to_spatial(const int32_t *coords, int64_t n, const float *feats, int64_t c, const float *logits,
+                              int32_t *out_coords, float *out_feats, int32_t *src_rows, float *sub) {
+  const int64_t cc = c / 8;
+  int64_t m = 0;
+  for (int64_t p = 0; p < n; ++p)
+    for (int s = 0; s < 8; ++s) {
+      const int leaf = logits[p * 8 + s] > 0.0f;
+      if (sub) sub[p * 8 + s] = leaf ? 1.0f : 0.0f;
+      if (!leaf) continue;
+      out_coords[3 * m] = coords[3 * p] * 2 + (s % 2);
+      out_coords[3 * m + 1] = coords[3 * p + 1] * 2 + (s / 2) % 2;
+      out_coords[3 * m + 2] = coords[3 * p + 2] * 2 + s / 4;
+      memcpy(out_feats + m * cc, feats + (p * 8 + s) * cc, sizeof(float) * (size_t)cc);
+      if (src_rows) src_rows[m] = (int32_t)(p * 8 + s);
+      ++m;
+    }
+  return m;
 }

@@ -135,6 +135,17 @@ void or_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *o
 void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
                     const float *bias, int out_dt, void *y, float *abs_sum);
 
+/* ---- TRELLIS.2 sparse ops (runtime/trellis2_sparse.rs) --------------------- */
+/* CoordMap + kernel_offset_delta: nbr[i][k] = row of coords[i] + delta(k), or
+ * -1 (k = kd*9 + kh*3 + kw, delta = (kd-1, kh-1, kw-1)); coords [n, 3]. */
+void or_sparse_neighbors(const int32_t *coords, int64_t n, int32_t *nbr);
+/* SparseConv3d::forward with the [27, Cout, Cin] kernel (f64 sums). */
+void or_sparse_conv3d(const float *x, int64_t n, int64_t cin, const int32_t *nbr, const float *w, const float *bias,
+                      int64_t cout, float *out, float *abs_sum);
+/* channel_to_spatial; returns the child count. */
+int64_t or_channel_to_spatial(const int32_t *coords, int64_t n, const float *feats, int64_t c, const float *logits,
+                              int32_t *out_coords, float *out_feats, int32_t *src_rows, float *sub);
+
 /* Scaled dot-product attention, exact_sdpa_heads (attention_math.rs:244-259):
  * q [BH, Lq, D], k and v [BH, Lk, D] contiguous in in_dt; out [BH, Lq, D] in
  * out_dt = softmax(q k^T * scale) v, summed in double and rounded once.

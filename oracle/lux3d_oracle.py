@@ -51,6 +51,9 @@ _SIG = {
     "or_timestep_embedding_cos_first": ([_P, _I, _I, _P], None),
     "or_dequant_q8_0": ([_P, _I, ctypes.c_int, _P], None),
     "or_q8_0_linear": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
+    "or_sparse_neighbors": ([_P, _I, _P], None),
+    "or_sparse_conv3d": ([_P, _I, _I, _P, _P, _P, _I, _P, _P], None),
+    "or_channel_to_spatial": ([_P, _I, _P, _I, _P, _P, _P, _P, _P], ctypes.c_int64),
     "or_sdpa": ([ctypes.c_int, _P, _P, _P, _I, _I, _I, _I, ctypes.c_double, ctypes.c_int, _P, _P], None),
 }
 
@@ -334,3 +337,40 @@ def sdpa(q, k, v, scale, dt=None, out_dt=None, with_abs=False):
     a = np.empty(q.shape, dtype=np.float32) if with_abs else None
     LIB.or_sdpa(dt, _ptr(q), _ptr(k), _ptr(v), bh, lq, lk, d, float(scale), out_dt, _ptr(out), _ptr(a))
     return (out, a) if with_abs else out
+
+
+def sparse_neighbors(coords):
+    """coords int32 [N, 3] -> neighbour rows int32 [N, 27] (-1: missing)."""
+    coords = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 3)
+    nbr = np.empty((coords.shape[0], 27), dtype=np.int32)
+    LIB.or_sparse_neighbors(_ptr(coords), coords.shape[0], _ptr(nbr))
+    return nbr
+
+
+def sparse_conv3d(x, nbr, w27, bias=None, with_abs=False):
+    """x f32 [R, Cin], nbr [N, 27] (rows of x), w27 f32 [27, Cout, Cin] ->
+    f32 [N, Cout] (N may be a subset of the rows: the output rows follow nbr)."""
+    x = _f32(x)
+    cin = x.shape[1]
+    w27 = _f32(w27)
+    cout = w27.shape[1]
+    nbr = np.ascontiguousarray(nbr, dtype=np.int32)
+    n = nbr.shape[0]
+    out = np.empty((n, cout), dtype=np.float32)
+    a = np.empty((n, cout), dtype=np.float32) if with_abs else None
+    LIB.or_sparse_conv3d(_ptr(x), n, cin, _ptr(nbr), _ptr(w27), _ptr(_f32(bias)), cout, _ptr(out), _ptr(a))
+    return (out, a) if with_abs else out
+
+
+def channel_to_spatial(coords, feats, logits):
+    """Returns (child coords [M, 3], child feats [M, C/8], src rows [M], sub [N, 8])."""
+    coords = np.ascontiguousarray(coords, dtype=np.int32).reshape(-1, 3)
+    feats, logits = _f32(feats), _f32(logits)
+    n, c = feats.shape
+    oc = np.empty((8 * n, 3), dtype=np.int32)
+    of = np.empty((8 * n, c // 8), dtype=np.float32)
+    src = np.empty(8 * n, dtype=np.int32)
+    sub = np.empty((n, 8), dtype=np.float32)
+    m = LIB.or_channel_to_spatial(_ptr(coords), n, _ptr(feats), c, _ptr(logits), _ptr(oc), _ptr(of), _ptr(src),
+                                  _ptr(sub))
+    return oc[:m].copy(), of[:m].copy(), src[:m].copy(), sub

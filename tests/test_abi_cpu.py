@@ -250,3 +250,33 @@ def test_sdpa_argument_errors():
     assert rc == _lib.ERR_LAYOUT
     rc, msg = status("lux3d_sdpa", None, k, v, 0.125, o, None)
     assert rc == _lib.ERR_NULL
+
+
+def test_sparse_argument_errors():
+    co, nbr = T([100, 3], _lib.I32), T([100, 27], _lib.I32)
+    rc, msg = status("lux3d_sparse_neighbors", co, T([128], _lib.I64), T([128], _lib.I32), nbr, None)
+    assert rc == _lib.ERR_SHAPE and "power-of-two" in msg        # 128 < 2 N
+    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I64), T([255], _lib.I32), nbr, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I32), T([256], _lib.I32), nbr, None)
+    assert rc == _lib.ERR_DTYPE
+    x, w, out = T([100, 64], _lib.F32), T([27, 32, 64], _lib.F32), T([100, 32], _lib.F32)
+    rc, msg = status("lux3d_sparse_conv3d", x, nbr, T([27, 32, 48], _lib.F32), None, out, None)
+    assert rc == _lib.ERR_SHAPE and "SparseConv3d expects" in msg
+    rc, msg = status("lux3d_sparse_conv3d", T([100, 64]), nbr, w, None, out, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_sparse_conv3d", x, nbr, w, T([31], _lib.F32), out, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.F32), T([5, 4]), None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.I32), T([5, 3]), None)
+    assert rc == _lib.ERR_SHAPE
+    f, lg = T([100, 12], _lib.F32), T([100, 8], _lib.F32)
+    args = [T([108], _lib.I32), T([800, 3], _lib.I32), T([800], _lib.I32), T([800, 1], _lib.F32),
+            T([100, 8], _lib.F32), T([1], _lib.I32), None]
+    rc, msg = status("lux3d_channel_to_spatial", co, f, lg, *args)
+    assert rc == _lib.ERR_SHAPE and "divisible by 8" in msg
+    rc, msg = status("lux3d_channel_to_spatial", co, T([100, 16], _lib.F32), T([100, 7], _lib.F32),
+                     T([108], _lib.I32), T([800, 3], _lib.I32), T([800], _lib.I32), T([800, 2], _lib.F32),
+                     T([100, 8], _lib.F32), T([1], _lib.I32), None)
+    assert rc == _lib.ERR_SHAPE and "subdivision logits must be" in msg

@@ -593,3 +593,130 @@ def test_sdpa_bf16_inputs_round_once():
     want = p @ v64
     assert np.array_equal(got, to_bf16_bits(want))
     assert np.allclose(wabs, p @ np.abs(v64), rtol=1e-6)
+
+
+# ---- TRELLIS.2 sparse ops ---------------------------------------------------
+
+def _delta(k):
+    return np.array([k // 9 - 1, (k % 9) // 3 - 1, k % 3 - 1])
+
+
+def _grid_with_holes(res=4):
+    """The reference's 4^3 grid skipping every 5th row-major cell
+    (tests/trellis2_sparse.rs:72-85)."""
+    return np.array([[x, y, z] for x in range(res) for y in range(res) for z in range(res)
+                     if (x * res * res + y * res + z) % 5 != 0], dtype=np.int32)
+
+
+def test_sparse_neighbors_kats_and_brute_force():
+    # kernel_offset_delta KATs (tests/trellis2_sparse.rs:50-66) through a pair of voxels
+    for k, want in ((0, (-1, -1, -1)), (13, (0, 0, 0)), (26, (1, 1, 1)), (5, (-1, 0, 1))):
+        assert tuple(_delta(k)) == want
+        if k == 13:
+            continue
+        c = np.array([[5, 5, 5], [5 + want[0], 5 + want[1], 5 + want[2]]], dtype=np.int32)
+        nbr = orc.sparse_neighbors(c)
+        assert nbr[0, k] == 1 and nbr[0, 13] == 0 and nbr[1, 26 - k] == 0
+        assert (nbr[0] >= 0).sum() == 2
+    # CoordMap KAT (tests/trellis2_sparse.rs:67-77)
+    nbr = orc.sparse_neighbors(np.array([[0, 0, 0], [1, 0, 3], [7, 2, 5]]))
+    assert list(nbr[:, 13]) == [0, 1, 2] and (nbr >= 0).sum() == 3
+    # brute force over all pairs on the reference's grid with holes
+    coords = _grid_with_holes()
+    nbr = orc.sparse_neighbors(coords)
+    for i in range(len(coords)):
+        for k in range(27):
+            hit = np.nonzero((coords == coords[i] + _delta(k)).all(axis=1))[0]
+            assert nbr[i, k] == (hit[0] if hit.size else -1), (i, k)
+    # a later duplicate overwrites (HashMap::insert)
+    nbr = orc.sparse_neighbors(np.array([[2, 2, 2], [2, 2, 2]]))
+    assert list(nbr[:, 13]) == [1, 1]
+
+
+def _pattern(idx):
+    return ((np.asarray(idx) % 23).astype(np.float32) - np.float32(11.0)) * np.float32(0.1)
+
+
+def _dense_conv_torch(coords, x, w27, bias, res):
+    """F.conv3d (padding 1) in f64 on the densified grid, read at the active sites."""
+    import torch.nn.functional as F
+    cin, cout = x.shape[1], w27.shape[1]
+    dense = torch.zeros((1, cin, res, res, res), dtype=torch.float64)
+    for i, (a, b, c) in enumerate(coords):
+        dense[0, :, a, b, c] = torch.from_numpy(x[i].astype(np.float64))
+    wt = torch.from_numpy(w27.astype(np.float64)).reshape(3, 3, 3, cout, cin).permute(3, 4, 0, 1, 2)
+    bt = None if bias is None else torch.from_numpy(bias.astype(np.float64))
+    y = F.conv3d(dense, wt, bt, padding=1)[0]
+    return np.stack([y[:, a, b, c].numpy() for a, b, c in coords])
+
+
+def test_sparse_conv3d_matches_dense_conv3d():
+    # the reference's parity case (tests/trellis2_sparse.rs:67-162): 3 -> 5 channels
+    coords = _grid_with_holes()
+    cin, cout = 3, 5
+    x = np.array([[_pattern(i * 13 + c * 7) for c in range(cin)] for i in range(len(coords))], dtype=np.float32)
+    w27 = np.zeros((27, cout, cin), dtype=np.float32)
+    for o in range(cout):
+        for k in range(27):
+            for c in range(cin):
+                w27[k, o, c] = _pattern(o * 31 + k * 5 + c * 3) * np.float32(0.5)
+    bias = np.array([((o * 3) % 7) * 0.02 - 0.06 for o in range(cout)], dtype=np.float32)
+    got = orc.sparse_conv3d(x, orc.sparse_neighbors(coords), w27, bias)
+    want = _dense_conv_torch(coords, x, w27, bias, 4)
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+    # a larger random case
+    rng = np.random.default_rng(4)
+    res = 8
+    cells = rng.choice(res ** 3, 200, replace=False)
+    coords = np.stack([cells // 64, (cells // 8) % 8, cells % 8], axis=1).astype(np.int32)
+    x = rng.standard_normal((200, 16)).astype(np.float32)
+    w27 = rng.standard_normal((27, 8, 16)).astype(np.float32)
+    got = orc.sparse_conv3d(x, orc.sparse_neighbors(coords), w27, None)
+    want = _dense_conv_torch(coords, x, w27, None, res)
+    assert np.all(np.abs(got - want) <= 2.0 ** -23 * np.abs(want) + 1e-12)
+
+
+def test_sparse_conv3d_identity_and_shift_kernels():
+    """tests/trellis2_sparse.rs:164-237: the centre tap as identity returns x;
+    the +x tap (k = 22) returns the +x neighbour's features or zero."""
+    coords = np.array([[0, 0, 0], [1, 0, 0], [1, 1, 0], [3, 0, 0]], dtype=np.int32)
+    x = _pattern(np.arange(8)).reshape(4, 2)
+    nbr = orc.sparse_neighbors(coords)
+    w = np.zeros((27, 2, 2), dtype=np.float32)
+    w[13] = np.eye(2)
+    assert np.array_equal(orc.sparse_conv3d(x, nbr, w), x)
+    w = np.zeros((27, 2, 2), dtype=np.float32)
+    w[22] = np.eye(2)
+    want = np.stack([x[1], np.zeros(2), np.zeros(2), np.zeros(2)]).astype(np.float32)
+    assert np.array_equal(orc.sparse_conv3d(x, nbr, w), want)
+
+
+def test_channel_to_spatial_kat_and_round_trip():
+    # tests/trellis2_sparse.rs:274-318
+    coords = np.array([[0, 0, 0], [1, 0, 0], [0, 1, 1]], dtype=np.int32)
+    feats = (np.arange(48, dtype=np.float32) / 10.0).reshape(3, 16)
+    logits = -np.ones((3, 8), dtype=np.float32)
+    logits[0, [0, 3, 5]] = 1.0
+    logits[1, 1] = 1.0
+    oc, of, src, sub = orc.channel_to_spatial(coords, feats, logits)
+    assert oc.tolist() == [[0, 0, 0], [1, 1, 0], [1, 0, 1], [3, 0, 0]]
+    flat = feats.reshape(24, 2)
+    assert np.array_equal(of, flat[[0, 3, 5, 9]]) and src.tolist() == [0, 3, 5, 9]
+    assert sub[0, 0] == 1 and sub[0, 1] == 0 and sub.reshape(-1)[9] == 1 and sub.size == 24
+    # S2C (numpy, trellis2_sparse.rs:365-412) then C2S with the occupancy as logits returns the input
+    rng = np.random.default_rng(9)
+    cells = rng.choice(8 ** 3, 60, replace=False)
+    child = np.stack([cells // 64, (cells // 8) % 8, cells % 8], axis=1).astype(np.int32)
+    cf = rng.standard_normal((60, 4)).astype(np.float32)
+    parents = sorted({tuple(c // 2) for c in child})
+    pidx = {p: i for i, p in enumerate(parents)}
+    s2c = np.zeros((len(parents), 8 * 4), dtype=np.float32)
+    occ = -np.ones((len(parents), 8), dtype=np.float32)
+    for i, c in enumerate(child):
+        p, s = pidx[tuple(c // 2)], int(c[0] % 2 + 2 * (c[1] % 2) + 4 * (c[2] % 2))
+        s2c[p, s * 4:(s + 1) * 4] = cf[i]
+        occ[p, s] = 1.0
+    oc, of, _, _ = orc.channel_to_spatial(np.array(parents, dtype=np.int32), s2c, occ)
+    order = np.lexsort((child[:, 2], child[:, 1], child[:, 0]))
+    got = {tuple(c): tuple(f) for c, f in zip(oc, of)}
+    assert len(got) == 60 and all(got[tuple(child[i])] == tuple(cf[i]) for i in order)
