@@ -26,6 +26,7 @@ sys.path.insert(0, os.path.join(ROOT, "candle-3d_amd"))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, TFLOP/s
+PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 matrix peak, TFLOP/s
 METRIC = "fused-op achieved HBM GB/s (% of MI355X peak) + µs/op at VGGT/DiT shapes"
 
 
@@ -267,6 +268,7 @@ def main():
             del wl
             continue
         cfg, dtype, shape, sets, note, flops = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note, wl.flops
+        peak_tf = wl.peak_tflops or PEAK_BF16_TFLOPS
         us = step_ops.get(tag)
         if us is None:
             n = wl.reps or (200 if wl.bytes < 64 << 20 else 50)
@@ -283,7 +285,8 @@ def main():
                       "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
                       "rotation_sets": sets, **({"note": note} if note else {}),
                       **({"bound": "mfma", "tflops": round(flops / us / 1e6, 1),
-                          "frac_mfma_peak": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4)} if flops else {})})
+                          "mfma_peak_tflops": peak_tf,
+                          "frac_mfma_peak": round(flops / us / 1e6 / peak_tf, 4)} if flops else {})})
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -396,6 +396,14 @@ std::vector<uint16_t> Tensor::to_vec_u16() const {
   return v;
 }
 
+std::vector<int32_t> Tensor::to_vec_i32() const {
+  if (dtype_ != DType::I32) fail(LUX3D_ERR_DTYPE, "to_vec_i32: int32 tensor expected");
+  const std::vector<uint8_t> b = gather_bytes();
+  std::vector<int32_t> v(b.size() / 4);
+  std::memcpy(v.data(), b.data(), b.size());
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm family
 // ---------------------------------------------------------------------------
@@ -693,6 +701,107 @@ Tensor QMatMul::forward(const Tensor &xs, const std::optional<Tensor> &bias, DTy
   abi_check(lux3d_q8_0_linear(Desc(xs).p(), Desc(qs_).p(), Desc(scales_).p(), Desc(bias).p(), Desc(y).p(),
                               xs.device().stream()));
   return y;
+}
+
+// ---------------------------------------------------------------------------
+// TRELLIS.2 sparse ops
+// ---------------------------------------------------------------------------
+
+Coord kernel_offset_delta(size_t k) {
+  if (k >= 27) fail(LUX3D_ERR_VALUE, "kernel offset " + std::to_string(k) + " out of range");
+  return {(int32_t)(k / 9) - 1, (int32_t)((k % 9) / 3) - 1, (int32_t)(k % 3) - 1};
+}
+
+namespace {
+Tensor coords_tensor(const std::vector<Coord> &coords, const Device &dev) {
+  std::vector<int32_t> flat(coords.size() * 3);
+  for (size_t i = 0; i < coords.size(); ++i)
+    for (int a = 0; a < 3; ++a) flat[3 * i + a] = coords[i][a];
+  return Tensor::from_i32(flat, {(int64_t)coords.size(), 3}, dev);
+}
+}  // namespace
+
+Tensor sparse_neighbors(const std::vector<Coord> &coords, const Device &dev) {
+  const int64_t n = (int64_t)coords.size();
+  int64_t cap = 16;
+  while (cap < 2 * n) cap *= 2;
+  const Tensor keys = Tensor::empty({cap}, DType::I64, dev), vals = Tensor::empty({cap}, DType::I32, dev);
+  Tensor nbr = Tensor::empty({n, 27}, DType::I32, dev);
+  abi_check(lux3d_sparse_neighbors(Desc(coords_tensor(coords, dev)).p(), Desc(keys).p(), Desc(vals).p(), Desc(nbr).p(),
+                                   dev.stream()));
+  return nbr;
+}
+
+Tensor index_select_rows(const Tensor &feats, const Tensor &ids) {
+  Shape shape = feats.dims();
+  if (shape.empty()) fail(LUX3D_ERR_SHAPE, "index_select_rows: scalar input");
+  shape[0] = ids.elem_count();
+  Tensor out = Tensor::empty(shape, feats.dtype(), feats.device());
+  abi_check(lux3d_index_select_rows(Desc(feats).p(), Desc(ids).p(), Desc(out).p(), feats.device().stream()));
+  return out;
+}
+
+SparseConv3d SparseConv3d::load(const Tensor &weight, const std::optional<Tensor> &bias, int64_t in_channels,
+                                int64_t out_channels) {
+  if (weight.elem_count() != out_channels * 27 * in_channels)
+    fail(LUX3D_ERR_SHAPE, "SparseConv3d weight " + dims_str(weight.dims()) + " is not [" + std::to_string(out_channels) +
+                              ", 3, 3, 3, " + std::to_string(in_channels) + "]");
+  // [Cout, 27, Cin] -> [27, Cout, Cin] (load time, on the host)
+  const std::vector<float> w = weight.to_vec_f32();
+  std::vector<float> t(w.size());
+  for (int64_t o = 0; o < out_channels; ++o)
+    for (int64_t k = 0; k < 27; ++k)
+      std::memcpy(&t[(k * out_channels + o) * in_channels], &w[(o * 27 + k) * in_channels],
+                  sizeof(float) * (size_t)in_channels);
+  SparseConv3d c;
+  c.w27_ = Tensor::from_f32(t, {27, out_channels, in_channels}, DType::F32, weight.device());
+  if (bias) {
+    if (bias->elem_count() != out_channels) fail(LUX3D_ERR_SHAPE, "SparseConv3d bias must have Cout elements");
+    c.bias_ = Tensor::from_f32(bias->to_vec_f32(), {out_channels}, DType::F32, bias->device());
+  }
+  c.in_ = in_channels;
+  c.out_ = out_channels;
+  return c;
+}
+
+Tensor SparseConv3d::forward_nbr(const Tensor &nbr, const Tensor &feats) const {
+  Tensor out = Tensor::empty({feats.dim(0), out_}, DType::F32, feats.device());
+  abi_check(lux3d_sparse_conv3d(Desc(feats).p(), Desc(nbr).p(), Desc(w27_).p(), Desc(bias_).p(), Desc(out).p(),
+                                feats.device().stream()));
+  return out;
+}
+
+Tensor SparseConv3d::forward(const std::vector<Coord> &coords, const Tensor &feats) const {
+  if (feats.rank() != 2 || feats.dim(0) != (int64_t)coords.size() || feats.dim(1) != in_)
+    fail(LUX3D_ERR_SHAPE, "SparseConv3d expects [N, " + std::to_string(in_) + "] with N = " +
+                              std::to_string(coords.size()) + " coords, got " + dims_str(feats.dims()));
+  return forward_nbr(sparse_neighbors(coords, feats.device()), feats);
+}
+
+Channel2SpatialOutput channel_to_spatial(const std::vector<Coord> &coords, const Tensor &feats,
+                                         const Tensor &subdiv_logits) {
+  const Device &dev = feats.device();
+  const int64_t n = (int64_t)coords.size();
+  if (feats.rank() != 2 || feats.dim(0) != n)
+    fail(LUX3D_ERR_SHAPE, "channel_to_spatial coords/features mismatch: " + std::to_string(n) + " coords vs " +
+                              std::to_string(feats.rank() ? feats.dim(0) : 0) + " rows");
+  const int64_t c = feats.dim(1);
+  const Tensor ws = Tensor::empty({n + (n + 1023) / 1024}, DType::I32, dev);
+  const Tensor oc = Tensor::empty({8 * n, 3}, DType::I32, dev), src = Tensor::empty({8 * n}, DType::I32, dev);
+  const Tensor of = Tensor::empty({8 * n, c / 8}, feats.dtype(), dev);
+  Tensor sub = Tensor::empty({n, 8}, DType::F32, dev);
+  const Tensor cnt = Tensor::empty({1}, DType::I32, dev);
+  abi_check(lux3d_channel_to_spatial(Desc(coords_tensor(coords, dev)).p(), Desc(feats).p(), Desc(subdiv_logits).p(),
+                                     Desc(ws).p(), Desc(oc).p(), Desc(src).p(), Desc(of).p(), Desc(sub).p(),
+                                     Desc(cnt).p(), dev.stream()));
+  const int64_t m = cnt.to_vec_i32()[0];  // the host needs the child count (the reference's Vec length)
+  Channel2SpatialOutput r;
+  const std::vector<int32_t> flat = oc.to_vec_i32();
+  r.coords.resize((size_t)m);
+  for (int64_t j = 0; j < m; ++j) r.coords[(size_t)j] = {flat[3 * j], flat[3 * j + 1], flat[3 * j + 2]};
+  r.feats = of.narrow(0, 0, m);
+  r.sub_binary = sub;
+  return r;
 }
 
 // ---------------------------------------------------------------------------

@@ -104,6 +104,7 @@ class Tensor {
   // Device -> host in logical (row-major) order; synchronises the stream.
   std::vector<float> to_vec_f32() const;
   std::vector<uint16_t> to_vec_u16() const;  // raw bf16 / f16 bits
+  std::vector<int32_t> to_vec_i32() const;   // int32 tensors
 
   // The C ABI descriptor of this view.
   lux3d_tensor_t desc() const;
@@ -297,6 +298,51 @@ class QMatMul {
  private:
   Tensor qs_, scales_;
 };
+
+// ---------------------------------------------------------------------------
+// TRELLIS.2 sparse voxel ops (runtime/trellis2_sparse.rs). Coordinates are
+// host vectors as in the reference (Vec<[i32; 3]>); features live on the
+// device.
+// ---------------------------------------------------------------------------
+
+using Coord = std::array<int32_t, 3>;
+
+// kernel_offset_delta (trellis2_sparse.rs:83-91): k = kd*9 + kh*3 + kw
+Coord kernel_offset_delta(size_t k);
+// CoordMap + the per-offset lookups, on the device: nbr int32 [N, 27]
+Tensor sparse_neighbors(const std::vector<Coord> &coords, const Device &dev);
+// index_select_rows (trellis2_sparse.rs:117-131)
+Tensor index_select_rows(const Tensor &feats, const Tensor &ids);
+
+class SparseConv3d {
+ public:
+  // SparseConv3d::load (trellis2_sparse.rs:147-180): `weight` in the
+  // checkpoint's flex_gemm layout [Cout, 3, 3, 3, Cin] (or flattened), any
+  // float dtype; kept as weight27 [27, Cout, Cin] f32.
+  static SparseConv3d load(const Tensor &weight, const std::optional<Tensor> &bias, int64_t in_channels,
+                           int64_t out_channels);
+  int64_t in_channels() const { return in_; }
+  int64_t out_channels() const { return out_; }
+  const Tensor &weight27() const { return w27_; }
+  // forward (trellis2_sparse.rs:197-243): feats f32 [N, Cin] -> [N, Cout] f32
+  Tensor forward(const std::vector<Coord> &coords, const Tensor &feats) const;
+  // the same with a neighbour table already built for these coordinates
+  Tensor forward_nbr(const Tensor &nbr, const Tensor &feats) const;
+
+ private:
+  Tensor w27_;
+  std::optional<Tensor> bias_;
+  int64_t in_ = 0, out_ = 0;
+};
+
+// channel_to_spatial (trellis2_sparse.rs:249-338)
+struct Channel2SpatialOutput {
+  std::vector<Coord> coords;  // children: parent order, ascending subidx
+  Tensor feats;               // [M, C / 8]
+  Tensor sub_binary;          // [N, 8] f32
+};
+Channel2SpatialOutput channel_to_spatial(const std::vector<Coord> &coords, const Tensor &feats,
+                                         const Tensor &subdiv_logits);
 
 // ---------------------------------------------------------------------------
 // Weight files (lux3d_weights.h underneath): VarBuilder::from_gguf and

@@ -36,6 +36,7 @@ class Workload:
     ideal_note: str = ""
     flops: int = 0       # matrix-core work per launch (GEMMs); 0 for streaming ops
     reps: int = 0        # launches per timing graph (0: chosen from the byte count)
+    peak_tflops: float = 0.0  # matrix peak the flops are priced against (0: dense bf16)
 
 
 def _cur() -> int:
@@ -455,6 +456,81 @@ def cfg3_sdpa(dev) -> Workload:
     return _sdpa(dev, "sdpa", 3, 1, 40000, 12, 128, "TRELLIS.2 SLAT, the 40k-voxel batch element", reps=5)
 
 
+def _shell_coords(n, res, seed):
+    """~n unique voxels of a thick sphere shell in a res^3 grid, shuffled: the
+    surface-like sets TRELLIS.2's sparse VAE decodes."""
+    rng = np.random.default_rng(seed)
+    pts = rng.standard_normal((n * 4, 3))
+    pts = pts / np.linalg.norm(pts, axis=1, keepdims=True) * (res * 0.4 + rng.uniform(-2, 2, (n * 4, 1))) + res / 2
+    c = np.unique(np.clip(np.floor(pts), 0, res - 1).astype(np.int32), axis=0)
+    return c[rng.permutation(len(c))[:n]]
+
+
+def _sparse_conv(dev, name, n, ch, res, reps):
+    """SparseConv3d (trellis2_sparse.rs:197-243) on shell voxels: x f32
+    [N, C] -> [N, C], the ConvNeXt block conv of a decoder stage."""
+    from . import _lib
+    coords = torch.from_numpy(_shell_coords(n, res, 11)).to(dev)
+    n = coords.shape[0]
+    nbr = ops.sparse_neighbors(coords)
+    s = synth.config_seed(3) + 900
+    xs = [_normal(s + j, (n, ch), dev, torch.float32) for j in range(2)]
+    w27 = _normal(s + 5, (27, ch, ch), dev, torch.float32, 0.0, 1.0 / (27 * ch) ** 0.5)
+    bias = _normal(s + 6, (ch,), dev, torch.float32)
+    outs = [torch.empty((n, ch), dtype=torch.float32, device=dev) for _ in range(2)]
+    used = int((nbr >= 0).sum().item())
+    dx, do = [ops.desc(v) for v in xs], [ops.desc(v) for v in outs]
+    dn, dw, db = ops.desc(nbr), ops.desc(w27), ops.desc(bias)
+
+    def launch(i):
+        _lib.call("lux3d_sparse_conv3d", dx[i % 2], dn, dw, db, do[i % 2], _cur())
+    nbytes = n * ch * 4 * 2 + n * 27 * 4 + 27 * ch * ch * 4
+    wl = Workload(name, 3, "sparse_conv_mfma_kernel<64,64>", "f32 -> f32 acc (MFMA f32)", nbytes,
+                  f"{n} shell voxels in {res}^3, C {ch} -> {ch}, {used / n:.1f} active taps per voxel", launch, 2,
+                  flops=2 * used * ch * ch, reps=reps, peak_tflops=157.3)
+    wl._keep = (coords, nbr, xs, w27, bias, outs, dx, do, dn, dw, db)
+    return wl
+
+
+def cfg3_sparse_conv_c1024(dev) -> Workload:
+    # decoder stage 0 (1024 channels) at the SLAT resolution 64
+    return _sparse_conv(dev, "sparse_conv_c1024", 24000, 1024, 64, 5)
+
+
+def cfg3_sparse_conv_c256(dev) -> Workload:
+    # decoder stage 2 (256 channels) at resolution 256
+    return _sparse_conv(dev, "sparse_conv_c256", 150000, 256, 256, 10)
+
+
+def cfg3_c2s(dev) -> Workload:
+    """channel_to_spatial (trellis2_sparse.rs:269-338) after the stage-0 C2S
+    conv1 (1024 -> 8 x 512 channels, f32) on 24k parents, about half the
+    children kept. Algorithmic bytes: logits + coords read, the kept child
+    rows read and written, coords and rows written."""
+    from . import _lib
+    coords = torch.from_numpy(_shell_coords(24000, 64, 12)).to(dev)
+    n, c = coords.shape[0], 4096
+    s = synth.config_seed(3) + 950
+    feats = _normal(s, (n, c), dev, torch.float32)
+    logits = _normal(s + 1, (n, 8), dev, torch.float32)
+    ws = torch.empty(n + (n + 1023) // 1024, dtype=torch.int32, device=dev)
+    oc = torch.empty((8 * n, 3), dtype=torch.int32, device=dev)
+    src = torch.empty(8 * n, dtype=torch.int32, device=dev)
+    of = torch.empty((8 * n, c // 8), dtype=torch.float32, device=dev)
+    sub = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    d = [ops.desc(v) for v in (coords, feats, logits, ws, oc, src, of, sub, cnt)]
+    m = int((logits > 0).sum().item())
+
+    def launch(i):
+        _lib.call("lux3d_channel_to_spatial", *d, _cur())
+    nbytes = n * 8 * 4 * 2 + n * 12 + m * (c // 8) * 4 * 2 + m * 16
+    wl = Workload("c2s", 3, "c2s_count/scan/emit + gather_rows", "f32", nbytes,
+                  f"{n} parents x 8 children, C {c} ({m} children kept)", launch, 1, reps=50)
+    wl._keep = (coords, feats, logits, ws, oc, src, of, sub, cnt, d)
+    return wl
+
+
 TARGETS: List[Callable] = [
     cfg1_residual_layer_norm,
     cfg1_qk_layernorm_rope2d,
@@ -481,4 +557,7 @@ EXTRAS: List[Callable] = [
     cfg1_sdpa_global,
     cfg2_sdpa,
     cfg3_sdpa,
+    cfg3_sparse_conv_c1024,
+    cfg3_sparse_conv_c256,
+    cfg3_c2s,
 ]

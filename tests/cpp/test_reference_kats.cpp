@@ -352,6 +352,116 @@ void sparse_attention_matches_naive(const Device &dev) {
   }
 }
 
+// tests/trellis2_sparse.rs: kernel offsets, the coordinate map, the sparse
+// conv against a dense loop reference, identity / shift kernels, the loader
+// transpose and the C2S order.
+void kernel_offset_deltas_cover_the_3x3x3_kernel(const Device &) {
+  CHECK((kernel_offset_delta(0) == Coord{-1, -1, -1}));
+  CHECK((kernel_offset_delta(13) == Coord{0, 0, 0}));
+  CHECK((kernel_offset_delta(26) == Coord{1, 1, 1}));
+  CHECK((kernel_offset_delta(5) == Coord{-1, 0, 1}));
+  for (size_t k = 0; k < 27; ++k) {
+    const Coord d = kernel_offset_delta(k);
+    CHECK((size_t)((d[0] + 1) * 9 + (d[1] + 1) * 3 + (d[2] + 1)) == k);
+  }
+}
+
+void coord_map_builds_and_looks_up(const Device &dev) {
+  const std::vector<Coord> coords = {{0, 0, 0}, {1, 0, 3}, {7, 2, 5}};
+  const std::vector<int32_t> nbr = sparse_neighbors(coords, dev).to_vec_i32();
+  for (int i = 0; i < 3; ++i) CHECK(nbr[i * 27 + 13] == i);
+  int found = 0;
+  for (int32_t v : nbr) found += v >= 0;
+  CHECK(found == 3);
+}
+
+std::vector<Coord> grid_with_holes() {
+  std::vector<Coord> c;
+  for (int x = 0; x < 4; ++x)
+    for (int y = 0; y < 4; ++y)
+      for (int z = 0; z < 4; ++z)
+        if ((x * 16 + y * 4 + z) % 5 != 0) c.push_back({x, y, z});
+  return c;
+}
+
+void sparse_conv_matches_dense_reference(const Device &dev) {
+  const size_t CIN = 3, COUT = 5;
+  const std::vector<Coord> coords = grid_with_holes();
+  CHECK(coords.size() == 64 - 13);
+  std::vector<float> feats(coords.size() * CIN), ck(COUT * 27 * CIN), bias(COUT);
+  for (size_t i = 0; i < coords.size(); ++i)
+    for (size_t c = 0; c < CIN; ++c) feats[i * CIN + c] = pattern_f32(i * 13 + c * 7);
+  for (size_t o = 0; o < COUT; ++o)
+    for (size_t k = 0; k < 27; ++k)
+      for (size_t c = 0; c < CIN; ++c) ck[(o * 27 + k) * CIN + c] = pattern_f32(o * 31 + k * 5 + c * 3) * 0.5f;
+  for (size_t o = 0; o < COUT; ++o) bias[o] = (float)((o * 3) % 7) * 0.02f - 0.06f;
+  const SparseConv3d conv = SparseConv3d::load(Tensor::from_f32(ck, {(int64_t)COUT, 3, 3, 3, (int64_t)CIN}, DType::F32, dev),
+                                               Tensor::from_f32(bias, {(int64_t)COUT}, DType::F32, dev), CIN, COUT);
+  const std::vector<float> out =
+      conv.forward(coords, Tensor::from_f32(feats, {(int64_t)coords.size(), (int64_t)CIN}, DType::F32, dev)).to_vec_f32();
+  float md = 0.f;
+  for (size_t i = 0; i < coords.size(); ++i)
+    for (size_t o = 0; o < COUT; ++o) {
+      float acc = bias[o];
+      for (size_t k = 0; k < 27; ++k) {
+        const Coord d = kernel_offset_delta(k);
+        for (size_t j = 0; j < coords.size(); ++j)
+          if (coords[j][0] == coords[i][0] + d[0] && coords[j][1] == coords[i][1] + d[1] &&
+              coords[j][2] == coords[i][2] + d[2])
+            for (size_t c = 0; c < CIN; ++c) acc += ck[(o * 27 + k) * CIN + c] * feats[j * CIN + c];
+      }
+      md = std::max(md, std::fabs(out[i * COUT + o] - acc));
+    }
+  CHECK(md < 1e-4f);
+}
+
+void sparse_conv_hand_picked_kernels(const Device &dev) {
+  const std::vector<Coord> coords = {{0, 0, 0}, {1, 0, 0}, {1, 1, 0}, {3, 0, 0}};
+  std::vector<float> x(8);
+  for (size_t i = 0; i < 8; ++i) x[i] = pattern_f32(i);
+  const Tensor feats = Tensor::from_f32(x, {4, 2}, DType::F32, dev);
+  for (int k : {13, 22}) {
+    std::vector<float> w(2 * 27 * 2, 0.f);
+    for (int c = 0; c < 2; ++c) w[(c * 27 + k) * 2 + c] = 1.f;
+    const SparseConv3d conv = SparseConv3d::load(Tensor::from_f32(w, {2, 3, 3, 3, 2}, DType::F32, dev), std::nullopt, 2, 2);
+    const std::vector<float> out = conv.forward(coords, feats).to_vec_f32();
+    for (int i = 0; i < 4; ++i)
+      for (int c = 0; c < 2; ++c) {
+        const float want = k == 13 ? x[i * 2 + c] : (i == 0 ? x[2 + c] : 0.f);  // +x neighbour of row 0 is row 1
+        CHECK(std::fabs(out[i * 2 + c] - want) < 1e-6f);
+      }
+  }
+}
+
+void sparse_conv_loader_transposes_flex_gemm_layout(const Device &dev) {
+  const int CIN = 2, COUT = 3;
+  std::vector<float> v(COUT * 27 * CIN);
+  for (size_t i = 0; i < v.size(); ++i) v[i] = ((float)i + 1.0f) / 100.0f;
+  const SparseConv3d conv = SparseConv3d::load(Tensor::from_f32(v, {COUT, 3, 3, 3, CIN}, DType::F32, dev), std::nullopt, CIN, COUT);
+  const std::vector<float> w27 = conv.weight27().to_vec_f32();
+  for (int k = 0; k < 27; ++k)
+    for (int o = 0; o < COUT; ++o)
+      for (int c = 0; c < CIN; ++c) CHECK(w27[(k * COUT + o) * CIN + c] == v[(o * 27 + k) * CIN + c]);
+}
+
+void c2s_order_and_feature_selection(const Device &dev) {
+  const std::vector<Coord> coords = {{0, 0, 0}, {1, 0, 0}, {0, 1, 1}};
+  std::vector<float> f(48), lg(24, -1.f);
+  for (int i = 0; i < 48; ++i) f[i] = (float)i / 10.0f;
+  lg[0] = lg[3] = lg[5] = 1.f;  // parent 0: children 0, 3, 5
+  lg[8 + 1] = 1.f;              // parent 1: child 1
+  const Channel2SpatialOutput out = channel_to_spatial(coords, Tensor::from_f32(f, {3, 16}, DType::F32, dev),
+                                                       Tensor::from_f32(lg, {3, 8}, DType::F32, dev));
+  CHECK((out.coords == std::vector<Coord>{{0, 0, 0}, {1, 1, 0}, {1, 0, 1}, {3, 0, 0}}));
+  const std::vector<float> sel = out.feats.to_vec_f32();
+  const int rows[4] = {0, 3, 5, 9};
+  CHECK(sel.size() == 8);
+  for (int r = 0; r < 4; ++r)
+    for (int c = 0; c < 2; ++c) CHECK(sel[r * 2 + c] == f[rows[r] * 2 + c]);
+  const std::vector<float> sub = out.sub_binary.to_vec_f32();
+  CHECK(sub.size() == 24 && sub[0] == 1.f && sub[1] == 0.f && sub[9] == 1.f);
+}
+
 // A GGUF container as the reference's quantizer lays it out
 // (tests/golden/tiny_q8.gguf, written by tests/golden/make_gguf.py): the Q8_0
 // weight becomes a QMatMul (VarBuilder::get_quantized + QMatMul::from_qtensor,
@@ -461,6 +571,12 @@ int main(int argc, char **argv) {
       {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
       {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
       {"gguf_q8_linear_from_file", gguf_q8_linear_from_file, true},
+      {"kernel_offset_deltas_cover_the_3x3x3_kernel", kernel_offset_deltas_cover_the_3x3x3_kernel, false},
+      {"coord_map_builds_and_looks_up", coord_map_builds_and_looks_up, true},
+      {"sparse_conv_matches_dense_reference", sparse_conv_matches_dense_reference, true},
+      {"sparse_conv_hand_picked_kernels", sparse_conv_hand_picked_kernels, true},
+      {"sparse_conv_loader_transposes_flex_gemm_layout", sparse_conv_loader_transposes_flex_gemm_layout, true},
+      {"c2s_order_and_feature_selection", c2s_order_and_feature_selection, true},
       {"errors_on_device", errors_on_device, true},
   };
   Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed
