@@ -19,7 +19,9 @@
 // workgroup stages x[BM x BK] and the dequantised W[BN x BK] as bf16 in LDS
 // (double-buffered, rows padded by 16 bytes against bank conflicts); the
 // next k-step's global loads are issued before the current step's MFMAs, so
-// one barrier per k-step suffices.
+// one barrier per k-step suffices. Global loads go through the caches: every
+// x tile is read by each column block and every weight tile by each row
+// block, so L2 and the Infinity Cache serve most of them.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -103,10 +105,10 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
   auto load_step = [&](int64_t kt) {
     const int64_t k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) ra[i] = ld16(xbase + a_off[i] + k0 * 2);
+    for (int i = 0; i < A_CHUNKS; ++i) ra[i] = ld16<false>(xbase + a_off[i] + k0 * 2);
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i) {
-      rb[i] = ld16(p.qs + b_row[i] * p.K + k0 + b_part[i] * 16);
+      rb[i] = ld16<false>(p.qs + b_row[i] * p.K + k0 + b_part[i] * 16);
       rd[i] = p.scales[b_row[i] * nblk + k0 / 32 + b_part[i] / 2];
     }
   };
@@ -188,23 +190,21 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
 }
 
 // Tile choice (measured on MI355X, TFLOP/s at 1029x1024x4096 /
-// 4096x2048x8192): 256x128 with k-step 64 is fastest once there are >= 512
-// workgroups (529 at the larger shape; 128 x 128: 510); below that
-// 128x128 with k-step 64 (312 at the configs[4] shape; 64 x 128: 247).
+// 4096x2048x8192): 128x128 tiles with 64-deep k-steps, cached global loads
+// (each x tile is read by every column block, each weight tile by every row
+// block) and two wavefronts per SIMD: 321 / 651. Non-temporal loads: 318 /
+// 516; 256x128: 217 / 553; 256x256: 130 / 605; 128x128 with k-steps of 32:
+// 277 / 519 (used when K is not a multiple of 64).
 template <typename OUT>
 hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
-  auto groups = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
   const dim3 block(kGemmThreads);
 #define LUX3D_GEMM_TILE(BM_, BN_, BK_, W_)                                                              \
   {                                                                                                     \
     const dim3 grid((unsigned)((p.N + BN_ - 1) / BN_), (unsigned)((p.M + BM_ - 1) / BM_));              \
-    hipLaunchKernelGGL((q8_0_gemm_kernel<OUT, BM_, BN_, BK_, W_>), grid, block, 0, s, p);              \
+    hipLaunchKernelGGL((q8_0_gemm_kernel<OUT, BM_, BN_, BK_, W_>), grid, block, 0, s, p); \
     return hipGetLastError();                                                                           \
   }
-  if (p.K % 64 == 0) {
-    if (groups(256, 128) >= 512) LUX3D_GEMM_TILE(256, 128, 64, 1)
-    LUX3D_GEMM_TILE(128, 128, 64, 1)
-  }
+  if (p.K % 64 == 0) LUX3D_GEMM_TILE(128, 128, 64, 2)
   LUX3D_GEMM_TILE(128, 128, 32, 1)
 #undef LUX3D_GEMM_TILE
 }
