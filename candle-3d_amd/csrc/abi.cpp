@@ -955,6 +955,63 @@ int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr, cons
   return hip_status(launch_sparse_conv(p, stream_of(stream)), fn);
 }
 
+int lux3d_sparse_rulebook(const lux3d_tensor_t *nbr, const lux3d_tensor_t *pairs, const lux3d_tensor_t *counts,
+                          lux3d_stream_t stream) {
+  const char *fn = "lux3d_sparse_rulebook";
+  int r;
+  if ((r = contiguous_of(nbr, fn, "nbr", LUX3D_I32, 2)) || (r = contiguous_of(pairs, fn, "pairs", LUX3D_I32, 3)) ||
+      (r = contiguous_of(counts, fn, "counts", LUX3D_I32, -1)))
+    return r;
+  const int64_t n = nbr->shape[0];
+  if (nbr->shape[1] != 27) return fail(LUX3D_ERR_SHAPE, "%s: nbr must be [N, 27]", fn);
+  if (pairs->shape[0] != 27 || pairs->shape[1] != n || pairs->shape[2] != 2 || numel(counts) != 27)
+    return fail(LUX3D_ERR_SHAPE, "%s: pairs must be [27, %lld, 2] and counts [27]", fn, (long long)n);
+  if (n > INT32_MAX / 27) return fail(LUX3D_ERR_SHAPE, "%s: too many voxels", fn);
+  return hip_status(launch_sparse_rulebook(static_cast<const int32_t *>(nbr->data), n,
+                                           static_cast<int32_t *>(pairs->data), static_cast<int32_t *>(counts->data),
+                                           stream_of(stream)),
+                    fn);
+}
+
+int lux3d_sparse_conv3d_rulebook(const lux3d_tensor_t *x, const lux3d_tensor_t *pairs, const lux3d_tensor_t *counts,
+                                 const lux3d_tensor_t *weight, const lux3d_tensor_t *bias, const lux3d_tensor_t *out,
+                                 lux3d_stream_t stream) {
+  const char *fn = "lux3d_sparse_conv3d_rulebook";
+  int r;
+  if ((r = contiguous_of(x, fn, "x", LUX3D_F32, 2)) || (r = contiguous_of(pairs, fn, "pairs", LUX3D_I32, 3)) ||
+      (r = contiguous_of(counts, fn, "counts", LUX3D_I32, -1)) ||
+      (r = contiguous_of(weight, fn, "weight", LUX3D_F32, 3)) || (r = contiguous_of(out, fn, "out", LUX3D_F32, 2)))
+    return r;
+  const int64_t n = x->shape[0], cin = x->shape[1], cout = weight->shape[1];
+  if (pairs->shape[0] != 27 || pairs->shape[1] != n || pairs->shape[2] != 2 || numel(counts) != 27)
+    return fail(LUX3D_ERR_SHAPE, "%s: pairs must be [27, %lld, 2] and counts [27]", fn, (long long)n);
+  if (weight->shape[0] != 27 || weight->shape[2] != cin)
+    return fail(LUX3D_ERR_SHAPE, "SparseConv3d expects [N, %lld] with weight [27, Cout, %lld]", (long long)cin,
+                (long long)weight->shape[2]);
+  if (out->shape[0] != n || out->shape[1] != cout) return fail(LUX3D_ERR_SHAPE, "%s: out must be [%lld, %lld]", fn,
+                                                                (long long)n, (long long)cout);
+  if (cin % 16 || cin == 0)
+    return fail(LUX3D_ERR_SHAPE, "%s: Cin must be a positive multiple of 16 (use lux3d_sparse_conv3d)", fn);
+  if (!aligned16(x->data) || !aligned16(weight->data))
+    return fail(LUX3D_ERR_LAYOUT, "%s: x and weight must be 16-byte aligned", fn);
+  const float *bp = nullptr;
+  if (bias) {
+    if ((r = contiguous_of(bias, fn, "bias", LUX3D_F32, -1))) return r;
+    if (numel(bias) != cout) return fail(LUX3D_ERR_SHAPE, "%s: bias must have %lld elements", fn, (long long)cout);
+    bp = static_cast<const float *>(bias->data);
+  }
+  SparseConvParams p;
+  p.x = static_cast<const float *>(x->data);
+  p.w = static_cast<const float *>(weight->data);
+  p.bias = bp;
+  p.out = static_cast<float *>(out->data);
+  p.n = n; p.cin = cin; p.cout = cout;
+  p.mfma = true;
+  return hip_status(launch_sparse_conv_rulebook(p, static_cast<const int32_t *>(pairs->data),
+                                                static_cast<const int32_t *>(counts->data), stream_of(stream)),
+                    fn);
+}
+
 int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids, const lux3d_tensor_t *out,
                             lux3d_stream_t stream) {
   const char *fn = "lux3d_index_select_rows";

@@ -141,6 +141,11 @@ struct SparseConvParams {
   bool mfma = false;              // cin % 16 == 0, 16-byte aligned x and w
 };
 hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s);
+// Rulebook: pairs [27, n, 2] (dst, src) per tap and counts [27] from nbr;
+// the conv then runs one gather-GEMM-add pass per tap (p.mfma must hold).
+hipError_t launch_sparse_rulebook(const int32_t *nbr, int64_t n, int32_t *pairs, int32_t *counts, hipStream_t s);
+hipError_t launch_sparse_conv_rulebook(const SparseConvParams &p, const int32_t *pairs, const int32_t *counts,
+                                       hipStream_t s);
 // out[m] = src[ids[m]] for m < rows (and m < *count when count is given);
 // rows of row_bytes bytes; ids out of range give zero rows.
 hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bool ids64, int64_t rows,

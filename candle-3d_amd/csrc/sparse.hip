@@ -249,6 +249,149 @@ __global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams 
   }
 }
 
+// ---- rulebook path: per-tap pair lists, one gather-GEMM-add pass per tap -------
+
+__global__ __launch_bounds__(256) void rulebook_clear_kernel(int32_t *counts) {
+  if (threadIdx.x < 27) counts[threadIdx.x] = 0;
+}
+
+// pairs[k][j] = (dst row i, src row nbr[i][k]) for every present neighbour;
+// the order inside a tap is arbitrary (each dst row occurs once per tap).
+__global__ __launch_bounds__(256) void rulebook_kernel(const int32_t *nbr, int64_t n, int32_t *pairs,
+                                                       int32_t *counts) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n * 27) return;
+  const int64_t i = t / 27;
+  const int k = (int)(t % 27);
+  const int32_t s = nbr[t];
+  if (s < 0 || s >= n) return;
+  const int32_t pos = atomicAdd(&counts[k], 1);
+  pairs[((int64_t)k * n + pos) * 2] = (int32_t)i;
+  pairs[((int64_t)k * n + pos) * 2 + 1] = s;
+}
+
+__global__ __launch_bounds__(256) void fill_rows_kernel(float *out, int64_t n, int64_t cout, const float *bias,
+                                                        bool add) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n * cout) return;
+  const float b = bias ? bias[t % cout] : 0.f;
+  out[t] = add ? out[t] + b : b;
+}
+
+// One tap: out[dst_j, :] += x[src_j, :] W_k^T for the count[k] pairs of tap
+// k, f32 MFMA, the same tiling as the output-stationary kernel. Rows of a
+// tile are distinct destinations, so the read-modify-write is race-free.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void sparse_tap_gemm_kernel(SparseConvParams p, const int32_t *pairs,
+                                                              const int32_t *counts, int k) {
+  constexpr int BK = 16;
+  constexpr int ROW = BK + 1;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int ACH = BM * BK / 4 / 256, BCH = BN * BK / 4 / 256;
+  static_assert(ACH >= 1 && BCH >= 1, "tile");
+  __shared__ float As[2][BM * ROW];
+  __shared__ float Bs[2][BN * ROW];
+  __shared__ int32_t src[BM], dst[BM];
+
+  const int64_t cnt = counts[k] < p.n ? counts[k] : p.n;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  if (m0 >= cnt) return;  // uniform: the whole workgroup leaves before any barrier
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t N = p.n, Cin = p.cin, Cout = p.cout;
+  const int32_t *pk = pairs + (int64_t)k * N * 2;
+  for (int r = t; r < BM; r += 256) {
+    const bool ok = m0 + r < cnt;
+    dst[r] = ok ? pk[(m0 + r) * 2] : -1;
+    const int32_t s = ok ? pk[(m0 + r) * 2 + 1] : -1;
+    src[r] = s >= 0 && s < N ? s : -1;
+  }
+  __syncthreads();
+
+  int a_row[ACH], a_part[ACH], b_row[BCH], b_part[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = t + i * 256;
+    a_row[i] = c / (BK / 4);
+    a_part[i] = c % (BK / 4);
+  }
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int c = t + i * 256;
+    b_row[i] = c / (BK / 4);
+    b_part[i] = c % (BK / 4);
+  }
+  float4 ra[ACH], rb[BCH];
+  const float *wk = p.w + (int64_t)k * Cout * Cin;
+  auto load_step = [&](int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int32_t s = src[a_row[i]];
+      ra[i] = s >= 0 ? *reinterpret_cast<const float4 *>(p.x + (int64_t)s * Cin + c0 + a_part[i] * 4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      int64_t o = n0 + b_row[i];
+      o = o < Cout ? o : Cout - 1;
+      rb[i] = *reinterpret_cast<const float4 *>(wk + o * Cin + c0 + b_part[i] * 4);
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      float *d = &As[buf][a_row[i] * ROW + a_part[i] * 4];
+      d[0] = ra[i].x; d[1] = ra[i].y; d[2] = ra[i].z; d[3] = ra[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      float *d = &Bs[buf][b_row[i] * ROW + b_part[i] * 4];
+      d[0] = rb[i].x; d[1] = rb[i].y; d[2] = rb[i].z; d[3] = rb[i].w;
+    }
+  };
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+  const int64_t nsteps = Cin / BK;
+  load_step(0);
+  store_step(0);
+  lds_barrier();
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int64_t st = 0; st < nsteps; ++st) {
+    const int buf = (int)(st & 1);
+    if (st + 1 < nsteps) load_step((st + 1) * BK);
+#pragma unroll
+    for (int s2 = 0; s2 < BK / 2; ++s2) {
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = As[buf][(wm * (BM / 2) + i * 32 + lrow) * ROW + s2 * 2 + lk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = Bs[buf][(wn * (BN / 2) + j * 32 + lrow) * ROW + s2 * 2 + lk];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (st + 1 < nsteps) store_step(buf ^ 1);
+    lds_barrier();
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+    if (col >= Cout) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int32_t d = dst[r];
+        if (d >= 0) p.out[(int64_t)d * Cout + col] += acc[i][j][e];
+      }
+  }
+}
+
 // Any Cin / Cout: one thread per output element, f32 sums in tap, channel order.
 __global__ __launch_bounds__(256) void sparse_conv_generic_kernel(SparseConvParams p) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -410,6 +553,30 @@ hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s) {
   }
   if ((p.n * p.cout + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(sparse_conv_generic_kernel, dim3(grid_of(p.n * p.cout)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_rulebook(const int32_t *nbr, int64_t n, int32_t *pairs, int32_t *counts, hipStream_t s) {
+  if ((n * 27 + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rulebook_clear_kernel, dim3(1), dim3(256), 0, s, counts);
+  if (n > 0) hipLaunchKernelGGL(rulebook_kernel, dim3(grid_of(n * 27)), dim3(256), 0, s, nbr, n, pairs, counts);
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_conv_rulebook(const SparseConvParams &p, const int32_t *pairs, const int32_t *counts,
+                                       hipStream_t s) {
+  if (p.n <= 0 || p.cout <= 0) return hipSuccess;
+  if ((p.n * p.cout + 255) / 256 > INT32_MAX || (p.n + 63) / 64 > 65535) return hipErrorInvalidValue;
+  // out = 0; out[dst] += x[src] W_k^T for k = 0..26 in order; out += bias:
+  // the reference's zeros / index_add / broadcast_add sequence
+  hipLaunchKernelGGL(fill_rows_kernel, dim3(grid_of(p.n * p.cout)), dim3(256), 0, s, p.out, p.n, p.cout,
+                     (const float *)nullptr, false);
+  const dim3 grid((unsigned)((p.cout + 63) / 64), (unsigned)((p.n + 63) / 64));
+  for (int k = 0; k < 27; ++k)
+    hipLaunchKernelGGL((sparse_tap_gemm_kernel<64, 64>), grid, dim3(256), 0, s, p, pairs, counts, k);
+  if (p.bias)
+    hipLaunchKernelGGL(fill_rows_kernel, dim3(grid_of(p.n * p.cout)), dim3(256), 0, s, p.out, p.n, p.cout, p.bias,
+                       true);
   return hipGetLastError();
 }
 

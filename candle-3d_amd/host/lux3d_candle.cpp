@@ -765,9 +765,19 @@ SparseConv3d SparseConv3d::load(const Tensor &weight, const std::optional<Tensor
 }
 
 Tensor SparseConv3d::forward_nbr(const Tensor &nbr, const Tensor &feats) const {
-  Tensor out = Tensor::empty({feats.dim(0), out_}, DType::F32, feats.device());
+  const Device &dev = feats.device();
+  Tensor out = Tensor::empty({feats.dim(0), out_}, DType::F32, dev);
+  if (in_ % 16 == 0 && feats.rank() == 2 && feats.dim(0) == nbr.dim(0)) {
+    // per-tap pair lists, then the reference's tap-ordered accumulation
+    const int64_t n = nbr.dim(0);
+    const Tensor pairs = Tensor::empty({27, n, 2}, DType::I32, dev), counts = Tensor::empty({27}, DType::I32, dev);
+    abi_check(lux3d_sparse_rulebook(Desc(nbr).p(), Desc(pairs).p(), Desc(counts).p(), dev.stream()));
+    abi_check(lux3d_sparse_conv3d_rulebook(Desc(feats).p(), Desc(pairs).p(), Desc(counts).p(), Desc(w27_).p(),
+                                           Desc(bias_).p(), Desc(out).p(), dev.stream()));
+    return out;
+  }
   abi_check(lux3d_sparse_conv3d(Desc(feats).p(), Desc(nbr).p(), Desc(w27_).p(), Desc(bias_).p(), Desc(out).p(),
-                                feats.device().stream()));
+                                dev.stream()));
   return out;
 }
 

@@ -433,14 +433,31 @@ class SparseConv3d:
         self.bias = None if bias is None else bias.to(torch.float32).contiguous()
         self.in_channels, self.out_channels = in_channels, out_channels
 
-    def forward(self, coords_or_nbr: torch.Tensor, feats: torch.Tensor) -> torch.Tensor:
-        """coords int32 [N, 3] (the neighbour table is built) or a prebuilt
-        nbr int32 [N, 27]; feats f32 [N, Cin] -> [N, Cout] f32."""
-        nbr = coords_or_nbr if coords_or_nbr.shape[-1] == 27 else sparse_neighbors(coords_or_nbr)
+    def forward(self, coords_or_nbr, feats: torch.Tensor) -> torch.Tensor:
+        """coords int32 [N, 3] (the neighbour table is built), a prebuilt nbr
+        int32 [N, 27], or a SparseRulebook; feats f32 [N, Cin] -> [N, Cout]."""
         out = torch.empty((feats.shape[0], self.out_channels), dtype=torch.float32, device=feats.device)
+        if isinstance(coords_or_nbr, SparseRulebook):
+            rb = coords_or_nbr
+            _lib.call("lux3d_sparse_conv3d_rulebook", desc(feats), desc(rb.pairs), desc(rb.counts),
+                      desc(self.weight27), desc(self.bias), desc(out), _stream(feats))
+            return out
+        nbr = coords_or_nbr if coords_or_nbr.shape[-1] == 27 else sparse_neighbors(coords_or_nbr)
         _lib.call("lux3d_sparse_conv3d", desc(feats), desc(nbr), desc(self.weight27), desc(self.bias), desc(out),
                   _stream(feats))
         return out
+
+
+class SparseRulebook:
+    """Per-tap (dst, src) pair lists of a coordinate set, built once and reused
+    by every convolution on it (lux3d_sparse_rulebook)."""
+
+    def __init__(self, nbr: torch.Tensor):
+        n = nbr.shape[0]
+        self.nbr = nbr
+        self.pairs = torch.empty((27, n, 2), dtype=torch.int32, device=nbr.device)
+        self.counts = torch.empty(27, dtype=torch.int32, device=nbr.device)
+        _lib.call("lux3d_sparse_rulebook", desc(nbr), desc(self.pairs), desc(self.counts), _stream(nbr))
 
 
 def index_select_rows(feats: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:

@@ -466,7 +466,7 @@ def _shell_coords(n, res, seed):
     return c[rng.permutation(len(c))[:n]]
 
 
-def _sparse_conv(dev, name, n, ch, res, reps):
+def _sparse_conv(dev, name, n, ch, res, reps, rulebook=True):
     """SparseConv3d (trellis2_sparse.rs:197-243) on shell voxels: x f32
     [N, C] -> [N, C], the ConvNeXt block conv of a decoder stage."""
     from . import _lib
@@ -482,13 +482,20 @@ def _sparse_conv(dev, name, n, ch, res, reps):
     dx, do = [ops.desc(v) for v in xs], [ops.desc(v) for v in outs]
     dn, dw, db = ops.desc(nbr), ops.desc(w27), ops.desc(bias)
 
+    rb = ops.SparseRulebook(nbr)
+    dp, dc = ops.desc(rb.pairs), ops.desc(rb.counts)
+
     def launch(i):
-        _lib.call("lux3d_sparse_conv3d", dx[i % 2], dn, dw, db, do[i % 2], _cur())
+        if rulebook:
+            _lib.call("lux3d_sparse_conv3d_rulebook", dx[i % 2], dp, dc, dw, db, do[i % 2], _cur())
+        else:
+            _lib.call("lux3d_sparse_conv3d", dx[i % 2], dn, dw, db, do[i % 2], _cur())
     nbytes = n * ch * 4 * 2 + n * 27 * 4 + 27 * ch * ch * 4
-    wl = Workload(name, 3, "sparse_conv_mfma_kernel<64,64>", "f32 -> f32 acc (MFMA f32)", nbytes,
+    kern = "sparse_tap_gemm_kernel<64,64> x 27 taps" if rulebook else "sparse_conv_mfma_kernel<64,64>"
+    wl = Workload(name, 3, kern, "f32 -> f32 acc (MFMA f32)", nbytes,
                   f"{n} shell voxels in {res}^3, C {ch} -> {ch}, {used / n:.1f} active taps per voxel", launch, 2,
                   flops=2 * used * ch * ch, reps=reps, peak_tflops=157.3)
-    wl._keep = (coords, nbr, xs, w27, bias, outs, dx, do, dn, dw, db)
+    wl._keep = (coords, nbr, xs, w27, bias, outs, dx, do, dn, dw, db, rb, dp, dc)
     return wl
 
 
@@ -500,6 +507,11 @@ def cfg3_sparse_conv_c1024(dev) -> Workload:
 def cfg3_sparse_conv_c256(dev) -> Workload:
     # decoder stage 2 (256 channels) at resolution 256
     return _sparse_conv(dev, "sparse_conv_c256", 150000, 256, 256, 10)
+
+
+def cfg3_sparse_conv_c256_output_stationary(dev) -> Workload:
+    # the one-kernel output-stationary path on the same set, for comparison
+    return _sparse_conv(dev, "sparse_conv_c256_output_stationary", 150000, 256, 256, 10, rulebook=False)
 
 
 def cfg3_c2s(dev) -> Workload:
@@ -559,5 +571,6 @@ EXTRAS: List[Callable] = [
     cfg3_sdpa,
     cfg3_sparse_conv_c1024,
     cfg3_sparse_conv_c256,
+    cfg3_sparse_conv_c256_output_stationary,
     cfg3_c2s,
 ]

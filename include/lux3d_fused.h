@@ -343,6 +343,23 @@ int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *k
 int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
                         const lux3d_tensor_t *weight, const lux3d_tensor_t *bias,
                         const lux3d_tensor_t *out, lux3d_stream_t stream);
+/* lux3d_sparse_rulebook + lux3d_sparse_conv3d_rulebook: the same convolution
+ * computed the reference's way round, without its host work and scatter
+ * kernels: per-tap pair lists (dst, src) built once per coordinate set
+ * (pairs int32 [27, N, 2] and counts int32 [27], from nbr), then
+ * out = 0; out[dst] += x[src] W_k^T for k = 0..26 in order; out += bias --
+ * the zeros / index_add / broadcast_add sequence of SparseConv3d::forward
+ * (trellis2_sparse.rs:205-242). Only present neighbours reach the matrix
+ * cores (f32 MFMA), so sparse sets run several times faster than the
+ * output-stationary kernel. Cin % 16 == 0 and 16-byte aligned x and weight
+ * are required (else LUX3D_ERR_SHAPE / LUX3D_ERR_LAYOUT: use
+ * lux3d_sparse_conv3d). */
+int lux3d_sparse_rulebook(const lux3d_tensor_t *nbr, const lux3d_tensor_t *pairs,
+                          const lux3d_tensor_t *counts, lux3d_stream_t stream);
+int lux3d_sparse_conv3d_rulebook(const lux3d_tensor_t *x, const lux3d_tensor_t *pairs,
+                                 const lux3d_tensor_t *counts, const lux3d_tensor_t *weight,
+                                 const lux3d_tensor_t *bias, const lux3d_tensor_t *out,
+                                 lux3d_stream_t stream);
 int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids,
                             const lux3d_tensor_t *out, lux3d_stream_t stream);
 int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t *feats,

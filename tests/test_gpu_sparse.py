@@ -114,8 +114,9 @@ def test_sparse_conv3d_reference_cases(dev, ops, orc):
     (777, 32, 40, 16, False),
     (20000, 256, 256, 64, True),
 ])
-def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface):
-    _case(op="conv3d", n=n, cin=cin, cout=cout, surface=surface)
+@pytest.mark.parametrize("path", ["output_stationary", "rulebook"])
+def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface, path):
+    _case(op="conv3d", n=n, cin=cin, cout=cout, surface=surface, path=path)
     coords = random_coords(n, res, n + cin, surface)
     n = len(coords)
     rng = np.random.default_rng(cin)
@@ -125,7 +126,8 @@ def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface):
     wt = torch.from_numpy(w27).permute(1, 0, 2).contiguous()  # back to [Cout, 27, Cin]
     conv = ops.SparseConv3d(wt.to(dev), torch.from_numpy(bias).to(dev), cin, cout)
     nbr_d = ops.sparse_neighbors(torch.from_numpy(coords).to(dev))
-    out = conv.forward(nbr_d, torch.from_numpy(x).to(dev))
+    arg = ops.SparseRulebook(nbr_d) if path == "rulebook" else nbr_d
+    out = conv.forward(arg, torch.from_numpy(x).to(dev))
     torch.cuda.synchronize()
     nbr = orc.sparse_neighbors(coords)
     rows = np.arange(n) if n * cin * cout <= 5e8 else np.sort(np.random.default_rng(1).choice(n, 600, replace=False))
@@ -178,3 +180,33 @@ def test_channel_to_spatial(dev, ops, orc, n, c, fdt, ldt):
     assert np.array_equal(sub.cpu().numpy(), wsub)
     if n == 3:
         assert oc.cpu().tolist() == [[0, 0, 0], [1, 1, 0], [1, 0, 1], [3, 0, 0]]
+
+
+def test_sparse_rulebook_pairs(dev, ops, orc):
+    """Every present neighbour appears once in its tap's list, nothing else."""
+    coords = random_coords(4000, 32, 21, True)
+    nbr = orc.sparse_neighbors(coords)
+    rb = ops.SparseRulebook(torch.from_numpy(nbr).to(dev))
+    torch.cuda.synchronize()
+    pairs, counts = rb.pairs.cpu().numpy(), rb.counts.cpu().numpy()
+    for k in range(27):
+        want = {(i, int(nbr[i, k])) for i in range(len(coords)) if nbr[i, k] >= 0}
+        got = {(int(d), int(s_)) for d, s_ in pairs[k, :counts[k]]}
+        assert counts[k] == len(want) and got == want, k
+
+
+def test_sparse_conv3d_rulebook_matches_reference_order(dev, ops, orc):
+    """The rulebook path adds the taps in the reference's order; on inputs
+    whose products and partial sums are exact in f32 it equals the oracle
+    bit for bit."""
+    coords = random_coords(2000, 24, 22, True)
+    rng = np.random.default_rng(23)
+    x = rng.integers(-4, 5, (len(coords), 32)).astype(np.float32)
+    w27 = (rng.integers(-3, 4, (27, 48, 32)) * 0.25).astype(np.float32)
+    bias = (rng.integers(-8, 9, 48) * 0.5).astype(np.float32)
+    conv = ops.SparseConv3d(torch.from_numpy(w27).permute(1, 0, 2).contiguous().to(dev), torch.from_numpy(bias).to(dev),
+                            32, 48)
+    nbr = ops.sparse_neighbors(torch.from_numpy(coords).to(dev))
+    got = conv.forward(ops.SparseRulebook(nbr), torch.from_numpy(x).to(dev)).cpu().numpy()
+    want = orc.sparse_conv3d(x, orc.sparse_neighbors(coords), w27, bias)
+    assert np.array_equal(got, want)
