@@ -433,6 +433,29 @@ void sparse_conv_hand_picked_kernels(const Device &dev) {
   }
 }
 
+// The identity and +x shift kernels again with 16 channels, which takes the
+// rulebook path (per-tap pair lists, tap-ordered accumulation).
+void sparse_conv_rulebook_identity_and_shift(const Device &dev) {
+  const int C = 16;
+  const std::vector<Coord> coords = {{0, 0, 0}, {1, 0, 0}, {1, 1, 0}, {3, 0, 0}, {2, 0, 0}};
+  std::vector<float> x(coords.size() * C);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = pattern_f32(i * 3);
+  const Tensor feats = Tensor::from_f32(x, {(int64_t)coords.size(), C}, DType::F32, dev);
+  for (int k : {13, 22}) {
+    std::vector<float> w(C * 27 * C, 0.f);
+    for (int c = 0; c < C; ++c) w[(c * 27 + k) * C + c] = 1.f;
+    const SparseConv3d conv = SparseConv3d::load(Tensor::from_f32(w, {C, 3, 3, 3, C}, DType::F32, dev), std::nullopt, C, C);
+    const std::vector<float> out = conv.forward(coords, feats).to_vec_f32();
+    // +x neighbours: row 0 -> row 1, row 1 -> row 4, row 4 -> row 3
+    const int plus_x[5] = {1, 4, -1, -1, 3};
+    for (size_t i = 0; i < coords.size(); ++i)
+      for (int c = 0; c < C; ++c) {
+        const int src = k == 13 ? (int)i : plus_x[i];
+        CHECK(out[i * C + c] == (src < 0 ? 0.f : x[src * C + c]));
+      }
+  }
+}
+
 void sparse_conv_loader_transposes_flex_gemm_layout(const Device &dev) {
   const int CIN = 2, COUT = 3;
   std::vector<float> v(COUT * 27 * CIN);
@@ -576,6 +599,7 @@ int main(int argc, char **argv) {
       {"sparse_conv_matches_dense_reference", sparse_conv_matches_dense_reference, true},
       {"sparse_conv_hand_picked_kernels", sparse_conv_hand_picked_kernels, true},
       {"sparse_conv_loader_transposes_flex_gemm_layout", sparse_conv_loader_transposes_flex_gemm_layout, true},
+      {"sparse_conv_rulebook_identity_and_shift", sparse_conv_rulebook_identity_and_shift, true},
       {"c2s_order_and_feature_selection", c2s_order_and_feature_selection, true},
       {"errors_on_device", errors_on_device, true},
   };
