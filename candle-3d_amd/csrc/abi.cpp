@@ -841,9 +841,64 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
   return hip_status(launch_q8_0_gemm(y->dtype, p, stream_of(stream)), fn);
 }
 
+namespace {
+// Validates q, k, v, out for attention and fills the strides; `mfma` tells
+// whether every row is 16-byte aligned with D 64 / 128 in a 2-byte type.
+int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v,
+                float scale, const lux3d_tensor_t *out, AttnParams &p);
+}  // namespace
+
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
                const lux3d_tensor_t *out, lux3d_stream_t stream) {
   const char *fn = "lux3d_sdpa";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w, const lux3d_tensor_t *q_b,
+                                float eps, const lux3d_tensor_t *cos_full, const lux3d_tensor_t *sin_alt_full,
+                                const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
+                                lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa_layernorm_rope2d";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  if (!q_w || !q_b) return fail(LUX3D_ERR_NULL, "%s: LayerNorm needs both weight and bias", fn);
+  const void *wp, *bp;
+  int wdt, bdt;
+  if ((r = param_vec(q_w, p.D, fn, "q_w", wp, wdt)) || (r = param_vec(q_b, p.D, fn, "q_b", bp, bdt))) return r;
+  if (!(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
+  if (p.D % 4) return fail(LUX3D_ERR_SHAPE, "%s: rope token_dim must be divisible by 4, got %lld", fn, (long long)p.D);
+  int64_t cB, cN, sB, sN;
+  if ((r = rope2d_table(cos_full, fn, "cos_full", p.B, p.Lq, p.D, cB, cN))) return r;
+  if ((r = rope2d_table(sin_alt_full, fn, "sin_alt_full", p.B, p.Lq, p.D, sB, sN))) return r;
+  if (cB != sB || cN != sN || cos_full->dtype != sin_alt_full->dtype)
+    return fail(LUX3D_ERR_LAYOUT, "%s: cos_full and sin_alt_full must share layout and dtype", fn);
+  // fused: the matrix-core path, and 16-byte aligned parameters and table rows
+  const int tb = elem_bytes(cos_full->dtype);
+  const bool fused = p.mfma && (p.D == 64 || p.D == 128) && aligned16(wp) && aligned16(bp) &&
+                     aligned16(cos_full->data) && aligned16(sin_alt_full->data) && (cN * tb) % 16 == 0 &&
+                     (cB * tb) % 16 == 0;
+  if (!fused) {
+    // the two launches, out holding the normalised q (each attention
+    // workgroup reads its query rows before it writes the same rows)
+    if ((r = lux3d_qk_layernorm_rope2d(q, q_w, q_b, nullptr, nullptr, nullptr, eps, cos_full, sin_alt_full, out,
+                                       nullptr, stream)))
+      return r;
+    return lux3d_sdpa(out, k, v, scale, out, stream);
+  }
+  p.qln = true;
+  p.qw = wp; p.qw_dt = wdt; p.qb = bp; p.qb_dt = bdt; p.eps = eps;
+  p.tab_c = cos_full->data; p.tab_s = sin_alt_full->data; p.tab_dt = cos_full->dtype;
+  p.tab_sB = cB; p.tab_sN = cN;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+namespace {
+int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v,
+                float scale, const lux3d_tensor_t *out, AttnParams &p) {
   int r;
   const lux3d_tensor_t *ts[4] = {q, k, v, out};
   const char *names[4] = {"q", "k", "v", "out"};
@@ -868,7 +923,7 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_ten
   if (B * H * Lq > 0 && Lk == 0) return fail(LUX3D_ERR_SHAPE, "%s: k and v have no tokens", fn);
   if (D > 512 || D < 1) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld outside 1..512", fn, (long long)D);
   if (!(scale > 0.f) || !std::isfinite(scale)) return fail(LUX3D_ERR_VALUE, "%s: scale must be finite and > 0", fn);
-  AttnParams p;
+  p = AttnParams();
   p.q = q->data; p.k = k->data; p.v = v->data; p.o = out->data;
   p.B = B; p.H = H; p.Lq = Lq; p.Lk = Lk; p.D = D;
   p.q_sb = q->stride[0]; p.q_sh = q->stride[1]; p.q_st = q->stride[2];
@@ -885,8 +940,9 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_ten
       if (t->shape[a] > 1 && t->stride[a] % 8) mfma = false;
   }
   p.mfma = mfma;
-  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+  return LUX3D_OK;
 }
+}  // namespace
 
 // ---- sparse ops --------------------------------------------------------------
 

@@ -106,7 +106,10 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
 // Measured on MI355X (TFLOP/s, VGGT frame / global, D 64): LAZY + DOT +
 // PHASED 617 / 795 against 579 / 700 without; D 128 (TripoSG / TRELLIS.2
 // 16k) LAZY + DOT 718 / 877 against 679 / 827, PHASED by key tile no gain.
-template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED>
+// QLN: q arrives raw; its LayerNorm and 2D RoPE (the QK kernel's arithmetic
+// and lane mapping, bit for bit) are applied while the Q fragments are
+// loaded, so the normalised q never goes through HBM.
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool QLN = false>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   using M = Mma<T>;
   using op_t = typename M::op_t;
@@ -118,8 +121,9 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   constexpr int NKT = BKV / 32;            // 32-key tiles per block
   constexpr int NDT = D / 32;              // 32-dim output tiles
   static_assert(KCH >= 1 && VGR >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
-  __shared__ __align__(16) uint16_t Ks[2][BKV * KROW];
-  __shared__ __align__(16) uint16_t Vt[2][D * VROW];
+  __shared__ __align__(16) uint16_t smem[2 * BKV * KROW + 2 * D * VROW];
+  uint16_t(*Ks)[BKV * KROW] = reinterpret_cast<uint16_t(*)[BKV * KROW]>(smem);
+  uint16_t(*Vt)[D * VROW] = reinterpret_cast<uint16_t(*)[D * VROW]>(smem + 2 * BKV * KROW);
 
   const int64_t lid = xcd_logical_id(blockIdx.x, nwg);
   const int64_t bh = lid / nqb, qb = lid % nqb;
@@ -139,9 +143,54 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   for (int qt = 0; qt < QT; ++qt) {
     int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
     qr = qr < Lq ? qr : Lq - 1;
+    if constexpr (!QLN) {
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c)
-      qf[qt][c] = *reinterpret_cast<const op_t *>(qbase + (qr * p.q_st + c * 16 + 8 * hh) * 2);
+      for (int c = 0; c < D / 16; ++c)
+        qf[qt][c] = *reinterpret_cast<const op_t *>(qbase + (qr * p.q_st + c * 16 + 8 * hh) * 2);
+    }
+  }
+  if constexpr (QLN) {
+    // LayerNorm + RoPE of the wavefront's query rows with the QK kernel's
+    // mapping (D / 8 lanes per row, 8 elements per lane, the same DPP sums
+    // and partner exchange), written as bf16 / f16 into the K / V staging
+    // area, which is not in use yet; then each lane reads its fragments.
+    static_assert(D == 64 || D == 128, "QLN head dims");
+    constexpr int LPR = D / 8, RPP = 64 / LPR;  // lanes per row, rows per pass
+    static_assert(4 * QT * 32 * D <= 2 * BKV * KROW + 2 * D * VROW, "Q staging fits the K / V buffers");
+    uint16_t *qs = smem + wave * (QT * 32 * D);
+    const int ch = lane % LPR;
+    float w8[8], b8[8];
+    param8(p.qw, p.qw_dt, ch * 8, 1.f, w8);
+    param8(p.qb, p.qb_dt, ch * 8, 0.f, b8);
+#pragma unroll 1
+    for (int row = lane / LPR; row < QT * 32; row += RPP) {
+      int64_t qr = qb * BQ + wave * QT * 32 + row;
+      qr = qr < Lq ? qr : Lq - 1;
+      float x[8];
+      Chunk<T>::template load<false>(qbase + (qr * p.q_st + ch * 8) * 2, x);
+      const float mean = group_sum<LPR>(ln_chunk_sum(x)) * (1.0f / D);
+      const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
+      ln_chunk_affine(x, rstd, w8, b8);
+      float C8[8], S8[8], pv[8];
+      const int64_t toff = bi * p.tab_sB + qr * p.tab_sN + ch * 8;
+      param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
+      param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 32>(x[k]);  // element j ^ D/4
+      u32x4_t pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pk[e] = M::pack(__fadd_rn(__fmul_rn(x[2 * e], C8[2 * e]), __fmul_rn(pv[2 * e], S8[2 * e])),
+                        __fadd_rn(__fmul_rn(x[2 * e + 1], C8[2 * e + 1]), __fmul_rn(pv[2 * e + 1], S8[2 * e + 1])));
+      *reinterpret_cast<u32x4_t *>(qs + row * D + ch * 8) = pk;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+        qf[qt][c] = *reinterpret_cast<const op_t *>(qs + (qt * 32 + l32) * D + c * 16 + 8 * hh);
+    lds_barrier();  // the staging area becomes the K / V buffers below
   }
 
   // Staging: K rows as 16-byte chunks; V as 4 keys x 4 dims, transposed in
@@ -458,6 +507,15 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
 
 template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED>
 hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
+  if (p.qln) {
+    constexpr int BQ = 4 * 32 * QT;
+    const int64_t nqb = (p.Lq + BQ - 1) / BQ;
+    const int64_t nwg = p.B * p.H * nqb;
+    if (nwg > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, true>), dim3((unsigned)nwg), dim3(256),
+                       0, s, p, nqb, nwg);
+    return hipGetLastError();
+  }
   constexpr int BQ = 4 * 32 * QT;
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
@@ -483,6 +541,7 @@ hipError_t launch_generic(const AttnParams &p, hipStream_t s) {
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
+  if (p.qln && !(p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);

@@ -261,6 +261,33 @@ template <int M> __device__ __forceinline__ float lane_xor(float v) {
   else return __shfl_xor(v, M, 64);
 }
 
+// LayerNorm over a head row held as 8-element chunks: the chunk sums and the
+// affine step, shared by every kernel that normalises head rows so that they
+// agree bit for bit (the row total is the pairwise tree of chunk sums
+// ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) for 8 chunks).
+__device__ __forceinline__ float ln_chunk_sum(const float (&x)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s += x[k];
+  return s;
+}
+__device__ __forceinline__ float ln_chunk_center_sq(float (&x)[8], float mean) {
+  float s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    x[k] -= mean;
+    s2 += x[k] * x[k];
+  }
+  return s2;
+}
+__device__ __forceinline__ void ln_chunk_affine(float (&x)[8], float rstd, const float (&w)[8], const float (&b)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = x[k] * rstd * w[k] + b[k];
+}
+__device__ __forceinline__ float ln_rstd(float sq_total, float inv_d, float eps) {
+  return 1.0f / sqrtf(sq_total * inv_d + eps);
+}
+
 // Workgroup barrier that orders LDS only: the fences are scoped to the
 // local (LDS) address space, so the wave waits for its own LDS accesses
 // (lgkmcnt) but not for outstanding global loads or stores, which stay in

@@ -124,6 +124,16 @@ struct AttnParams {
   int64_t o_sb = 0, o_sh = 0, o_st = 0;
   float scale = 0.f;
   bool mfma = false;
+  // q LayerNorm + 2D RoPE applied in the Q load (matrix-core path): q is the
+  // raw head view; qw / qb the LayerNorm affine (D elements); tables the
+  // Rope2d cos_full / sin_alt_full, element (b, n, j) at b*tab_sB + n*tab_sN + j.
+  bool qln = false;
+  const void *qw = nullptr, *qb = nullptr;
+  int qw_dt = -1, qb_dt = -1;
+  float eps = 0.f;
+  const void *tab_c = nullptr, *tab_s = nullptr;
+  int tab_dt = -1;
+  int64_t tab_sB = 0, tab_sN = 0;
 };
 hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
 

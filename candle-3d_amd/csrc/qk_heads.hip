@@ -166,19 +166,9 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
     for (int r = 0; r < R; ++r) {
       float (&x)[8] = v[q][r];
       if constexpr (NORM == HN_LN) {
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s += x[k];
-        const float mean = group_sum<LPR>(s) * (1.0f / D);
-        float s2 = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          x[k] -= mean;
-          s2 += x[k] * x[k];
-        }
-        const float rstd = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = x[k] * rstd * w[q][k] + bias[q][k];
+        const float mean = group_sum<LPR>(ln_chunk_sum(x)) * (1.0f / D);
+        const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
+        ln_chunk_affine(x, rstd, w[q], bias[q]);
       } else if constexpr (NORM == HN_RMS) {
         float s2 = 0.f;
 #pragma unroll

@@ -679,6 +679,16 @@ Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float
   return out;
 }
 
+Tensor sdpa_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeEmbeddings &embeddings,
+                           const Tensor &k, const Tensor &v, float scale) {
+  Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
+  const Tensor b = bias_or_zeros(q_norm);
+  abi_check(lux3d_sdpa_layernorm_rope2d(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(b).p(), (float)q_norm.eps(),
+                                        Desc(embeddings.cos_full).p(), Desc(embeddings.sin_alt_full).p(), Desc(k).p(),
+                                        Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
+  return out;
+}
+
 Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale, size_t) {
   return exact_sdpa_heads(q, k, v, scale);
 }

@@ -282,6 +282,12 @@ Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out);
 Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale,
                                 size_t chunk_size = SIZE_MAX);
 Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float scale);
+// exact_query_chunked_sdpa(apply_layernorm_rope(q, q_norm, embeddings), k, v,
+// scale) (vggt.rs:170-183) with q's LayerNorm + 2D RoPE in the attention
+// kernel's Q load; k already normalised and rotated. Bit-identical to the
+// two calls.
+Tensor sdpa_layernorm_rope(const Tensor &q, const class LayerNorm &q_norm, const struct RopeEmbeddings &embeddings,
+                           const Tensor &k, const Tensor &v, float scale);
 
 // QMatMul over a Q8_0 weight [n, k] (QMatMul::from_qtensor and forward,
 // runtime/nn_blocks.rs:83-93, 145-150). from_q8_0 repacks the GGML blocks

@@ -388,6 +388,20 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     return out
 
 
+def sdpa_layernorm_rope2d(q_raw: torch.Tensor, q_norm, embeddings: "RopeEmbeddings", k: torch.Tensor,
+                          v: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """exact_query_chunked_sdpa(apply_layernorm_rope(q_raw, q_norm, rope), k, v,
+    scale) (vggt.rs:170-183) with q's LayerNorm + 2D RoPE done in the
+    attention kernel's Q load; q_norm is (weight, bias, eps); k already
+    normalised and rotated."""
+    w, b, eps = q_norm
+    if out is None:
+        out = torch.empty(q_raw.shape, dtype=q_raw.dtype, device=q_raw.device)
+    _lib.call("lux3d_sdpa_layernorm_rope2d", desc(q_raw), desc(w), desc(b), float(eps), desc(embeddings.cos_full),
+              desc(embeddings.sin_alt_full), desc(k), desc(v), float(scale), desc(out), _stream(q_raw))
+    return out
+
+
 def exact_query_chunked_sdpa(q, k, v, scale: float, chunk_size: int = 0) -> torch.Tensor:
     """attention_math.rs:199-241. chunk_size only bounded the reference's
     scores buffer; this kernel keeps no such buffer, so it is ignored."""

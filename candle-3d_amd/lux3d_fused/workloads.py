@@ -440,6 +440,40 @@ def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50) -> Workload:
     return wl
 
 
+def cfg1_sdpa_frame_qln(dev) -> Workload:
+    """VGGT frame attention with q's LayerNorm + 2D RoPE fused into the Q
+    load (lux3d_sdpa_layernorm_rope2d): raw q from the qkv buffer, keys
+    normalised beforehand, Rope2d tables of the 37 x 37 grid."""
+    from . import _lib
+    b, n, h, d = 8, 1374, 16, 64
+    s = synth.config_seed(1) + 720
+    qkv0 = _normal(s, (b, n, 3, h, d), dev, torch.bfloat16)
+    n_sets = 2
+    qkvs = [_fill_like(qkv0, j) for j in range(n_sets)]
+    outs = [torch.empty((b, h, n, d), dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+    qw = _normal(s + 1, (d,), dev, torch.float32, 1.0, 0.02)
+    qb = _normal(s + 2, (d,), dev, torch.float32, 0.0, 0.02)
+    emb = ops.Rope2d(100.0).embeddings(torch.from_numpy(synth.vggt_positions(b, 37, 37)).to(dev), d)
+    descs = []
+    ks = []
+    for qkv, o in zip(qkvs, outs):
+        v = qkv.permute(2, 0, 3, 1, 4)
+        kn = ops.apply_layernorm_rope(v[1], (qw, qb, 1e-6), emb)
+        ks.append(kn)
+        descs.append((ops.desc(v[0]), ops.desc(kn), ops.desc(v[2]), ops.desc(o)))
+    dw, db, dc, dsn = ops.desc(qw), ops.desc(qb), ops.desc(emb.cos_full), ops.desc(emb.sin_alt_full)
+
+    def launch(i):
+        dq, dk, dv, do = descs[i % n_sets]
+        _lib.call("lux3d_sdpa_layernorm_rope2d", dq, dw, db, 1e-6, dc, dsn, dk, dv, 0.125, do, _cur())
+    nbytes = 4 * b * h * n * d * 2
+    wl = Workload("sdpa_frame_qln", 1, "attn_mfma_kernel<BF16,64,...,QLN>", "bf16 -> f32 acc", nbytes,
+                  f"raw q + normalised k, v [{b},{h},{n},{d}]: q LayerNorm + 2D RoPE in the Q load", launch,
+                  n_sets, flops=4 * b * h * n * n * d, reps=50)
+    wl._keep = (qkvs, outs, qw, qb, emb, ks, descs, dw, db, dc, dsn)
+    return wl
+
+
 def cfg1_sdpa_frame(dev) -> Workload:
     return _sdpa(dev, "sdpa_frame", 1, 8, 1374, 16, 64, "VGGT frame attention")
 
@@ -566,6 +600,7 @@ EXTRAS: List[Callable] = [
     cfg4_q8_0_linear,
     cfg2_q8_0_linear,
     cfg1_sdpa_frame,
+    cfg1_sdpa_frame_qln,
     cfg1_sdpa_global,
     cfg2_sdpa,
     cfg3_sdpa,

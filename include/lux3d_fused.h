@@ -386,6 +386,26 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
                lux3d_stream_t stream);
 
+/* lux3d_sdpa_layernorm_rope2d: the VGGT / Pi3 attention of vggt.rs:170-183,
+ * exact_query_chunked_sdpa(apply_layernorm_rope(q, q_norm, rope), k, v,
+ * scale), with q's LayerNorm + 2D RoPE (attention_math.rs:127-150) applied
+ * inside the attention kernel's Q load: the normalised q never goes through
+ * HBM. q is the raw [B, H, N, D] head view (bf16 / f16); q_w, q_b the
+ * LayerNorm affine ([D], any float dtype); cos_full / sin_alt_full the Rope2d
+ * tables as lux3d_qk_layernorm_rope2d takes them; k the already normalised
+ * and rotated keys (lux3d_qk_layernorm_rope2d on k alone); v, scale and out
+ * as lux3d_sdpa (out [B, H, N, D]; it may be the view the caller transposes
+ * next). The normalised q equals lux3d_qk_layernorm_rope2d's bit for bit, so
+ * the result equals that call followed by lux3d_sdpa. D = 64 / 128 with
+ * 16-byte aligned rows, parameters and table rows runs fused; any other
+ * layout runs exactly those two launches, with out as the intermediate q.   */
+int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w,
+                                const lux3d_tensor_t *q_b, float eps,
+                                const lux3d_tensor_t *cos_full,
+                                const lux3d_tensor_t *sin_alt_full, const lux3d_tensor_t *k,
+                                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
+                                lux3d_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

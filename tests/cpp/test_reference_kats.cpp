@@ -260,6 +260,26 @@ void vggt_qk_layernorm_rope_specials_are_plain_layernorm(const Device &dev) {
   }
 }
 
+// VGGT attention (vggt.rs:170-183) with q's LayerNorm + RoPE fused into the
+// attention kernel equals apply_layernorm_rope followed by
+// exact_query_chunked_sdpa bit for bit.
+void vggt_attention_fused_equals_two_calls(const Device &dev) {
+  const int64_t B = 2, N = 300, H = 3, D = 64;
+  std::vector<float> qkv((size_t)(B * N * 3 * H * D));
+  for (size_t i = 0; i < qkv.size(); ++i) qkv[i] = std::sin(0.013f * (float)i) * 2.0f + 0.3f;
+  const Tensor perm = Tensor::from_f32(qkv, {B, N, 3, H, D}, DType::BF16, dev).permute({2, 0, 3, 1, 4});
+  std::vector<float> w(D), bias(D);
+  for (int64_t j = 0; j < D; ++j) w[j] = 1.0f + 0.01f * (float)(j % 7), bias[j] = 0.02f * (float)(j % 5) - 0.04f;
+  const LayerNorm ln(Tensor::from_f32(w, {D}, DType::F32, dev), Tensor::from_f32(bias, {D}, DType::F32, dev), 1e-6);
+  std::vector<int32_t> pos((size_t)(B * N * 2));
+  for (int64_t i = 0; i < B * N; ++i) pos[2 * i] = (int32_t)((i % N) / 17), pos[2 * i + 1] = (int32_t)((i % N) % 17);
+  const RopeEmbeddings emb = Rope2d(100.0f).embeddings(Tensor::from_i32(pos, {B, N, 2}, dev), (size_t)D);
+  const Tensor k = apply_layernorm_rope(perm.get(1), ln, emb);
+  const Tensor fused = sdpa_layernorm_rope(perm.get(0), ln, emb, k, perm.get(2), 0.125f);
+  const Tensor two = exact_query_chunked_sdpa(apply_layernorm_rope(perm.get(0), ln, emb), k, perm.get(2), 0.125f);
+  CHECK(fused.to_vec_u16() == two.to_vec_u16());
+}
+
 // Q8_0: w = f16(d) * int8(q), exact.
 void dequantize_q8_0_exact(const Device &dev) {
   std::vector<uint8_t> blk(34);
@@ -593,6 +613,7 @@ int main(int argc, char **argv) {
       {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
       {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
       {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
+      {"vggt_attention_fused_equals_two_calls", vggt_attention_fused_equals_two_calls, true},
       {"gguf_q8_linear_from_file", gguf_q8_linear_from_file, true},
       {"kernel_offset_deltas_cover_the_3x3x3_kernel", kernel_offset_deltas_cover_the_3x3x3_kernel, false},
       {"coord_map_builds_and_looks_up", coord_map_builds_and_looks_up, true},

@@ -280,3 +280,19 @@ def test_sparse_argument_errors():
                      T([108], _lib.I32), T([800, 3], _lib.I32), T([800], _lib.I32), T([800, 2], _lib.F32),
                      T([100, 8], _lib.F32), T([1], _lib.I32), None)
     assert rc == _lib.ERR_SHAPE and "subdivision logits must be" in msg
+
+
+def test_sdpa_layernorm_rope2d_argument_errors():
+    q, k, v, o = T([2, 4, 33, 64]), T([2, 4, 50, 64]), T([2, 4, 50, 64]), T([2, 4, 33, 64])
+    w, b = T([64], _lib.F32), T([64], _lib.F32)
+    cs, sn = T([2, 33, 64], _lib.F32), T([2, 33, 64], _lib.F32)
+    rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, None, b, 1e-5, cs, sn, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_NULL and "weight and bias" in msg
+    rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, T([63], _lib.F32), b, 1e-5, cs, sn, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, w, b, 1e-5, T([2, 34, 64], _lib.F32), sn, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_SHAPE and "cos_full" in msg
+    rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, w, b, -1.0, cs, sn, k, v, 0.125, o, None)
+    assert rc == _lib.ERR_VALUE
+    rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, w, b, 1e-5, cs, sn, k, v, 0.0, o, None)
+    assert rc == _lib.ERR_VALUE

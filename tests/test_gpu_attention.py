@@ -208,3 +208,44 @@ def test_sdpa_graph_replay_matches_eager(dev, ops):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("d,case", [(64, "fused"), (128, "fused"), (64, "unaligned_q"), (64, "bf16_tables")])
+def test_sdpa_layernorm_rope2d_equals_the_two_launches(dev, ops, orc, d, case):
+    """VGGT attention with q's LayerNorm + 2D RoPE in the Q load
+    (vggt.rs:170-183) equals lux3d_qk_layernorm_rope2d followed by lux3d_sdpa
+    bit for bit (the same arithmetic); the fused result is also checked
+    against the oracle's LayerNorm+RoPE then attention."""
+    from lux3d_fused import synth
+    _print_case(op="sdpa_layernorm_rope2d", d=d, case=case)
+    b, h = 2, 4
+    pos = synth.vggt_positions(b, 37, 37)           # [b, 1374, 2]: 5 specials + the 37 x 37 grid
+    n = pos.shape[1]
+    g = torch.Generator(device="cpu").manual_seed(d + len(case))
+    width = d + 1 if case == "unaligned_q" else d
+    qkv = (torch.randn((b, n, 3, h, width), generator=g) * 2 + 0.5).to(dev).to(torch.bfloat16).permute(2, 0, 3, 1, 4)
+    q_raw, k_raw, v = qkv[0][..., -d:], qkv[1][..., :d], qkv[2][..., :d]
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    qb = (0.1 * torch.randn(d, generator=g)).to(dev)
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    kb = (0.1 * torch.randn(d, generator=g)).to(dev)
+    emb = ops.Rope2d(100.0).embeddings(torch.from_numpy(pos).to(dev), d)
+    if case == "bf16_tables":
+        emb = ops.RopeEmbeddings(emb.cos_full.to(torch.bfloat16), emb.sin_alt_full.to(torch.bfloat16))
+    k_n = ops.apply_layernorm_rope(k_raw, (kw, kb, 1e-6), emb)
+    scale = 1.0 / np.sqrt(d)
+    fused = ops.sdpa_layernorm_rope2d(q_raw, (qw, qb, 1e-6), emb, k_n, v, scale)
+    q_n = ops.apply_layernorm_rope(q_raw, (qw, qb, 1e-6), emb)
+    two = ops.sdpa(q_n, k_n, v, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two)
+    if case == "fused":
+        qo = orc.layernorm_rope2d(host(q_raw, "bf16"), qw.cpu().numpy(), qb.cpu().numpy(), 1e-6,
+                                  emb.cos_full.reshape(b, n, d).cpu().numpy(),
+                                  emb.sin_alt_full.reshape(b, n, d).cpu().numpy(), dt=orc.BF16)
+        want, wabs = orc.sdpa(qo, host(k_n, "bf16"), host(v, "bf16"), scale, dt=orc.BF16, with_abs=True)
+        # the oracle's q may differ from the kernel's by the LayerNorm+RoPE
+        # tolerance (2 bf16 ulp): allow that on top of the attention bound
+        g64, w64 = to_f64(host(fused, "bf16"), "bf16"), to_f64(want, "bf16")
+        bound = 2 * ULP["bf16"] * np.abs(w64) + 4 * ULP["bf16"] * wabs.astype(np.float64) + 1e-6
+        assert np.all(np.abs(g64 - w64) <= bound)
