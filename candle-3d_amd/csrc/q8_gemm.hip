@@ -13,15 +13,17 @@
 // are only 2-byte aligned, into int8 [N, K] row-major plus f32 scales
 // [N, K/32], so the GEMM streams them with 16-byte loads.
 //
-// GEMM tiling: a 256-thread workgroup computes a BM x BN tile of y; its four
-// wavefronts each own (BM/2) x (BN/2) as 32 x 32 MFMA tiles with f32
-// accumulators. Per k-step of BK (two Q8_0 blocks where k allows) the
-// workgroup stages x[BM x BK] and the dequantised W[BN x BK] as bf16 in LDS
-// (double-buffered, rows padded by 16 bytes against bank conflicts); the
-// next k-step's global loads are issued before the current step's MFMAs, so
-// one barrier per k-step suffices. Global loads go through the caches: every
-// x tile is read by each column block and every weight tile by each row
-// block, so L2 and the Infinity Cache serve most of them.
+// Two GEMM kernels (both one rounding of the f32 sum per output):
+// - q8_0_gemm_ring_kernel (K % 64 == 0, the common case): a 512-thread
+//   workgroup per CU computes a 256 x 256 tile; x, the int8 weights and the
+//   scales stream through a 3-stage LDS ring by direct global->LDS loads;
+//   each wavefront dequantises its own 32 weight columns once per k-step.
+// - q8_0_gemm_kernel (any K % 32 == 0): a 256-thread workgroup computes a
+//   128 x 128 tile; x and the dequantised W are staged as bf16 in LDS,
+//   double-buffered, through registers.
+// Within a k-step the two kernels assign k to MFMA sub-steps differently, so
+// their outputs can differ in the last bit of the f32 sum; each is
+// deterministic.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -189,14 +191,289 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
   }
 }
 
-// Tile choice (measured on MI355X, TFLOP/s at 1029x1024x4096 /
-// 4096x2048x8192): 128x128 tiles with 64-deep k-steps, cached global loads
-// (each x tile is read by every column block, each weight tile by every row
-// block) and two wavefronts per SIMD: 321 / 651. Non-temporal loads: 318 /
-// 516; 256x128: 217 / 553; 256x256: 130 / 605; 128x128 with k-steps of 32:
-// 277 / 519 (used when K is not a multiple of 64).
+// ---- GEMM through an LDS ring fed by direct loads ---------------------------
+//
+// One 512-thread workgroup per CU computes a 256 x 256 tile of y. Its eight
+// wavefronts each own 32 columns and all 256 rows (eight 32 x 32 MFMA tiles),
+// so every weight element is dequantised by exactly one wavefront and
+// amortised over 256 rows of x.
+//
+// Operands reach LDS by direct global->LDS loads (buffer_load ... lds, 16 or
+// 4 bytes per lane, written in lane order at the address in M0) through a
+// RING_STAGES-deep ring; no global load targets registers inside the k loop,
+// so the loads of the next stages stay in flight across k-steps. One stage
+// (k-step of 64) holds:
+//   x       256 rows x 128 bytes, chunk c of row r in slot c ^ ((r >> 1) & 7)
+//           (conflict-free fragment reads without padding);
+//   weights per wavefront 2 KB: lane l's 16-byte half q (q = 0, 1) of the
+//           32 int8 it needs at q * 1024 + l * 16;
+//   scales  per wavefront 256 bytes: lane l's f32 scale at l * 4.
+// k order: within a k-step, lane half h (lane / 32) of sub-step s holds
+// k = 32 h + 8 s + e (e < 8) for both operands, so each lane's weight bytes
+// for the step are 32 contiguous int8 of one Q8_0 block with one scale.
+// The loads are inline assembly: the compiler then neither counts them nor
+// inserts conservative waits for them, and the waits below are explicit
+// (vmcnt counts a wavefront's own loads in issue order).
+//
+// Sub-steps are software-pipelined: the fragments and dequantised weights of
+// sub-step s + 1 are produced while the MFMAs of s run; the barrier sits
+// before the last sub-step's MFMAs, which then overlap the first reads of the
+// next stage. The epilogue stages each wavefront's block through the ring
+// (bias added, rounded once) and writes whole 16-byte row pieces.
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRingStages = 3;
+constexpr int kRingThreads = 512;
+constexpr int kRingA = 256 * 128, kRingW = 256 * 64, kRingS = 256 * 8;
+constexpr int kRingStage = kRingA + kRingW + kRingS;  // 51,200 bytes
+constexpr int kRingOps = 4 + 2 + 1;                   // direct loads per wavefront per stage
+
+// A raw buffer descriptor (no stride, num_records bytes from base) for the
+// direct loads; the fields are wave-uniform, readfirstlane keeps them scalar.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, int64_t bytes) {
+  const uint64_t b = (uint64_t)base;
+  const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
+  return i32x4_t{(int)__builtin_amdgcn_readfirstlane((uint32_t)b), (int)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)),
+                 __builtin_amdgcn_readfirstlane(n), 0x00020000};
+}
+// Each lane reads 16 (4) bytes at voff + soff of the buffer; the wavefront
+// writes them in lane order at LDS byte address lds.
+__device__ __forceinline__ void lds_load16(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
+               : "memory", "m0");
+}
+// s_waitcnt immediates (gfx9 layout): vmcnt(n) with lgkmcnt(0), and vmcnt(n) alone
+constexpr int waitcnt_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// 8 int8 (two dwords) -> bf16(f32(q) * d), RNE; q * d is exact in f32
+__device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) {
+  uint32_t pk[4];
+  const uint32_t w2[2] = {lo, hi};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t v = w2[j];
+    const float f0 = (float)(int8_t)(v & 0xFFu) * d, f1 = (float)(int8_t)((v >> 8) & 0xFFu) * d;
+    const float f2 = (float)(int8_t)((v >> 16) & 0xFFu) * d, f3 = (float)(int8_t)(v >> 24) * d;
+    pk[2 * j] = pack_bf16x2(f0, f1);
+    pk[2 * j + 1] = pack_bf16x2(f2, f3);
+  }
+  return __builtin_bit_cast(bf16x8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+}
+
+// Needs K % 64 == 0 and every descriptor extent below 2^31 bytes (checked by
+// the dispatcher). Tile order: workgroup ids are dealt round-robin to the 8
+// XCDs; they are renumbered so that each XCD takes a contiguous range, walked
+// in groups of GM row tiles (columns fastest within a group), so the tiles
+// running on one XCD share x rows and weight columns in its L2.
+template <typename OUT, int GM>
+__global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
+  constexpr int BM = 256, BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
+  __shared__ __align__(16) char ring[NS * kRingStage];
+
+  const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
+  const int per = G / 8, rem = G % 8, xcd = bid % 8, pos = bid / 8;
+  const int lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + pos;
+  const int group = lid / (GM * tiles_n), first_m = group * GM;
+  const int gsize = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+  const int in_group = lid - group * GM * tiles_n;
+  const int tm = first_m + in_group % gsize, tn = in_group / gsize;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5, lrow = lane & 31;
+  const int64_t m0 = (int64_t)tm * BM, c0 = (int64_t)tn * BN;
+  const int64_t ncol = c0 + wave * 32 + lrow, nc = ncol < p.N ? ncol : p.N - 1;  // past N: clamped, never stored
+  const int64_t nblk = p.K / 32;
+  const int nk = (int)(p.K / BK);
+
+  // direct-load sources: descriptors on the tile's first row / column, a
+  // fixed per-lane offset, the k-step advance in the scalar offset
+  uint32_t xoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = wave * 4 + i;  // 1 KB segment = 8 rows
+    const int r = 8 * g + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+    const int64_t gr = m0 + r < p.M ? m0 + r : p.M - 1;  // rows past M: clamped, never stored
+    xoff[i] = (uint32_t)(((gr - m0) * p.ldx + 8 * c) * 2);
+  }
+  const i32x4_t xr = buffer_rsrc(reinterpret_cast<const char *>(p.x) + m0 * p.ldx * 2, ((p.M - 1 - m0) * p.ldx + p.K) * 2);
+  const i32x4_t wr = buffer_rsrc(p.qs + c0 * p.K, (p.N - c0) * p.K);
+  const i32x4_t sr = buffer_rsrc(p.scales + c0 * nblk, (p.N - c0) * nblk * 4);
+  const uint32_t woff = (uint32_t)((nc - c0) * p.K + 32 * h);
+  const uint32_t soff = (uint32_t)(((nc - c0) * nblk + h) * 4);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring;
+  auto issue = [&](int kt, int buf) {
+    const uint32_t st = lds0 + buf * kRingStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 2, __builtin_amdgcn_readfirstlane(st + (wave * 4 + i) * 1024));
+    lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048));
+    lds_load16(wr, woff, (uint32_t)kt * BK + 16, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048 + 1024));
+    lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + kRingW + wave * 256));
+  };
+
+  // fragment of M-tile i, sub-step s at fbase[s] + i * 4096 (the swizzle only
+  // depends on the row within a 32-row tile)
+  int fbase[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) fbase[s] = lrow * 128 + (((4 * h + s) ^ ((lrow >> 1) & 7)) << 4);
+  uint4 w0, w1;
+  float sc;
+  auto read_w = [&](const char *st) {
+    w0 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + lane * 16);
+    w1 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + 1024 + lane * 16);
+    sc = *reinterpret_cast<const float *>(st + kRingA + kRingW + wave * 256 + lane * 4);
+  };
+  auto make_b = [&](int s) {
+    const uint4 &v = s < 2 ? w0 : w1;
+    return (s & 1) ? dequant8(v.z, v.w, sc) : dequant8(v.x, v.y, sc);
+  };
+  auto read_a = [&](const char *st, int s, bf16x8_t (&a)[TM]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const bf16x8_t *>(st + fbase[s] + i * 4096);
+  };
+  f32x16_t acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) acc[i] = f32x16_t{};
+  auto mfmas = [&](const bf16x8_t (&a)[TM], bf16x8_t b) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b, acc[i], 0, 0, 0);
+  };
+
+  // Prologue: stages 0 .. NS-2. The loop body is branch-free: past the last
+  // k-step it reloads the last stage (in bounds) into a slot that is not read
+  // for data again, so the wait counts are the same every step.
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) issue(st < nk ? st : nk - 1, st);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kRingOps));  // stage 0 landed
+  __builtin_amdgcn_s_barrier();
+
+  bf16x8_t a0[TM], a1[TM], b0, b1;
+  read_w(ring);
+  read_a(ring, 0, a0);
+  b0 = make_b(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    // the slot refilled here was last read in step kt - 1, before its barrier
+    issue(kt + NS - 1 < nk ? kt + NS - 1 : nk - 1, (kt + NS - 1) % NS);
+    __builtin_amdgcn_sched_barrier(0);
+    const char *st = ring + (kt % NS) * kRingStage;
+    read_a(st, 1, a1);
+    b1 = make_b(1);
+    mfmas(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(st, 2, a0);
+    b0 = make_b(2);
+    mfmas(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(st, 3, a1);
+    b1 = make_b(3);
+    mfmas(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage kt + 1 landed (only the stages issued after it may be in flight)
+    // and this wavefront's reads of stage kt are done; then every one's
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0((NS - 2) * kRingOps));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const char *nx = ring + ((kt + 1) % NS) * kRingStage;
+    read_w(nx);
+    read_a(nx, 0, a0);
+    mfmas(a1, b1);
+    b0 = make_b(0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // the trailing reloads and reads
+
+  char *ybase = reinterpret_cast<char *>(p.y);
+  const float bias = (p.bias && ncol < p.N) ? p.bias[ncol] : 0.f;
+  constexpr int EB = OUT::code == LUX3D_F32 ? 4 : 2;
+  if (((uintptr_t)p.y % 16 == 0) && ((p.ldy * EB) % 16 == 0)) {
+    // stage the wavefront's 256 x 32 block through the ring, 128 rows per
+    // pass (rows padded by 16 bytes), and store whole 16-byte row pieces
+    constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, REGION = 128 * LROW, CPR = ROW_B / 16, EPC = 16 / EB;
+    static_assert(8 * REGION <= NS * kRingStage, "epilogue staging fits the ring");
+    __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
+    char *reg = ring + wave * REGION;
+    const int64_t c0w = c0 + wave * 32;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+      for (int ii = 0; ii < TM / 2; ++ii)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = ii * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          const float v = acc[pass * (TM / 2) + ii][e] + bias;
+          if constexpr (EB == 4) *reinterpret_cast<float *>(reg + r * LROW + lrow * 4) = v;
+          else if constexpr (OUT::code == LUX3D_BF16)
+            *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+          else *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
+        }
+#pragma unroll
+      for (int it = 0; it < 128 * CPR / 64; ++it) {
+        const int q = it * 64 + lane, r = q / CPR, part = q % CPR;
+        const int64_t row = m0 + pass * 128 + r, col = c0w + part * EPC;
+        if (row >= p.M || col >= p.N) continue;
+        const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * LROW + part * 16);
+        char *dst = ybase + (row * p.ldy + col) * EB;
+        if (col + EPC <= p.N) {
+          *reinterpret_cast<uint4 *>(dst) = v;
+        } else {
+          const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int k = 0; k < EPC; ++k)
+            if (col + k < p.N) {
+              if constexpr (EB == 4) reinterpret_cast<uint32_t *>(dst)[k] = w4[k];
+              else reinterpret_cast<uint16_t *>(dst)[k] = (uint16_t)(w4[k >> 1] >> (16 * (k & 1)));
+            }
+        }
+      }
+    }
+    return;
+  }
+  // y rows not 16-byte aligned: one element per store
+  if (ncol < p.N) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row >= p.M) continue;
+        store1<OUT>(ybase, row * p.ldy + ncol, acc[i][e] + bias);
+      }
+  }
+}
+
+// The ring kernel's buffer descriptors address at most 2^31 - 1 bytes from
+// the first row / column of a tile; 32-bit per-lane offsets cover a tile.
+bool ring_fits(const Q8GemmParams &p) {
+  const int64_t lim = 0x7FFFFFFF;
+  return p.K % 64 == 0 && ((p.M - 1) * p.ldx + p.K) * 2 <= lim && p.N * p.K <= lim && p.N * (p.K / 32) * 4 <= lim &&
+         (p.M + 255) / 256 * ((p.N + 255) / 256) <= INT32_MAX;
+}
+
+// Kernel choice (measured on MI355X, graph-timed over rotating inputs):
+// the ring kernel when K % 64 == 0, its descriptors fit and its 256 x 256
+// tiles cover every CU at least once: 1,018 TFLOP/s at 4096x2048x8192
+// (512 tiles). With fewer tiles, one workgroup per CU leaves CUs idle and
+// the 128 x 128 kernel (four times the workgroups) is faster: 307 against
+// 267 TFLOP/s at 1029x1024x4096 (80 ring tiles). That kernel runs 64-deep
+// k-steps, cached loads, two wavefronts per SIMD; 32-deep k-steps when K is
+// not a multiple of 64.
+constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
+
 template <typename OUT>
 hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
+  const int64_t ring_tiles = (p.M + 255) / 256 * ((p.N + 255) / 256);
+  if (ring_fits(p) && ring_tiles >= kRingMinTiles) {
+    const int tiles_m = (int)((p.M + 255) / 256), tiles_n = (int)((p.N + 255) / 256);
+    hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0, s, p,
+                       tiles_m, tiles_n);
+    return hipGetLastError();
+  }
   const dim3 block(kGemmThreads);
 #define LUX3D_GEMM_TILE(BM_, BN_, BK_, W_)                                                              \
   {                                                                                                     \

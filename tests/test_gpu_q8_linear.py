@@ -74,7 +74,11 @@ def make_problem(synth, orc, dev, m, k, n, seed, bias=True):
     return xd, blocks, b
 
 
-@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136), (77, 96, 100)])
+# These shapes take the 128 x 128 kernel (64-deep k-steps, or 32-deep for
+# (77, 96, 100)); the ring kernel needs at least 256 of its 256 x 256 tiles
+# (test_q8_0_linear_ring_kernel below).
+@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136), (77, 96, 100),
+                                   (64, 128, 100)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_q8_0_linear_matches_oracle(dev, ops, orc, synth, m, k, n, out):
     print(f"\n[case] q8_0_linear m={m} k={k} n={n} out={out}", flush=True)
@@ -114,6 +118,34 @@ def test_q8_0_linear_no_bias_f16_out_and_strided_rows(dev, ops, orc, synth):
     want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, None, orc.F16, with_abs=True)
     assert_gemm_close(host(ywide[:, :n], "f16"), want, abs_sum, "f16", "f16 out, strided rows")
     assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("extra", [0, 3])
+def test_q8_0_linear_ring_kernel(dev, ops, orc, synth, out, extra):
+    """The 256 x 256 LDS-ring kernel: x [4353, 128] -> [4353, 3700] is 18 x 15
+    = 270 tiles (not a multiple of the 8 XCDs), the last tile row holds one
+    row and the last column piece 4 columns. y is a view of a buffer `extra`
+    columns wider: 16-byte aligned rows (extra 0) take the LDS-staged
+    epilogue, unaligned rows (extra 3) the one-element-per-store one. The
+    oracle checks the first and last 40 rows and 48 sampled between."""
+    m, k, n = 4353, 128, 3700
+    print(f"\n[case] q8_0_linear ring kernel out={out} ldy={n + extra}", flush=True)
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 760 + extra)
+    ywide = torch.zeros((m, n + extra), dtype=TDT[out], device=dev)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    bd = torch.from_numpy(b).to(dev)
+    from lux3d_fused import _lib
+    _lib.call("lux3d_q8_0_linear", ops.desc(xd), ops.desc(qs), ops.desc(scales), ops.desc(bd), ops.desc(ywide[:, :n]),
+              None)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(40), np.arange(m - 40, m),
+                                     np.random.default_rng(6).choice(m, 48, replace=False)]))
+    code = {"bf16": orc.BF16, "f32": orc.F32, "f16": orc.F16}[out]
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16")[rows], blocks, n, b, code, with_abs=True)
+    assert_gemm_close(host(ywide[:, :n], out)[rows], want, abs_sum, out, "ring kernel")
+    if extra:
+        assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
 
 
 def test_q8_0_linear_large_sampled_rows(dev, ops, orc, synth):
