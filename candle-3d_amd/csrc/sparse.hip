@@ -255,19 +255,55 @@ __global__ __launch_bounds__(256) void rulebook_clear_kernel(int32_t *counts) {
   if (threadIdx.x < 27) counts[threadIdx.x] = 0;
 }
 
-// pairs[k][j] = (dst row i, src row nbr[i][k]) for every present neighbour;
-// the order inside a tap is arbitrary (each dst row occurs once per tap).
+// pairs[k][j] = (dst row i, src row nbr[i][k]) for every present neighbour.
+// One thread per voxel; a workgroup reserves each tap's slots with a single
+// global atomic (wave counts from ballots, summed in LDS) and places its pairs
+// in voxel order within that range, so the atomics are 27 per 256 voxels
+// instead of one per present neighbour. The order of the workgroups' ranges
+// inside a tap is arbitrary (each dst row occurs once per tap).
 __global__ __launch_bounds__(256) void rulebook_kernel(const int32_t *nbr, int64_t n, int32_t *pairs,
                                                        int32_t *counts) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= n * 27) return;
-  const int64_t i = t / 27;
-  const int k = (int)(t % 27);
-  const int32_t s = nbr[t];
-  if (s < 0 || s >= n) return;
-  const int32_t pos = atomicAdd(&counts[k], 1);
-  pairs[((int64_t)k * n + pos) * 2] = (int32_t)i;
-  pairs[((int64_t)k * n + pos) * 2 + 1] = s;
+  __shared__ int32_t rows[256 * 27];
+  __shared__ int32_t wcnt[27][4];
+  __shared__ int32_t base[27];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t i0 = (int64_t)blockIdx.x * 256, i = i0 + t;
+  const int64_t nrow = n - i0 < 256 ? n - i0 : 256;
+  // the workgroup's rows of the neighbour table, read coalesced
+  for (int e = t; e < nrow * 27; e += 256) rows[e] = nbr[i0 * 27 + e];
+  __syncthreads();
+  uint32_t present = 0;
+#pragma unroll
+  for (int k = 0; k < 27; ++k) {
+    const int32_t sk = i < n ? rows[t * 27 + k] : -1;
+    const bool pk = sk >= 0 && sk < n;
+    present |= (uint32_t)pk << k;
+    const uint64_t b = __builtin_amdgcn_ballot_w64(pk);
+    if (lane == 0) wcnt[k][wave] = __builtin_popcountll(b);
+  }
+  __syncthreads();
+  if (t < 27) {
+    int32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int32_t c = wcnt[t][w];
+      wcnt[t][w] = run;  // exclusive prefix over the waves
+      run += c;
+    }
+    base[t] = run ? atomicAdd(&counts[t], run) : 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 27; ++k) {
+    const bool pk = (present >> k) & 1u;
+    const uint64_t b = __builtin_amdgcn_ballot_w64(pk);
+    if (pk) {
+      const int32_t below = (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
+      const int64_t pos = (int64_t)k * n + base[k] + wcnt[k][wave] + below;
+      pairs[pos * 2] = (int32_t)i;
+      pairs[pos * 2 + 1] = rows[t * 27 + k];
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_rows_kernel(float *out, int64_t n, int64_t cout, const float *bias,
@@ -559,7 +595,7 @@ hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s) {
 hipError_t launch_sparse_rulebook(const int32_t *nbr, int64_t n, int32_t *pairs, int32_t *counts, hipStream_t s) {
   if ((n * 27 + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rulebook_clear_kernel, dim3(1), dim3(256), 0, s, counts);
-  if (n > 0) hipLaunchKernelGGL(rulebook_kernel, dim3(grid_of(n * 27)), dim3(256), 0, s, nbr, n, pairs, counts);
+  if (n > 0) hipLaunchKernelGGL(rulebook_kernel, dim3(grid_of(n)), dim3(256), 0, s, nbr, n, pairs, counts);
   return hipGetLastError();
 }
 

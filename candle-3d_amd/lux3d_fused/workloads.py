@@ -548,6 +548,30 @@ def cfg3_sparse_conv_c256_output_stationary(dev) -> Workload:
     return _sparse_conv(dev, "sparse_conv_c256_output_stationary", 150000, 256, 256, 10, rulebook=False)
 
 
+def cfg3_sparse_rulebook(dev) -> Workload:
+    """The per-tap pair lists of a coordinate set (lux3d_sparse_rulebook),
+    built once per set and shared by every conv on it; the 150k shell set at
+    resolution 256. Algorithmic bytes: the neighbour table read, the pairs
+    written (8 bytes each) and the 27 counters."""
+    from . import _lib
+    coords = torch.from_numpy(_shell_coords(150000, 256, 11)).to(dev)
+    n = coords.shape[0]
+    nbr = ops.sparse_neighbors(coords)
+    used = int((nbr >= 0).sum().item())
+    pairs = [torch.empty((27, n, 2), dtype=torch.int32, device=dev) for _ in range(2)]
+    counts = [torch.empty(27, dtype=torch.int32, device=dev) for _ in range(2)]
+    dn = ops.desc(nbr)
+    dp, dc = [ops.desc(v) for v in pairs], [ops.desc(v) for v in counts]
+
+    def launch(i):
+        _lib.call("lux3d_sparse_rulebook", dn, dp[i % 2], dc[i % 2], _cur())
+    nbytes = n * 27 * 4 + used * 8 + 27 * 4
+    wl = Workload("sparse_rulebook", 3, "rulebook_kernel", "int32", nbytes,
+                  f"{n} shell voxels in 256^3, {used / n:.1f} active taps per voxel", launch, 2, reps=20)
+    wl._keep = (coords, nbr, pairs, counts, dn, dp, dc)
+    return wl
+
+
 def cfg3_c2s(dev) -> Workload:
     """channel_to_spatial (trellis2_sparse.rs:269-338) after the stage-0 C2S
     conv1 (1024 -> 8 x 512 channels, f32) on 24k parents, about half the
@@ -607,5 +631,6 @@ EXTRAS: List[Callable] = [
     cfg3_sparse_conv_c1024,
     cfg3_sparse_conv_c256,
     cfg3_sparse_conv_c256_output_stationary,
+    cfg3_sparse_rulebook,
     cfg3_c2s,
 ]
