@@ -18,7 +18,7 @@
 //   workgroup per CU computes a 256 x 256 tile; x, the int8 weights and the
 //   scales stream through a 3-stage LDS ring by direct global->LDS loads;
 //   each wavefront dequantises its own 32 weight columns once per k-step.
-// - q8_0_gemm_kernel (any K % 32 == 0): a 256-thread workgroup computes a
+// - q8_0_gemm_kernel (K % 64 == 32): a 256-thread workgroup computes a
 //   128 x 128 tile; x and the dequantised W are staged as bf16 in LDS,
 //   double-buffered, through registers.
 // Within a k-step the two kernels assign k to MFMA sub-steps differently, so
@@ -193,17 +193,18 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
 
 // ---- GEMM through an LDS ring fed by direct loads ---------------------------
 //
-// One 512-thread workgroup per CU computes a 256 x 256 tile of y. Its eight
-// wavefronts each own 32 columns and all 256 rows (eight 32 x 32 MFMA tiles),
-// so every weight element is dequantised by exactly one wavefront and
-// amortised over 256 rows of x.
+// One 512-thread workgroup per CU computes a BM x 256 tile of y (BM = 256,
+// or 128 for problems too small to give every CU a 256-row tile). Its eight
+// wavefronts each own 32 columns and all BM rows (BM / 32 MFMA tiles of
+// 32 x 32), so every weight element is dequantised by exactly one wavefront
+// and amortised over BM rows of x.
 //
 // Operands reach LDS by direct global->LDS loads (buffer_load ... lds, 16 or
 // 4 bytes per lane, written in lane order at the address in M0) through a
 // RING_STAGES-deep ring; no global load targets registers inside the k loop,
 // so the loads of the next stages stay in flight across k-steps. One stage
 // (k-step of 64) holds:
-//   x       256 rows x 128 bytes, chunk c of row r in slot c ^ ((r >> 1) & 7)
+//   x       BM rows x 128 bytes, chunk c of row r in slot c ^ ((r >> 1) & 7)
 //           (conflict-free fragment reads without padding);
 //   weights per wavefront 2 KB: lane l's 16-byte half q (q = 0, 1) of the
 //           32 int8 it needs at q * 1024 + l * 16;
@@ -225,9 +226,7 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kRingStages = 3;
 constexpr int kRingThreads = 512;
-constexpr int kRingA = 256 * 128, kRingW = 256 * 64, kRingS = 256 * 8;
-constexpr int kRingStage = kRingA + kRingW + kRingS;  // 51,200 bytes
-constexpr int kRingOps = 4 + 2 + 1;                   // direct loads per wavefront per stage
+constexpr int kRingW = 256 * 64, kRingS = 256 * 8;  // weights and scales per stage (256 columns)
 
 // A raw buffer descriptor (no stride, num_records bytes from base) for the
 // direct loads; the fields are wave-uniform, readfirstlane keeps them scalar.
@@ -271,9 +270,13 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) 
 // XCDs; they are renumbered so that each XCD takes a contiguous range, walked
 // in groups of GM row tiles (columns fastest within a group), so the tiles
 // running on one XCD share x rows and weight columns in its L2.
-template <typename OUT, int GM>
+template <typename OUT, int GM, int BM>
 __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
-  constexpr int BM = 256, BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
+  constexpr int BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
+  constexpr int kRingA = BM * 128, kRingStage = kRingA + kRingW + kRingS;  // 51,200 / 34,816 bytes
+  constexpr int SEGW = BM / 64;                    // x segments (1 KB = 8 rows) per wavefront
+  constexpr int kRingOps = SEGW + 2 + 1;           // direct loads per wavefront per stage
+  static_assert(BM == 128 || BM == 256, "tile rows");
   __shared__ __align__(16) char ring[NS * kRingStage];
 
   const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
@@ -293,25 +296,28 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
 
   // direct-load sources: descriptors on the tile's first row / column, a
   // fixed per-lane offset, the k-step advance in the scalar offset
-  uint32_t xoff[4];
+  uint32_t xoff[SEGW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = wave * 4 + i;  // 1 KB segment = 8 rows
+  for (int i = 0; i < SEGW; ++i) {
+    const int g = wave * SEGW + i;  // 1 KB segment = 8 rows
     const int r = 8 * g + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
     const int64_t gr = m0 + r < p.M ? m0 + r : p.M - 1;  // rows past M: clamped, never stored
     xoff[i] = (uint32_t)(((gr - m0) * p.ldx + 8 * c) * 2);
   }
-  const i32x4_t xr = buffer_rsrc(reinterpret_cast<const char *>(p.x) + m0 * p.ldx * 2, ((p.M - 1 - m0) * p.ldx + p.K) * 2);
-  const i32x4_t wr = buffer_rsrc(p.qs + c0 * p.K, (p.N - c0) * p.K);
-  const i32x4_t sr = buffer_rsrc(p.scales + c0 * nblk, (p.N - c0) * nblk * 4);
+  // each descriptor spans just the tile's rows / columns
+  const int64_t last_row = p.M - 1 - m0 < BM - 1 ? p.M - 1 - m0 : BM - 1;
+  const int64_t ncols = p.N - c0 < BN ? p.N - c0 : BN;
+  const i32x4_t xr = buffer_rsrc(reinterpret_cast<const char *>(p.x) + m0 * p.ldx * 2, (last_row * p.ldx + p.K) * 2);
+  const i32x4_t wr = buffer_rsrc(p.qs + c0 * p.K, ncols * p.K);
+  const i32x4_t sr = buffer_rsrc(p.scales + c0 * nblk, ncols * nblk * 4);
   const uint32_t woff = (uint32_t)((nc - c0) * p.K + 32 * h);
   const uint32_t soff = (uint32_t)(((nc - c0) * nblk + h) * 4);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring;
   auto issue = [&](int kt, int buf) {
     const uint32_t st = lds0 + buf * kRingStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 2, __builtin_amdgcn_readfirstlane(st + (wave * 4 + i) * 1024));
+    for (int i = 0; i < SEGW; ++i)
+      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 2, __builtin_amdgcn_readfirstlane(st + (wave * SEGW + i) * 1024));
     lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048));
     lds_load16(wr, woff, (uint32_t)kt * BK + 16, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048 + 1024));
     lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + kRingW + wave * 256));
@@ -392,30 +398,31 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
   const float bias = (p.bias && ncol < p.N) ? p.bias[ncol] : 0.f;
   constexpr int EB = OUT::code == LUX3D_F32 ? 4 : 2;
   if (((uintptr_t)p.y % 16 == 0) && ((p.ldy * EB) % 16 == 0)) {
-    // stage the wavefront's 256 x 32 block through the ring, 128 rows per
+    // stage the wavefront's BM x 32 block through the ring, RP rows per
     // pass (rows padded by 16 bytes), and store whole 16-byte row pieces
-    constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, REGION = 128 * LROW, CPR = ROW_B / 16, EPC = 16 / EB;
+    constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB;
+    constexpr int RP = 8 * 128 * LROW <= NS * kRingStage ? 128 : 64, REGION = RP * LROW;
     static_assert(8 * REGION <= NS * kRingStage, "epilogue staging fits the ring");
     __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
     char *reg = ring + wave * REGION;
     const int64_t c0w = c0 + wave * 32;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int pass = 0; pass < BM / RP; ++pass) {
 #pragma unroll
-      for (int ii = 0; ii < TM / 2; ++ii)
+      for (int ii = 0; ii < RP / 32; ++ii)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int r = ii * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-          const float v = acc[pass * (TM / 2) + ii][e] + bias;
+          const float v = acc[pass * (RP / 32) + ii][e] + bias;
           if constexpr (EB == 4) *reinterpret_cast<float *>(reg + r * LROW + lrow * 4) = v;
           else if constexpr (OUT::code == LUX3D_BF16)
             *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
           else *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
         }
 #pragma unroll
-      for (int it = 0; it < 128 * CPR / 64; ++it) {
+      for (int it = 0; it < RP * CPR / 64; ++it) {
         const int q = it * 64 + lane, r = q / CPR, part = q % CPR;
-        const int64_t row = m0 + pass * 128 + r, col = c0w + part * EPC;
+        const int64_t row = m0 + pass * RP + r, col = c0w + part * EPC;
         if (row >= p.M || col >= p.N) continue;
         const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * LROW + part * 16);
         char *dst = ybase + (row * p.ldy + col) * EB;
@@ -447,43 +454,40 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
   }
 }
 
-// The ring kernel's buffer descriptors address at most 2^31 - 1 bytes from
-// the first row / column of a tile; 32-bit per-lane offsets cover a tile.
+// The ring kernel's buffer descriptors span one tile (at most 256 rows of x,
+// 256 weight rows and their scales) and must stay below 2^31 bytes; its
+// per-lane offsets are 32-bit.
 bool ring_fits(const Q8GemmParams &p) {
   const int64_t lim = 0x7FFFFFFF;
-  return p.K % 64 == 0 && ((p.M - 1) * p.ldx + p.K) * 2 <= lim && p.N * p.K <= lim && p.N * (p.K / 32) * 4 <= lim &&
-         (p.M + 255) / 256 * ((p.N + 255) / 256) <= INT32_MAX;
+  return p.K % 64 == 0 && (255 * p.ldx + p.K) * 2 <= lim && 256 * p.K <= lim &&
+         (p.M + 127) / 128 * ((p.N + 255) / 256) <= INT32_MAX;
 }
 
 // Kernel choice (measured on MI355X, graph-timed over rotating inputs):
-// the ring kernel when K % 64 == 0, its descriptors fit and its 256 x 256
-// tiles cover every CU at least once: 1,018 TFLOP/s at 4096x2048x8192
-// (512 tiles). With fewer tiles, one workgroup per CU leaves CUs idle and
-// the 128 x 128 kernel (four times the workgroups) is faster: 307 against
-// 267 TFLOP/s at 1029x1024x4096 (80 ring tiles). That kernel runs 64-deep
-// k-steps, cached loads, two wavefronts per SIMD; 32-deep k-steps when K is
-// not a multiple of 64.
+// the ring kernel whenever K % 64 == 0 (every shape of the models): 256-row
+// tiles when they cover every CU at least once (1,018 TFLOP/s at
+// 4096x2048x8192, 512 tiles), else 128-row tiles (1029x1024x4096: 9 x 16
+// tiles, 402 against 314 TFLOP/s for the 128 x 128 kernel in a probe). The
+// 128 x 128 kernel with 32-deep k-steps covers K % 64 == 32.
 constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
 
 template <typename OUT>
 hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
-  const int64_t ring_tiles = (p.M + 255) / 256 * ((p.N + 255) / 256);
-  if (ring_fits(p) && ring_tiles >= kRingMinTiles) {
-    const int tiles_m = (int)((p.M + 255) / 256), tiles_n = (int)((p.N + 255) / 256);
-    hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0, s, p,
-                       tiles_m, tiles_n);
+  if (ring_fits(p)) {
+    const int64_t tiles_n = (p.N + 255) / 256, tiles_m256 = (p.M + 255) / 256;
+    if (tiles_m256 * tiles_n >= kRingMinTiles) {
+      hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 256>), dim3((unsigned)(tiles_m256 * tiles_n)), dim3(kRingThreads),
+                         0, s, p, (int)tiles_m256, (int)tiles_n);
+    } else {
+      const int64_t tiles_m = (p.M + 127) / 128;
+      hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 128>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0,
+                         s, p, (int)tiles_m, (int)tiles_n);
+    }
     return hipGetLastError();
   }
-  const dim3 block(kGemmThreads);
-#define LUX3D_GEMM_TILE(BM_, BN_, BK_, W_)                                                              \
-  {                                                                                                     \
-    const dim3 grid((unsigned)((p.N + BN_ - 1) / BN_), (unsigned)((p.M + BM_ - 1) / BM_));              \
-    hipLaunchKernelGGL((q8_0_gemm_kernel<OUT, BM_, BN_, BK_, W_>), grid, block, 0, s, p); \
-    return hipGetLastError();                                                                           \
-  }
-  if (p.K % 64 == 0) LUX3D_GEMM_TILE(128, 128, 64, 2)
-  LUX3D_GEMM_TILE(128, 128, 32, 1)
-#undef LUX3D_GEMM_TILE
+  const dim3 grid((unsigned)((p.N + 127) / 128), (unsigned)((p.M + 127) / 128));
+  hipLaunchKernelGGL((q8_0_gemm_kernel<OUT, 128, 128, 32, 1>), grid, dim3(kGemmThreads), 0, s, p);
+  return hipGetLastError();
 }
 
 }  // namespace

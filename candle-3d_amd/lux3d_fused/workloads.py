@@ -398,7 +398,7 @@ def _q8_linear(dev, cfg, m, k, n, what) -> Workload:
     def launch(i):
         j = i % n_sets
         _lib.call("lux3d_q8_0_linear", dx[j], dq, dsc, db, dy[j], _cur())
-    wl = Workload("q8_0_linear", cfg, "q8_0_gemm_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
+    wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
                   f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
     wl._keep = (xs, ys, qs, scales, bias, blocks, dx, dy, dq, dsc, db)
     return wl

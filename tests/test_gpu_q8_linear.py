@@ -74,9 +74,10 @@ def make_problem(synth, orc, dev, m, k, n, seed, bias=True):
     return xd, blocks, b
 
 
-# These shapes take the 128 x 128 kernel (64-deep k-steps, or 32-deep for
-# (77, 96, 100)); the ring kernel needs at least 256 of its 256 x 256 tiles
-# (test_q8_0_linear_ring_kernel below).
+# K % 64 == 0 takes the LDS-ring kernel with 128-row tiles at these sizes
+# (fewer than 256 tiles of 256 rows); (77, 96, 100) takes the 128 x 128
+# kernel with 32-deep k-steps. The 256-row ring tiles: the ring-kernel test
+# and the large sampled test below.
 @pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136), (77, 96, 100),
                                    (64, 128, 100)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
@@ -123,9 +124,9 @@ def test_q8_0_linear_no_bias_f16_out_and_strided_rows(dev, ops, orc, synth):
 @pytest.mark.parametrize("out", ["bf16", "f32", "f16"])
 @pytest.mark.parametrize("extra", [0, 3])
 def test_q8_0_linear_ring_kernel(dev, ops, orc, synth, out, extra):
-    """The 256 x 256 LDS-ring kernel: x [4353, 128] -> [4353, 3700] is 18 x 15
-    = 270 tiles (not a multiple of the 8 XCDs), the last tile row holds one
-    row and the last column piece 4 columns. y is a view of a buffer `extra`
+    """The LDS-ring kernel with 256-row tiles: x [4353, 128] -> [4353, 3700]
+    is 18 x 15 = 270 tiles (not a multiple of the 8 XCDs), the last tile row
+    holds one row and the last column piece 4 columns. y is a view of a buffer `extra`
     columns wider: 16-byte aligned rows (extra 0) take the LDS-staged
     epilogue, unaligned rows (extra 3) the one-element-per-store one. The
     oracle checks the first and last 40 rows and 48 sampled between."""
