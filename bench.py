@@ -269,10 +269,13 @@ def main():
             continue
         cfg, dtype, shape, sets, note, flops = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note, wl.flops
         peak_tf = wl.peak_tflops or PEAK_BF16_TFLOPS
+        n = wl.reps or (200 if wl.bytes < 64 << 20 else 50)
         us = step_ops.get(tag)
         if us is None:
-            n = wl.reps or (200 if wl.bytes < 64 << 20 else 50)
             us = time_graph(torch, wl.launch, n)
+        # warm: every launch on rotation set 0, so inputs below the 256 MB
+        # Infinity Cache stay resident between launches
+        us_warm = time_graph(torch, lambda i: wl.launch(0), n)
         gbs = wl.bytes / us / 1e3
         nbytes = wl.bytes
         del wl
@@ -280,6 +283,7 @@ def main():
         cus = copy_ceiling_us(torch, dev, nbytes, 200 if nbytes < 64 << 20 else 50)
         table.append({"op": tag, "config": cfg, "dtype": dtype, "shape": shape,
                       "bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
+                      "warm_us": round(us_warm, 3), "warm_gbs": round(nbytes / us_warm / 1e3, 1),
                       "frac_peak": round(gbs / PEAK_GBS, 4), "runtime_copy_us": round(cus, 3),
                       "speed_vs_runtime_copy": round(cus / us, 4), "target_70pct": bool(target),
                       "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
