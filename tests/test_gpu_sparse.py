@@ -182,9 +182,11 @@ def test_channel_to_spatial(dev, ops, orc, n, c, fdt, ldt):
         assert oc.cpu().tolist() == [[0, 0, 0], [1, 1, 0], [1, 0, 1], [3, 0, 0]]
 
 
-def test_sparse_rulebook_pairs(dev, ops, orc):
-    """Every present neighbour appears once in its tap's list, nothing else."""
-    coords = random_coords(4000, 32, 21, True)
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 4000])
+def test_sparse_rulebook_pairs(dev, ops, orc, n):
+    """Every present neighbour appears once in its tap's list, nothing else
+    (one workgroup per 256 voxels: partial, exact and one-over sizes)."""
+    coords = random_coords(n, 32 if n > 300 else 8, 21 + n, n > 300)[:n]
     nbr = orc.sparse_neighbors(coords)
     rb = ops.SparseRulebook(torch.from_numpy(nbr).to(dev))
     torch.cuda.synchronize()
