@@ -878,7 +878,7 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
     return fail(LUX3D_ERR_LAYOUT, "%s: cos_full and sin_alt_full must share layout and dtype", fn);
   // fused: the matrix-core path, and 16-byte aligned parameters and table rows
   const int tb = elem_bytes(cos_full->dtype);
-  const bool fused = p.mfma && (p.D == 64 || p.D == 128) && aligned16(wp) && aligned16(bp) &&
+  const bool fused = p.mfma && q->dtype != LUX3D_F32 && (p.D == 64 || p.D == 128) && aligned16(wp) && aligned16(bp) &&
                      aligned16(cos_full->data) && aligned16(sin_alt_full->data) && (cN * tb) % 16 == 0 &&
                      (cB * tb) % 16 == 0;
   if (!fused) {
@@ -931,13 +931,14 @@ int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k
   p.v_sb = v->stride[0]; p.v_sh = v->stride[1]; p.v_st = v->stride[2];
   p.o_sb = out->stride[0]; p.o_sh = out->stride[1]; p.o_st = out->stride[2];
   p.scale = scale;
-  // matrix cores: 2-byte types, D 64 / 128, every row start 16-byte aligned
-  bool mfma = q->dtype != LUX3D_F32 && (D == 64 || D == 128);
+  // matrix cores: D 64 / 128, every row start 16-byte aligned
+  bool mfma = D == 64 || D == 128;
+  const int64_t align_el = 16 / elem_bytes(q->dtype);
   for (int i = 0; i < 4 && mfma; ++i) {
     const lux3d_tensor_t *t = ts[i];
     mfma = aligned16(t->data);
     for (int a = 0; a < 3 && mfma; ++a)
-      if (t->shape[a] > 1 && t->stride[a] % 8) mfma = false;
+      if (t->shape[a] > 1 && t->stride[a] % align_el) mfma = false;
   }
   p.mfma = mfma;
   return LUX3D_OK;

@@ -32,6 +32,9 @@
 // XCD (hardware places workgroup i on XCD i % 8) and share its L2 copy of K
 // and V.
 //
+// f32 matrix-core kernel (attn_mfma_f32_kernel): the same scheme on
+// v_mfma_f32_32x32x2_f32 for f32 inputs with D 64 / 128, f32 throughout.
+//
 // Generic kernel (attn_generic_kernel): one wavefront per query row, f32
 // arithmetic throughout (lanes over keys for the scores, over head dims for
 // the output); any float dtype, any alignment, D <= 512.
@@ -427,6 +430,175 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   }
 }
 
+// ---- f32 matrix-core kernel ----------------------------------------------------
+//
+// v_mfma_f32_32x32x2_f32 keeps everything in f32: scores, probabilities (not
+// rounded) and output sums; that is exact_sdpa_heads (attention_math.rs:
+// 244-259) up to the order of the sums. A workgroup of 4 wavefronts owns 128
+// queries (32 per wavefront) of one (batch, head); K and V blocks of BKV keys
+// are double-buffered in LDS, as in the 2-byte kernel.
+//   S^T = K Q^T   k-step c covers dims {c, D/2 + c}: lane half hh supplies
+//                 dim hh * D/2 + c, so each lane's K and Q values are
+//                 contiguous (four k-steps per 16-byte LDS read; Q held in
+//                 registers).
+//   O^T += V^T P^T  k-step i of a 32-key tile pairs the two keys the lane
+//                 halves hold in S^T's i-th accumulator, 8 (i/4) + 4 hh +
+//                 i % 4: each lane passes its own probability, and V is read
+//                 in its natural [key][dim] layout (no transpose).
+template <int D, int BKV, int MINW>
+__global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+  constexpr int BQ = 128;
+  constexpr int KROW = D + 4;              // floats per K row: 16-byte fragment reads conflict-free
+  constexpr int VROW = D + 8;              // floats per V row: the lane halves' rows (4 apart) 32 banks apart
+  constexpr int KCH = BKV * D / 4 / 256;   // 16-byte chunks of K (and of V) per thread per block
+  constexpr int NKT = BKV / 32, NDT = D / 32, HD = D / 2;
+  static_assert(KCH >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
+  __shared__ __align__(16) float smem[2 * BKV * KROW + 2 * BKV * VROW];
+  float(*Ks)[BKV * KROW] = reinterpret_cast<float(*)[BKV * KROW]>(smem);
+  float(*Vs)[BKV * VROW] = reinterpret_cast<float(*)[BKV * VROW]>(smem + 2 * BKV * KROW);
+
+  const int64_t lid = xcd_logical_id(blockIdx.x, nwg);
+  const int64_t bh = lid / nqb, qb = lid % nqb;
+  const int64_t bi = bh / p.H, hi = bh % p.H;
+  const float *qbase = reinterpret_cast<const float *>(p.q) + bi * p.q_sb + hi * p.q_sh;
+  const float *kbase = reinterpret_cast<const float *>(p.k) + bi * p.k_sb + hi * p.k_sh;
+  const float *vbase = reinterpret_cast<const float *>(p.v) + bi * p.v_sb + hi * p.v_sh;
+  float *obase = reinterpret_cast<float *>(p.o) + bi * p.o_sb + hi * p.o_sh;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int64_t Lq = p.Lq, Lk = p.Lk;
+
+  // Q as the B operand: lane holds Q[query l32][hh * D/2 + c], c < D/2
+  float qf[HD];
+  {
+    int64_t qr = qb * BQ + wave * 32 + l32;
+    qr = qr < Lq ? qr : Lq - 1;
+#pragma unroll
+    for (int c4 = 0; c4 < HD / 4; ++c4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(qbase + qr * p.q_st + hh * HD + c4 * 4);
+      qf[c4 * 4] = v4.x; qf[c4 * 4 + 1] = v4.y; qf[c4 * 4 + 2] = v4.z; qf[c4 * 4 + 3] = v4.w;
+    }
+  }
+  // staging: chunk c = t + 256 i holds K / V row c / (D/4), floats 4 (c % (D/4)) ..
+  int s_row[KCH], s_part[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = t + i * 256;
+    s_row[i] = c / (D / 4);
+    s_part[i] = c % (D / 4);
+  }
+  float4 rk[KCH], rv[KCH];
+  // keys past Lk read row Lk - 1 (finite data; their scores are masked)
+  auto load_kv = [&](int64_t j) {
+    const int64_t key0 = j * BKV;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      int64_t key = key0 + s_row[i];
+      key = key < Lk ? key : Lk - 1;
+      rk[i] = *reinterpret_cast<const float4 *>(kbase + key * p.k_st + s_part[i] * 4);
+      rv[i] = *reinterpret_cast<const float4 *>(vbase + key * p.v_st + s_part[i] * 4);
+    }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      *reinterpret_cast<float4 *>(&Ks[buf][s_row[i] * KROW + s_part[i] * 4]) = rk[i];
+      *reinterpret_cast<float4 *>(&Vs[buf][s_row[i] * VROW + s_part[i] * 4]) = rv[i];
+    }
+  };
+
+  f32x16_t o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16_t{};
+  float m = -INFINITY, l = 0.f;
+  const float c2 = p.scale * kLog2e;
+  const int64_t nkv = (Lk + BKV - 1) / BKV;
+  const bool tail = (Lk % BKV) != 0;
+
+  load_kv(0);
+  store_kv(0);
+  lds_barrier();
+
+  auto step = [&](int64_t j, auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    const int buf = (int)(j & 1);
+    if (j + 1 < nkv) load_kv(j + 1);
+    f32x16_t s[NKT];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      s[kt] = f32x16_t{};
+#pragma unroll
+      for (int c4 = 0; c4 < HD / 4; ++c4) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(&Ks[buf][(kt * 32 + l32) * KROW + hh * HD + c4 * 4]);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, qf[c4 * 4], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, qf[c4 * 4 + 1], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, qf[c4 * 4 + 2], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, qf[c4 * 4 + 3], s[kt], 0, 0, 0);
+      }
+    }
+    if constexpr (MASK) {
+      const int lim = (int)(Lk - j * BKV) - 4 * hh;  // local key offsets >= lim + 4 hh are past Lk
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (kt * 32 + 8 * (i >> 2) + (i & 3) >= lim) s[kt][i] = -INFINITY;
+    }
+    // online softmax; the reference maximum moves only when a block's maximum
+    // exceeds it by 2^8 (probabilities stay <= 256), as in the 2-byte kernel
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+    const float cand = half_swap_max(mx) * c2;
+    float mn = m;
+    if (cand > mn + 8.f) mn = cand;
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    m = mn;
+    float ls = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][i], c2, -mn));
+        ls += s[kt][i];
+      }
+    l = l * alpha + ls;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float *vr = &Vs[buf][(kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3)) * VROW + l32];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[dt * 32], s[kt][i], o[dt], 0, 0, 0);
+      }
+    if (j + 1 < nkv) store_kv(buf ^ 1);
+    lds_barrier();
+  };
+  const int64_t nfull = tail ? nkv - 1 : nkv;
+  for (int64_t j = 0; j < nfull; ++j) step(j, std::false_type{});
+  if (tail) step(nkv - 1, std::true_type{});
+
+  // out[query][dim]: lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
+  const int64_t qr = qb * BQ + wave * 32 + l32;
+  const float inv = 1.f / half_swap_sum(l);
+  if (qr < Lq) {
+    float *orow = obase + qr * p.o_st;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4 *>(orow + dt * 32 + 8 * g + 4 * hh) =
+            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+  }
+}
+
 // ---- generic kernel ----------------------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -539,13 +711,27 @@ hipError_t launch_generic(const AttnParams &p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int D, int BKV, int MINW>
+hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
+  const int64_t nqb = (p.Lq + 127) / 128;
+  const int64_t nwg = p.B * p.H * nqb;
+  if (nwg > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
-  if (p.qln && !(p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
+  if (p.qln && !(T::code != LUX3D_F32 && p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);
       if (p.D == 128) return launch_mfma<T, 128, 1, 64, 2, true, true, false>(p, s);
+    }
+  } else {
+    if (p.mfma) {
+      if (p.D == 64) return launch_mfma_f32<64, 64, 2>(p, s);
+      if (p.D == 128) return launch_mfma_f32<128, 32, 2>(p, s);
     }
   }
   return launch_generic<T>(p, s);

@@ -414,15 +414,16 @@ def cfg2_q8_0_linear(dev) -> Workload:
     return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection")
 
 
-def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50) -> Workload:
+def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16) -> Workload:
     """Attention over q, k, v taken as the permuted views of a fused
     [B, N, 3, H, D] qkv buffer (vggt.rs:161-168), output [B, H, N, D]."""
     from . import _lib
     s = synth.config_seed(cfg) + 700
-    qkv0 = _normal(s, (b, n, 3, h, d), dev, torch.bfloat16)
-    n_sets = max(2, _n_sets(qkv0.numel() * 2 + b * h * n * d * 2))
+    esz = torch.empty((), dtype=dt).element_size()
+    qkv0 = _normal(s, (b, n, 3, h, d), dev, dt)
+    n_sets = max(2, _n_sets(qkv0.numel() * esz + b * h * n * d * esz))
     qkvs = [_fill_like(qkv0, j) for j in range(n_sets)]
-    outs = [torch.empty((b, h, n, d), dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+    outs = [torch.empty((b, h, n, d), dtype=dt, device=dev) for _ in range(n_sets)]
     descs = []
     for qkv, o in zip(qkvs, outs):
         v = qkv.permute(2, 0, 3, 1, 4)
@@ -432,12 +433,24 @@ def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50) -> Workload:
     def launch(i):
         dq, dk, dv, do = descs[i % n_sets]
         _lib.call("lux3d_sdpa", dq, dk, dv, scale, do, _cur())
-    nbytes = 4 * b * h * n * d * 2
-    wl = Workload(name, cfg, f"attn_mfma_kernel<BF16,{d}>", "bf16 -> f32 acc", nbytes,
+    nbytes = 4 * b * h * n * d * esz
+    f32 = dt == torch.float32
+    wl = Workload(name, cfg, f"attn_mfma_f32_kernel<{d}>" if f32 else f"attn_mfma_kernel<BF16,{d}>",
+                  "f32 (f32 matrix cores)" if f32 else "bf16 -> f32 acc", nbytes,
                   f"q,k,v [{b},{h},{n},{d}] from qkv [{b},{n},3,{h},{d}] ({what})", launch, n_sets,
-                  flops=4 * b * h * n * n * d, reps=reps)
+                  flops=4 * b * h * n * n * d, reps=reps, peak_tflops=157.3 if f32 else 0.0)
     wl._keep = (qkvs, outs, descs)
     return wl
+
+
+def cfg1_sdpa_frame_f32(dev) -> Workload:
+    # the same VGGT frame attention in f32, the reference's default VGGT
+    # precision (vggt.rs:571-574)
+    return _sdpa(dev, "sdpa_frame_f32", 1, 8, 1374, 16, 64, "VGGT frame attention, f32", dt=torch.float32)
+
+
+def cfg2_sdpa_f32(dev) -> Workload:
+    return _sdpa(dev, "sdpa_f32", 2, 2, 2048, 16, 128, "TripoSG self-attention, f32", dt=torch.float32)
 
 
 def cfg1_sdpa_frame_qln(dev) -> Workload:
@@ -625,6 +638,8 @@ EXTRAS: List[Callable] = [
     cfg2_q8_0_linear,
     cfg1_sdpa_frame,
     cfg1_sdpa_frame_qln,
+    cfg1_sdpa_frame_f32,
+    cfg2_sdpa_f32,
     cfg1_sdpa_global,
     cfg2_sdpa,
     cfg3_sdpa,

@@ -377,11 +377,13 @@ int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t 
  *   one dtype for all four (f32, bf16 or f16); any batch / head / token
  *   strides (the permuted views of a fused qkv buffer pass as they are),
  *   unit innermost stride; Lk >= 1; D <= 512; scale finite and > 0.
- * bf16 / f16 with D = 64 or 128 and every row 16-byte aligned run on the
- * matrix cores: f32 scores, f32 softmax, the probabilities rounded to the
- * input type for P v (f32 accumulation), one rounding of the output. Other
- * cases run a generic kernel in f32 throughout, the arithmetic of
- * exact_sdpa_heads. out must not overlap q, k or v.                          */
+ * D = 64 or 128 with every row 16-byte aligned runs on the matrix cores:
+ * bf16 / f16 with f32 scores, f32 softmax, the probabilities rounded to the
+ * input type for P v (f32 accumulation) and one rounding of the output; f32
+ * on the f32 matrix cores with scores, probabilities and sums all in f32.
+ * Other cases run a generic kernel in f32 throughout. The f32 paths are the
+ * arithmetic of exact_sdpa_heads up to the order of the sums. out must not
+ * overlap q, k or v.                                                         */
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
                lux3d_stream_t stream);

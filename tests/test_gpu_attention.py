@@ -157,15 +157,15 @@ def test_sdpa_reference_kat_f32(dev, ops, orc, t, tkv, seeds):
     assert_attn_close(out, want, wabs, "f32", False, f"kat {t}x{tkv}")
 
 
-@pytest.mark.parametrize("case", ["f32_d64", "bf16_d80", "bf16_unaligned", "f16_d32", "bf16_d256"])
+@pytest.mark.parametrize("case", ["f32_unaligned", "bf16_d80", "bf16_unaligned", "f16_d32", "bf16_d256"])
 def test_sdpa_generic_kernel(dev, ops, orc, case):
     _print_case(case=case)
     dt = case.split("_")[0]
-    d = {"f32_d64": 64, "bf16_d80": 80, "bf16_unaligned": 64, "f16_d32": 32, "bf16_d256": 256}[case]
+    d = {"f32_unaligned": 64, "bf16_d80": 80, "bf16_unaligned": 64, "f16_d32": 32, "bf16_d256": 256}[case]
     g = torch.Generator(device="cpu").manual_seed(len(case) * 31 + d)
     lq, lk = 77, 130
-    if case == "bf16_unaligned":
-        # rows start 2 bytes past a 16-byte boundary: the generic kernel takes it
+    if case.endswith("_unaligned"):
+        # rows start one element past a 16-byte boundary: the generic kernel takes it
         qb = torch.randn((1, 2, lq, d + 1), generator=g).to(dev).to(TDT[dt])
         q = qb[..., 1:]
     else:
@@ -177,6 +177,28 @@ def test_sdpa_generic_kernel(dev, ops, orc, case):
     torch.cuda.synchronize()
     want, wabs = oracle(orc, q, k, v, scale, dt)
     assert_attn_close(out, want, wabs, dt, False, case)
+
+
+@pytest.mark.parametrize("b,n,h,d,lk", [(2, 300, 3, 64, None), (1, 257, 2, 128, None), (1, 77, 2, 128, 130),
+                                         (1, 1, 1, 64, 1), (1, 33, 2, 64, 1000)])
+def test_sdpa_f32_matrix_cores(dev, ops, orc, b, n, h, d, lk):
+    """f32 q, k, v with D 64 / 128 take the f32 matrix-core kernel
+    (v_mfma_f32_32x32x2_f32, f32 scores and probabilities): self-attention on
+    the permuted views of a fused qkv buffer, and cross-attention with key
+    counts that leave a partial block."""
+    _print_case(op="sdpa f32 mfma", b=b, n=n, h=h, d=d, lk=lk)
+    if lk is None:
+        q, k, v = qkv_views(dev, b, n, h, d, "f32", 17 + n)
+    else:
+        g = torch.Generator(device="cpu").manual_seed(n + lk)
+        q = torch.randn((b, h, n, d), generator=g).to(dev)
+        k = torch.randn((b, h, lk, d), generator=g).to(dev)
+        v = torch.randn((b, h, lk, d), generator=g).to(dev)
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, "f32")
+    assert_attn_close(out, want, wabs, "f32", False, f"f32 mfma {b}x{h}x{n}x{d} lk={lk}")
 
 
 def test_sdpa_vggt_global_attention_sampled(dev, ops, orc):
