@@ -809,7 +809,10 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
   const char *fn = "lux3d_q8_0_linear";
   int r;
   RowView xv, yv;
-  if ((r = row_tensor(x, fn, "x", LUX3D_BF16, xv))) return r;
+  if ((r = row_tensor(x, fn, "x", -1, xv))) return r;
+  if (x->dtype != LUX3D_BF16 && x->dtype != LUX3D_F32)
+    return fail(LUX3D_ERR_DTYPE, "%s: x must be bf16 or f32", fn);
+  const bool xf32 = x->dtype == LUX3D_F32;
   if ((r = row_tensor(y, fn, "y", -1, yv))) return r;
   if ((r = check_desc(qs, fn, "qs")) || (r = check_desc(scales, fn, "scales"))) return r;
   if (qs->dtype != LUX3D_I8 || qs->rank != 2 || !is_contiguous(qs))
@@ -818,6 +821,7 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
   if (k != xv.d) return fail(LUX3D_ERR_SHAPE, "%s: x has %lld features, the weight %lld", fn, (long long)xv.d,
                              (long long)k);
   if (k % 32 || k == 0) return fail(LUX3D_ERR_SHAPE, "%s: k must be a positive multiple of 32", fn);
+  if (xf32 && k % 64) return fail(LUX3D_ERR_SHAPE, "%s: f32 x needs k to be a multiple of 64", fn);
   if (scales->dtype != LUX3D_F32 || !is_contiguous(scales) || numel(scales) != n * (k / 32))
     return fail(LUX3D_ERR_SHAPE, "%s: scales must be a contiguous f32 [n, k/32]", fn);
   if (yv.d != n || yv.rows != xv.rows)
@@ -829,10 +833,12 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
       return fail(LUX3D_ERR_SHAPE, "%s: bias must be a contiguous f32 [n]", fn);
     bp = reinterpret_cast<const float *>(bias->data);
   }
-  if (!aligned16(x->data) || (xv.rows > 1 && (xv.rs * 2) % 16) || !aligned16(qs->data))
+  if (!aligned16(x->data) || (xv.rows > 1 && (xv.rs * (xf32 ? 4 : 2)) % 16) || !aligned16(qs->data))
     return fail(LUX3D_ERR_LAYOUT, "%s: x rows and qs must be 16-byte aligned", fn);
+  if (xf32 && (xv.rs > (int64_t(1) << 20) || k > (int64_t(1) << 22)))
+    return fail(LUX3D_ERR_SHAPE, "%s: f32 x rows of more than 2^20 elements are not supported", fn);
   Q8GemmParams p;
-  p.x = xv.p; p.ldx = xv.rs;
+  p.x = xv.p; p.ldx = xv.rs; p.x_f32 = xf32;
   p.qs = reinterpret_cast<const int8_t *>(qs->data);
   p.scales = reinterpret_cast<const float *>(scales->data);
   p.bias = bp;

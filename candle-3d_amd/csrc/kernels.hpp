@@ -100,7 +100,8 @@ hipError_t launch_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_d
 // ---- Q8_0 quantized linear ---------------------------------------------------
 // y[m, n] = sum_k x[m, k] * bf16(q[n, k] * scale[n, k / 32]) (+ bias[n]).
 struct Q8GemmParams {
-  const void *x = nullptr; int64_t ldx = 0;   // bf16 [M, K] rows, 16-byte aligned
+  const void *x = nullptr; int64_t ldx = 0;   // bf16 (or f32 when x_f32) [M, K] rows, 16-byte aligned
+  bool x_f32 = false;                         // f32 activations: exact f32 weights, f32 matrix cores
   const int8_t *qs = nullptr;                 // [N, K] contiguous, 16-byte aligned
   const float *scales = nullptr;              // [N, K / 32] contiguous
   const float *bias = nullptr;                // [N] or null

@@ -21,7 +21,9 @@
 // - q8_0_gemm_kernel (K % 64 == 32): a 256-thread workgroup computes a
 //   128 x 128 tile; x and the dequantised W are staged as bf16 in LDS,
 //   double-buffered, through registers.
-// Within a k-step the two kernels assign k to MFMA sub-steps differently, so
+// - q8_0_gemm_ring_f32_kernel (f32 x, K % 64 == 0): the ring scheme with the
+//   exact f32 weights q * d and f32 products on v_mfma_f32_32x32x2_f32.
+// Within a k-step the kernels assign k to MFMA sub-steps differently, so
 // their outputs can differ in the last bit of the f32 sum; each is
 // deterministic.
 #include "common.hpp"
@@ -454,6 +456,199 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
   }
 }
 
+// ---- f32 activations ------------------------------------------------------------
+//
+// The ring scheme with f32 x: each weight is the exact f32 product q * d (the
+// reference's own Q8_0 dequant target, nn_blocks.rs:140), products and sums
+// in f32 on v_mfma_f32_32x32x2_f32. 128-row tiles keep a stage at 51,200
+// bytes: x 128 rows x 256 bytes, 16-byte chunk c of row r in slot c ^ (r & 15)
+// (conflict-free fragment reads), then the weights and scales exactly as in
+// the bf16 kernel. MFMA k-step (c4, e) of a 64-deep k-step pairs k = c and
+// k = 32 + c (c = 4 c4 + e): lane half hh supplies k = 32 hh + c, so its x
+// values are contiguous (one 16-byte read per four k-steps) and its weight
+// bytes are the same 32 int8 of one Q8_0 block the bf16 kernel uses.
+template <typename OUT, int GM>
+__global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_f32_kernel(Q8GemmParams p, int tiles_m,
+                                                                              int tiles_n) {
+  constexpr int BM = 128, BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
+  constexpr int kRingA = BM * 256, kRingStage = kRingA + kRingW + kRingS;  // 51,200 bytes
+  constexpr int SEGW = kRingA / 1024 / 8;          // x segments (1 KB = 4 rows) per wavefront
+  constexpr int kRingOps = SEGW + 2 + 1;
+  __shared__ __align__(16) char ring[NS * kRingStage];
+
+  const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
+  const int per = G / 8, rem = G % 8, xcd = bid % 8, pos = bid / 8;
+  const int lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + pos;
+  const int group = lid / (GM * tiles_n), first_m = group * GM;
+  const int gsize = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+  const int in_group = lid - group * GM * tiles_n;
+  const int tm = first_m + in_group % gsize, tn = in_group / gsize;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5, lrow = lane & 31;
+  const int64_t m0 = (int64_t)tm * BM, c0 = (int64_t)tn * BN;
+  const int64_t ncol = c0 + wave * 32 + lrow, nc = ncol < p.N ? ncol : p.N - 1;
+  const int64_t nblk = p.K / 32;
+  const int nk = (int)(p.K / BK);
+
+  uint32_t xoff[SEGW];
+#pragma unroll
+  for (int i = 0; i < SEGW; ++i) {
+    const int g = wave * SEGW + i;
+    const int r = 4 * g + (lane >> 4), c = (lane & 15) ^ (r & 15);
+    const int64_t gr = m0 + r < p.M ? m0 + r : p.M - 1;
+    xoff[i] = (uint32_t)(((gr - m0) * p.ldx + 4 * c) * 4);
+  }
+  const int64_t last_row = p.M - 1 - m0 < BM - 1 ? p.M - 1 - m0 : BM - 1;
+  const int64_t ncols = p.N - c0 < BN ? p.N - c0 : BN;
+  const i32x4_t xr = buffer_rsrc(reinterpret_cast<const char *>(p.x) + m0 * p.ldx * 4, (last_row * p.ldx + p.K) * 4);
+  const i32x4_t wr = buffer_rsrc(p.qs + c0 * p.K, ncols * p.K);
+  const i32x4_t sr = buffer_rsrc(p.scales + c0 * nblk, ncols * nblk * 4);
+  const uint32_t woff = (uint32_t)((nc - c0) * p.K + 32 * h);
+  const uint32_t soff = (uint32_t)(((nc - c0) * nblk + h) * 4);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring;
+  auto issue = [&](int kt, int buf) {
+    const uint32_t st = lds0 + buf * kRingStage;
+#pragma unroll
+    for (int i = 0; i < SEGW; ++i)
+      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 4, __builtin_amdgcn_readfirstlane(st + (wave * SEGW + i) * 1024));
+    lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048));
+    lds_load16(wr, woff, (uint32_t)kt * BK + 16, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048 + 1024));
+    lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + kRingW + wave * 256));
+  };
+  // x fragment of M-tile i, four k-steps c4: row i * 32 + lrow, logical
+  // chunk 8 h + c4 (the swizzle only depends on the row within the tile)
+  int fbase[8];
+#pragma unroll
+  for (int c4 = 0; c4 < 8; ++c4) fbase[c4] = lrow * 256 + (((8 * h + c4) ^ (lrow & 15)) << 4);
+  uint4 w0, w1;
+  float sc;
+  auto read_w = [&](const char *st) {
+    w0 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + lane * 16);
+    w1 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + 1024 + lane * 16);
+    sc = *reinterpret_cast<const float *>(st + kRingA + kRingW + wave * 256 + lane * 4);
+  };
+  // the four exact weights of k-steps 4 c4 .. 4 c4 + 3 (bytes of w0 / w1)
+  auto make_w = [&](int c4, float (&wv)[4]) {
+    const uint4 &v = c4 < 4 ? w0 : w1;
+    const uint32_t word = (c4 & 3) == 0 ? v.x : (c4 & 3) == 1 ? v.y : (c4 & 3) == 2 ? v.z : v.w;
+    wv[0] = (float)(int8_t)(word & 0xFFu) * sc;
+    wv[1] = (float)(int8_t)((word >> 8) & 0xFFu) * sc;
+    wv[2] = (float)(int8_t)((word >> 16) & 0xFFu) * sc;
+    wv[3] = (float)(int8_t)(word >> 24) * sc;
+  };
+  auto read_a = [&](const char *st, int c4, float4 (&a)[TM]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const float4 *>(st + fbase[c4] + i * 32 * 256);
+  };
+  f32x16_t acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) acc[i] = f32x16_t{};
+  auto mfmas = [&](const float4 (&a)[TM], const float (&wv)[4]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, wv[0], acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, wv[1], acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, wv[2], acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, wv[3], acc[i], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) issue(st < nk ? st : nk - 1, st);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kRingOps));
+  __builtin_amdgcn_s_barrier();
+
+  float4 a0[TM], a1[TM];
+  float b0[4], b1[4];
+  read_w(ring);
+  read_a(ring, 0, a0);
+  make_w(0, b0);
+  for (int kt = 0; kt < nk; ++kt) {
+    issue(kt + NS - 1 < nk ? kt + NS - 1 : nk - 1, (kt + NS - 1) % NS);
+    __builtin_amdgcn_sched_barrier(0);
+    const char *st = ring + (kt % NS) * kRingStage;
+#pragma unroll
+    for (int c4 = 0; c4 < 7; c4 += 2) {
+      read_a(st, c4 + 1, a1);
+      make_w(c4 + 1, b1);
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c4 + 2 < 8) {
+        read_a(st, c4 + 2, a0);
+        make_w(c4 + 2, b0);
+        mfmas(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // a1 / b1 hold k-steps 28..31; stage kt + 1 landed and this wavefront's
+    // reads of stage kt are done; then every wavefront's
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0((NS - 2) * kRingOps));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const char *nx = ring + ((kt + 1) % NS) * kRingStage;
+    read_w(nx);
+    read_a(nx, 0, a0);
+    mfmas(a1, b1);
+    make_w(0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+
+  char *ybase = reinterpret_cast<char *>(p.y);
+  const float bias = (p.bias && ncol < p.N) ? p.bias[ncol] : 0.f;
+  constexpr int EB = OUT::code == LUX3D_F32 ? 4 : 2;
+  if (((uintptr_t)p.y % 16 == 0) && ((p.ldy * EB) % 16 == 0)) {
+    constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB, RP = 128;
+    constexpr int REGION = RP * LROW;
+    static_assert(8 * REGION <= NS * kRingStage, "epilogue staging fits the ring");
+    __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
+    char *reg = ring + wave * REGION;
+    const int64_t c0w = c0 + wave * 32;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        const float v = acc[i][e] + bias;
+        if constexpr (EB == 4) *reinterpret_cast<float *>(reg + r * LROW + lrow * 4) = v;
+        else if constexpr (OUT::code == LUX3D_BF16)
+          *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+        else *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
+      }
+#pragma unroll
+    for (int it = 0; it < RP * CPR / 64; ++it) {
+      const int q = it * 64 + lane, r = q / CPR, part = q % CPR;
+      const int64_t row = m0 + r, col = c0w + part * EPC;
+      if (row >= p.M || col >= p.N) continue;
+      const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * LROW + part * 16);
+      char *dst = ybase + (row * p.ldy + col) * EB;
+      if (col + EPC <= p.N) {
+        *reinterpret_cast<uint4 *>(dst) = v;
+      } else {
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int kk = 0; kk < EPC; ++kk)
+          if (col + kk < p.N) {
+            if constexpr (EB == 4) reinterpret_cast<uint32_t *>(dst)[kk] = w4[kk];
+            else reinterpret_cast<uint16_t *>(dst)[kk] = (uint16_t)(w4[kk >> 1] >> (16 * (kk & 1)));
+          }
+      }
+    }
+    return;
+  }
+  if (ncol < p.N) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row >= p.M) continue;
+        store1<OUT>(ybase, row * p.ldy + ncol, acc[i][e] + bias);
+      }
+  }
+}
+
 // The ring kernel's buffer descriptors span one tile (at most 256 rows of x,
 // 256 weight rows and their scales) and must stay below 2^31 bytes; its
 // per-lane offsets are 32-bit.
@@ -473,6 +668,14 @@ constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
 
 template <typename OUT>
 hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
+  if (p.x_f32) {
+    // f32 activations: the f32 ring kernel (K % 64 == 0, checked by the caller)
+    const int64_t tiles_m = (p.M + 127) / 128, tiles_n = (p.N + 255) / 256;
+    if (tiles_m * tiles_n > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((q8_0_gemm_ring_f32_kernel<OUT, 8>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0,
+                       s, p, (int)tiles_m, (int)tiles_n);
+    return hipGetLastError();
+  }
   if (ring_fits(p)) {
     const int64_t tiles_n = (p.N + 255) / 256, tiles_m256 = (p.M + 255) / 256;
     if (tiles_m256 * tiles_n >= kRingMinTiles) {
@@ -503,6 +706,8 @@ hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs
 hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
   if (p.K <= 0 || p.K % kBK) return hipErrorInvalidValue;
+  if (p.x_f32 && (p.K % 64 || (127 * p.ldx + p.K) * 4 > 0x7FFFFFFF || 256 * p.K > 0x7FFFFFFF))
+    return hipErrorInvalidValue;
   if ((p.N + 127) / 128 > INT32_MAX || (p.M + 127) / 128 > 65535) return hipErrorInvalidValue;
   switch (out_dt) {
     case LUX3D_BF16: return launch_tiles<BF16>(p, s);

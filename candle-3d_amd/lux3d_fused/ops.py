@@ -354,7 +354,8 @@ def q8_0_repack(blocks: torch.Tensor, n: int, k: int):
 def q8_0_linear(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 out_dtype=torch.bfloat16) -> torch.Tensor:
     """`Linear::forward` for a Q8_0 weight (runtime/nn_blocks.rs:83-93):
-    y = x @ dequant(W)^T (+ bias), x bf16 [..., k] -> y [..., n]."""
+    y = x @ dequant(W)^T (+ bias), x bf16 or f32 [..., k] -> y [..., n]
+    (f32 x: the weights dequantized exactly to f32, k a multiple of 64)."""
     n = qs.shape[0]
     y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=out_dtype, device=x.device)
     _lib.call("lux3d_q8_0_linear", desc(x), desc(qs), desc(scales), desc(bias), desc(y), _stream(x))

@@ -376,19 +376,20 @@ def cfg4_dinov3_rope(dev) -> Workload:
 
 
 # The configs[1..4] ops BASELINE.md names (the >=70%-of-peak targets), then extras.
-def _q8_linear(dev, cfg, m, k, n, what) -> Workload:
+def _q8_linear(dev, cfg, m, k, n, what, xdt=torch.bfloat16) -> Workload:
     """Q8_0 quantized linear y = x @ dequant(W)^T + bias at a model's shape.
     The weight is repacked once (load time, outside the timed launch); x
     rotates over sets that exceed the Infinity Cache, the weight stays one
     tensor, as a layer's weight does across the tokens of a step."""
     from . import _lib
     s = synth.config_seed(cfg) + 500
-    x0 = _normal(s, (m, k), dev, torch.bfloat16)
+    xe = 4 if xdt == torch.float32 else 2
+    x0 = _normal(s, (m, k), dev, xdt)
     blocks = _t(synth.q8_0_blocks(s + 1, n * k // 32), dev)
     qs, scales = ops.q8_0_repack(blocks, n, k)
     bias = _normal(s + 2, (n,), dev, torch.float32, 0.0, 0.5)
-    nbytes = m * k * 2 + n * k + n * (k // 32) * 4 + n * 4 + m * n * 2
-    n_sets = _n_sets(m * k * 2 + m * n * 2)
+    nbytes = m * k * xe + n * k + n * (k // 32) * 4 + n * 4 + m * n * 2
+    n_sets = _n_sets(m * k * xe + m * n * 2)
     xs = [_fill_like(x0, j) for j in range(n_sets)]
     ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
     dx = [ops.desc(v) for v in xs]
@@ -398,8 +399,13 @@ def _q8_linear(dev, cfg, m, k, n, what) -> Workload:
     def launch(i):
         j = i % n_sets
         _lib.call("lux3d_q8_0_linear", dx[j], dq, dsc, db, dy[j], _cur())
-    wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
-                  f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
+    if xe == 4:
+        wl = Workload("q8_0_linear_f32", cfg, "q8_0_gemm_ring_f32_kernel<BF16>", "f32 x f32(Q8_0) -> f32 acc",
+                      nbytes, f"x[{m},{k}] f32 @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n,
+                      peak_tflops=157.3)
+    else:
+        wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
+                      f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
     wl._keep = (xs, ys, qs, scales, bias, blocks, dx, dy, dq, dsc, db)
     return wl
 
@@ -412,6 +418,11 @@ def cfg4_q8_0_linear(dev) -> Workload:
 def cfg2_q8_0_linear(dev) -> Workload:
     # TripoSG width 2048 -> 4x feed-forward, both CFG halves (2 x 2048 tokens)
     return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection")
+
+
+def cfg2_q8_0_linear_f32(dev) -> Workload:
+    # the same projection with f32 activations (a model run in f32)
+    return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection", torch.float32)
 
 
 def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16) -> Workload:
@@ -636,6 +647,7 @@ EXTRAS: List[Callable] = [
     cfg4_dinov3_rope,
     cfg4_q8_0_linear,
     cfg2_q8_0_linear,
+    cfg2_q8_0_linear_f32,
     cfg1_sdpa_frame,
     cfg1_sdpa_frame_qln,
     cfg1_sdpa_frame_f32,

@@ -287,15 +287,17 @@ int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y,
  * lux3d_q8_0_linear: y = x * W^T (+ bias) for the LinearInner::Quant branch
  * of Linear::forward (runtime/nn_blocks.rs:83-93, QMatMul::forward then
  * broadcast_add(bias)).
- *   x: bf16 [..., k] rows with a unit inner stride, 16-byte aligned rows;
+ *   x: bf16 or f32 [..., k] rows with a unit inner stride, 16-byte aligned
+ *      rows (f32 x: k % 64 == 0, else LUX3D_ERR_SHAPE);
  *   qs, scales: from lux3d_q8_0_repack for the weight [n, k];
  *   bias: f32 [n] or NULL;
  *   y: [..., n] rows, bf16 / f16 / f32.
- * Each weight is dequantized exactly as lux3d_dequant_q8_0 does to bf16
- * (RNE of the exact product), products accumulate in f32 (MFMA), the bias
- * is added in f32 and y is rounded once. This is the dequantize-then-matmul
- * path of candle's GPU backends with a bf16 dequant target; candle's CPU
- * path instead quantizes x to Q8_0 blocks and takes integer dot products.   */
+ * Each weight is dequantized exactly as lux3d_dequant_q8_0 does, to x's
+ * dtype (bf16: RNE of the exact product; f32: the exact product), products
+ * accumulate in f32 (MFMA), the bias is added in f32 and y is rounded once.
+ * This is the dequantize-then-matmul path of candle's GPU backends; candle's
+ * CPU path instead quantizes x to Q8_0 blocks and takes integer dot
+ * products.                                                                 */
 int lux3d_q8_0_repack(const lux3d_tensor_t *blocks, int64_t n, int64_t k,
                       const lux3d_tensor_t *qs, const lux3d_tensor_t *scales,
                       lux3d_stream_t stream);

@@ -28,6 +28,8 @@
  *   or_dequant_q8_0          brute force over all int8 x f16 scale sweep
  *   or_q8_0_linear           numpy f64 matmul of the dequantized weight; identity
  *                            weight; tiny brute force (tests/test_oracle_pins.py)
+ *   or_q8_0_linear_f32       numpy f64 matmul of the f32-dequantized weight; identity
+ *                            weight returns x; tiny brute force
  *   or_sparse_neighbors      reference KATs (tests/trellis2_sparse.rs:67-93) + brute
  *                            force over all pairs
  *   or_sparse_conv3d         torch conv3d (f64) on the densified grid; the
@@ -878,6 +880,19 @@ void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *bloc
   ql_ctx c = {xf, wf, bias, K, N, out_dt, y, abs_sum};
   parallel_rows(M, ql_rows, &c);
   free(xf); free(wf); free(wb);
+}
+
+/* The same with f32 activations: each weight is the exact f32 product q * d
+ * (the reference's own Q8_0 dequant target, nn_blocks.rs:140), the sum of
+ * the f32 products in f64, one rounding. */
+void or_q8_0_linear_f32(const float *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
+                        const float *bias, int out_dt, void *y, float *abs_sum) {
+  float *wf = (float *)malloc(sizeof(float) * (size_t)(N * K));
+  if (!wf) return;
+  or_dequant_q8_0(blocks, N * (K / 32), OR_F32, wf);
+  ql_ctx c = {x, wf, bias, K, N, out_dt, y, abs_sum};
+  parallel_rows(M, ql_rows, &c);
+  free(wf);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -134,6 +134,9 @@ void or_dequant_q8_0(const uint8_t *blocks, int64_t nblocks, int out_dt, void *o
  * f32 accumulation error. */
 void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
                     const float *bias, int out_dt, void *y, float *abs_sum);
+/* The same with f32 x [M, K] and the exact f32 weights q * d. */
+void or_q8_0_linear_f32(const float *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
+                        const float *bias, int out_dt, void *y, float *abs_sum);
 
 /* ---- TRELLIS.2 sparse ops (runtime/trellis2_sparse.rs) --------------------- */
 /* CoordMap + kernel_offset_delta: nbr[i][k] = row of coords[i] + delta(k), or

@@ -51,6 +51,7 @@ _SIG = {
     "or_timestep_embedding_cos_first": ([_P, _I, _I, _P], None),
     "or_dequant_q8_0": ([_P, _I, ctypes.c_int, _P], None),
     "or_q8_0_linear": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
+    "or_q8_0_linear_f32": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
     "or_sparse_neighbors": ([_P, _I, _P], None),
     "or_sparse_conv3d": ([_P, _I, _I, _P, _P, _P, _I, _P, _P], None),
     "or_channel_to_spatial": ([_P, _I, _P, _I, _P, _P, _P, _P, _P], ctypes.c_int64),
@@ -308,16 +309,19 @@ def dequant_q8_0(blocks, out_dt=BF16):
 
 
 def q8_0_linear(x_bits, blocks, n, bias=None, out_dt=BF16, with_abs=False):
-    """x: bf16 bits [M, K]; blocks: Q8_0 bytes of the weight [n, K]. Returns
-    y [M, n] (uint16 bits for bf16 / f16, f32 otherwise) and, with_abs,
-    sum_k |x * w| as f32 [M, n]."""
-    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    """x: bf16 bits [M, K] (uint16), or f32 [M, K] for the f32-activation
+    form (weights dequantized exactly to f32); blocks: Q8_0 bytes of the
+    weight [n, K]. Returns y [M, n] (uint16 bits for bf16 / f16, f32
+    otherwise) and, with_abs, sum_k |x * w| as f32 [M, n]."""
+    f32x = np.asarray(x_bits).dtype == np.float32
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.float32 if f32x else np.uint16)
     m, k = x_bits.shape
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
     assert blocks.size == n * (k // 32) * 34
     y = np.empty((m, n), dtype=np.float32 if out_dt == F32 else np.uint16)
     a = np.empty((m, n), dtype=np.float32) if with_abs else None
-    LIB.or_q8_0_linear(_ptr(x_bits), m, k, _ptr(blocks), n, _ptr(_f32(bias)), out_dt, _ptr(y), _ptr(a))
+    fn = LIB.or_q8_0_linear_f32 if f32x else LIB.or_q8_0_linear
+    fn(_ptr(x_bits), m, k, _ptr(blocks), n, _ptr(_f32(bias)), out_dt, _ptr(y), _ptr(a))
     return (y, a) if with_abs else y
 
 

@@ -208,10 +208,13 @@ def test_q8_0_linear_argument_errors():
     assert rc == _lib.ERR_DTYPE
     rc, msg = status("lux3d_q8_0_repack", blocks, n, k, T([n, k], _lib.I8, data=FAKE + 8), scales, None)
     assert rc == _lib.ERR_LAYOUT
-    # linear: x bf16 with k features, rows 16-byte aligned; y [rows, n]
+    # linear: x bf16 (or f32 with k % 64 == 0) with k features, rows 16-byte
+    # aligned; y [rows, n]
     x, y = T([10, k]), T([10, n])
+    rc, msg = status("lux3d_q8_0_linear", T([10, k], _lib.F16), qs, scales, None, y, None)
+    assert rc == _lib.ERR_DTYPE and "bf16 or f32" in msg
     rc, msg = status("lux3d_q8_0_linear", T([10, k], _lib.F32), qs, scales, None, y, None)
-    assert rc == _lib.ERR_DTYPE
+    assert rc == _lib.ERR_SHAPE and "multiple of 64" in msg
     rc, msg = status("lux3d_q8_0_linear", T([10, k + 32]), qs, scales, None, y, None)
     assert rc == _lib.ERR_SHAPE and "features" in msg
     rc, msg = status("lux3d_q8_0_linear", x, qs, scales, None, T([10, n + 1]), None)

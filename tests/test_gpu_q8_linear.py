@@ -161,3 +161,53 @@ def test_q8_0_linear_large_sampled_rows(dev, ops, orc, synth):
     xs = host(xd, "bf16")[rows]
     want, abs_sum = orc.q8_0_linear(xs, blocks, n, b, orc.BF16, with_abs=True)
     assert_gemm_close(host(y, "bf16")[rows], want, abs_sum, "bf16", "sampled rows")
+
+
+# f32 activations: the weights are dequantized exactly to f32 (q * d) and the
+# products summed in f32 on the f32 matrix cores; the same f32 accumulation
+# tolerance as above. (4353, 128, 3700) has 35 x 15 = 525 tiles of 128 rows,
+# the last holding one row, the last column piece 116 columns.
+@pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136),
+                                   (4353, 128, 3700)])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_q8_0_linear_f32_activations(dev, ops, orc, synth, m, k, n, out):
+    print(f"\n[case] q8_0_linear f32 x m={m} k={k} n={n} out={out}", flush=True)
+    x = synth.normal(1300 + m, m * k).reshape(m, k)
+    xd = torch.from_numpy(x).to(dev)
+    blocks = synth.q8_0_blocks(1301 + m, n * k // 32)
+    b = synth.normal(1302 + m, n, 0.0, 0.5)
+    mm = ops.QMatMul.from_q8_0(torch.from_numpy(blocks).to(dev), n, k)
+    y = mm.forward(xd, torch.from_numpy(b).to(dev), TDT[out])
+    torch.cuda.synchronize()
+    rows = np.arange(m) if m <= 1100 else np.unique(np.concatenate(
+        [np.arange(40), np.arange(m - 40, m), np.random.default_rng(8).choice(m, 48, replace=False)]))
+    want, abs_sum = orc.q8_0_linear(np.ascontiguousarray(x[rows]), blocks, n, b,
+                                    orc.F32 if out == "f32" else orc.BF16, with_abs=True)
+    assert_gemm_close(host(y, out)[rows], want, abs_sum, out, f"q8_0_linear f32 x {m}x{k}x{n}")
+
+
+def test_q8_0_linear_f32_strided_and_rejects_k96(dev, ops, orc, synth):
+    """f32 x and bf16 y as row-strided views (x rows 16-byte aligned, y rows
+    not: the one-element-per-store epilogue); f32 x with k % 64 != 0 is
+    rejected before any launch."""
+    from lux3d_fused import _lib
+    from lux3d_fused._lib import Lux3dError
+    m, k, n = 333, 320, 264
+    print(f"\n[case] q8_0_linear f32 x strided m={m} k={k} n={n}", flush=True)
+    x = synth.normal(1400, m * k).reshape(m, k)
+    xwide = torch.zeros((m, k + 4), dtype=torch.float32, device=dev)
+    xwide[:, :k] = torch.from_numpy(x).to(dev)
+    ywide = torch.zeros((m, n + 3), dtype=torch.bfloat16, device=dev)
+    blocks = synth.q8_0_blocks(1401, n * k // 32)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    _lib.call("lux3d_q8_0_linear", ops.desc(xwide[:, :k]), ops.desc(qs), ops.desc(scales), None,
+              ops.desc(ywide[:, :n]), None)
+    torch.cuda.synchronize()
+    want, abs_sum = orc.q8_0_linear(x, blocks, n, None, orc.BF16, with_abs=True)
+    assert_gemm_close(host(ywide[:, :n], "bf16"), want, abs_sum, "bf16", "f32 x, strided rows")
+    assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
+    x96 = torch.zeros((4, 96), dtype=torch.float32, device=dev)
+    q96, s96 = ops.q8_0_repack(torch.from_numpy(synth.q8_0_blocks(1402, 32 * 3)).to(dev), 32, 96)
+    y96 = torch.zeros((4, 32), dtype=torch.float32, device=dev)
+    with pytest.raises(Lux3dError, match="multiple of 64"):
+        _lib.call("lux3d_q8_0_linear", ops.desc(x96), ops.desc(q96), ops.desc(s96), None, ops.desc(y96), None)

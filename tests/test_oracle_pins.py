@@ -532,6 +532,43 @@ def test_q8_0_linear_identity_weight_and_brute_force():
             assert abs(got[i, j] - acc) <= 2.0 ** -23 * abs(acc) + 1e-30, (i, j)
 
 
+def test_q8_0_linear_f32_activations():
+    """f32 x with the exact f32 weights q * d: against a numpy f64 matmul of
+    the dequantized weight decoded independently, an identity weight, and a
+    pure-Python brute force on the block bytes."""
+    m, k, n = 7, 96, 10
+    x = synth.normal(97, m * k).reshape(m, k).astype(np.float32)
+    blocks = synth.q8_0_blocks(98, n * k // 32)
+    bias = synth.normal(99, n, 0.0, 0.5)
+    raw = blocks.reshape(n, k // 32, 34)
+    d = raw[:, :, 0:2].copy().view(np.float16).astype(np.float64)          # [n, k/32, 1]
+    q = raw[:, :, 2:].view(np.int8).astype(np.float64)                      # [n, k/32, 32]
+    w = (q * d).reshape(n, k)
+    want = x.astype(np.float64) @ w.T + bias.astype(np.float64)
+    got = orc.q8_0_linear(x, blocks, n, bias, orc.F32)
+    assert np.all(np.abs(got - want) <= 2.0 ** -24 * np.abs(want) + 1e-30)
+    gb = orc.q8_0_linear(x, blocks, n, bias, orc.BF16)
+    assert np.array_equal(gb, to_bf16_bits(want))
+    # identity weight (d = 1, q = 1 on the diagonal) returns x exactly
+    kk = 64
+    ident = np.zeros((kk, kk // 32, 34), dtype=np.uint8)
+    ident[:, :, 0], ident[:, :, 1] = 0x00, 0x3C
+    for i in range(kk):
+        ident[i, i // 32, 2 + i % 32] = 1
+    xi = synth.normal(100, 3 * kk).reshape(3, kk).astype(np.float32)
+    assert np.array_equal(orc.q8_0_linear(xi, ident.reshape(-1), kk, None, orc.F32), xi)
+    # brute force
+    for i in range(m):
+        for j in range(n):
+            acc = float(bias[j])
+            for t in range(k):
+                blk = raw[j, t // 32]
+                dd = float(np.frombuffer(bytes(blk[0:2]), dtype="<f2")[0])
+                qv = int(blk[2 + t % 32]) - 256 * (blk[2 + t % 32] > 127)
+                acc += float(x[i, t]) * (qv * dd)
+            assert abs(got[i, j] - acc) <= 2.0 ** -23 * abs(acc) + 1e-30, (i, j)
+
+
 def _pattern_f32(index):
     """The reference's sparse-attention test inputs (tests/trellis2_sparse.rs:23-25)."""
     return ((np.asarray(index) % 23).astype(np.float32) - np.float32(11.0)) * np.float32(0.1)
