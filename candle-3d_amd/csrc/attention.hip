@@ -19,14 +19,15 @@
 //                  The 32 x 32 result leaves every lane with ONE query
 //                  (lane % 32) and 16 keys, so the row max needs a single
 //                  exchange with lane ^ 32 and no other cross-lane traffic.
-//   O^T += V^T P^T A operand: V^T from LDS (V is transposed while staged),
-//                  B operand: the probabilities exactly where the S^T
+//   O^T += V^T P^T A operand: V^T fragments read from V's [key][dim] rows in
+//                  LDS by ds_read_b64_tr_b16 (the transpose happens in the
+//                  LDS read), B operand: the probabilities exactly where the S^T
 //                  accumulator left them (the key order inside a 16-key
 //                  k-step is permuted identically on both operands, which a
 //                  sum over keys does not see). O^T again gives each lane its
 //                  own query, so the rescale by exp2(m_old - m_new) and the
 //                  final 1/l are per-lane multiplies.
-// K and V^T blocks are double-buffered in LDS; the next block's global loads
+// K and V blocks are double-buffered in LDS; the next block's global loads
 // are issued before the current block's math, one LDS barrier per block.
 // Workgroups are numbered so that the query blocks of one head run on one
 // XCD (hardware places workgroup i on XCD i % 8) and share its L2 copy of K
@@ -117,16 +118,14 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   using M = Mma<T>;
   using op_t = typename M::op_t;
   constexpr int BQ = 4 * 32 * QT;
-  constexpr int KROW = D + 8;              // 2-byte elements per K row in LDS (16-byte pad)
-  constexpr int VROW = BKV + 4;            // per V^T row (8-byte pad)
-  constexpr int KCH = BKV * D / 8 / 256;   // 16-byte K chunks per thread per block
-  constexpr int VGR = BKV * D / 16 / 256;  // 4 keys x 4 dims V groups per thread per block
+  constexpr int KROW = D + 8;              // 2-byte elements per K / V row in LDS (16-byte pad)
+  constexpr int KCH = BKV * D / 8 / 256;   // 16-byte K (and V) chunks per thread per block
   constexpr int NKT = BKV / 32;            // 32-key tiles per block
   constexpr int NDT = D / 32;              // 32-dim output tiles
-  static_assert(KCH >= 1 && VGR >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
-  __shared__ __align__(16) uint16_t smem[2 * BKV * KROW + 2 * D * VROW];
+  static_assert(KCH >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
+  __shared__ __align__(16) uint16_t smem[4 * BKV * KROW];
   uint16_t(*Ks)[BKV * KROW] = reinterpret_cast<uint16_t(*)[BKV * KROW]>(smem);
-  uint16_t(*Vt)[D * VROW] = reinterpret_cast<uint16_t(*)[D * VROW]>(smem + 2 * BKV * KROW);
+  uint16_t(*Vs)[BKV * KROW] = reinterpret_cast<uint16_t(*)[BKV * KROW]>(smem + 2 * BKV * KROW);
 
   const int64_t lid = xcd_logical_id(blockIdx.x, nwg);
   const int64_t bh = lid / nqb, qb = lid % nqb;
@@ -159,7 +158,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     // area, which is not in use yet; then each lane reads its fragments.
     static_assert(D == 64 || D == 128, "QLN head dims");
     constexpr int LPR = D / 8, RPP = 64 / LPR;  // lanes per row, rows per pass
-    static_assert(4 * QT * 32 * D <= 2 * BKV * KROW + 2 * D * VROW, "Q staging fits the K / V buffers");
+    static_assert(4 * QT * 32 * D <= 4 * BKV * KROW, "Q staging fits the K / V buffers");
     uint16_t *qs = smem + wave * (QT * 32 * D);
     const int ch = lane % LPR;
     float w8[8], b8[8];
@@ -196,31 +195,25 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     lds_barrier();  // the staging area becomes the K / V buffers below
   }
 
-  // Staging: K rows as 16-byte chunks; V as 4 keys x 4 dims, transposed in
-  // registers and written as 4 rows of V^T. Keys past Lk are clamped to
-  // Lk - 1 (finite data; their scores are masked).
-  int k_row[KCH], k_part[KCH], v_dg[VGR], v_kg[VGR];
+  // Staging: K and V rows as 16-byte chunks, both in their [key][dim]
+  // layout. Keys past Lk are clamped to Lk - 1 (finite data; their scores
+  // are masked).
+  int k_row[KCH], k_part[KCH];
 #pragma unroll
   for (int i = 0; i < KCH; ++i) {
     const int c = t + i * 256;
     k_row[i] = c / (D / 8);
     k_part[i] = c % (D / 8);
   }
-#pragma unroll
-  for (int i = 0; i < VGR; ++i) {
-    const int g = t + i * 256;
-    v_dg[i] = g % (D / 4);
-    v_kg[i] = g / (D / 4);
-  }
   // byte offsets of this thread's rows relative to a block's first key
-  int64_t k_off[KCH], v_off[VGR];
+  int64_t k_off[KCH], v_off[KCH];
 #pragma unroll
-  for (int i = 0; i < KCH; ++i) k_off[i] = ((int64_t)k_row[i] * p.k_st + k_part[i] * 8) * 2;
-#pragma unroll
-  for (int i = 0; i < VGR; ++i) v_off[i] = ((int64_t)v_kg[i] * 4 * p.v_st + v_dg[i] * 4) * 2;
-  const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2, vrow = p.v_st * 2;
-  uint4 rk[KCH];
-  uint2 rv[VGR][4];
+  for (int i = 0; i < KCH; ++i) {
+    k_off[i] = ((int64_t)k_row[i] * p.k_st + k_part[i] * 8) * 2;
+    v_off[i] = ((int64_t)k_row[i] * p.v_st + k_part[i] * 8) * 2;
+  }
+  const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2;
+  uint4 rk[KCH], rv[KCH];
   // `clamp` (the tail block only): keys past Lk read row Lk - 1
   auto load_kv = [&](int64_t j, bool clamp) {
     if (!clamp) {
@@ -228,9 +221,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 #pragma unroll
       for (int i = 0; i < KCH; ++i) rk[i] = ld16<false>(kb + k_off[i]);
 #pragma unroll
-      for (int i = 0; i < VGR; ++i)
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) rv[i][kk] = *reinterpret_cast<const uint2 *>(vb + v_off[i] + kk * vrow);
+      for (int i = 0; i < KCH; ++i) rv[i] = ld16<false>(vb + v_off[i]);
       return;
     }
     const int64_t key0 = j * BKV;
@@ -239,32 +230,14 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       int64_t key = key0 + k_row[i];
       key = key < Lk ? key : Lk - 1;
       rk[i] = ld16<false>(kbase + (key * p.k_st + k_part[i] * 8) * 2);
+      rv[i] = ld16<false>(vbase + (key * p.v_st + k_part[i] * 8) * 2);
     }
-#pragma unroll
-    for (int i = 0; i < VGR; ++i)
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        int64_t key = key0 + v_kg[i] * 4 + kk;
-        key = key < Lk ? key : Lk - 1;
-        rv[i][kk] = *reinterpret_cast<const uint2 *>(vbase + (key * p.v_st + v_dg[i] * 4) * 2);
-      }
   };
   auto store_kv = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) *reinterpret_cast<uint4 *>(&Ks[buf][k_row[i] * KROW + k_part[i] * 8]) = rk[i];
-#pragma unroll
-    for (int i = 0; i < VGR; ++i) {
-      // rv[kk] = {dims 0,1 | dims 2,3} of key kk -> row dd = {keys 0,1 | keys 2,3}
-      const uint2 a = rv[i][0], b = rv[i][1], c = rv[i][2], d = rv[i][3];
-      const uint2 r0 = make_uint2((a.x & 0xFFFFu) | (b.x << 16), (c.x & 0xFFFFu) | (d.x << 16));
-      const uint2 r1 = make_uint2((a.x >> 16) | (b.x & 0xFFFF0000u), (c.x >> 16) | (d.x & 0xFFFF0000u));
-      const uint2 r2 = make_uint2((a.y & 0xFFFFu) | (b.y << 16), (c.y & 0xFFFFu) | (d.y << 16));
-      const uint2 r3 = make_uint2((a.y >> 16) | (b.y & 0xFFFF0000u), (c.y >> 16) | (d.y & 0xFFFF0000u));
-      uint16_t *dst = &Vt[buf][(v_dg[i] * 4) * VROW + v_kg[i] * 4];
-      *reinterpret_cast<uint2 *>(dst) = r0;
-      *reinterpret_cast<uint2 *>(dst + VROW) = r1;
-      *reinterpret_cast<uint2 *>(dst + 2 * VROW) = r2;
-      *reinterpret_cast<uint2 *>(dst + 3 * VROW) = r3;
+    for (int i = 0; i < KCH; ++i) {
+      *reinterpret_cast<uint4 *>(&Ks[buf][k_row[i] * KROW + k_part[i] * 8]) = rk[i];
+      *reinterpret_cast<uint4 *>(&Vs[buf][k_row[i] * KROW + k_part[i] * 8]) = rv[i];
     }
   };
 
@@ -363,10 +336,22 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       }
     };
     // A = V^T[dim l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of tile kt
+    // A = V^T[dim dt * 32 + l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of
+    // tile kt (the accumulator order of the probabilities), read from V's
+    // [key][dim] rows: ds_read_b64_tr_b16 hands lane i of each 16-lane group
+    // element i % 4 of the 8 bytes that lane 4 e + i / 4 addressed, e = 0..3.
+    // Lanes 4 e .. 4 e + 3 of a group address key row 4 hh + e and dims
+    // 16 * ((lane / 16) % 2) + 4 * (lane % 4) .. + 3, so lane i receives dim
+    // lane % 32 of keys 4 hh + 0..3; the second read, of keys 8 on.
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
     auto vfrag = [&](int dt, int kt, int jj) {
-      const uint16_t *vr = &Vt[buf][(dt * 32 + l32) * VROW + kt * 32 + 16 * jj + 4 * hh];
-      const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi2 = *reinterpret_cast<const uint2 *>(vr + 8);
-      return __builtin_bit_cast(op_t, u32x4_t{lo.x, lo.y, hi2.x, hi2.y});
+      const int g16 = lane & 15;
+      const uint16_t *vr = &Vs[buf][(kt * 32 + 16 * jj + 4 * hh + (g16 >> 2)) * KROW + dt * 32 +
+                                    16 * ((lane >> 4) & 1) + 4 * (g16 & 3)];
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr));
+      const s16x4_t hi2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr + 8 * KROW));
+      return __builtin_bit_cast(op_t, __builtin_shufflevector(lo, hi2, 0, 1, 2, 3, 4, 5, 6, 7));
     };
     if constexpr (PHASED && QT == 2) {
       // P v of query tile 0 has no dependence on the softmax of tile 1:
