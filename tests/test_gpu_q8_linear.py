@@ -149,6 +149,22 @@ def test_q8_0_linear_ring_kernel(dev, ops, orc, synth, out, extra):
         assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
 
 
+def test_q8_0_linear_ring_kernel_128_row_tiles(dev, ops, orc, synth):
+    """x [3800, 128] -> [3800, 4096]: 15 x 16 tiles of 256 rows would leave
+    CUs idle, so the ring kernel runs with 30 x 16 tiles of 128 rows (the
+    last holding 88 rows); sampled rows."""
+    m, k, n = 3800, 128, 4096
+    print(f"\n[case] q8_0_linear ring kernel 128-row tiles {m}x{k}x{n}", flush=True)
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 780)
+    mm = ops.QMatMul.from_q8_0(torch.from_numpy(blocks).to(dev), n, k)
+    y = mm.forward(xd, torch.from_numpy(b).to(dev))
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(24), np.arange(m - 100, m),
+                                     np.random.default_rng(9).choice(m, 40, replace=False)]))
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16")[rows], blocks, n, b, orc.BF16, with_abs=True)
+    assert_gemm_close(host(y, "bf16")[rows], want, abs_sum, "bf16", "ring kernel, 128-row tiles")
+
+
 def test_q8_0_linear_large_sampled_rows(dev, ops, orc, synth):
     """A TripoSG-sized projection (x [4096, 2048] -> [4096, 8192]); the oracle
     checks a sample of 96 rows."""
