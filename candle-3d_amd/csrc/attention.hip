@@ -705,12 +705,20 @@ hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// D = 64 with short query sequences (VGGT frame attention, 1,374 tokens):
+// 128-query workgroups at three wavefronts per SIMD, which fill the CUs in
+// more, shorter rounds than the 256-query ones.
+constexpr int64_t kShortQ = 4096;
+
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if (p.qln && !(T::code != LUX3D_F32 && p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
-      if (p.D == 64) return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);
+      if (p.D == 64) {
+        if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, true, false>(p, s);
+        return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);
+      }
       if (p.D == 128) return launch_mfma<T, 128, 1, 64, 2, true, true, false>(p, s);
     }
   } else {

@@ -506,6 +506,11 @@ def cfg1_sdpa_global(dev) -> Workload:
     return _sdpa(dev, "sdpa_global", 1, 1, 8 * 1374, 16, 64, "VGGT global attention", reps=20)
 
 
+def cfg4_sdpa_dinov3(dev) -> Workload:
+    # the DINOv3 encoder's attention over its 1029 tokens (TRELLIS.2 image conditioning)
+    return _sdpa(dev, "sdpa_dinov3", 4, 1, 1029, 16, 64, "DINOv3 self-attention, 1029 tokens")
+
+
 def cfg2_sdpa(dev) -> Workload:
     return _sdpa(dev, "sdpa", 2, 2, 2048, 16, 128, "TripoSG DiT self-attention, CFG pair")
 
@@ -655,6 +660,7 @@ EXTRAS: List[Callable] = [
     cfg1_sdpa_global,
     cfg2_sdpa,
     cfg3_sdpa,
+    cfg4_sdpa_dinov3,
     cfg3_sparse_conv_c1024,
     cfg3_sparse_conv_c256,
     cfg3_sparse_conv_c256_output_stationary,
