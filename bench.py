@@ -281,6 +281,7 @@ def main():
         del wl
         torch.cuda.empty_cache()
         cus = copy_ceiling_us(torch, dev, nbytes, 200 if nbytes < 64 << 20 else 50)
+        print(f"[bench] {tag}: {us:.2f} us (warm {us_warm:.2f})", file=sys.stderr, flush=True)
         table.append({"op": tag, "config": cfg, "dtype": dtype, "shape": shape,
                       "bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
                       "warm_us": round(us_warm, 3), "warm_gbs": round(nbytes / us_warm / 1e3, 1),
