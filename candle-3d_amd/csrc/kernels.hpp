@@ -74,6 +74,9 @@ struct HeadParams {
   // Vector path allowed: D is 64 or 128 and every head row and per-channel
   // parameter vector is 16-byte aligned. Otherwise the generic kernel runs.
   bool vec = true;
+  // Filled by the launcher: x / H and x / N for x < 2^31 as (x * m) >> s.
+  uint32_t div_h_m = 0, div_n_m = 0;
+  int div_h_s = 0, div_n_s = 0;
 };
 
 hipError_t launch_heads(int norm, int rot, int dt, const HeadParams &p, hipStream_t s);

@@ -26,6 +26,36 @@ template <int D> struct RotPartner<HR_R2_TAB, D> { static constexpr int M = 1; }
 template <int D> struct RotPartner<HR_R2_COORD, D> { static constexpr int M = 1; };
 template <int D> struct RotPartner<HR_R3_TAB, D> { static constexpr int M = D / 2; };
 
+// x / d for x < 2^31 from the launcher's (m, s) = (ceil(2^s / d), 31 +
+// ceil(log2 d)): x m / 2^s exceeds x / d by less than 2^31 / 2^s <= 1 / d,
+// which cannot reach the next integer. Three instructions instead of the
+// ~10 of a runtime 32-bit division.
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, uint32_t m, int s) {
+  return (uint32_t)(((uint64_t)x * m) >> s);
+}
+void div_magic(int64_t d, uint32_t &m, int &s) {
+  int l = 0;
+  while ((int64_t(1) << l) < d) ++l;
+  s = 31 + l;
+  m = (uint32_t)(((uint64_t(1) << s) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
+// Element offset of (b, h, n) + c in a [B, H, N, D] view. O32: the launcher
+// has checked that every byte offset of the views is below 2^31 and that
+// every index and every stride of an axis longer than 1 is below 2^24, so
+// the products are full-rate 24-bit multiplies (an axis of length 1 has
+// index 0, whatever its stride).
+template <bool O32> __device__ __forceinline__ uint32_t imul(uint32_t a, uint32_t b) {
+  if constexpr (O32) return __umul24(a, b);
+  else return a * b;
+}
+template <bool O32>
+__device__ __forceinline__ auto view_off(uint32_t b, uint32_t h, uint32_t n, int64_t sB, int64_t sH, int64_t sN,
+                                         uint32_t c) {
+  if constexpr (O32) return imul<O32>(b, (uint32_t)sB) + imul<O32>(h, (uint32_t)sH) + imul<O32>(n, (uint32_t)sN) + c;
+  else return (int64_t)b * sB + (int64_t)h * sH + (int64_t)n * sN + c;
+}
+
 __device__ __forceinline__ int64_t load_index(const void *p, int dt, int64_t i) {
   return dt == LUX3D_I64 ? reinterpret_cast<const int64_t *>(p)[i]
                          : (int64_t)reinterpret_cast<const int32_t *>(p)[i];
@@ -44,7 +74,7 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
       const int t = e / D, j = e % D;
       uint32_t tok = tok0 + t;
       tok = tok < ntok ? tok : ntok - 1;
-      const uint32_t b = tok / N, n = tok % N;
+      const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s), n = tok - b * N;
       float C = 1.f, S = 0.f;
       if constexpr (ROT == HR_R1_TAB) {
         const int64_t off = (int64_t)b * p.tab_sB + (int64_t)n * p.tab_sN + j;
@@ -64,7 +94,7 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
       const int t = e / half, a = e % half;
       uint32_t tok = tok0 + t;
       tok = tok < ntok ? tok : ntok - 1;
-      const uint32_t b = tok / N, n = tok % N;
+      const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s), n = tok - b * N;
       float cv, sv;
       int j0, j1;
       if constexpr (ROT == HR_R1_POS) {
@@ -113,7 +143,7 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
 // rotate / store. Each workgroup therefore waits on one HBM round trip. Rows
 // of one head are adjacent in the [B, H, N, D] output across the tile's
 // tokens, so a head's stores form contiguous runs of tb*D elements.
-template <typename T, int D, int NORM, int ROT, int R, int NTB>
+template <typename T, int D, int NORM, int ROT, int R, int NTB, bool O32>
 __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   constexpr int LPR = D / 8;
   constexpr int M = RotPartner<ROT, D>::M;
@@ -133,11 +163,12 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const uint32_t it = (uint32_t)(r * ipp) + threadIdx.x / LPR;
-    uint32_t t = it / H, h = it % H;
+    uint32_t t = fdiv(it, p.div_h_m, p.div_h_s), h = it - imul<O32>(t, H);
     uint32_t tok = tok0 + t;
     live[r] = it < items && tok < ntok;
     if (!live[r]) { t = 0; h = 0; tok = tok0; }
-    tt[r] = t; hh[r] = h; nn[r] = tok % N; bb[r] = tok / N;
+    const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s);
+    tt[r] = t; hh[r] = h; nn[r] = tok - imul<O32>(b, N); bb[r] = b;
   }
   float v[NTB][R][8];
   float w[NTB][8], bias[NTB][8];
@@ -147,7 +178,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const char *xp = reinterpret_cast<const char *>(io.x) +
-                       ((int64_t)bb[r] * io.sB + (int64_t)hh[r] * io.sH + (int64_t)nn[r] * io.sN + lane * 8) * EB;
+                       view_off<O32>(bb[r], hh[r], nn[r], io.sB, io.sH, io.sN, lane * 8) * EB;
       Chunk<T>::load(xp, v[q][r]);
     }
     if constexpr (NORM == HN_LN || NORM == HN_RMS) param8(io.p0, io.p0_dt, lane * 8, 1.f, w[q]);
@@ -207,8 +238,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         }
       }
       if (live[r]) {
-        char *yp = reinterpret_cast<char *>(io.y) +
-                   ((int64_t)bb[r] * io.oB + (int64_t)hh[r] * io.oH + (int64_t)nn[r] * io.oN + lane * 8) * EB;
+        char *yp = reinterpret_cast<char *>(io.y) + view_off<O32>(bb[r], hh[r], nn[r], io.oB, io.oH, io.oN, lane * 8) * EB;
         Chunk<T>::store(yp, v[q][r]);
       }
     }
@@ -357,25 +387,38 @@ hipError_t launch_any(int norm, int rot, const HeadParams &p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-template <typename T, int D, int NTB>
-hipError_t launch_dn(int norm, int rot, const HeadParams &p, hipStream_t s) {
-  const int64_t tokens = p.B * p.N;
-  constexpr int LPR = D / 8;
+// Every byte offset the vector kernel forms in the views of p is below 2^31
+// (non-negative strides), and every index and every stride of an axis longer
+// than 1 below 2^24: offsets may then be computed in 32 bits from 24-bit
+// products.
+bool offsets_fit_32(const HeadParams &p, int eb) {
+  const int64_t lim = (int64_t(1) << 31) / eb, lim24 = int64_t(1) << 24;
+  const int64_t ext[3] = {p.B - 1, p.H - 1, p.N - 1};
+  for (int a = 0; a < 3; ++a)
+    if (ext[a] >= lim24) return false;
+  for (int i = 0; i < p.ntens; ++i) {
+    const HeadIO &io = p.io[i];
+    const int64_t in[3] = {io.sB, io.sH, io.sN}, out[3] = {io.oB, io.oH, io.oN};
+    int64_t mi = p.D, mo = p.D;
+    for (int a = 0; a < 3; ++a) {
+      if (in[a] < 0 || out[a] < 0) return false;
+      if (ext[a] > 0 && (in[a] >= lim24 || out[a] >= lim24)) return false;
+      mi += ext[a] * in[a];
+      mo += ext[a] * out[a];
+    }
+    if (mi >= lim || mo >= lim) return false;
+  }
+  return true;
+}
+
+template <typename T, int D, int NTB, bool O32>
+hipError_t launch_cases(int norm, int rot, const HeadParams &p, int tb, const dim3 &grid, const dim3 &block, size_t lds,
+                        hipStream_t s) {
   constexpr int R = T::bytes == 4 ? 1 : 2;
-  // Whole heads per pass: threads = k*H*LPR rounded to wavefronts, <= 256.
-  const int64_t hl = p.H * LPR;
-  int64_t k = hl >= 256 ? 1 : 256 / hl;
-  int64_t threads = ((k * hl + 63) / 64) * 64;
-  if (threads > 256) threads = 256;
-  const int64_t ipp = threads / LPR;
-  int64_t tb = (R * ipp) / p.H;
-  if (tb < 1) return hipErrorInvalidValue;  // more heads than one pass holds (H*D > 2048)
-  const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
-  const dim3 grid((unsigned)((tokens + tb - 1) / tb), NTB == 2 ? 1u : (unsigned)p.ntens), block((unsigned)threads);
-#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                                 \
-  if (norm == NORM_ && rot == ROT_) {                                                                \
-    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R, NTB>), grid, block, lds, s, p, (int)tb);   \
-    return hipGetLastError();                                                                        \
+#define LUX3D_HEAD_CASE(NORM_, ROT_)                                                                          \
+  if (norm == NORM_ && rot == ROT_) {                                                                         \
+    hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R, NTB, O32>), grid, block, lds, s, p, tb);            \
+    return hipGetLastError();                                                                                 \
   }
   LUX3D_HEAD_CASE(HN_LN, HR_R1_TAB) LUX3D_HEAD_CASE(HN_LN, HR_R1_POS)
   LUX3D_HEAD_CASE(HN_NONE, HR_R1_TAB) LUX3D_HEAD_CASE(HN_NONE, HR_R1_POS)
@@ -387,6 +430,28 @@ hipError_t launch_dn(int norm, int rot, const HeadParams &p, hipStream_t s) {
   LUX3D_HEAD_CASE(HN_NONE, HR_NONE)
 #undef LUX3D_HEAD_CASE
   return hipErrorInvalidValue;
+}
+
+template <typename T, int D, int NTB>
+hipError_t launch_dn(int norm, int rot, const HeadParams &p0, hipStream_t s) {
+  const int64_t tokens = p0.B * p0.N;
+  constexpr int LPR = D / 8;
+  constexpr int R = T::bytes == 4 ? 1 : 2;
+  // Whole heads per pass: threads = k*H*LPR rounded to wavefronts, <= 256.
+  const int64_t hl = p0.H * LPR;
+  int64_t k = hl >= 256 ? 1 : 256 / hl;
+  int64_t threads = ((k * hl + 63) / 64) * 64;
+  if (threads > 256) threads = 256;
+  const int64_t ipp = threads / LPR;
+  int64_t tb = (R * ipp) / p0.H;
+  if (tb < 1) return hipErrorInvalidValue;  // more heads than one pass holds (H*D > 2048)
+  HeadParams p = p0;
+  div_magic(p.H, p.div_h_m, p.div_h_s);
+  div_magic(p.N, p.div_n_m, p.div_n_s);
+  const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
+  const dim3 grid((unsigned)((tokens + tb - 1) / tb), NTB == 2 ? 1u : (unsigned)p.ntens), block((unsigned)threads);
+  if (offsets_fit_32(p, T::bytes)) return launch_cases<T, D, NTB, true>(norm, rot, p, (int)tb, grid, block, lds, s);
+  return launch_cases<T, D, NTB, false>(norm, rot, p, (int)tb, grid, block, lds, s);
 }
 
 // q and k share a workgroup for D = 128 (measured: configs[2] RMS and

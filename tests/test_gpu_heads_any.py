@@ -241,3 +241,30 @@ def test_kat_timestep_embedding(dev, ops):
     f1 = np.float32(math.exp(-math.log(10000.0) / 2.0))
     want = [math.cos(500.0), math.cos(np.float32(500.0) * f1), math.sin(500.0), math.sin(np.float32(500.0) * f1)]
     assert np.all(np.abs(out - np.array(want, dtype=np.float32)) < 1e-5), out
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_head_kernel_64bit_offsets_match_32bit(dev, ops, D):
+    """The vector head kernel forms its offsets in 32 bits (24-bit products)
+    when every byte offset of the views is below 2^31 and every stride of an
+    axis longer than 1 below 2^24, else in 64 bits. A batch stride of
+    2^24 + 64 elements takes the 64-bit instance; its q and k equal, bit for
+    bit, the same rows normalised from compact tensors (32-bit instance)."""
+    B, H, L = 2, 4, 40
+    sb = (1 << 24) + 64
+    print(f"\n[case] head kernel 64-bit offsets D={D} batch stride {sb}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(11 + D)
+    q = torch.randn(B, H, L, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(B, H, L, D, generator=g).to(torch.bfloat16).to(dev)
+    wq = (torch.rand(D, generator=g) + 0.5).to(dev)
+    wk = (torch.rand(D, generator=g) + 0.5).to(dev)
+    bq = torch.zeros(sb * B, dtype=torch.bfloat16, device=dev)
+    bk = torch.zeros(sb * B, dtype=torch.bfloat16, device=dev)
+    qv = bq.as_strided((B, H, L, D), (sb, L * D, D, 1))
+    kv = bk.as_strided((B, H, L, D), (sb, L * D, D, 1))
+    qv.copy_(q)
+    kv.copy_(k)
+    got_q, got_k = ops.rms_norm_heads(qv, wq, 1e-6, k=kv, k_weight=wk)
+    want_q, want_k = ops.rms_norm_heads(q, wq, 1e-6, k=k, k_weight=wk)
+    torch.cuda.synchronize()
+    assert torch.equal(got_q, want_q) and torch.equal(got_k, want_k)
