@@ -723,7 +723,10 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
     }
   } else {
     if (p.mfma) {
-      if (p.D == 64) return launch_mfma_f32<64, 64, 2>(p, s);
+      // 32-key blocks at D 64: 127 VGPRs and 36 KB of LDS, four wavefronts
+      // per SIMD (VGGT frame attention in f32: 572 against 670 us for 64-key
+      // blocks at two)
+      if (p.D == 64) return launch_mfma_f32<64, 32, 2>(p, s);
       if (p.D == 128) return launch_mfma_f32<128, 32, 2>(p, s);
     }
   }
