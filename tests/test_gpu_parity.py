@@ -567,3 +567,35 @@ def test_dequant_q8_0(dev, ops, orc, synth, out, which):
     u = np.uint32 if out == "f32" else np.uint16
     assert np.array_equal(host_view(y3, out).reshape(-1).view(u), want.view(u)), "2-byte aligned blocks"
     assert np.array_equal(host_view(y4, out).reshape(-1).view(u), want[:nb * 32].view(u)), "ragged block count"
+
+
+def test_empty_inputs_are_no_ops(dev, ops, synth):
+    """Zero rows / tokens / queries / blocks: every entry returns OK and an
+    empty result without launching (candle's ops on empty tensors are
+    no-ops)."""
+    print("\n[case] empty inputs", flush=True)
+    bf = torch.bfloat16
+    C = 1024
+    x0 = torch.empty((0, C), dtype=bf, device=dev)
+    g = torch.ones(C, device=dev)
+    h, y = ops.residual_layer_norm(x0, x0, g, g, torch.zeros(C, device=dev), 1e-5)
+    assert h.shape == (0, C) and y.shape == (0, C)
+    assert ops.gated_residual(x0, x0, g).shape == (0, C)
+    assert ops.gelu_erf(x0).shape == (0, C) and ops.gelu(x0).shape == (0, C) and ops.silu(x0).shape == (0, C)
+    q = torch.empty((2, 0, 3, 16, 64), dtype=bf, device=dev)
+    qv, kv = q[:, :, 0].permute(0, 2, 1, 3), q[:, :, 1].permute(0, 2, 1, 3)
+    w64, b64 = torch.ones(64, device=dev), torch.zeros(64, device=dev)
+    pos = torch.empty((2, 0, 2), dtype=torch.int32, device=dev)
+    qo, ko = ops.qk_layernorm_rope2d(qv, kv, (w64, b64, 1e-5), (w64, b64, 1e-5), positions=pos)
+    assert qo.shape == (2, 16, 0, 64) and ko.shape == (2, 16, 0, 64)
+    r = torch.empty((2, 16, 0, 128), dtype=bf, device=dev)
+    assert ops.rms_norm_heads(r, torch.ones(128, device=dev), 1e-6).shape == (2, 16, 0, 128)
+    t0 = torch.empty((0,), dtype=torch.float32, device=dev)
+    assert ops.timestep_embedding(t0, 256).shape == (0, 256)
+    assert ops.dequantize_q8_0(torch.empty((0,), dtype=torch.uint8, device=dev), (0, 32)).shape == (0, 32)
+    blocks = torch.from_numpy(synth.q8_0_blocks(5, 64 * 128 // 32)).to(dev)
+    mm = ops.QMatMul.from_q8_0(blocks, 64, 128)
+    assert mm.forward(torch.empty((0, 128), dtype=bf, device=dev)).shape == (0, 64)
+    kk = torch.randn((1, 4, 5, 64), device=dev).to(bf)
+    assert ops.sdpa(torch.empty((1, 4, 0, 64), dtype=bf, device=dev), kk, kk, 0.125).shape == (1, 4, 0, 64)
+    torch.cuda.synchronize()
