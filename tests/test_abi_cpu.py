@@ -299,3 +299,24 @@ def test_sdpa_layernorm_rope2d_argument_errors():
     assert rc == _lib.ERR_VALUE
     rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, w, b, 1e-5, cs, sn, k, v, 0.0, o, None)
     assert rc == _lib.ERR_VALUE
+
+
+def test_integration_ffi_block_lists_every_entry():
+    """The Rust extern blocks that INTEGRATION.md gives a maintainer declare
+    exactly the functions of include/lux3d_fused.h and include/lux3d_weights.h,
+    each with the header's parameter count."""
+    def header_sigs(path):
+        text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+        out = {}
+        for name, args in re.findall(r"\b(lux3d_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+            a = " ".join(args.split())
+            out[name] = 0 if a in ("", "void") else a.count(",") + 1
+        return out
+    want = header_sigs(HEADER)
+    want.update(header_sigs(os.path.join(ROOT, "include", "lux3d_weights.h")))
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    got = {}
+    for name, args in re.findall(r"pub fn (lux3d_[a-z0-9_]+)\(([^;]*?)\)\s*(?:->[^;]*)?;", doc, flags=re.S):
+        a = " ".join(args.split())
+        got[name] = 0 if not a else a.count(",") + 1
+    assert got == want
