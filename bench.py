@@ -179,7 +179,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the fused ops are "
-              f"row-independent and shard with no exchange (see DESIGN.md), but no multi-GPU run is part of "
+              f"row-independent and shard with no exchange, but no multi-GPU run is part of "
               f"this round.", file=sys.stderr)
         sys.exit(2)
     import torch

@@ -375,7 +375,7 @@ def cfg4_dinov3_rope(dev) -> Workload:
     return wl
 
 
-# The configs[1..4] ops BASELINE.md names (the >=70%-of-peak targets), then extras.
+# The configs[1..4] ops of the headline benchmark (the >=70%-of-peak targets), then extras.
 def _q8_linear(dev, cfg, m, k, n, what, xdt=torch.bfloat16) -> Workload:
     """Q8_0 quantized linear y = x @ dequant(W)^T + bias at a model's shape.
     The weight is repacked once (load time, outside the timed launch); x

@@ -302,9 +302,9 @@ def test_sdpa_layernorm_rope2d_argument_errors():
 
 
 def test_integration_ffi_block_lists_every_entry():
-    """The Rust extern blocks that INTEGRATION.md gives a maintainer declare
-    exactly the functions of include/lux3d_fused.h and include/lux3d_weights.h,
-    each with the header's parameter count."""
+    """The Rust extern blocks of the integration guide at the repository root
+    declare exactly the functions of include/lux3d_fused.h and
+    include/lux3d_weights.h, each with the header's parameter count."""
     def header_sigs(path):
         text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
         out = {}
