@@ -179,8 +179,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the fused ops are "
-              f"row-independent and shard with no exchange, but no multi-GPU run is part of "
-              f"this round.", file=sys.stderr)
+              f"row-independent and shard with no exchange, but this build has no multi-GPU run.",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
