@@ -272,13 +272,15 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) 
 // XCDs; they are renumbered so that each XCD takes a contiguous range, walked
 // in groups of GM row tiles (columns fastest within a group), so the tiles
 // running on one XCD share x rows and weight columns in its L2.
-template <typename OUT, int GM, int BM>
-__global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
-  constexpr int BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
-  constexpr int kRingA = BM * 128, kRingStage = kRingA + kRingW + kRingS;  // 51,200 / 34,816 bytes
-  constexpr int SEGW = BM / 64;                    // x segments (1 KB = 8 rows) per wavefront
+template <typename OUT, int GM, int BM, int NW = 8>
+__global__ __launch_bounds__(64 * NW, 1) void q8_0_gemm_ring_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
+  // NW wavefronts, each owning 32 columns: BN = 32 NW (256 or 128)
+  constexpr int BN = 32 * NW, BK = 64, TM = BM / 32, NS = kRingStages;
+  constexpr int RW = BN * 64, RS = BN * 8;          // weights and scales per stage
+  constexpr int kRingA = BM * 128, kRingStage = kRingA + RW + RS;  // 51,200 / 34,816 / 25,600 bytes
+  constexpr int SEGW = BM / (8 * NW);              // x segments (1 KB = 8 rows) per wavefront
   constexpr int kRingOps = SEGW + 2 + 1;           // direct loads per wavefront per stage
-  static_assert(BM == 128 || BM == 256, "tile rows");
+  static_assert((BM == 128 || BM == 256) && (NW == 4 || NW == 8) && SEGW >= 1, "tile shape");
   __shared__ __align__(16) char ring[NS * kRingStage];
 
   const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
       lds_load16(xr, xoff[i], (uint32_t)kt * BK * 2, __builtin_amdgcn_readfirstlane(st + (wave * SEGW + i) * 1024));
     lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048));
     lds_load16(wr, woff, (uint32_t)kt * BK + 16, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048 + 1024));
-    lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + kRingW + wave * 256));
+    lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + RW + wave * 256));
   };
 
   // fragment of M-tile i, sub-step s at fbase[s] + i * 4096 (the swizzle only
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
   auto read_w = [&](const char *st) {
     w0 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + lane * 16);
     w1 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + 1024 + lane * 16);
-    sc = *reinterpret_cast<const float *>(st + kRingA + kRingW + wave * 256 + lane * 4);
+    sc = *reinterpret_cast<const float *>(st + kRingA + RW + wave * 256 + lane * 4);
   };
   auto make_b = [&](int s) {
     const uint4 &v = s < 2 ? w0 : w1;
@@ -403,8 +405,8 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_kernel(Q8GemmP
     // stage the wavefront's BM x 32 block through the ring, RP rows per
     // pass (rows padded by 16 bytes), and store whole 16-byte row pieces
     constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB;
-    constexpr int RP = 8 * 128 * LROW <= NS * kRingStage ? 128 : 64, REGION = RP * LROW;
-    static_assert(8 * REGION <= NS * kRingStage, "epilogue staging fits the ring");
+    constexpr int RP = NW * 128 * LROW <= NS * kRingStage ? 128 : 64, REGION = RP * LROW;
+    static_assert(NW * REGION <= NS * kRingStage, "epilogue staging fits the ring");
     __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
     char *reg = ring + wave * REGION;
     const int64_t c0w = c0 + wave * 32;
@@ -681,10 +683,16 @@ hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
     if (tiles_m256 * tiles_n >= kRingMinTiles) {
       hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 256>), dim3((unsigned)(tiles_m256 * tiles_n)), dim3(kRingThreads),
                          0, s, p, (int)tiles_m256, (int)tiles_n);
-    } else {
+    } else if ((p.M + 127) / 128 * tiles_n >= kRingMinTiles) {
       const int64_t tiles_m = (p.M + 127) / 128;
       hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 128>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0,
                          s, p, (int)tiles_m, (int)tiles_n);
+    } else {
+      // fewer 128 x 256 tiles than CUs: 128 x 128 tiles of four wavefronts
+      // (two workgroups per CU by LDS) spread the same wavefronts over more CUs
+      const int64_t tiles_m = (p.M + 127) / 128, tiles_n128 = (p.N + 127) / 128;
+      hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 128, 4>), dim3((unsigned)(tiles_m * tiles_n128)), dim3(256), 0,
+                         s, p, (int)tiles_m, (int)tiles_n128);
     }
     return hipGetLastError();
   }

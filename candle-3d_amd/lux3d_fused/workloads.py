@@ -404,7 +404,7 @@ def _q8_linear(dev, cfg, m, k, n, what, xdt=torch.bfloat16) -> Workload:
                       nbytes, f"x[{m},{k}] f32 @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n,
                       peak_tflops=157.3)
     else:
-        wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
+        wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16,...>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
                       f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
     wl._keep = (xs, ys, qs, scales, bias, blocks, dx, dy, dq, dsc, db)
     return wl
