@@ -1,8 +1,8 @@
 // q8_gemm.hip -- the Q8_0 quantized linear for gfx950: y = x * W^T (+ bias)
 // with W stored as GGML Q8_0 (int8 values, one scale per 32 along K).
 //
-// Semantics: W is dequantized exactly as the Q8_0 -> bf16 op does it
-// (w = RNE_bf16(f32(q) * d), the product q * d being exact in f32), x is
+// Semantics (bf16 x): W is dequantized exactly as the Q8_0 -> bf16 op does
+// it (w = RNE_bf16(f32(q) * d), the product q * d being exact in f32), x is
 // bf16, products accumulate in f32 on the matrix cores
 // (v_mfma_f32_32x32x16_bf16), the bias is added in f32 and the result is
 // rounded once to y's dtype. That is candle's dequantize-then-matmul path
@@ -14,10 +14,11 @@
 // [N, K/32], so the GEMM streams them with 16-byte loads.
 //
 // Two GEMM kernels (both one rounding of the f32 sum per output):
-// - q8_0_gemm_ring_kernel (K % 64 == 0, the common case): a 512-thread
-//   workgroup per CU computes a 256 x 256 tile; x, the int8 weights and the
-//   scales stream through a 3-stage LDS ring by direct global->LDS loads;
-//   each wavefront dequantises its own 32 weight columns once per k-step.
+// - q8_0_gemm_ring_kernel (K % 64 == 0, the common case): a workgroup of NW
+//   wavefronts (8, or 4 for small shapes) computes a BM x 32 NW tile; x, the
+//   int8 weights and the scales stream through a 3-stage LDS ring by direct
+//   global->LDS loads; each wavefront dequantises its own 32 weight columns
+//   once per k-step.
 // - q8_0_gemm_kernel (K % 64 == 32): a 256-thread workgroup computes a
 //   128 x 128 tile; x and the dequantised W are staged as bf16 in LDS,
 //   double-buffered, through registers.
@@ -663,9 +664,10 @@ bool ring_fits(const Q8GemmParams &p) {
 // Kernel choice (measured on MI355X, graph-timed over rotating inputs):
 // the ring kernel whenever K % 64 == 0 (every shape of the models): 256-row
 // tiles when they cover every CU at least once (1,018 TFLOP/s at
-// 4096x2048x8192, 512 tiles), else 128-row tiles (1029x1024x4096: 9 x 16
-// tiles, 402 against 314 TFLOP/s for the 128 x 128 kernel in a probe). The
-// 128 x 128 kernel with 32-deep k-steps covers K % 64 == 32.
+// 4096x2048x8192, 512 tiles), else 128-row tiles of 8 wavefronts when those
+// do, else 128 x 128 tiles of 4 wavefronts (1029x1024x4096: 9 x 32 tiles,
+// 24.0 us against 26.8 us for 9 x 16 tiles of 8 wavefronts). The 128 x 128
+// kernel with 32-deep k-steps covers K % 64 == 32.
 constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
 
 template <typename OUT>
