@@ -513,6 +513,73 @@ __global__ __launch_bounds__(256) void c2s_count_kernel(const void *logits, int6
 }
 
 // exclusive scan of the block totals in place (one workgroup); total -> count
+// The same counts and offsets with coalesced loads (logits, and sub when
+// given, 16-byte aligned): the block's logits arrive as 16-byte chunks in
+// lane order, their leaf flags go to LDS (and to sub), and each thread then
+// counts its 4 parents from LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void c2s_count_vec_kernel(const void *logits, int64_t n, float *sub,
+                                                            int32_t *offs, int32_t *block_sums) {
+  constexpr int PER = 16 / T::bytes;                // logits per 16-byte chunk
+  constexpr int CHUNKS = kScanBlock * 8 / PER;      // chunks per workgroup
+  __shared__ __align__(16) uint8_t leaf[kScanBlock * 8];
+  __shared__ int32_t wsum[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t l0 = (int64_t)blockIdx.x * kScanBlock * 8, nl = n * 8;
+  for (int c = t; c < CHUNKS; c += 256) {
+    const int64_t l = l0 + (int64_t)c * PER;
+    if (l >= nl) break;  // n * 8 logits: a multiple of PER, so every chunk is whole
+    const uint4 u = ld16<false>(reinterpret_cast<const char *>(logits) + l * T::bytes);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float f[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      if constexpr (T::bytes == 4) f[e] = __uint_as_float(w[e]);
+      else if constexpr (T::code == LUX3D_BF16) f[e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
+      else f[e] = f16_bits_to_f32((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu));
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) leaf[c * PER + e] = f[e] > 0.f;
+    if (sub) {
+#pragma unroll
+      for (int e = 0; e < PER; e += 4)
+        *reinterpret_cast<float4 *>(sub + l + e) = make_float4(f[e] > 0.f ? 1.f : 0.f, f[e + 1] > 0.f ? 1.f : 0.f,
+                                                               f[e + 2] > 0.f ? 1.f : 0.f, f[e + 3] > 0.f ? 1.f : 0.f);
+    }
+  }
+  __syncthreads();
+  const int64_t p0 = (int64_t)blockIdx.x * kScanBlock + t * 4;
+  int32_t c[4];
+  int32_t tot = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int32_t cnt = 0;
+    if (p0 + q < n) {
+      const uint2 b = *reinterpret_cast<const uint2 *>(&leaf[(t * 4 + q) * 8]);  // 8 flags of 0 / 1
+      cnt = (int32_t)(__builtin_popcount(b.x) + __builtin_popcount(b.y));
+    }
+    c[q] = cnt;
+    tot += cnt;
+  }
+  int32_t incl = tot;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  int32_t run = base + incl - tot;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (p0 + q < n) offs[p0 + q] = run;
+    run += c[q];
+  }
+  if (t == 255) block_sums[blockIdx.x] = base + incl;
+}
+
 __global__ __launch_bounds__(256) void c2s_scan_kernel(int32_t *block_sums, int64_t nb, int32_t *count) {
   __shared__ int32_t wsum[4];
   __shared__ int32_t carry;
@@ -647,18 +714,31 @@ hipError_t launch_c2s(const C2SParams &p, hipStream_t s) {
     hipLaunchKernelGGL(c2s_scan_kernel, dim3(1), dim3(256), 0, s, p.block_sums, (int64_t)0, p.count);
     return hipGetLastError();
   }
+  const bool vec = (uintptr_t)p.logits % 16 == 0 && (uintptr_t)p.sub % 16 == 0;
   switch (p.logits_dt) {
     case LUX3D_F32:
-      hipLaunchKernelGGL((c2s_count_kernel<F32>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
-                         p.block_sums);
+      if (vec)
+        hipLaunchKernelGGL((c2s_count_vec_kernel<F32>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub,
+                           p.offs, p.block_sums);
+      else
+        hipLaunchKernelGGL((c2s_count_kernel<F32>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
+                           p.block_sums);
       break;
     case LUX3D_BF16:
-      hipLaunchKernelGGL((c2s_count_kernel<BF16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
-                         p.block_sums);
+      if (vec)
+        hipLaunchKernelGGL((c2s_count_vec_kernel<BF16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub,
+                           p.offs, p.block_sums);
+      else
+        hipLaunchKernelGGL((c2s_count_kernel<BF16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub,
+                           p.offs, p.block_sums);
       break;
     case LUX3D_F16:
-      hipLaunchKernelGGL((c2s_count_kernel<F16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub, p.offs,
-                         p.block_sums);
+      if (vec)
+        hipLaunchKernelGGL((c2s_count_vec_kernel<F16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub,
+                           p.offs, p.block_sums);
+      else
+        hipLaunchKernelGGL((c2s_count_kernel<F16>), dim3((unsigned)nb), dim3(256), 0, s, p.logits, p.n, p.sub,
+                           p.offs, p.block_sums);
       break;
     default: return hipErrorInvalidValue;
   }
