@@ -212,3 +212,28 @@ def test_sparse_conv3d_rulebook_matches_reference_order(dev, ops, orc):
     got = conv.forward(ops.SparseRulebook(nbr), torch.from_numpy(x).to(dev)).cpu().numpy()
     want = orc.sparse_conv3d(x, orc.sparse_neighbors(coords), w27, bias)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("ldt", ["f32", "bf16"])
+def test_channel_to_spatial_unaligned_logits(dev, ops, orc, ldt):
+    """Logits that start 1 element past a 16-byte boundary take the count
+    kernel's per-element path; children, features and sub_binary equal the
+    oracle's, as on the aligned path."""
+    n, c = 2000, 64
+    _case(op="c2s unaligned logits", n=n, c=c, logits=ldt)
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16}[ldt]
+    coords = random_coords(n, 64, 17)
+    rng = np.random.default_rng(17)
+    feats = rng.standard_normal((n, c)).astype(np.float32)
+    logits = rng.standard_normal((n, 8)).astype(np.float32)
+    lt = torch.from_numpy(logits).to(tdt)
+    buf = torch.empty(n * 8 + 1, dtype=tdt, device=dev)
+    lv = buf[1:].view(n, 8)
+    lv.copy_(lt.to(dev))
+    assert lv.data_ptr() % 16 != 0
+    oc, of, sub = ops.channel_to_spatial(torch.from_numpy(coords).to(dev), torch.from_numpy(feats).to(dev), lv)
+    torch.cuda.synchronize()
+    woc, wof, _, wsub = orc.channel_to_spatial(coords, feats, lt.float().numpy())
+    assert np.array_equal(oc.cpu().numpy(), woc)
+    assert torch.equal(of.cpu(), torch.from_numpy(wof))
+    assert np.array_equal(sub.cpu().numpy(), wsub)
