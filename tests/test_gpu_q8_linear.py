@@ -227,3 +227,27 @@ def test_q8_0_linear_f32_strided_and_rejects_k96(dev, ops, orc, synth):
     y96 = torch.zeros((4, 32), dtype=torch.float32, device=dev)
     with pytest.raises(Lux3dError, match="multiple of 64"):
         _lib.call("lux3d_q8_0_linear", ops.desc(x96), ops.desc(q96), ops.desc(s96), None, ops.desc(y96), None)
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+@pytest.mark.parametrize("extra", [0, 3])
+def test_q8_0_linear_four_wavefront_tiles(dev, ops, orc, synth, out, extra):
+    """x [300, 256] -> [300, 200]: 3 x 1 tiles of 128 x 256 cannot fill the
+    CUs, so the ring kernel runs 3 x 2 tiles of 128 x 128 with four
+    wavefronts (the last column tile holds 72 columns, the last row tile 44
+    rows). y is a view of a buffer `extra` columns wider: aligned rows take
+    the staged epilogue, unaligned rows the per-element stores."""
+    m, k, n = 300, 256, 200
+    print(f"\n[case] q8_0_linear four-wavefront tiles out={out} ldy={n + extra}", flush=True)
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 820 + extra)
+    ywide = torch.zeros((m, n + extra), dtype=TDT[out], device=dev)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    from lux3d_fused import _lib
+    _lib.call("lux3d_q8_0_linear", ops.desc(xd), ops.desc(qs), ops.desc(scales), ops.desc(torch.from_numpy(b).to(dev)),
+              ops.desc(ywide[:, :n]), None)
+    torch.cuda.synchronize()
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, b, orc.F32 if out == "f32" else orc.BF16,
+                                    with_abs=True)
+    assert_gemm_close(host(ywide[:, :n], out), want, abs_sum, out, "four-wavefront tiles")
+    if extra:
+        assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
