@@ -113,12 +113,15 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
 // QLN: q arrives raw; its LayerNorm and 2D RoPE (the QK kernel's arithmetic
 // and lane mapping, bit for bit) are applied while the Q fragments are
 // loaded, so the normalised q never goes through HBM.
-template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool QLN = false>
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool QLN = false,
+          bool DMA = false>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   using M = Mma<T>;
   using op_t = typename M::op_t;
   constexpr int BQ = 4 * 32 * QT;
-  constexpr int KROW = D + 8;              // 2-byte elements per K / V row in LDS (16-byte pad)
+  // 2-byte elements per K / V row in LDS: padded by 16 bytes, or (DMA)
+  // unpadded with 16-byte chunk c of row r in slot c ^ ((r & 7) * D / 64)
+  constexpr int KROW = DMA ? D : D + 8;
   constexpr int KCH = BKV * D / 8 / 256;   // 16-byte K (and V) chunks per thread per block
   constexpr int NKT = BKV / 32;            // 32-key tiles per block
   constexpr int NDT = D / 32;              // 32-dim output tiles
@@ -212,6 +215,32 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     k_off[i] = ((int64_t)k_row[i] * p.k_st + k_part[i] * 8) * 2;
     v_off[i] = ((int64_t)k_row[i] * p.v_st + k_part[i] * 8) * 2;
   }
+  // DMA: load i of a wavefront fills LDS bytes [seg * 1024, + 1024) of a
+  // buffer, seg = wave * KCH + i, in lane order; the lane loads the logical
+  // chunk that its slot holds. Keys past Lk fall outside the descriptors and
+  // read as zeros (finite; their scores are masked).
+  constexpr int SWZ = D / 64;
+  uint32_t dk_off[KCH], dv_off[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int byte = (wave * KCH + i) * 1024 + lane * 16, r = byte / (2 * D), sl = (byte % (2 * D)) / 16;
+    const int c = sl ^ ((r & 7) * SWZ);
+    dk_off[i] = (uint32_t)(r * p.k_st * 2 + c * 16);
+    dv_off[i] = (uint32_t)(r * p.v_st * 2 + c * 16);
+  }
+  const i32x4_t krs = buffer_rsrc(kbase, ((Lk - 1) * p.k_st + D) * 2);
+  const i32x4_t vrs = buffer_rsrc(vbase, ((Lk - 1) * p.v_st + D) * 2);
+  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
+  const uint32_t lds_v = lds_k + 2 * BKV * KROW * 2;
+  auto dma_kv = [&](int64_t j, int buf) {
+    const uint32_t sk = (uint32_t)(j * BKV * p.k_st * 2), sv = (uint32_t)(j * BKV * p.v_st * 2);
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const uint32_t off = (uint32_t)((wave * KCH + i) * 1024 + buf * BKV * KROW * 2);
+      lds_load16(krs, dk_off[i], sk, __builtin_amdgcn_readfirstlane(lds_k + off));
+      lds_load16(vrs, dv_off[i], sv, __builtin_amdgcn_readfirstlane(lds_v + off));
+    }
+  };
   const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2;
   uint4 rk[KCH], rv[KCH];
   // `clamp` (the tail block only): keys past Lk read row Lk - 1
@@ -254,15 +283,24 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   const int64_t nkv = (Lk + BKV - 1) / BKV;
   const bool tail = (Lk % BKV) != 0;
 
-  load_kv(0, nkv == 1 && tail);
-  store_kv(0);
+  if constexpr (DMA) {
+    dma_kv(0, 0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  } else {
+    load_kv(0, nkv == 1 && tail);
+    store_kv(0);
+  }
   lds_barrier();
 
   // one block of keys; MASK (the partial tail block) sets scores past Lk to -inf
   auto step = [&](int64_t j, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
     const int buf = (int)(j & 1);
-    if (j + 1 < nkv) load_kv(j + 1, tail && j + 2 == nkv);
+    if constexpr (DMA) {
+      if (j + 1 < nkv) dma_kv(j + 1, buf ^ 1);
+    } else {
+      if (j + 1 < nkv) load_kv(j + 1, tail && j + 2 == nkv);
+    }
 
     // S^T = K Q^T: lane holds key 8 * (i / 4) + 4 * hh + i % 4 of each 32-key tile, query l32.
     f32x16_t s[QT][NKT];
@@ -274,7 +312,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
-        const op_t a = *reinterpret_cast<const op_t *>(&Ks[buf][(kt * 32 + l32) * KROW + c * 16 + 8 * hh]);
+        const int krow = kt * 32 + l32, kch = DMA ? ((2 * c + hh) ^ ((krow & 7) * SWZ)) : 2 * c + hh;
+        const op_t a = *reinterpret_cast<const op_t *>(&Ks[buf][krow * KROW + kch * 8]);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) s[qt][kt] = M::run(a, qf[qt][c], s[qt][kt]);
       }
@@ -347,8 +386,10 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
     auto vfrag = [&](int dt, int kt, int jj) {
       const int g16 = lane & 15;
-      const uint16_t *vr = &Vs[buf][(kt * 32 + 16 * jj + 4 * hh + (g16 >> 2)) * KROW + dt * 32 +
-                                    16 * ((lane >> 4) & 1) + 4 * (g16 & 3)];
+      const int vrow = kt * 32 + 16 * jj + 4 * hh + (g16 >> 2);
+      const int vcol = dt * 32 + 16 * ((lane >> 4) & 1) + 4 * (g16 & 3);  // rows vrow and vrow + 8 swizzle alike
+      const int vch = DMA ? ((vcol >> 3) ^ ((vrow & 7) * SWZ)) : vcol >> 3;
+      const uint16_t *vr = &Vs[buf][vrow * KROW + vch * 8 + (vcol & 7)];
       const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr));
       const s16x4_t hi2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr + 8 * KROW));
       return __builtin_bit_cast(op_t, __builtin_shufflevector(lo, hi2, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -390,7 +431,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
           }
     }
 
-    if (j + 1 < nkv) store_kv(buf ^ 1);
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wavefront's block j + 1 landed
+    else if (j + 1 < nkv) store_kv(buf ^ 1);
     lds_barrier();
   };
   const int64_t nfull = tail ? nkv - 1 : nkv;
@@ -662,23 +704,18 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
   }
 }
 
-template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED>
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool DMA>
 hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
-  if (p.qln) {
-    constexpr int BQ = 4 * 32 * QT;
-    const int64_t nqb = (p.Lq + BQ - 1) / BQ;
-    const int64_t nwg = p.B * p.H * nqb;
-    if (nwg > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, true>), dim3((unsigned)nwg), dim3(256),
-                       0, s, p, nqb, nwg);
-    return hipGetLastError();
-  }
   constexpr int BQ = 4 * 32 * QT;
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED>), dim3((unsigned)nwg), dim3(256), 0, s, p,
-                     nqb, nwg);
+  if (p.qln)
+    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, true, DMA>), dim3((unsigned)nwg),
+                       dim3(256), 0, s, p, nqb, nwg);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, false, DMA>), dim3((unsigned)nwg),
+                       dim3(256), 0, s, p, nqb, nwg);
   return hipGetLastError();
 }
 
@@ -705,10 +742,17 @@ hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// D = 64 with short query sequences (VGGT frame attention, 1,374 tokens):
-// 128-query workgroups at three wavefronts per SIMD, which fill the CUs in
-// more, shorter rounds than the 256-query ones.
+// D 128: K / V as direct global -> LDS loads (DMA) when every key offset of
+// a head fits the 32-bit buffer offsets (TripoSG 87.2 against 92.3 us,
+// TRELLIS.2 40k voxels 10.3 against 11.2 ms, bit-identical). D 64 stays
+// register-staged (with rotating inputs DMA gained nothing there):
+// 128-query workgroups for short sequences, which fill the CUs in more,
+// shorter rounds, and 256-query ones (the phased form) for long ones.
 constexpr int64_t kShortQ = 4096;
+bool dma_fits(const AttnParams &p) {
+  const int64_t st = p.k_st > p.v_st ? p.k_st : p.v_st;
+  return p.k_st >= 0 && p.v_st >= 0 && (p.Lk + 64) * st * 2 + 2 * p.D < (int64_t(1) << 31);
+}
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
@@ -716,10 +760,13 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {
-        if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, true, false>(p, s);
-        return launch_mfma<T, 64, 2, 64, 2, true, true, true>(p, s);
+        if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
+        return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);
       }
-      if (p.D == 128) return launch_mfma<T, 128, 1, 64, 2, true, true, false>(p, s);
+      if (p.D == 128) {
+        if (dma_fits(p)) return launch_mfma<T, 128, 1, 64, 2, true, true, false, true>(p, s);
+        return launch_mfma<T, 128, 1, 64, 2, true, true, false, false>(p, s);
+      }
     }
   } else {
     if (p.mfma) {

@@ -225,33 +225,9 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
 // next stage. The epilogue stages each wavefront's block through the ring
 // (bias added, rounded once) and writes whole 16-byte row pieces.
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kRingStages = 3;
 constexpr int kRingThreads = 512;
 constexpr int kRingW = 256 * 64, kRingS = 256 * 8;  // weights and scales per stage (256 columns)
-
-// A raw buffer descriptor (no stride, num_records bytes from base) for the
-// direct loads; the fields are wave-uniform, readfirstlane keeps them scalar.
-__device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, int64_t bytes) {
-  const uint64_t b = (uint64_t)base;
-  const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
-  return i32x4_t{(int)__builtin_amdgcn_readfirstlane((uint32_t)b), (int)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)),
-                 __builtin_amdgcn_readfirstlane(n), 0x00020000};
-}
-// Each lane reads 16 (4) bytes at voff + soff of the buffer; the wavefront
-// writes them in lane order at LDS byte address lds.
-__device__ __forceinline__ void lds_load16(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_load4(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
-               : "memory", "m0");
-}
-// s_waitcnt immediates (gfx9 layout): vmcnt(n) with lgkmcnt(0), and vmcnt(n) alone
-constexpr int waitcnt_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
-constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
 // 8 int8 (two dwords) -> bf16(f32(q) * d), RNE; q * d is exact in f32
 __device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) {
