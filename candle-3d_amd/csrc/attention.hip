@@ -472,11 +472,15 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 //                 halves hold in S^T's i-th accumulator, 8 (i/4) + 4 hh +
 //                 i % 4: each lane passes its own probability, and V is read
 //                 in its natural [key][dim] layout (no transpose).
-template <int D, int BKV, int MINW>
+template <int D, int BKV, int MINW, bool DMA = false>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   constexpr int BQ = 128;
-  constexpr int KROW = D + 4;              // floats per K row: 16-byte fragment reads conflict-free
-  constexpr int VROW = D + 8;              // floats per V row: the lane halves' rows (4 apart) 32 banks apart
+  // Padded rows: K + 4 floats (16-byte fragment reads conflict-free), V + 8
+  // (the lane halves' rows, 4 apart, 32 banks apart). DMA: unpadded rows,
+  // 16-byte chunk c of row r in slot c ^ sw(r), sw(r) = (r & 3) | 8 ((r >> 2) & 1),
+  // which keeps both reads conflict-free.
+  constexpr int KROW = DMA ? D : D + 4;
+  constexpr int VROW = DMA ? D : D + 8;
   constexpr int KCH = BKV * D / 4 / 256;   // 16-byte chunks of K (and of V) per thread per block
   constexpr int NKT = BKV / 32, NDT = D / 32, HD = D / 2;
   static_assert(KCH >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
@@ -515,6 +519,30 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
     s_part[i] = c % (D / 4);
   }
   float4 rk[KCH], rv[KCH];
+  auto sw = [](int r) { return (r & 3) | (((r >> 2) & 1) << 3); };
+  // DMA: load i of a wavefront fills LDS bytes [seg * 1024, + 1024) of a
+  // buffer (seg = wave * KCH + i) in lane order; keys past Lk fall outside the
+  // descriptors and read as zeros (finite; their scores are masked)
+  uint32_t dk_off[KCH], dv_off[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int byte = (wave * KCH + i) * 1024 + lane * 16, r = byte / (4 * D), c = ((byte % (4 * D)) / 16) ^ sw(r);
+    dk_off[i] = (uint32_t)((r * p.k_st + c * 4) * 4);
+    dv_off[i] = (uint32_t)((r * p.v_st + c * 4) * 4);
+  }
+  const i32x4_t krs = buffer_rsrc(kbase, ((Lk - 1) * p.k_st + D) * 4);
+  const i32x4_t vrs = buffer_rsrc(vbase, ((Lk - 1) * p.v_st + D) * 4);
+  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)smem;
+  const uint32_t lds_v = lds_k + 2 * BKV * KROW * 4;
+  auto dma_kv = [&](int64_t j, int buf) {
+    const uint32_t sk = (uint32_t)(j * BKV * p.k_st * 4), sv = (uint32_t)(j * BKV * p.v_st * 4);
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const uint32_t off = (uint32_t)((wave * KCH + i) * 1024);
+      lds_load16(krs, dk_off[i], sk, __builtin_amdgcn_readfirstlane(lds_k + off + buf * BKV * KROW * 4));
+      lds_load16(vrs, dv_off[i], sv, __builtin_amdgcn_readfirstlane(lds_v + off + buf * BKV * VROW * 4));
+    }
+  };
   // keys past Lk read row Lk - 1 (finite data; their scores are masked)
   auto load_kv = [&](int64_t j) {
     const int64_t key0 = j * BKV;
@@ -542,21 +570,31 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
   const int64_t nkv = (Lk + BKV - 1) / BKV;
   const bool tail = (Lk % BKV) != 0;
 
-  load_kv(0);
-  store_kv(0);
+  if constexpr (DMA) {
+    dma_kv(0, 0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  } else {
+    load_kv(0);
+    store_kv(0);
+  }
   lds_barrier();
 
   auto step = [&](int64_t j, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
     const int buf = (int)(j & 1);
-    if (j + 1 < nkv) load_kv(j + 1);
+    if constexpr (DMA) {
+      if (j + 1 < nkv) dma_kv(j + 1, buf ^ 1);
+    } else {
+      if (j + 1 < nkv) load_kv(j + 1);
+    }
     f32x16_t s[NKT];
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
       s[kt] = f32x16_t{};
 #pragma unroll
       for (int c4 = 0; c4 < HD / 4; ++c4) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(&Ks[buf][(kt * 32 + l32) * KROW + hh * HD + c4 * 4]);
+        const int krow = kt * 32 + l32, kch = DMA ? ((hh * (HD / 4) + c4) ^ sw(krow)) : hh * (HD / 4) + c4;
+        const float4 a4 = *reinterpret_cast<const float4 *>(&Ks[buf][krow * KROW + kch * 4]);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, qf[c4 * 4], s[kt], 0, 0, 0);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, qf[c4 * 4 + 1], s[kt], 0, 0, 0);
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, qf[c4 * 4 + 2], s[kt], 0, 0, 0);
@@ -601,11 +639,16 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float *vr = &Vs[buf][(kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3)) * VROW + l32];
+        const int vrow = kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        const float *vr = &Vs[buf][vrow * VROW];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[dt * 32], s[kt][i], o[dt], 0, 0, 0);
+        for (int dt = 0; dt < NDT; ++dt) {
+          const int vcol = dt * 32 + l32, vc = DMA ? (((vcol >> 2) ^ sw(vrow)) << 2) | (vcol & 3) : vcol;
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[vc], s[kt][i], o[dt], 0, 0, 0);
+        }
       }
-    if (j + 1 < nkv) store_kv(buf ^ 1);
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wavefront's block j + 1 landed
+    else if (j + 1 < nkv) store_kv(buf ^ 1);
     lds_barrier();
   };
   const int64_t nfull = tail ? nkv - 1 : nkv;
@@ -733,12 +776,25 @@ hipError_t launch_generic(const AttnParams &p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Every key offset of a head (in bytes, elements of eb bytes) fits the
+// 32-bit offsets of the direct loads
+bool dma_fits(const AttnParams &p, int eb) {
+  const int64_t st = p.k_st > p.v_st ? p.k_st : p.v_st;
+  return p.k_st >= 0 && p.v_st >= 0 && ((p.Lk + 64) * st + p.D) * eb < (int64_t(1) << 31);
+}
+
+// K / V as direct global -> LDS loads when every key offset of a head fits
+// the 32-bit buffer offsets (bit-identical; VGGT frame attention 537 against
+// 568 us, TripoSG 519 against 676 us), else register-staged.
 template <int D, int BKV, int MINW>
 hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
   const int64_t nqb = (p.Lq + 127) / 128;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  if (dma_fits(p, 4))
+    hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW, true>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  else
+    hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW, false>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
   return hipGetLastError();
 }
 
@@ -749,10 +805,6 @@ hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
 // 128-query workgroups for short sequences, which fill the CUs in more,
 // shorter rounds, and 256-query ones (the phased form) for long ones.
 constexpr int64_t kShortQ = 4096;
-bool dma_fits(const AttnParams &p) {
-  const int64_t st = p.k_st > p.v_st ? p.k_st : p.v_st;
-  return p.k_st >= 0 && p.v_st >= 0 && (p.Lk + 64) * st * 2 + 2 * p.D < (int64_t(1) << 31);
-}
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
@@ -764,7 +816,7 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
         return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);
       }
       if (p.D == 128) {
-        if (dma_fits(p)) return launch_mfma<T, 128, 1, 64, 2, true, true, false, true>(p, s);
+        if (dma_fits(p, 2)) return launch_mfma<T, 128, 1, 64, 2, true, true, false, true>(p, s);
         return launch_mfma<T, 128, 1, 64, 2, true, true, false, false>(p, s);
       }
     }
