@@ -217,8 +217,11 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   }
   // DMA: load i of a wavefront fills LDS bytes [seg * 1024, + 1024) of a
   // buffer, seg = wave * KCH + i, in lane order; the lane loads the logical
-  // chunk that its slot holds. Keys past Lk fall outside the descriptors and
-  // read as zeros (finite; their scores are masked).
+  // chunk that its slot holds. Each block's descriptors start at the block's
+  // first key and end at the head's last byte, and the per-lane offset (the
+  // part of the address the hardware range-checks; the scalar offset is not
+  // checked) carries the whole in-block offset: keys past Lk fall outside
+  // and read as zeros (finite; their scores are masked).
   constexpr int SWZ = D / 64;
   uint32_t dk_off[KCH], dv_off[KCH];
 #pragma unroll
@@ -228,20 +231,20 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     dk_off[i] = (uint32_t)(r * p.k_st * 2 + c * 16);
     dv_off[i] = (uint32_t)(r * p.v_st * 2 + c * 16);
   }
-  const i32x4_t krs = buffer_rsrc(kbase, ((Lk - 1) * p.k_st + D) * 2);
-  const i32x4_t vrs = buffer_rsrc(vbase, ((Lk - 1) * p.v_st + D) * 2);
+  const int64_t kbytes = ((Lk - 1) * p.k_st + D) * 2, vbytes = ((Lk - 1) * p.v_st + D) * 2;
+  const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2;
   const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
   const uint32_t lds_v = lds_k + 2 * BKV * KROW * 2;
   auto dma_kv = [&](int64_t j, int buf) {
-    const uint32_t sk = (uint32_t)(j * BKV * p.k_st * 2), sv = (uint32_t)(j * BKV * p.v_st * 2);
+    const i32x4_t krs = buffer_rsrc(kbase + j * kstep, kbytes - j * kstep);
+    const i32x4_t vrs = buffer_rsrc(vbase + j * vstep, vbytes - j * vstep);
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const uint32_t off = (uint32_t)((wave * KCH + i) * 1024 + buf * BKV * KROW * 2);
-      lds_load16(krs, dk_off[i], sk, __builtin_amdgcn_readfirstlane(lds_k + off));
-      lds_load16(vrs, dv_off[i], sv, __builtin_amdgcn_readfirstlane(lds_v + off));
+      lds_load16(krs, dk_off[i], 0, __builtin_amdgcn_readfirstlane(lds_k + off));
+      lds_load16(vrs, dv_off[i], 0, __builtin_amdgcn_readfirstlane(lds_v + off));
     }
   };
-  const int64_t kstep = BKV * p.k_st * 2, vstep = BKV * p.v_st * 2;
   uint4 rk[KCH], rv[KCH];
   // `clamp` (the tail block only): keys past Lk read row Lk - 1
   auto load_kv = [&](int64_t j, bool clamp) {
@@ -521,8 +524,11 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
   float4 rk[KCH], rv[KCH];
   auto sw = [](int r) { return (r & 3) | (((r >> 2) & 1) << 3); };
   // DMA: load i of a wavefront fills LDS bytes [seg * 1024, + 1024) of a
-  // buffer (seg = wave * KCH + i) in lane order; keys past Lk fall outside the
-  // descriptors and read as zeros (finite; their scores are masked)
+  // buffer (seg = wave * KCH + i) in lane order. Per block, the descriptors
+  // start at the block's first key and the range-checked per-lane offset
+  // holds the in-block offset (the scalar offset is not range-checked), so
+  // keys past Lk fall outside and read as zeros (finite; their scores are
+  // masked)
   uint32_t dk_off[KCH], dv_off[KCH];
 #pragma unroll
   for (int i = 0; i < KCH; ++i) {
@@ -530,17 +536,18 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
     dk_off[i] = (uint32_t)((r * p.k_st + c * 4) * 4);
     dv_off[i] = (uint32_t)((r * p.v_st + c * 4) * 4);
   }
-  const i32x4_t krs = buffer_rsrc(kbase, ((Lk - 1) * p.k_st + D) * 4);
-  const i32x4_t vrs = buffer_rsrc(vbase, ((Lk - 1) * p.v_st + D) * 4);
+  const int64_t kbytes = ((Lk - 1) * p.k_st + D) * 4, vbytes = ((Lk - 1) * p.v_st + D) * 4;
   const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)smem;
   const uint32_t lds_v = lds_k + 2 * BKV * KROW * 4;
   auto dma_kv = [&](int64_t j, int buf) {
-    const uint32_t sk = (uint32_t)(j * BKV * p.k_st * 4), sv = (uint32_t)(j * BKV * p.v_st * 4);
+    const int64_t sk = j * BKV * p.k_st * 4, sv = j * BKV * p.v_st * 4;
+    const i32x4_t krs = buffer_rsrc(reinterpret_cast<const char *>(kbase) + sk, kbytes - sk);
+    const i32x4_t vrs = buffer_rsrc(reinterpret_cast<const char *>(vbase) + sv, vbytes - sv);
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const uint32_t off = (uint32_t)((wave * KCH + i) * 1024);
-      lds_load16(krs, dk_off[i], sk, __builtin_amdgcn_readfirstlane(lds_k + off + buf * BKV * KROW * 4));
-      lds_load16(vrs, dv_off[i], sv, __builtin_amdgcn_readfirstlane(lds_v + off + buf * BKV * VROW * 4));
+      lds_load16(krs, dk_off[i], 0, __builtin_amdgcn_readfirstlane(lds_k + off + buf * BKV * KROW * 4));
+      lds_load16(vrs, dv_off[i], 0, __builtin_amdgcn_readfirstlane(lds_v + off + buf * BKV * VROW * 4));
     }
   };
   // keys past Lk read row Lk - 1 (finite data; their scores are masked)

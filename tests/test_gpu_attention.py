@@ -271,3 +271,62 @@ def test_sdpa_layernorm_rope2d_equals_the_two_launches(dev, ops, orc, d, case):
         g64, w64 = to_f64(host(fused, "bf16"), "bf16"), to_f64(want, "bf16")
         bound = 2 * ULP["bf16"] * np.abs(w64) + 4 * ULP["bf16"] * wabs.astype(np.float64) + 1e-6
         assert np.all(np.abs(g64 - w64) <= bound)
+
+
+@pytest.mark.parametrize("dt,d,lk", [("f32", 64, 200), ("f32", 128, 77), ("bf16", 128, 200), ("bf16", 64, 130),
+                                     ("f16", 128, 33)])
+def test_sdpa_keys_past_lk_are_not_read(dev, ops, orc, dt, d, lk):
+    """K and V are views into a larger buffer whose rows Lk .. Lk + 63 of
+    every head hold NaN: every read stays inside the allocation, and a kernel
+    that fetched a key past Lk would turn the masked 0 * V into NaN outputs.
+    Lk leaves a partial last block on every path (32-key f32 blocks, 64-key
+    bf16 / f16 blocks), including the direct-load ones (f32 D 64 / 128,
+    bf16 / f16 D 128)."""
+    _print_case(op="sdpa nan tail", dt=dt, d=d, lk=lk)
+    b, h, lq = 2, 3, 96
+    g = torch.Generator(device="cpu").manual_seed(lk * 3 + d)
+    buf = torch.full((2, b, h, lk + 64, d), float("nan"))
+    buf[:, :, :, :lk] = torch.randn((2, b, h, lk, d), generator=g)
+    buf = buf.to(dev).to(TDT[dt])
+    k, v = buf[0, :, :, :lk], buf[1, :, :, :lk]
+    q = torch.randn((b, h, lq, d), generator=g).to(dev).to(TDT[dt])
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all(), "a key past Lk reached the output"
+    want, wabs = oracle(orc, q, k, v, scale, dt)
+    assert_attn_close(out, want, wabs, dt, dt != "f32", f"nan tail {dt} d={d} lk={lk}")
+
+
+def _reversed_keys(t):
+    """Descriptor of [B, H, L, D] `t` read with the token order reversed
+    (data at the last token, a negative token stride)."""
+    from lux3d_fused import _lib
+    import ctypes
+    st = list(t.stride())
+    ptr = t.data_ptr() + (t.shape[2] - 1) * st[2] * t.element_size()
+    code = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}[t.dtype]
+    return ctypes.pointer(_lib.descriptor(ptr, code, list(t.shape), [st[0], st[1], -st[2], st[3]]))
+
+
+@pytest.mark.parametrize("dt,d,lk", [("f32", 64, 200), ("f32", 128, 77), ("bf16", 128, 200), ("f16", 128, 65)])
+def test_sdpa_register_staged_path_matches_direct_loads(dev, ops, dt, d, lk):
+    """The register-staged K / V kernels run when the direct loads cannot
+    address a head's keys (a negative token stride here). Keys and values
+    read backwards through a negative stride, and the same keys flipped into
+    a contiguous buffer, are the same logical sequence: the two paths must
+    agree bit for bit."""
+    from lux3d_fused import _lib
+    _print_case(op="sdpa register path", dt=dt, d=d, lk=lk)
+    b, h, lq = 1, 2, 130
+    g = torch.Generator(device="cpu").manual_seed(lk + d)
+    k = torch.randn((b, h, lk, d), generator=g).to(dev).to(TDT[dt])
+    v = torch.randn((b, h, lk, d), generator=g).to(dev).to(TDT[dt])
+    q = torch.randn((b, h, lq, d), generator=g).to(dev).to(TDT[dt])
+    scale = 1.0 / np.sqrt(d)
+    direct = ops.sdpa(q, k.flip(2).contiguous(), v.flip(2).contiguous(), scale)
+    staged = torch.empty_like(direct)
+    _lib.call("lux3d_sdpa", ops.desc(q), _reversed_keys(k), _reversed_keys(v), float(scale), ops.desc(staged),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(direct, staged)
