@@ -441,6 +441,44 @@ int lux3d_gated_residual(const lux3d_tensor_t *x, const lux3d_tensor_t *h, const
   return hip_status(launch_rows(ROW_GATE, x->dtype, p, vec, stream_of(stream)), fn);
 }
 
+int lux3d_gated_residual_adaln_modulate(const lux3d_tensor_t *x, const lux3d_tensor_t *h,
+                                        const lux3d_tensor_t *seg_offsets, const lux3d_tensor_t *gate,
+                                        const lux3d_tensor_t *gate_base, const lux3d_tensor_t *shift,
+                                        const lux3d_tensor_t *shift_base, const lux3d_tensor_t *scale,
+                                        const lux3d_tensor_t *scale_base, float eps, const lux3d_tensor_t *x_out,
+                                        const lux3d_tensor_t *y, lux3d_stream_t stream) {
+  const char *fn = "lux3d_gated_residual_adaln_modulate";
+  RowView xv, hv, xov, yv;
+  int r;
+  if ((r = row_tensor(x, fn, "x", -1, xv))) return r;
+  if ((r = row_tensor(h, fn, "h", x->dtype, hv))) return r;
+  if ((r = row_tensor(x_out, fn, "x_out", x->dtype, xov))) return r;
+  if ((r = row_tensor(y, fn, "y", x->dtype, yv))) return r;
+  if ((r = same_rows(xv, hv, fn, "h")) || (r = same_rows(xv, xov, fn, "x_out")) || (r = same_rows(xv, yv, fn, "y")))
+    return r;
+  if (!(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
+  if (xv.d == 0) return fail(LUX3D_ERR_SHAPE, "%s: empty rows", fn);
+  if (!shift || !scale) return fail(LUX3D_ERR_NULL, "%s: `shift` and `scale` are required", fn);
+  if (xv.rows > 0 && (yv.p == xv.p || yv.p == xov.p))
+    return fail(LUX3D_ERR_LAYOUT, "%s: `y` must not alias `x` or `x_out`", fn);
+  RowParams p;
+  int64_t s_sh = 0, s_sc = 0, s_g = 0;
+  if ((r = mod_piece(shift, shift_base, xv.d, fn, "shift", p.shift, s_sh))) return r;
+  if ((r = mod_piece(scale, scale_base, xv.d, fn, "scale", p.scale, s_sc))) return r;
+  if ((r = mod_piece(gate, gate_base, xv.d, fn, "gate", p.gate, s_g))) return r;
+  if (s_sh != s_sc || (gate && s_g != s_sh))
+    return fail(LUX3D_ERR_SHAPE, "%s: shift/scale/gate have different segment counts", fn);
+  if ((r = segments(seg_offsets, xv.rows, s_sh, fn, p))) return r;
+  p.x = xv.p; p.x_rs = xv.rs;
+  p.a = hv.p; p.a_rs = hv.rs;
+  p.h = const_cast<void *>(xov.p); p.h_rs = xov.rs;
+  p.y = const_cast<void *>(yv.p); p.y_rs = yv.rs;
+  p.rows = xv.rows; p.d = xv.d; p.eps = eps;
+  const bool vec = vec_ok_rows({xv, hv, xov, yv}) && vec_ok_piece(p.shift) && vec_ok_piece(p.scale) &&
+                   vec_ok_piece(p.gate);
+  return hip_status(launch_rows(ROW_GATE_MOD, x->dtype, p, vec, stream_of(stream)), fn);
+}
+
 // ---------------------------------------------------------------------------
 
 namespace {

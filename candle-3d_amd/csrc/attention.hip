@@ -185,8 +185,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       u32x4_t pk;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        pk[e] = M::pack(__fadd_rn(__fmul_rn(x[2 * e], C8[2 * e]), __fmul_rn(pv[2 * e], S8[2 * e])),
-                        __fadd_rn(__fmul_rn(x[2 * e + 1], C8[2 * e + 1]), __fmul_rn(pv[2 * e + 1], S8[2 * e + 1])));
+        pk[e] = M::pack(rotate1(x[2 * e], C8[2 * e], pv[2 * e], S8[2 * e]),
+                        rotate1(x[2 * e + 1], C8[2 * e + 1], pv[2 * e + 1], S8[2 * e + 1]));
       *reinterpret_cast<u32x4_t *>(qs + row * D + ch * 8) = pk;
     }
     lds_barrier();

@@ -53,6 +53,32 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t v) {
 }
 
 // ---------------------------------------------------------------------------
+// Rounding control. HIP compiles with floating-point contraction on, so
+// `a * b + c` (also when written with __fmul_rn / __fadd_rn, which are plain
+// operators in this toolchain) may become one FMA with a single rounding.
+// mul_rn / add_rn are never contracted: each is one IEEE f32 operation,
+// rounded on its own, as the reference's Rust (which never contracts)
+// computes. Used where a result must match the reference bit for bit (the
+// residual streams).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+// One rotated element y*c + p*s (p: the element's rotation partner) as
+// fma(y, c, p*s): one rounding fewer than the reference's separately rounded
+// products and sum (at most 1 f32 ulp apart before the output rounding, well
+// inside the parity tolerance), and one instruction fewer per element. Every
+// kernel that rotates uses this form, so their results agree bit for bit.
+__device__ __forceinline__ float rotate1(float y, float c, float p, float s) {
+  return __builtin_fmaf(y, c, mul_rn(p, s));
+}
+
+// ---------------------------------------------------------------------------
 // 16-byte streaming accesses. Activations are touched exactly once per op, so
 // they are loaded and stored non-temporally (the "nt" cache policy: streamed
 // through L2 / the Infinity Cache without displacing reused data such as the

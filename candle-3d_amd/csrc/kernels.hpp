@@ -10,7 +10,9 @@
 namespace lux3d {
 
 // ---- row family: LayerNorm / residual+LayerNorm / AdaLN modulate / gate ----
-enum RowMode : int { ROW_LN = 0, ROW_RESID_LN = 1, ROW_MODULATE = 2, ROW_GATE = 3 };
+// ROW_GATE_MOD: the gated residual x + h*gate stored as the new residual
+// stream, then AdaLN modulate of it (one pass: read x, h; write x', y).
+enum RowMode : int { ROW_LN = 0, ROW_RESID_LN = 1, ROW_MODULATE = 2, ROW_GATE = 3, ROW_GATE_MOD = 4 };
 
 // A modulation piece p[s, c] (+ base[c]); dt < 0 when absent.
 struct ModPiece {
@@ -23,8 +25,8 @@ struct ModPiece {
 
 struct RowParams {
   const void *x = nullptr;  int64_t x_rs = 0;   // input rows
-  const void *a = nullptr;  int64_t a_rs = 0;   // residual branch (RESID) or h (GATE)
-  void *h = nullptr;        int64_t h_rs = 0;   // RESID: stored residual stream
+  const void *a = nullptr;  int64_t a_rs = 0;   // residual branch (RESID) or h (GATE, GATE_MOD)
+  void *h = nullptr;        int64_t h_rs = 0;   // RESID, GATE_MOD: stored residual stream
   void *y = nullptr;        int64_t y_rs = 0;   // output rows
   int64_t rows = 0, d = 0;
   float eps = 0.f;

@@ -1,6 +1,7 @@
 // norm_rows.hip -- row-reduction kernels for gfx950: LayerNorm (affine or
 // not), LayerScale + residual + LayerNorm, AdaLN modulate (dense or ragged
-// segments) and the gated residual.
+// segments), the gated residual, and the gated residual followed by the next
+// AdaLN modulate in one pass.
 //
 // Mapping. A row of D elements is owned by TPR threads (one wavefront for
 // TPR = 64, or 2 / 4 wavefronts reducing through LDS for short row counts).
@@ -65,14 +66,15 @@ __device__ __forceinline__ void stage_pieces(const RowParams &p, int64_t seg, fl
   const int64_t d = p.d;
   const bool has_gate = MODE == ROW_GATE || p.gate.dt >= 0;
   float *q = lds;
-  if constexpr (MODE == ROW_MODULATE) {
+  constexpr bool MOD = MODE == ROW_MODULATE || MODE == ROW_GATE_MOD;
+  if constexpr (MOD) {
     st.shift = q; q += d;
     st.scale1 = q; q += d;
   }
   st.gate = has_gate ? q : nullptr;
   for (int64_t e = threadIdx.x; e < d / 8; e += BLOCK) {
     float a[8];
-    if constexpr (MODE == ROW_MODULATE) {
+    if constexpr (MOD) {
       mod8(p.shift, seg, e * 8, 0.f, a);
 #pragma unroll
       for (int k = 0; k < 8; ++k) st.shift[e * 8 + k] = a[k];
@@ -99,7 +101,9 @@ __device__ __forceinline__ void lds8(const float *src, int64_t idx, float (&v)[8
 template <typename T, int TPR, int NC, int MODE, int BLOCK = kBlock, bool STAGE = false>
 __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   static_assert(BLOCK % TPR == 0, "a block holds whole rows");
-  static_assert(!STAGE || MODE == ROW_MODULATE || MODE == ROW_GATE, "only segment pieces are staged");
+  static_assert(!STAGE || MODE == ROW_MODULATE || MODE == ROW_GATE || MODE == ROW_GATE_MOD,
+                "only segment pieces are staged");
+  constexpr bool SEGMENTED = MODE == ROW_MODULATE || MODE == ROW_GATE || MODE == ROW_GATE_MOD;
   constexpr int RPB = BLOCK / TPR;
   constexpr int EB = T::bytes;
   __shared__ float red_a[BLOCK / 64], red_b[BLOCK / 64];
@@ -115,12 +119,20 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   const char *xr = reinterpret_cast<const char *>(p.x) + row * p.x_rs * EB;
 #pragma unroll
   for (int c = 0; c < NC; ++c) Chunk<T>::load(xr + (int64_t)(c * TPR + t) * 8 * EB, v[c]);
+  // GATE_MOD: the branch rows are loaded with x, ahead of the segment lookup
+  // and the staging barrier, so both streams are in flight together
+  float hb[MODE == ROW_GATE_MOD ? NC : 1][8];
+  if constexpr (MODE == ROW_GATE_MOD) {
+    const char *ar = reinterpret_cast<const char *>(p.a) + row * p.a_rs * EB;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) Chunk<T>::load(ar + (int64_t)(c * TPR + t) * 8 * EB, hb[c]);
+  }
 
   // segment of this row; with STAGE, whether the workgroup shares one
   bool staged = false;
   Staged st{};
   int64_t seg = 0;
-  if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE) {
+  if constexpr (SEGMENTED) {
     if constexpr (STAGE) {
       const int64_t last = row0 + RPB - 1 < p.rows ? row0 + RPB - 1 : p.rows - 1;
       const int64_t seg0 = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row0);
@@ -144,10 +156,34 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       if (staged) lds8(st.gate, idx, g);
       else mod8(p.gate, seg, idx, 1.f, g);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[c][k] = __fadd_rn(v[c][k], __fmul_rn(hv[k], g[k]));
+      for (int k = 0; k < 8; ++k) v[c][k] = add_rn(v[c][k], mul_rn(hv[k], g[k]));
       if (live) Chunk<T>::store(yr + idx * EB, v[c]);
     }
     return;
+  }
+
+  if constexpr (MODE == ROW_GATE_MOD) {
+    // x' = x + h*gate (gate absent: 1, so x' = x + h exactly), two roundings
+    // as broadcast_mul then add; the norm reads the stored x'
+    // (no gate: nothing is staged for it and the factor is 1)
+    char *hr = reinterpret_cast<char *>(p.h) + row * p.h_rs * EB;
+    const bool gated = p.gate.dt >= 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      float g[8];
+      if (!gated) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) g[k] = 1.f;
+      } else if (staged) {
+        lds8(st.gate, idx, g);
+      } else {
+        mod8(p.gate, seg, idx, 1.f, g);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[c][k] = Chunk<T>::round_trip(add_rn(v[c][k], mul_rn(hb[c][k], g[k])));
+      if (live) Chunk<T>::store(hr + idx * EB, v[c]);
+    }
   }
 
   if constexpr (MODE == ROW_RESID_LN) {
@@ -163,8 +199,8 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       for (int k = 0; k < 8; ++k) {
         // LayerScale product and residual add as two roundings (no FMA
         // contraction), exactly broadcast_mul then add.
-        const float ls = p.g_dt >= 0 ? __fmul_rn(av[k], g[k]) : av[k];
-        v[c][k] = Chunk<T>::round_trip(__fadd_rn(ls, v[c][k]));  // the norm reads the stored h
+        const float ls = p.g_dt >= 0 ? mul_rn(av[k], g[k]) : av[k];
+        v[c][k] = Chunk<T>::round_trip(add_rn(ls, v[c][k]));  // the norm reads the stored h
       }
       if (live) Chunk<T>::store(hr + idx * EB, v[c]);
     }
@@ -190,7 +226,7 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   const float rstd = 1.0f / sqrtf(var + p.eps);
 
   char *yr = reinterpret_cast<char *>(p.y) + row * p.y_rs * EB;
-  if constexpr (MODE == ROW_MODULATE) {
+  if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t idx = (int64_t)(c * TPR + t) * 8;
@@ -206,7 +242,7 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * sc1[k] + sh[k];
-      if (p.gate.dt >= 0) {
+      if (MODE == ROW_MODULATE && p.gate.dt >= 0) {  // M1' output gate (GATE_MOD's gate is the residual's)
         float g[8];
         if (staged) lds8(st.gate, idx, g);
         else mod8(p.gate, seg, idx, 1.f, g);
@@ -236,23 +272,26 @@ __global__ __launch_bounds__(kBlock) void row_kernel_any(RowParams p) {
   __shared__ float red_a[kBlock / 64], red_b[kBlock / 64];
   const int64_t row = blockIdx.x;
   const int64_t seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
-  auto inval = [&](int64_t c) -> float {
-    float xv = load1<T>(p.x, row * p.x_rs + c);
-    if constexpr (MODE == ROW_RESID_LN) {
-      float av = load1<T>(p.a, row * p.a_rs + c);
-      const float ls = p.g_dt >= 0 ? __fmul_rn(av, param1(p.g, p.g_dt, c, 1.f)) : av;
-      xv = Chunk<T>::round_trip(__fadd_rn(ls, xv));
-    }
-    return xv;
-  };
   auto piece = [&](const ModPiece &m, int64_t c, float dflt) -> float {
     float v = param1(m.p, m.dt, seg * m.ld + c, dflt);
     return m.base_dt >= 0 ? param1(m.base, m.base_dt, c, 0.f) + v : v;
   };
+  auto inval = [&](int64_t c) -> float {
+    float xv = load1<T>(p.x, row * p.x_rs + c);
+    if constexpr (MODE == ROW_RESID_LN) {
+      float av = load1<T>(p.a, row * p.a_rs + c);
+      const float ls = p.g_dt >= 0 ? mul_rn(av, param1(p.g, p.g_dt, c, 1.f)) : av;
+      xv = Chunk<T>::round_trip(add_rn(ls, xv));
+    } else if constexpr (MODE == ROW_GATE_MOD) {
+      const float hv = load1<T>(p.a, row * p.a_rs + c);
+      xv = Chunk<T>::round_trip(add_rn(xv, mul_rn(hv, piece(p.gate, c, 1.f))));
+    }
+    return xv;
+  };
   if constexpr (MODE == ROW_GATE) {
     for (int64_t c = threadIdx.x; c < p.d; c += kBlock) {
       float hv = load1<T>(p.a, row * p.a_rs + c);
-      store1<T>(p.y, row * p.y_rs + c, __fadd_rn(load1<T>(p.x, row * p.x_rs + c), __fmul_rn(hv, piece(p.gate, c, 1.f))));
+      store1<T>(p.y, row * p.y_rs + c, add_rn(load1<T>(p.x, row * p.x_rs + c), mul_rn(hv, piece(p.gate, c, 1.f))));
     }
     return;
   }
@@ -268,11 +307,11 @@ __global__ __launch_bounds__(kBlock) void row_kernel_any(RowParams p) {
   const float rstd = 1.0f / sqrtf(row_total<kBlock>(s2, red_b) * inv_d + p.eps);
   for (int64_t c = threadIdx.x; c < p.d; c += kBlock) {
     const float xv = inval(c);
-    if constexpr (MODE == ROW_RESID_LN) store1<T>(p.h, row * p.h_rs + c, xv);
+    if constexpr (MODE == ROW_RESID_LN || MODE == ROW_GATE_MOD) store1<T>(p.h, row * p.h_rs + c, xv);
     float out;
-    if constexpr (MODE == ROW_MODULATE) {
+    if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) {
       out = (xv - mean) * rstd * (piece(p.scale, c, 0.f) + 1.0f) + piece(p.shift, c, 0.f);
-      if (p.gate.dt >= 0) out = piece(p.gate, c, 1.f) * out + xv;
+      if (MODE == ROW_MODULATE && p.gate.dt >= 0) out = piece(p.gate, c, 1.f) * out + xv;
     } else {
       out = (xv - mean) * rstd * param1(p.w, p.w_dt, c, 1.f) + param1(p.b, p.b_dt, c, 0.f);
     }
@@ -292,7 +331,9 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   // 2 wavefronts with one or two chunks per lane (configs[1] F1: 18.0 us vs
   // 20.4 us on one wavefront; the gate without a base vector on 4 wavefronts
   // when a row is 256 chunks), the single-stream LayerNorm / modulate on one
-  // wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs 9.4 us).
+  // wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs 9.4 us),
+  // and so does the gated residual + modulate (configs[2]: 13.1 us against
+  // 19.2 us on 2 wavefronts and 18.9 us on 4).
   // 256-thread workgroups of several rows let modulate / gate share the
   // staged segment pieces.
   int tpr = 0, nc = 0;
@@ -327,12 +368,13 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   const int64_t rpb = block / tpr;
   const dim3 grid((unsigned)((p.rows + rpb - 1) / rpb));
   // Stage the segment pieces in LDS when a workgroup holds several rows.
-  const int npieces = MODE == ROW_MODULATE ? 2 + (p.gate.dt >= 0 ? 1 : 0) : (MODE == ROW_GATE ? 1 : 0);
+  const int npieces = (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) ? 2 + (p.gate.dt >= 0 ? 1 : 0)
+                                                                      : (MODE == ROW_GATE ? 1 : 0);
   const size_t lds = (size_t)npieces * (size_t)p.d * sizeof(float);
   const bool stage = npieces > 0 && rpb > 1 && lds <= 64 * 1024;
 #define LUX3D_ROW_CASE(TPR_, NC_, BLK_)                                                                 \
   if (tpr == TPR_ && nc == NC_ && block == BLK_) {                                                      \
-    if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE) {                                           \
+    if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE || MODE == ROW_GATE_MOD) {                   \
       if (stage && BLK_ > TPR_) {                                                                       \
         hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_, (BLK_ > TPR_)>), grid, dim3(BLK_), lds, s, p); \
         return hipGetLastError();                                                                       \
@@ -357,6 +399,7 @@ hipError_t launch_mode(int mode, const RowParams &p, bool vec, hipStream_t s) {
     case ROW_RESID_LN: return launch_typed<T, ROW_RESID_LN>(p, vec, s);
     case ROW_MODULATE: return launch_typed<T, ROW_MODULATE>(p, vec, s);
     case ROW_GATE: return launch_typed<T, ROW_GATE>(p, vec, s);
+    case ROW_GATE_MOD: return launch_typed<T, ROW_GATE_MOD>(p, vec, s);
   }
   return hipErrorInvalidValue;
 }

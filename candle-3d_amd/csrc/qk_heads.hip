@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
           const float *C = Cs + tt[r] * D + lane * 8;
           const float *S = Ss + tt[r] * D + lane * 8;
 #pragma unroll
-          for (int k = 0; k < 8; ++k) x[k] = __fadd_rn(__fmul_rn(x[k], C[k]), __fmul_rn(pv[k], S[k]));
+          for (int k = 0; k < 8; ++k) x[k] = rotate1(x[k], C[k], pv[k], S[k]);
         }
       }
       if (live[r]) {
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void head_kernel_any(HeadParams p) {
       float C, S;
       int64_t pj;
       phase_any<ROT>(p, b, n, j, C, S, pj);
-      if (pj != j) out = __fadd_rn(__fmul_rn(out, C), __fmul_rn(normed(pj), S));
+      if (pj != j) out = rotate1(out, C, normed(pj), S);
     }
     store1<T>(io.y, yo + j, out);
   }

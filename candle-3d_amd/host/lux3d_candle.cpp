@@ -467,6 +467,20 @@ Tensor gated_residual(const Tensor &x, const Tensor &h, const Tensor &gate, cons
   return out;
 }
 
+std::pair<Tensor, Tensor> gated_residual_adaln_modulate(const Tensor &x, const Tensor &h,
+                                                        const std::optional<Tensor> &gate,
+                                                        const std::optional<Tensor> &gate_base,
+                                                        const Modulation &next, double eps,
+                                                        const std::optional<Tensor> &seg_offsets) {
+  if (next.gate) fail(LUX3D_ERR_VALUE, "gated_residual_adaln_modulate: the next modulate takes no output gate");
+  Tensor xo = empty_like(x), y = empty_like(x);
+  abi_check(lux3d_gated_residual_adaln_modulate(
+      Desc(x).p(), Desc(h).p(), Desc(seg_offsets).p(), Desc(gate).p(), Desc(gate_base).p(), Desc(next.shift).p(),
+      Desc(next.shift_base).p(), Desc(next.scale).p(), Desc(next.scale_base).p(), (float)eps, Desc(xo).p(),
+      Desc(y).p(), x.device().stream()));
+  return {xo, y};
+}
+
 // ---------------------------------------------------------------------------
 // VGGT / Pi3 2D RoPE
 // ---------------------------------------------------------------------------

@@ -183,6 +183,17 @@ Tensor gated_residual(const Tensor &x, const Tensor &h, const Tensor &gate,
                       const std::optional<Tensor> &gate_base = std::nullopt,
                       const std::optional<Tensor> &seg_offsets = std::nullopt);
 
+// `xs = xs + h * gate` (gate absent: `xs + h`) followed by the next
+// `layer_norm_no_affine(xs) * (1 + scale) + shift`, one launch: the sparse
+// block's MLP entry (runtime/trellis2_blocks.rs:708-713) and the dense
+// block's cross-attention add + MLP modulate (:637-642). Returns (xs, y).
+// `next` holds shift / scale (+ bases); its gate must be empty.
+std::pair<Tensor, Tensor> gated_residual_adaln_modulate(const Tensor &x, const Tensor &h,
+                                                        const std::optional<Tensor> &gate,
+                                                        const std::optional<Tensor> &gate_base,
+                                                        const Modulation &next, double eps,
+                                                        const std::optional<Tensor> &seg_offsets = std::nullopt);
+
 // ---- VGGT / Pi3 2D RoPE (runtime/attention_math.rs) -------------------------
 
 struct RopeEmbeddings {

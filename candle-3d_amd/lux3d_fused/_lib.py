@@ -49,6 +49,7 @@ SIGNATURES = {
     "lux3d_residual_layer_norm": [TP, TP, TP, TP, TP, ctypes.c_float, TP, TP, S],
     "lux3d_adaln_modulate": [TP, TP, TP, TP, TP, TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_gated_residual": [TP, TP, TP, TP, TP, TP, S],
+    "lux3d_gated_residual_adaln_modulate": [TP, TP, TP, TP, TP, TP, TP, TP, TP, ctypes.c_float, TP, TP, S],
     "lux3d_qk_layernorm_rope2d": [TP, TP, TP, TP, TP, TP, ctypes.c_float, TP, TP, TP, TP, S],
     "lux3d_qk_layernorm_rope2d_pos": [TP, TP, TP, TP, TP, TP, ctypes.c_float, TP, ctypes.c_float, TP, TP, S],
     "lux3d_rope2d_tables": [TP, ctypes.c_float, TP, TP, S],

@@ -100,6 +100,23 @@ def gated_residual(x: torch.Tensor, h: torch.Tensor, gate: torch.Tensor, *, gate
     return o
 
 
+def gated_residual_adaln_modulate(x: torch.Tensor, h: torch.Tensor, gate: Optional[torch.Tensor],
+                                  shift: torch.Tensor, scale: torch.Tensor, *, gate_base=None,
+                                  shift_base=None, scale_base=None,
+                                  seg_offsets: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                                  x_out: Optional[torch.Tensor] = None):
+    """One pass of `xs = xs.add(h.broadcast_mul(gate))` (gate None: `xs.add(h)`)
+    followed by `layer_norm_no_affine(xs)*(1 + scale) + shift`
+    (runtime/trellis2_blocks.rs:708-713 sparse block, :637-642 dense block).
+    Returns (x_out, y); x_out may be x (in-place residual update)."""
+    xo = torch.empty(x.shape, dtype=x.dtype, device=x.device) if x_out is None else x_out
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.call("lux3d_gated_residual_adaln_modulate", desc(x), desc(h), desc(seg_offsets), desc(gate),
+              desc(gate_base), desc(shift), desc(shift_base), desc(scale), desc(scale_base), eps, desc(xo),
+              desc(y), _stream(x))
+    return xo, y
+
+
 def chunk_modulation(mod_vec: torch.Tensor):
     """chunk_modulation (runtime/trellis2_blocks.rs:264-277): six [B, 1, C]
     views (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp)

@@ -244,6 +244,66 @@ def cfg3_gated_residual_ragged(dev) -> Workload:
     return _modulate(dev, 3, (24000, 40000), 1536, gate_only=True)
 
 
+def _gated_modulate(dev, cfg, rows_per_seg, C, two_launches=False) -> Workload:
+    """The gated residual and the next AdaLN modulate of a TRELLIS.2 block
+    (trellis2_blocks.rs:708-713): x' = x + h*gate_msa, y = L3(x')*(1 +
+    scale_mlp) + shift_mlp, the pieces chunk views of t_emb plus the block's
+    `modulation` vector. One launch of lux3d_gated_residual_adaln_modulate, or
+    (two_launches) lux3d_gated_residual then lux3d_adaln_modulate, the
+    sequence it replaces; both are priced at the fused op's algorithmic bytes
+    (read x, h; write x', y)."""
+    from . import _lib
+    S = len(rows_per_seg)
+    rows = sum(rows_per_seg)
+    s = synth.config_seed(cfg)
+    x0 = _normal(s, (rows, C), dev, torch.bfloat16)
+    h0 = _normal(s + 9, (rows, C), dev, torch.bfloat16)
+    t_emb = _normal(s + 4, (S, 6 * C), dev, torch.float32, 0.0, 0.1)
+    modulation = _normal(s + 5, (6 * C,), dev, torch.float32, 0.0, 0.1)
+    pieces = ops.chunk_modulation(t_emb)
+    base = modulation.chunk(6)
+    ragged = len(set(rows_per_seg)) > 1
+    offs = _t(np.concatenate([[0], np.cumsum(rows_per_seg)]).astype(np.int64), dev) if ragged else None
+    nbytes = rows * C * 2 * 4 + 3 * S * C * 4 + 3 * C * 4 + ((S + 1) * 8 if ragged else 0)
+    n = _n_sets(nbytes)
+    xs = [_fill_like(x0, k) for k in range(n)]
+    hs = [_fill_like(h0, k + 1) for k in range(n)]
+    xos = [torch.empty_like(x0) for _ in range(n)]
+    ys = [torch.empty_like(x0) for _ in range(n)]
+    D = [(ops.desc(xs[k]), ops.desc(hs[k]), ops.desc(xos[k]), ops.desc(ys[k])) for k in range(n)]
+    dg, dsh, dsc = ops.desc(pieces[2]), ops.desc(pieces[3]), ops.desc(pieces[4])
+    dbg, dbsh, dbsc = ops.desc(base[2]), ops.desc(base[3]), ops.desc(base[4])
+    do = ops.desc(offs)
+
+    def launch(i):
+        dx, dh, dxo, dy = D[i % n]
+        if two_launches:
+            _lib.call("lux3d_gated_residual", dx, dh, do, dg, dbg, dxo, _cur())
+            _lib.call("lux3d_adaln_modulate", dxo, do, dsh, dbsh, dsc, dbsc, None, None, 1e-6, dy, _cur())
+        else:
+            _lib.call("lux3d_gated_residual_adaln_modulate", dx, dh, do, dg, dbg, dsh, dbsh, dsc, dbsc, 1e-6, dxo,
+                      dy, _cur())
+    name = "gated_residual_adaln_modulate" + ("_ragged" if ragged else "") + ("_two_launches" if two_launches else "")
+    kern = ("row_kernel<BF16,GATE> + row_kernel<BF16,MODULATE>" if two_launches
+            else "row_kernel<BF16,GATE_MOD>")
+    wl = Workload(name, cfg, kern, "bf16", nbytes, f"[{rows},{C}] segs {list(rows_per_seg)}", launch, n,
+                  "two launches, priced at the fused op's bytes" if two_launches else "")
+    wl._keep = (xs, hs, xos, ys, t_emb, modulation, pieces, base, offs, D, dg, dsh, dsc, dbg, dbsh, dbsc, do)
+    return wl
+
+
+def cfg3_gated_residual_adaln_modulate(dev) -> Workload:
+    return _gated_modulate(dev, 3, (24000, 40000), 1536)
+
+
+def cfg3_gated_residual_adaln_modulate_two_launches(dev) -> Workload:
+    return _gated_modulate(dev, 3, (24000, 40000), 1536, two_launches=True)
+
+
+def cfg2_gated_residual_adaln_modulate(dev) -> Workload:
+    return _gated_modulate(dev, 2, (2048, 2048), 2048)
+
+
 def cfg2_rms_norm_heads(dev) -> Workload:
     from . import _lib
     B, L, H, D = 2, 2048, 16, 128
@@ -641,6 +701,8 @@ TARGETS: List[Callable] = [
     cfg3_qk_l2norm_rope3d,
     cfg4_residual_layer_norm,
     cfg4_dequant_q8_0,
+    cfg2_gated_residual_adaln_modulate,
+    cfg3_gated_residual_adaln_modulate,
 ]
 EXTRAS: List[Callable] = [
     cfg0_layer_norm,
@@ -649,6 +711,7 @@ EXTRAS: List[Callable] = [
     cfg2_gelu_erf,
     cfg2_silu,
     cfg3_gated_residual_ragged,
+    cfg3_gated_residual_adaln_modulate_two_launches,
     cfg4_dinov3_rope,
     cfg4_q8_0_linear,
     cfg2_q8_0_linear,

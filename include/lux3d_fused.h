@@ -137,6 +137,32 @@ int lux3d_gated_residual(const lux3d_tensor_t *x, const lux3d_tensor_t *h,
                          const lux3d_tensor_t *out, lux3d_stream_t stream);
 
 /* --------------------------------------------------------------------------
+ * Gated residual, then the next AdaLN modulate, in one pass over the rows:
+ *   x_out = x + h*gate          (gate == NULL: x_out = x + h)
+ *   y     = LayerNorm_no_affine(x_out, eps)*(scale + 1) + shift
+ * with y computed from the stored (rounded) x_out. x_out is bit-identical to
+ * lux3d_gated_residual's; y is lux3d_adaln_modulate's arithmetic on it (the
+ * row statistics may be summed in another order). Reads x and h once and
+ * writes x_out and y once: 4 row passes in one launch instead of 5 in two.
+ * gate / shift / scale (+ *_base) and seg_offsets as in lux3d_adaln_modulate;
+ * all pieces share one segment count. x_out may alias x (the residual
+ * stream updated in place); y must not alias x or x_out.
+ * Replaces the block-internal sequences
+ *   h.broadcast_mul(gate_msa); xs.add(h); layer_norm_no_affine(xs, 1e-6);
+ *   .broadcast_mul(scale_mlp.affine(1, 1)); .broadcast_add(shift_mlp)
+ * of Trellis2SparseBlock::forward (runtime/trellis2_blocks.rs:708-713) and
+ *   xs.add(h) (cross-attention output, no gate); layer_norm_no_affine;
+ *   modulate by scale_mlp / shift_mlp
+ * of Trellis2DenseBlock::forward (runtime/trellis2_blocks.rs:637-642).      */
+int lux3d_gated_residual_adaln_modulate(const lux3d_tensor_t *x, const lux3d_tensor_t *h,
+                                        const lux3d_tensor_t *seg_offsets,
+                                        const lux3d_tensor_t *gate, const lux3d_tensor_t *gate_base,
+                                        const lux3d_tensor_t *shift, const lux3d_tensor_t *shift_base,
+                                        const lux3d_tensor_t *scale, const lux3d_tensor_t *scale_base,
+                                        float eps, const lux3d_tensor_t *x_out,
+                                        const lux3d_tensor_t *y, lux3d_stream_t stream);
+
+/* --------------------------------------------------------------------------
  * VGGT/Pi3 2D RoPE (R1) on Q and K head views, optionally after a per-head
  * affine LayerNorm (the q_norm/k_norm of the attention).
  *   q, k: [B, H, N, D] views with any outer strides (e.g. the permuted

@@ -18,6 +18,9 @@
  *   or_residual_layer_norm   f64 closed form + LayerScale=0 reduction
  *   or_adaln_modulate        chunk-order KAT (tests/trellis2_blocks.rs:205-225) + f64 form
  *   or_gated_residual        f64 closed form + gate=0 identity
+ *   or_gated_residual_modulate  torch f64 closed form of the stored residual
+ *                            and its modulated norm; gate = 0 / scale = shift
+ *                            = 0 reductions; ungated add (tests/test_oracle_pins.py)
  *   or_rms_norm_heads        f64 closed form + scale invariance
  *   or_qk_l2norm             KAT tests/trellis2_blocks.rs:126-153
  *   or_rope2d_*              complex-rotation (f64) + identity at p=0 + norm preservation
@@ -429,6 +432,58 @@ void or_gated_residual(int dt, const void *x, const void *h, int64_t rows, int64
                        int64_t ld_gate, const float *gate_base, void *out) {
   gate_ctx c = {dt, x, h, d, seg_off, nseg, gate, ld_gate, gate_base, out};
   parallel_rows(rows, gate_rows, &c);
+}
+
+/* G1 followed by L3 + M1 on the stored residual stream:
+ * Trellis2SparseBlock::forward (trellis2_blocks.rs:708-713):
+ *   h = h.broadcast_mul(gate_msa); xs = xs.add(h);
+ *   n = layer_norm_no_affine(xs, 1e-6);
+ *   n.broadcast_mul(scale_mlp.affine(1, 1)).broadcast_add(shift_mlp)
+ * and Trellis2DenseBlock::forward (:637-642), where the cross-attention
+ * output is added without a gate (gate == NULL here: x + h). The norm reads
+ * xs as stored in the activation dtype. */
+typedef struct {
+  int dt;
+  const void *x, *h;
+  int64_t d;
+  const int64_t *seg_off;
+  int64_t nseg;
+  const float *gate, *gate_base, *shift, *shift_base, *scale, *scale_base;
+  int64_t ld_gate, ld_shift, ld_scale;
+  float eps;
+  void *x_out, *y;
+} gmod_ctx;
+
+static void gmod_rows(const void *p, int64_t r0, int64_t r1) {
+  const gmod_ctx *c = (const gmod_ctx *)p;
+  for (int64_t r = r0; r < r1; ++r) {
+    int64_t s = seg_of_row(c->seg_off, c->nseg, r);
+    int64_t base = r * c->d;
+    for (int64_t k = 0; k < c->d; ++k) {
+      float hv = ld(c->dt, c->h, base + k);
+      if (c->gate) hv = hv * mod_piece(c->gate, c->ld_gate, c->gate_base, s, k);
+      st(c->dt, c->x_out, base + k, ld(c->dt, c->x, base + k) + hv);
+    }
+    float mean;
+    float den = slow_ln_stats(c->dt, c->x_out, base, c->d, c->eps, &mean);
+    for (int64_t k = 0; k < c->d; ++k) {
+      float n = (ld(c->dt, c->x_out, base + k) - mean) / den;
+      float sc = mod_piece(c->scale, c->ld_scale, c->scale_base, s, k);
+      float sh = mod_piece(c->shift, c->ld_shift, c->shift_base, s, k);
+      st(c->dt, c->y, base + k, n * affine(sc, 1.0, 1.0) + sh);
+    }
+  }
+}
+
+void or_gated_residual_modulate(int dt, const void *x, const void *h, int64_t rows, int64_t d,
+                                const int64_t *seg_off, int64_t nseg, const float *gate,
+                                int64_t ld_gate, const float *gate_base, const float *shift,
+                                int64_t ld_shift, const float *shift_base, const float *scale,
+                                int64_t ld_scale, const float *scale_base, float eps,
+                                void *x_out, void *y) {
+  gmod_ctx c = {dt, x, h, d, seg_off, nseg, gate, gate_base, shift, shift_base, scale,
+                scale_base, ld_gate, ld_shift, ld_scale, eps, x_out, y};
+  parallel_rows(rows, gmod_rows, &c);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -70,6 +70,15 @@ void or_gated_residual(int dt, const void *x, const void *h, int64_t rows,
                        int64_t d, const int64_t *seg_off, int64_t nseg,
                        const float *gate, int64_t ld_gate, const float *gate_base,
                        void *out);
+/* G1 then L3 + M1 on the stored result (trellis2_blocks.rs:708-713, and
+ * :637-642 with gate == NULL, a plain residual add): x_out = x + h*gate,
+ * y = L3(x_out)*(scale + 1) + shift. */
+void or_gated_residual_modulate(int dt, const void *x, const void *h, int64_t rows, int64_t d,
+                                const int64_t *seg_off, int64_t nseg,
+                                const float *gate, int64_t ld_gate, const float *gate_base,
+                                const float *shift, int64_t ld_shift, const float *shift_base,
+                                const float *scale, int64_t ld_scale, const float *scale_base,
+                                float eps, void *x_out, void *y);
 /* N1: rms_norm_heads (triposg_dit.rs:515-521). */
 void or_rms_norm_heads(int dt, const void *x, int64_t rows, int64_t d,
                        const float *w, float eps, void *y);

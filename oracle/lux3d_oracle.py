@@ -34,6 +34,8 @@ _SIG = {
     "or_residual_layer_norm": ([ctypes.c_int, _P, _P, _P, _I, _I, _P, _P, _F, _P, _P], None),
     "or_adaln_modulate": ([ctypes.c_int, _P, _I, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _F, _P], None),
     "or_gated_residual": ([ctypes.c_int, _P, _P, _I, _I, _P, _I, _P, _I, _P, _P], None),
+    "or_gated_residual_modulate": ([ctypes.c_int, _P, _P, _I, _I, _P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P,
+                                    _F, _P, _P], None),
     "or_rms_norm_heads": ([ctypes.c_int, _P, _I, _I, _P, _F, _P], None),
     "or_qk_l2norm": ([ctypes.c_int, _P, _I, _I, _I, _P, _P], None),
     "or_rope2d_tables": ([_P, _I, _I, _I, _F, _P, _P], None),
@@ -182,6 +184,23 @@ def gated_residual(x, h, seg_off, gate, gate_base=None, dt=None):
     LIB.or_gated_residual(dt, _ptr(x), _ptr(h), x.size // d, d, _ptr(seg_off), seg_off.size - 1, _ptr(g), ldg,
                           _ptr(_f32(gate_base)), _ptr(out))
     return out
+
+
+def gated_residual_modulate(x, h, seg_off, gate, shift, scale, gate_base=None, shift_base=None, scale_base=None,
+                            eps=1e-6, dt=None):
+    """x_out = x + h*gate (gate None: x + h), y = L3(x_out)*(scale+1) + shift.
+    Pieces are [S, C] f32 arrays; seg_off int64 [S+1]. Returns (x_out, y)."""
+    dt = dt_of(x, dt)
+    xo, y = _like(x), _like(x)
+    d = x.shape[-1]
+    seg_off = np.ascontiguousarray(seg_off, dtype=np.int64)
+    g, ldg = _piece(gate)
+    sh, ldsh = _piece(shift)
+    sc, ldsc = _piece(scale)
+    LIB.or_gated_residual_modulate(dt, _ptr(x), _ptr(h), x.size // d, d, _ptr(seg_off), seg_off.size - 1, _ptr(g),
+                                   ldg, _ptr(_f32(gate_base)), _ptr(sh), ldsh, _ptr(_f32(shift_base)), _ptr(sc),
+                                   ldsc, _ptr(_f32(scale_base)), eps, _ptr(xo), _ptr(y))
+    return xo, y
 
 
 def rms_norm_heads(x, w, eps, dt=None):

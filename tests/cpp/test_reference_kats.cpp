@@ -148,6 +148,37 @@ void ada_ln_modulation_chunks_in_reference_order(const Device &dev) {
   }
 }
 
+// The sparse block's gated residual + MLP modulate (trellis2_blocks.rs:708-713)
+// in one launch, on exact small-integer inputs: gate 0.5 with h = 2 adds 1 to
+// every element of x; a row [a, a+1, ..., a+7] then normalises to the
+// standard scores of 0..7, so y = z * (1 + scale) + shift with z known in
+// closed form. Without a gate (the dense block's cross-attention add,
+// :637-642) x_out = x + h exactly.
+void gated_residual_modulate_closed_form(const Device &dev) {
+  std::vector<float> xv(2 * 8), hv(2 * 8, 2.0f);
+  for (int r = 0; r < 2; ++r)
+    for (int c = 0; c < 8; ++c) xv[r * 8 + c] = (float)(10 * r + c);
+  const Tensor x = Tensor::from_f32(xv, {2, 8}, DType::F32, dev);
+  const Tensor h = Tensor::from_f32(hv, {2, 8}, DType::F32, dev);
+  const Tensor gate = Tensor::from_f32(std::vector<float>(8, 0.5f), {1, 8}, DType::F32, dev);
+  Modulation next{Tensor::from_f32(std::vector<float>(8, 0.25f), {1, 8}, DType::F32, dev),
+                  Tensor::from_f32(std::vector<float>(8, 1.0f), {1, 8}, DType::F32, dev)};
+  auto [xo, y] = gated_residual_adaln_modulate(x, h, gate, std::nullopt, next, 0.0);
+  const std::vector<float> xs = xo.to_vec_f32(), ys = y.to_vec_f32();
+  const double sd = std::sqrt(5.25);  // population std of 0..7
+  for (int r = 0; r < 2; ++r)
+    for (int c = 0; c < 8; ++c) {
+      CHECK(xs[r * 8 + c] == xv[r * 8 + c] + 1.0f);
+      CHECK_NEAR(ys[r * 8 + c], (c - 3.5) / sd * 2.0 + 0.25, 2e-6);
+    }
+  auto [xo2, y2] = gated_residual_adaln_modulate(x, h, std::nullopt, std::nullopt, next, 0.0);
+  const std::vector<float> xs2 = xo2.to_vec_f32();
+  for (size_t i = 0; i < xs2.size(); ++i) CHECK(xs2[i] == xv[i] + 2.0f);
+  Modulation gated = next;
+  gated.gate = gate;
+  CHECK(throws_with([&] { gated_residual_adaln_modulate(x, h, gate, std::nullopt, gated, 0.0); }, "no output gate"));
+}
+
 // ---------------------------------------------------------------------------
 // src/runtime/trellis2_dino.rs tests
 // ---------------------------------------------------------------------------
@@ -606,6 +637,7 @@ int main(int argc, char **argv) {
       {"qk_rms_norm_matches_reference", qk_rms_norm_matches_reference, true},
       {"timestep_embedding_matches_reference", timestep_embedding_matches_reference, true},
       {"ada_ln_modulation_chunks_in_reference_order", ada_ln_modulation_chunks_in_reference_order, true},
+      {"gated_residual_modulate_closed_form", gated_residual_modulate_closed_form, true},
       {"dinov3_rope_tables_match_hand_computed_cos_sin", dinov3_rope_tables_match_hand_computed_cos_sin, true},
       {"dinov3_rope_applies_to_patches_only", dinov3_rope_applies_to_patches_only, true},
       {"residual_layer_norm_closed_form", residual_layer_norm_closed_form, true},

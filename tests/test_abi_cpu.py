@@ -109,6 +109,32 @@ def test_residual_and_modulate_errors():
     assert rc == _lib.ERR_NULL
 
 
+def test_gated_residual_adaln_modulate_errors():
+    fn = "lux3d_gated_residual_adaln_modulate"
+    x = T([8, 128])
+    x2 = T([8, 128], data=FAKE + 0x10000)
+    y = T([8, 128], data=FAKE + 0x20000)
+    sh = T([2, 128], _lib.F32)
+    rc, msg = status(fn, x, x2, None, sh, None, None, None, sh, None, 1e-6, x, y, None)
+    assert rc == _lib.ERR_NULL and "`shift` and `scale`" in msg
+    # y may not alias x or x_out
+    rc, msg = status(fn, x, x2, None, sh, None, sh, None, sh, None, 1e-6, x, x, None)
+    assert rc == _lib.ERR_LAYOUT and "alias" in msg
+    # pieces must share one segment count
+    rc, msg = status(fn, x, x2, None, T([4, 128], _lib.F32), None, sh, None, sh, None, 1e-6, x, y, None)
+    assert rc == _lib.ERR_SHAPE and "segment counts" in msg
+    # h's shape and dtype follow x
+    rc, msg = status(fn, x, T([8, 64]), None, sh, None, sh, None, sh, None, 1e-6, x, y, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status(fn, x, T([8, 128], _lib.F32), None, sh, None, sh, None, sh, None, 1e-6, x, y, None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status(fn, x, x2, None, sh, None, sh, None, sh, None, -1.0, x, y, None)
+    assert rc == _lib.ERR_VALUE
+    # a base vector without its piece
+    rc, msg = status(fn, x, x2, None, None, T([128], _lib.F32), sh, None, sh, None, 1e-6, x, y, None)
+    assert rc == _lib.ERR_NULL
+
+
 def test_head_op_errors():
     q = T([2, 16, 10, 64], strides=[10 * 3 * 16 * 64, 64, 3 * 16 * 64, 1])
     out = T([2, 16, 10, 64])

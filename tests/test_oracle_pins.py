@@ -196,6 +196,48 @@ def test_gated_residual():
     assert np.array_equal(orc.gated_residual(x, h, offs, np.zeros((2, C), np.float32)), x)
 
 
+def test_gated_residual_modulate_against_torch_and_reductions():
+    """G1 then L3 + M1 on the stored residual stream (trellis2_blocks.rs:
+    708-713; :637-642 ungated): torch f64 on the same ragged segments, and
+    the reductions that a dropped or misplaced term would break."""
+    rows, C = 40, 256
+    x = synth.normal(36, rows * C).reshape(rows, C)
+    h = synth.normal(37, rows * C).reshape(rows, C)
+    offs = np.array([0, 17, 40], dtype=np.int64)
+    t_emb = synth.normal(38, 2 * 6 * C, 0.0, 0.1).reshape(2, 6 * C)
+    modulation = synth.normal(39, 6 * C, 0.0, 0.1)
+    piece = lambda k: np.ascontiguousarray(t_emb[:, k * C:(k + 1) * C])  # noqa: E731
+    base = lambda k: modulation[k * C:(k + 1) * C]  # noqa: E731
+    # the sparse block's MLP half: gate_msa (chunk 2), then scale_mlp / shift_mlp (chunks 4 / 3)
+    xo, y = orc.gated_residual_modulate(x, h, offs, piece(2), piece(3), piece(4), base(2), base(3), base(4))
+    ref_x = torch.empty((rows, C), dtype=torch.float64)
+    ref_y = torch.empty((rows, C), dtype=torch.float64)
+    for s in range(2):
+        r0, r1 = offs[s], offs[s + 1]
+        mv = f64(modulation) + f64(t_emb[s])
+        g, sh, sc = mv[2 * C:3 * C], mv[3 * C:4 * C], mv[4 * C:5 * C]
+        ref_x[r0:r1] = f64(x[r0:r1]) + f64(h[r0:r1]) * g
+        n = F.layer_norm(f64(xo[r0:r1]), (C,), eps=1e-6)   # the norm reads the stored x_out
+        ref_y[r0:r1] = n * (1.0 + sc) + sh
+    assert np.max(np.abs(xo - ref_x.numpy())) < 1e-6
+    assert_f32_close(y, ref_y.numpy(), what="G1 + M1 ragged")
+    # gate = 0: x_out == x exactly, y == the plain modulate of x
+    z = np.zeros((2, C), np.float32)
+    xo0, y0 = orc.gated_residual_modulate(x, h, offs, z, piece(3), piece(4))
+    assert np.array_equal(xo0, x)
+    assert np.array_equal(y0, orc.adaln_modulate(x, offs, piece(3), piece(4), eps=1e-6))
+    # no gate (the dense block's cross-attention add): x_out == x + h exactly
+    xo1, y1 = orc.gated_residual_modulate(x, h, offs, None, z, z)
+    assert np.array_equal(xo1, (x + h).astype(np.float32))
+    # scale = shift = 0: y is L3 of the stored x_out
+    assert np.array_equal(y1, orc.layer_norm_no_affine(xo1, 1e-6))
+    # bf16: x_out equals the gated residual, y the modulate of the stored x_out
+    xb, hb = orc.bf16_bits(x), orc.bf16_bits(h)
+    xob, yb = orc.gated_residual_modulate(xb, hb, offs, piece(2), piece(3), piece(4), dt=orc.BF16)
+    assert np.array_equal(xob, orc.gated_residual(xb, hb, offs, piece(2), dt=orc.BF16))
+    assert np.array_equal(yb, orc.adaln_modulate(xob, offs, piece(3), piece(4), eps=1e-6, dt=orc.BF16))
+
+
 # ---------------------------------------------------------------------------
 # Head norms
 # ---------------------------------------------------------------------------
