@@ -10,10 +10,22 @@ QK-LayerNorm + 2D RoPE over q, k [8, 16, 1374, 64] read straight from the
 packed qkv buffer. `value` = algorithmic bytes of one step / measured time per
 step (HIP events on the launch stream, inputs resident in HBM, buffers rotated
 so nothing is served from the 256 MB Infinity Cache). Every other configs[0..4]
-op is timed the same way and reported under "ops".
+op is timed the same way and reported under "ops", each with:
+  - `us`: cold graph-replay average (the value the roofline fractions use);
+  - `copy_us` / `pattern_us`: this build's copy kernels moving the op's exact
+    bytes with no arithmetic, as contiguous streams and in the op's own access
+    pattern (csrc/ceiling.hip), timed the same way: the achievable bandwidth
+    at that size and layout on this chip;
+  - `trace_us`: the kernel's average duration in the committed rocprofv3
+    kernel trace of `bench.py --profile <op>` (profiles/kernel_trace_<op>.md),
+    and `traffic_bytes` from the committed FETCH_SIZE / WRITE_SIZE summary
+    (profiles/traffic_<op>.md), when those exist;
+  - `cpu`: the oracle (a C restatement of candle's CPU path) on a bounded
+    sample of the same op, on all threads of the box's CPU share and on one
+    thread (median of 20 runs after 3 warm-ups).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
-       python bench.py --profile NAME --iters K    (one op, for rocprofv3)
+       python bench.py --profile NAME [--iters K]   (one op, for rocprofv3)
 """
 import argparse
 import json
@@ -28,6 +40,7 @@ PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, TFLOP/s
 PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 matrix peak, TFLOP/s
 METRIC = "fused-op achieved HBM GB/s (% of MI355X peak) + µs/op at VGGT/DiT shapes"
+CPU_SHARE = 16             # host threads of the GPU box's CPU share for one GPU
 
 
 def parse():
@@ -38,24 +51,9 @@ def parse():
     ap.add_argument("--only", nargs="*", default=None, help="restrict the per-op table to these names")
     ap.add_argument("--profile", default=None, help="run only this op (name or cfgN_name) for --iters launches")
     ap.add_argument("--iters", type=int, default=100)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-runs", type=int, default=20)
     return ap.parse_args()
-
-
-def time_launches(torch, wl, n, warm=5):
-    """Average us per launch over n back-to-back launches (HIP events on the
-    launch stream; each launch uses the next rotation set)."""
-    for i in range(warm):
-        wl.launch(i)
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(n):
-        wl.launch(warm + i)
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) * 1000.0 / n
 
 
 def time_graph(torch, launches, per_graph, replays=5):
@@ -87,13 +85,11 @@ def time_graph(torch, launches, per_graph, replays=5):
     return us
 
 
-def copy_ceiling_us(torch, dev, nbytes, n=50):
+def runtime_copy_us(torch, dev, nbytes, n=50):
     """Average us of the runtime's device-to-device copy (hipMemcpyAsync via
     torch's copy_) moving the same bytes as an op (nbytes/2 read + nbytes/2
     written per launch), graph-timed like the ops, rotating over buffer pairs
-    that together exceed the 256 MB Infinity Cache. A reference point for what
-    a plain streaming kernel of the runtime gets at this transfer size; it is
-    not an upper bound (the fused kernels beat it at most sizes)."""
+    that together exceed the 256 MB Infinity Cache."""
     half = max(256, (nbytes // 2 + 255) // 256 * 256)
     sets = min(64, max(3, -(-(768 << 20) // (2 * half))))
     bufs = [(torch.ones(half, dtype=torch.uint8, device=dev), torch.empty(half, dtype=torch.uint8, device=dev))
@@ -104,17 +100,52 @@ def copy_ceiling_us(torch, dev, nbytes, n=50):
     return us
 
 
+def ceilings(torch, dev, pattern, n):
+    """(copy_us, pattern_us, bytes) of this build's copy kernels for an op's
+    access pattern (lux3d_fused.ceiling)."""
+    from lux3d_fused import ceiling as C
+    same = C.Copy(dev, C.same_size_streams(pattern), same_size=True)
+    cu = time_graph(torch, same.launch, n)
+    nbytes = same.bytes
+    del same
+    torch.cuda.empty_cache()
+    if pattern["kind"] == "streams":
+        return cu, cu, nbytes
+    pat = C.Copy(dev, pattern, same_size=False)
+    pu = time_graph(torch, pat.launch, n)
+    del pat
+    torch.cuda.empty_cache()
+    return cu, pu, nbytes
+
+
+def _json_block(path):
+    text = open(path).read()
+    return json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+
+
 def committed_traffic(tag):
-    """HBM bytes per launch of op `tag` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary profiles/traffic_<tag>.md (calibrated against a copy of
-    known size), or None when no such summary exists."""
+    """HBM bytes per launch of op `tag` from profiles/traffic_<tag>.md
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated against a copy of known
+    size), or None when no such summary exists."""
     path = os.path.join(ROOT, "profiles", f"traffic_{tag}.md")
     if not os.path.exists(path):
         return None
-    text = open(path).read()
     try:
-        blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
-        return max(v["hbm_bytes"] for v in blob["kernels"].values())
+        return max(v["hbm_bytes"] for v in _json_block(path)["kernels"].values())
+    except (IndexError, ValueError, KeyError):
+        return None
+
+
+def committed_trace(tag):
+    """(kernel name, average us, launches) of the dominant kernel in
+    profiles/kernel_trace_<tag>.md (rocprofv3 --kernel-trace --stats of
+    `bench.py --profile <tag>`), or None."""
+    path = os.path.join(ROOT, "profiles", f"kernel_trace_{tag}.md")
+    if not os.path.exists(path):
+        return None
+    try:
+        k = _json_block(path)["kernels"][0]
+        return k["name"], k["avg_us"], k["calls"]
     except (IndexError, ValueError, KeyError):
         return None
 
@@ -124,55 +155,143 @@ def all_workloads():
     return [(f, True) for f in W.TARGETS] + [(f, False) for f in W.EXTRAS]
 
 
-def cpu_baseline(seconds):
-    """configs[1] step on the CPU oracle (C restatement of candle's CPU path,
-    threaded over rows), on a bounded sample: one frame of the 8 (1374 tokens),
-    repeated for about `seconds`. Throughput in the metric's unit (GB/s of the
-    sample's algorithmic bytes)."""
+# ---------------------------------------------------------------------------
+# CPU baselines: the oracle (the C restatement of candle's CPU path, threaded
+# over rows like candle's rayon-over-rows) on a bounded sample of each op.
+# ---------------------------------------------------------------------------
+
+def _cpu_samples():
+    """op tag -> (description, algorithmic bytes of the sample, run()) built
+    from the shared seeded generator; each sample is a fixed fraction of the
+    op's configs shape (whole rows / tokens), so GB/s compares directly."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import lux3d_oracle as orc
     from lux3d_fused import synth
-    threads = max(1, min(16, os.cpu_count() or 1))
-    orc.set_threads(threads)
-    N, C, H, D = 1374, 1024, 16, 64
-    s = synth.config_seed(1)
-    x = orc.bf16_bits(synth.normal(s, N * C).reshape(N, C))
-    a = orc.bf16_bits(synth.normal(s + 100, N * C).reshape(N, C))
-    g = synth.normal(s + 200, C, 1.0, 0.02)
-    w = synth.normal(s + 300, C, 1.0, 0.02)
-    b = synth.normal(s + 400, C, 0.0, 0.02)
-    q = orc.bf16_bits(synth.normal(s + 7, H * N * D).reshape(1, H, N, D))
-    k = orc.bf16_bits(synth.normal(s + 8, H * N * D).reshape(1, H, N, D))
-    qw, qb = synth.normal(s + 21, D, 1.0, 0.02), synth.normal(s + 22, D, 0.0, 0.02)
-    pos = synth.vggt_positions(1, 37, 37)
-    sample_bytes = N * C * 2 * 4 + 3 * C * 4 + 2 * H * N * D * 2 * 2 + 4 * D * 4 + N * 2 * 4
+    bf = orc.bf16_bits
+    S = {}
 
-    def one():
-        orc.residual_layer_norm(x, a, g, w, b, 1e-5, dt=orc.BF16)
-        cos, sin = orc.rope2d_tables(pos, D, 100.0)
-        orc.layernorm_rope2d(q, qw, qb, 1e-5, cos, sin, dt=orc.BF16)
-        orc.layernorm_rope2d(k, qw, qb, 1e-5, cos, sin, dt=orc.BF16)
+    def rows_bf16(seed, rows, c):
+        return bf(synth.normal(seed, rows * c).reshape(rows, c))
 
-    for _ in range(2):
-        one()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
+    # configs[0]: LayerNorm f32 [1374, 1024], whole
+    x0 = synth.normal(1, 1374 * 1024).reshape(1374, 1024)
+    w0, b0 = synth.normal(2, 1024, 1.0, 0.02), synth.normal(3, 1024, 0.0, 0.02)
+    S["cfg0_layer_norm"] = ("[1374,1024] f32 (whole)", 1374 * 1024 * 8 + 2 * 1024 * 4,
+                            lambda: orc.layer_norm(x0, w0, b0, 1e-6))
+    # configs[1]: F1 on one frame of 8; QK LN + RoPE on q, k of one frame (tables built per call)
+    x1, a1 = rows_bf16(11, 1374, 1024), rows_bf16(12, 1374, 1024)
+    g1, w1, b1 = synth.normal(13, 1024, 1.0, 0.02), synth.normal(14, 1024, 1.0, 0.02), synth.normal(15, 1024, 0.0, 0.02)
+    S["cfg1_residual_layer_norm"] = ("[1374,1024] bf16 (1 of 8 frames)", 1374 * 1024 * 2 * 4 + 3 * 1024 * 4,
+                                     lambda: orc.residual_layer_norm(x1, a1, g1, w1, b1, 1e-5, dt=orc.BF16))
+    q1 = bf(synth.normal(16, 16 * 1374 * 64).reshape(1, 16, 1374, 64))
+    k1 = bf(synth.normal(17, 16 * 1374 * 64).reshape(1, 16, 1374, 64))
+    qw, qb = synth.normal(18, 64, 1.0, 0.02), synth.normal(19, 64, 0.0, 0.02)
+    pos1 = synth.vggt_positions(1, 37, 37)
+
+    def qk1():
+        cos, sin = orc.rope2d_tables(pos1, 64, 100.0)
+        orc.layernorm_rope2d(q1, qw, qb, 1e-5, cos, sin, dt=orc.BF16)
+        orc.layernorm_rope2d(k1, qw, qb, 1e-5, cos, sin, dt=orc.BF16)
+    S["cfg1_qk_layernorm_rope2d"] = ("q,k [1,16,1374,64] bf16 + Rope2d tables (1 of 8 frames)",
+                                     2 * 16 * 1374 * 64 * 2 * 2 + 4 * 64 * 4 + 1374 * 2 * 4, qk1)
+    # configs[2]: 512 of the 4096 rows (modulate / gate / gated modulate), 256 of 2048 tokens (heads)
+    r2, c2 = 512, 2048
+    x2, h2 = rows_bf16(21, r2, c2), rows_bf16(22, r2, c2)
+    sh2, sc2 = synth.normal(23, 2 * c2, 0.0, 0.1).reshape(2, c2), synth.normal(24, 2 * c2, 0.0, 0.1).reshape(2, c2)
+    gt2 = synth.normal(25, 2 * c2, 0.0, 0.1).reshape(2, c2)
+    off2 = np.array([0, r2 // 2, r2], dtype=np.int64)
+    S["cfg2_adaln_modulate"] = ("[512,2048] bf16 (1/8 of the rows)", r2 * c2 * 4 + 2 * 2 * c2 * 4,
+                                lambda: orc.adaln_modulate(x2, off2, sh2, sc2, eps=1e-6, dt=orc.BF16))
+    S["cfg2_gated_residual"] = ("[512,2048] bf16 (1/8 of the rows)", r2 * c2 * 6 + 2 * c2 * 4,
+                                lambda: orc.gated_residual(x2, h2, off2, gt2, dt=orc.BF16))
+    S["cfg2_gated_residual_adaln_modulate"] = (
+        "[512,2048] bf16 (1/8 of the rows)", r2 * c2 * 8 + 3 * 2 * c2 * 4,
+        lambda: orc.gated_residual_modulate(x2, h2, off2, gt2, sh2, sc2, dt=orc.BF16))
+    qh = bf(synth.normal(26, 16 * 256 * 128).reshape(1, 16, 256, 128))
+    kh = bf(synth.normal(27, 16 * 256 * 128).reshape(1, 16, 256, 128))
+    wr = synth.normal(28, 128, 1.0, 0.02)
+
+    def rms2():
+        orc.rms_norm_heads(qh, wr, 1e-6, dt=orc.BF16)
+        orc.rms_norm_heads(kh, wr, 1e-6, dt=orc.BF16)
+    S["cfg2_rms_norm_heads"] = ("q,k [1,16,256,128] bf16 (1/16 of the tokens)", 2 * 16 * 256 * 128 * 4 + 2 * 128 * 4,
+                                rms2)
+    xg = bf(synth.normal(29, 128 * 8192).reshape(128, 8192))
+    S["cfg2_gelu_tanh"] = ("[128,8192] bf16 (1/32 of the rows)", 128 * 8192 * 4,
+                           lambda: orc.gelu_tanh(xg, dt=orc.BF16))
+    # configs[3]: 4000 of the 64000 voxel rows, the two segments scaled alike (1500 + 2500)
+    r3, c3 = 4000, 1536
+    x3, h3 = rows_bf16(31, r3, c3), rows_bf16(32, r3, c3)
+    off3 = np.array([0, 1500, r3], dtype=np.int64)
+    sh3, sc3 = synth.normal(33, 2 * c3, 0.0, 0.1).reshape(2, c3), synth.normal(34, 2 * c3, 0.0, 0.1).reshape(2, c3)
+    gt3 = synth.normal(35, 2 * c3, 0.0, 0.1).reshape(2, c3)
+    S["cfg3_adaln_modulate_ragged"] = ("[4000,1536] bf16 ragged 1500+2500 (1/16 of the rows)",
+                                       r3 * c3 * 4 + 2 * 2 * c3 * 4 + 24,
+                                       lambda: orc.adaln_modulate(x3, off3, sh3, sc3, eps=1e-6, dt=orc.BF16))
+    S["cfg3_gated_residual_adaln_modulate_ragged"] = (
+        "[4000,1536] bf16 ragged 1500+2500 (1/16 of the rows)", r3 * c3 * 8 + 3 * 2 * c3 * 4 + 24,
+        lambda: orc.gated_residual_modulate(x3, h3, off3, gt3, sh3, sc3, dt=orc.BF16))
+    coords = synth.unique_voxels(36, r3, 64)
+    q3 = bf(synth.normal(37, r3 * 12 * 128).reshape(1, r3, 12, 128))
+    k3 = bf(synth.normal(38, r3 * 12 * 128).reshape(1, r3, 12, 128))
+    gq = synth.normal(39, 12 * 128, 1.0, 0.02).reshape(12, 128)
+
+    def qk3():
+        cos, sin = orc.rope3d_tables(coords, 128, 10000.0)
+        orc.qk_l2norm_rope3d(q3, gq, cos, sin, dt=orc.BF16)
+        orc.qk_l2norm_rope3d(k3, gq, cos, sin, dt=orc.BF16)
+    S["cfg3_qk_l2norm_rope3d_ragged"] = ("q,k [1,4000,12,128] bf16 + 3D RoPE tables (1/16 of the voxels)",
+                                         2 * r3 * 12 * 128 * 4 + r3 * 12 + 2 * 12 * 128 * 4, qk3)
+    # configs[4]: F1 f32 [1029, 1024] and Q8_0 [4096, 1024], whole
+    x4, a4 = synth.normal(41, 1029 * 1024).reshape(1029, 1024), synth.normal(42, 1029 * 1024).reshape(1029, 1024)
+    g4, w4, b4 = synth.normal(43, 1024, 1e-5, 1e-6), synth.normal(44, 1024, 1.0, 0.02), synth.normal(45, 1024, 0.0, 0.02)
+    S["cfg4_residual_layer_norm"] = ("[1029,1024] f32 (whole)", 1029 * 1024 * 16 + 3 * 1024 * 4,
+                                     lambda: orc.residual_layer_norm(x4, a4, g4, w4, b4, 1e-5))
+    blocks = synth.q8_0_blocks(46, 4096 * 1024 // 32)
+    S["cfg4_dequant_q8_0"] = ("W [4096,1024] Q8_0 -> bf16 (whole)", 131072 * 34 + 4096 * 1024 * 2,
+                              lambda: orc.dequant_q8_0(blocks, out_dt=orc.BF16))
+    return S, orc
+
+
+def _median_runs(fn, runs, warm=3):
+    import numpy as np
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return {
-        "value": round(sample_bytes / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"configs[1] step on 1 of 8 frames (F1 residual+LayerScale+LN on [1374,1024] bf16, "
-                   f"Rope2d tables, QK LN+RoPE on q,k [1,16,1374,64] bf16); median of {len(times)} reps "
-                   f"= {med * 1e3:.3f} ms over ~{seconds:.0f} s; C oracle, {threads} threads"),
-        "ms_per_sample": round(med * 1e3, 4),
-    }
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baselines(runs):
+    """Per-op CPU throughput on the box's host cores, on all threads of its
+    share and on one thread: {tag: {...}} plus the machine facts."""
+    samples, orc = _cpu_samples()
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = nproc
+    threads = max(1, min(CPU_SHARE, avail))
+    out = {}
+    for tag, (what, nbytes, fn) in samples.items():
+        orc.set_threads(threads)
+        t_all = _median_runs(fn, runs)
+        orc.set_threads(1)
+        t_one = _median_runs(fn, runs)
+        out[tag] = {"sample": what, "sample_bytes": nbytes, "threads": threads,
+                    "us": round(t_all * 1e6, 1), "gbs": round(nbytes / t_all / 1e9, 3),
+                    "us_1thread": round(t_one * 1e6, 1), "gbs_1thread": round(nbytes / t_one / 1e9, 3)}
+        print(f"[cpu] {tag}: {out[tag]['gbs']} GB/s on {threads} threads, {out[tag]['gbs_1thread']} on 1",
+              file=sys.stderr, flush=True)
+    facts = {"os_cpu_count": nproc, "affinity_cpus": avail, "threads_used": threads,
+             "what": "C restatement of candle's CPU path (oracle/lux3d_oracle.c, gcc -O2), rows split over "
+                     "threads like candle's rayon-over-rows; candle itself is not buildable here",
+             "statistic": f"median of {runs} runs after 3 warm-ups, per thread count"}
+    return out, facts
 
 
 def main():
@@ -201,14 +320,19 @@ def main():
         print(json.dumps({"op": "copy_1gib", "bytes_read": 1 << 30, "bytes_written": 1 << 30}), flush=True)
         return
     if args.profile:
+        # the op's cold launches exactly as the per-op table times them (a
+        # graph of --iters launches over the rotation sets, replayed 5 times
+        # after 3 eager warm-ups), so the kernel trace of this command and
+        # the table's graph timing describe the same launches
         for f, _ in all_workloads():
             wl = f(dev)
             tag = f"cfg{wl.config}_{wl.name}"
             if args.profile in (wl.name, tag):
                 print(f"[profile] {tag} {wl.shape} sets={wl.sets} iters={args.iters}", flush=True)
-                us = time_launches(torch, wl, args.iters)
-                print(json.dumps({"op": tag, "us_per_launch_events": round(us, 3),
-                                  "gbs": round(wl.bytes / us / 1e3, 1), "bytes": wl.bytes}), flush=True)
+                us = time_graph(torch, wl.launch, args.iters)
+                print(json.dumps({"op": tag, "us_per_launch_graph": round(us, 3),
+                                  "gbs": round(wl.bytes / us / 1e3, 1), "bytes": wl.bytes,
+                                  "launches": 3 + 6 * args.iters}), flush=True)
                 return
             del wl
             torch.cuda.empty_cache()
@@ -239,24 +363,29 @@ def main():
     torch.cuda.synchronize()
     ms_per_step_eager = s.elapsed_time(e) / args.steps
 
-    # per-kernel averages (graph replay, events on the replay stream)
-    n_k = max(50, args.steps)
+    # per-kernel averages (graph replay, events on the replay stream), as the
+    # per-op table and `--profile` time them
+    n_k = 100
     us_f1 = time_graph(torch, f1.launch, n_k)
     us_qk = time_graph(torch, qk.launch, n_k)
     dom, us_dom = (qk, us_qk) if us_qk >= us_f1 else (f1, us_f1)
+    dom_tag = f"cfg{dom.config}_{dom.name}"
     achieved = dom.bytes / us_dom / 1e3
-    traffic = committed_traffic(f"cfg{dom.config}_{dom.name}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                "kernel": dom.kernel, "op": f"cfg{dom.config}_{dom.name}", "us": round(us_dom, 3),
-                "algorithmic_bytes": dom.bytes}
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": committed_traffic(dom_tag),
+                "kernel": dom.kernel, "op": dom_tag, "us": round(us_dom, 3), "algorithmic_bytes": dom.bytes,
+                "timing": f"HIP events around a graph of {n_k} cold launches replayed 5 times (the launch stream)"}
+    tr = committed_trace(dom_tag)
+    if tr:
+        roofline["trace"] = {"file": f"profiles/kernel_trace_{dom_tag}.md", "kernel": tr[0], "us": tr[1],
+                             "launches": tr[2], "frac": round(dom.bytes / tr[1] / 1e3 / PEAK_GBS, 4),
+                             "events_over_trace": round(us_dom / tr[1], 4)}
     step_ops = {f"cfg1_{f1.name}": us_f1, f"cfg1_{qk.name}": us_qk}
     dom_bytes = dom.bytes
     del f1, qk, dom
     torch.cuda.empty_cache()
-    copy_us = copy_ceiling_us(torch, dev, dom_bytes)
+    copy_us = runtime_copy_us(torch, dev, dom_bytes)
     roofline["runtime_copy"] = {"us": round(copy_us, 3), "gbs": round(dom_bytes / copy_us / 1e3, 1),
-                                "speed_vs_runtime_copy": round(copy_us / us_dom, 4),
                                 "what": "hipMemcpyAsync D2D of the same bytes (half read, half written)"}
 
     # ---- every op at its config shape ----------------------------------------------
@@ -268,8 +397,9 @@ def main():
             del wl
             continue
         cfg, dtype, shape, sets, note, flops = wl.config, wl.dtype, wl.shape, wl.sets, wl.ideal_note, wl.flops
+        pattern = wl.pattern
         peak_tf = wl.peak_tflops or PEAK_BF16_TFLOPS
-        n = wl.reps or (200 if wl.bytes < 64 << 20 else 50)
+        n = wl.reps or 100
         us = step_ops.get(tag)
         if us is None:
             us = time_graph(torch, wl.launch, n)
@@ -280,20 +410,50 @@ def main():
         nbytes = wl.bytes
         del wl
         torch.cuda.empty_cache()
-        cus = copy_ceiling_us(torch, dev, nbytes, 200 if nbytes < 64 << 20 else 50)
-        print(f"[bench] {tag}: {us:.2f} us (warm {us_warm:.2f})", file=sys.stderr, flush=True)
-        table.append({"op": tag, "config": cfg, "dtype": dtype, "shape": shape,
-                      "bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
-                      "warm_us": round(us_warm, 3), "warm_gbs": round(nbytes / us_warm / 1e3, 1),
-                      "frac_peak": round(gbs / PEAK_GBS, 4), "runtime_copy_us": round(cus, 3),
-                      "speed_vs_runtime_copy": round(cus / us, 4), "target_70pct": bool(target),
-                      "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
-                      "rotation_sets": sets, **({"note": note} if note else {}),
-                      **({"bound": "mfma", "tflops": round(flops / us / 1e6, 1),
-                          "mfma_peak_tflops": peak_tf,
-                          "frac_mfma_peak": round(flops / us / 1e6 / peak_tf, 4)} if flops else {})})
+        row = {"op": tag, "config": cfg, "dtype": dtype, "shape": shape,
+               "bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
+               "warm_us": round(us_warm, 3), "warm_gbs": round(nbytes / us_warm / 1e3, 1),
+               "frac_peak": round(gbs / PEAK_GBS, 4), "target_70pct": bool(target),
+               "meets_70pct": (gbs / PEAK_GBS >= 0.70) if target else None,
+               "rotation_sets": sets, **({"note": note} if note else {})}
+        if flops:
+            row.update({"bound": "mfma", "tflops": round(flops / us / 1e6, 1), "mfma_peak_tflops": peak_tf,
+                        "frac_mfma_peak": round(flops / us / 1e6 / peak_tf, 4)})
+        else:
+            row["runtime_copy_us"] = round(runtime_copy_us(torch, dev, nbytes, n), 3)
+        if pattern:
+            cu, pu, cbytes = ceilings(torch, dev, pattern, n)
+            row.update({"copy_us": round(cu, 3), "pattern_us": round(pu, 3), "copy_bytes": cbytes,
+                        "frac_of_pattern": round(pu / us, 4)})
+        tr = committed_trace(tag)
+        if tr:
+            row.update({"trace_us": tr[1], "trace_frac_peak": round(nbytes / tr[1] / 1e3 / PEAK_GBS, 4),
+                        "trace_kernel": tr[0]})
+        tb = committed_traffic(tag)
+        if tb:
+            row["traffic_bytes"] = tb
+        print(f"[bench] {tag}: {us:.2f} us (warm {us_warm:.2f}"
+              + (f", copy {row['copy_us']:.2f}, pattern {row['pattern_us']:.2f}" if pattern else "") + ")",
+              file=sys.stderr, flush=True)
+        table.append(row)
 
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    # ---- CPU: per op, and the step sample as the headline baseline ---------------------
+    cpu = None
+    if not args.no_cpu:
+        per_op, facts = cpu_baselines(args.cpu_runs)
+        for row in table:
+            if row["op"] in per_op:
+                c = per_op[row["op"]]
+                row["cpu"] = c
+                row["gpu_over_cpu"] = round(row["gbs"] / c["gbs"], 1)
+        a, b = per_op["cfg1_residual_layer_norm"], per_op["cfg1_qk_layernorm_rope2d"]
+        nbytes = a["sample_bytes"] + b["sample_bytes"]
+        cpu = {"value": round(nbytes / ((a["us"] + b["us"]) * 1e-6) / 1e9, 3), "unit": "GB/s",
+               "cores": facts["threads_used"], "kind": "port",
+               "sample": ("configs[1] step on 1 of 8 frames: F1 residual+LayerScale+LN on [1374,1024] bf16, "
+                          "Rope2d tables, QK LN+RoPE on q,k [1,16,1374,64] bf16; " + facts["statistic"]),
+               "value_1thread": round(nbytes / ((a["us_1thread"] + b["us_1thread"]) * 1e-6) / 1e9, 3),
+               **facts}
 
     out = {
         "metric": METRIC,

@@ -1,0 +1,248 @@
+// ceiling.hip -- copy kernels that move exactly the bytes of a fused op, with
+// no arithmetic, for bench.py's per-op bandwidth ceiling. Measurement code
+// only (liblux3d_ceiling.so); it is not part of the C ABI in
+// include/lux3d_fused.h and nothing in liblux3d_fused.so uses it.
+//
+// Three forms:
+//  - streams: NIN contiguous inputs and NOUT contiguous outputs, one 16-byte
+//    chunk per thread per stream (the activation kernels' layout); inputs and
+//    outputs may differ in size (Q8_0 dequant reads 34-byte blocks and writes
+//    twice as many bytes);
+//  - rows: the row kernels' layout -- a row of `row_bytes` owned by TPR
+//    threads, thread t holding chunks c*TPR + t (c < NC) of 8 elements
+//    (16 bytes for 2-byte types, 32 for f32), 256-thread workgroups of whole
+//    rows (or one row per workgroup when TPR is 128 / 256 and the op runs a
+//    row per workgroup);
+//  - heads: the head kernels' layout -- [B, H, N, D] views with any outer
+//    strides, D / 8 lanes per head row, two rows per thread (one for f32),
+//    workgroups of `tb` consecutive tokens x all heads, q and k in
+//    grid.y (or both in one workgroup, as the D = 128 kernels do).
+// Every output word is the XOR of the loaded words that map to it, so no
+// load can be dropped by the compiler.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ld(const char *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ void st(char *p, u32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p)); }
+
+struct Streams {
+  const char *in[4];
+  char *out[4];
+  int64_t in_chunks, out_chunks;  // 16-byte chunks per input / output stream
+};
+
+template <int NIN, int NOUT>
+__global__ __launch_bounds__(256) void streams_kernel(Streams s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  if (i < s.in_chunks) {
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) acc ^= ld(s.in[k] + i * 16);
+  }
+  if (i < s.out_chunks) {
+#pragma unroll
+    for (int k = 0; k < NOUT; ++k) st(s.out[k] + i * 16, acc);
+  }
+}
+
+struct Rows {
+  const char *in[4];
+  char *out[4];
+  int64_t rows, row_bytes;
+};
+
+template <int CB, int TPR, int NC, int NIN, int NOUT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void rows_kernel(Rows p) {
+  constexpr int RPB = BLOCK / TPR;
+  const int t = threadIdx.x % TPR;
+  int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool live = row < p.rows;
+  row = live ? row : p.rows - 1;
+  u32x4 v[NC][CB / 16];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int h = 0; h < CB / 16; ++h) v[c][h] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) {
+    const char *r = p.in[k] + row * p.row_bytes;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int h = 0; h < CB / 16; ++h) v[c][h] ^= ld(r + (int64_t)(c * TPR + t) * CB + h * 16);
+  }
+  if (!live) return;
+#pragma unroll
+  for (int k = 0; k < NOUT; ++k) {
+    char *r = p.out[k] + row * p.row_bytes;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int h = 0; h < CB / 16; ++h) st(r + (int64_t)(c * TPR + t) * CB + h * 16, v[c][h]);
+  }
+}
+
+struct Heads {
+  const char *x[2];
+  char *y[2];
+  int64_t sB, sH, sN, oB, oH, oN;  // element strides (input, output)
+  int64_t B, H, N;
+  int ntens, tb;
+};
+
+// EB: element bytes; D: head dim; R: rows per thread; NTB: tensors per workgroup
+template <int EB, int D, int R, int NTB>
+__global__ __launch_bounds__(256) void heads_kernel(Heads p) {
+  constexpr int LPR = D / 8, CB = 8 * EB;
+  const int lane = threadIdx.x % LPR, ipp = blockDim.x / LPR;
+  // token and head counts below 2^31 (checked on the host): 32-bit indices
+  const uint32_t H = (uint32_t)p.H, N = (uint32_t)p.N, ntok = (uint32_t)(p.B * p.N);
+  const uint32_t tok0 = blockIdx.x * (uint32_t)p.tb, items = (uint32_t)p.tb * H;
+  int64_t xo[R], yo[R];
+  bool live[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t it = (uint32_t)(r * ipp) + threadIdx.x / LPR;
+    uint32_t t = it / H, h = it - t * H, tok = tok0 + t;
+    live[r] = it < items && tok < ntok;
+    if (!live[r]) { h = 0; tok = tok0; }
+    const uint32_t b = tok / N, n = tok - b * N;
+    xo[r] = ((int64_t)b * p.sB + (int64_t)h * p.sH + (int64_t)n * p.sN) * EB + lane * CB;
+    yo[r] = ((int64_t)b * p.oB + (int64_t)h * p.oH + (int64_t)n * p.oN) * EB + lane * CB;
+  }
+  u32x4 v[NTB][R][CB / 16];
+#pragma unroll
+  for (int q = 0; q < NTB; ++q) {
+    const char *x = p.x[NTB == 1 ? blockIdx.y : q];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int h = 0; h < CB / 16; ++h) v[q][r][h] = ld(x + xo[r] + h * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < NTB; ++q) {
+    char *y = p.y[NTB == 1 ? blockIdx.y : q];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (live[r])
+#pragma unroll
+        for (int h = 0; h < CB / 16; ++h) st(y + yo[r] + h * 16, v[q][r][h]);
+  }
+}
+
+int status(hipError_t e) { return e == hipSuccess ? 0 : -5; }
+
+}  // namespace
+
+extern "C" {
+
+// nin / nout in 1..4; in_bytes / out_bytes per stream, multiples of 16.
+int lux3d_ceiling_streams(const void *const *in, int nin, void *const *out, int nout, int64_t in_bytes,
+                          int64_t out_bytes, void *stream) {
+  if (nin < 1 || nin > 4 || nout < 1 || nout > 4 || in_bytes % 16 || out_bytes % 16) return -6;
+  Streams s{};
+  for (int k = 0; k < nin; ++k) s.in[k] = static_cast<const char *>(in[k]);
+  for (int k = 0; k < nout; ++k) s.out[k] = static_cast<char *>(out[k]);
+  s.in_chunks = in_bytes / 16;
+  s.out_chunks = out_bytes / 16;
+  const int64_t n = s.in_chunks > s.out_chunks ? s.in_chunks : s.out_chunks;
+  if (n == 0) return 0;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define LUX3D_STREAMS(I, O)                                                    \
+  if (nin == I && nout == O) {                                                 \
+    hipLaunchKernelGGL((streams_kernel<I, O>), grid, dim3(256), 0, st, s);     \
+    return status(hipGetLastError());                                          \
+  }
+  LUX3D_STREAMS(1, 1) LUX3D_STREAMS(2, 1) LUX3D_STREAMS(2, 2) LUX3D_STREAMS(1, 2)
+#undef LUX3D_STREAMS
+  return -6;
+}
+
+// Contiguous rows of row_bytes; elem_bytes 2 or 4; tpr 64 / 128 / 256;
+// row_per_block: one row per workgroup of tpr threads (else 256-thread
+// workgroups of 256 / tpr rows). row_bytes must be tpr * nc * 8 * elem_bytes
+// for nc in 1..4.
+int lux3d_ceiling_rows(const void *const *in, int nin, void *const *out, int nout, int64_t rows, int64_t row_bytes,
+                       int elem_bytes, int tpr, int row_per_block, void *stream) {
+  if (rows <= 0) return 0;
+  const int cb = 8 * elem_bytes;
+  if ((cb != 16 && cb != 32) || (tpr != 64 && tpr != 128 && tpr != 256)) return -6;
+  if (row_bytes % ((int64_t)tpr * cb)) return -6;
+  const int nc = (int)(row_bytes / ((int64_t)tpr * cb));
+  if (nc < 1 || nc > 4) return -6;
+  Rows p{};
+  for (int k = 0; k < nin; ++k) p.in[k] = static_cast<const char *>(in[k]);
+  for (int k = 0; k < nout; ++k) p.out[k] = static_cast<char *>(out[k]);
+  p.rows = rows;
+  p.row_bytes = row_bytes;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int block = row_per_block ? tpr : 256;
+  const dim3 grid((unsigned)((rows + block / tpr - 1) / (block / tpr)));
+#define LUX3D_ROWS(CB_, TPR_, NC_, I, O, BLK)                                                          \
+  if (cb == CB_ && tpr == TPR_ && nc == NC_ && nin == I && nout == O && block == BLK) {                \
+    hipLaunchKernelGGL((rows_kernel<CB_, TPR_, NC_, I, O, BLK>), grid, dim3(BLK), 0, st, p);           \
+    return status(hipGetLastError());                                                                  \
+  }
+#define LUX3D_ROWS_IO(CB_, TPR_, NC_, BLK)                                                              \
+  LUX3D_ROWS(CB_, TPR_, NC_, 1, 1, BLK) LUX3D_ROWS(CB_, TPR_, NC_, 2, 1, BLK)                           \
+  LUX3D_ROWS(CB_, TPR_, NC_, 2, 2, BLK)
+#define LUX3D_ROWS_NC(CB_, TPR_, BLK)                                                                   \
+  LUX3D_ROWS_IO(CB_, TPR_, 1, BLK) LUX3D_ROWS_IO(CB_, TPR_, 2, BLK) LUX3D_ROWS_IO(CB_, TPR_, 3, BLK)    \
+  LUX3D_ROWS_IO(CB_, TPR_, 4, BLK)
+  LUX3D_ROWS_NC(16, 64, 256) LUX3D_ROWS_NC(16, 128, 256) LUX3D_ROWS_NC(16, 256, 256)
+  LUX3D_ROWS_NC(16, 128, 128)
+  LUX3D_ROWS_NC(32, 64, 256) LUX3D_ROWS_NC(32, 128, 256) LUX3D_ROWS_NC(32, 256, 256)
+  LUX3D_ROWS_NC(32, 128, 128)
+#undef LUX3D_ROWS_NC
+#undef LUX3D_ROWS_IO
+#undef LUX3D_ROWS
+  return -6;
+}
+
+// q, k: [B, H, N, D] views (element strides in_s = {sB, sH, sN}, unit inner
+// stride) -> contiguous-or-strided outputs (out_s); k / ko may be NULL.
+// D 64 / 128; elem_bytes 2 / 4; both_in_one: q and k in one workgroup.
+// Workgroup shape as the head kernels: whole heads per pass, tb tokens.
+int lux3d_ceiling_heads(const void *q, const void *k, void *qo, void *ko, int64_t B, int64_t H, int64_t N, int64_t D,
+                        int elem_bytes, const int64_t *in_s, const int64_t *out_s, int both_in_one, void *stream) {
+  if (B * N <= 0 || H <= 0) return 0;
+  if ((D != 64 && D != 128) || (elem_bytes != 2 && elem_bytes != 4)) return -6;
+  if (B * N >= (int64_t(1) << 31) || H > 4096) return -6;
+  const int ntens = k ? 2 : 1;
+  const int lpr = (int)(D / 8), r = elem_bytes == 4 ? 1 : 2;
+  const int64_t hl = H * lpr;
+  const int64_t kk = hl >= 256 ? 1 : 256 / hl;
+  int64_t threads = ((kk * hl + 63) / 64) * 64;
+  if (threads > 256) threads = 256;
+  const int64_t ipp = threads / lpr, tb = (r * ipp) / H;
+  if (tb < 1) return -6;
+  Heads p{};
+  p.x[0] = static_cast<const char *>(q);
+  p.x[1] = static_cast<const char *>(k);
+  p.y[0] = static_cast<char *>(qo);
+  p.y[1] = static_cast<char *>(ko);
+  p.sB = in_s[0]; p.sH = in_s[1]; p.sN = in_s[2];
+  p.oB = out_s[0]; p.oH = out_s[1]; p.oN = out_s[2];
+  p.B = B; p.H = H; p.N = N; p.ntens = ntens; p.tb = (int)tb;
+  const bool two = both_in_one && ntens == 2;
+  const dim3 grid((unsigned)((B * N + tb - 1) / tb), two ? 1u : (unsigned)ntens), block((unsigned)threads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define LUX3D_HEADS(EB, D_, R_, NTB)                                                         \
+  if (elem_bytes == EB && D == D_ && (two ? 2 : 1) == NTB) {                               \
+    hipLaunchKernelGGL((heads_kernel<EB, D_, R_, NTB>), grid, block, 0, st, p);            \
+    return status(hipGetLastError());                                                      \
+  }
+  LUX3D_HEADS(2, 64, 2, 1) LUX3D_HEADS(2, 64, 2, 2) LUX3D_HEADS(2, 128, 2, 1) LUX3D_HEADS(2, 128, 2, 2)
+  LUX3D_HEADS(4, 64, 1, 1) LUX3D_HEADS(4, 64, 1, 2) LUX3D_HEADS(4, 128, 1, 1) LUX3D_HEADS(4, 128, 1, 2)
+#undef LUX3D_HEADS
+  return -6;
+}
+
+}  // extern "C"

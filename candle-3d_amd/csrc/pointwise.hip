@@ -306,15 +306,30 @@ __global__ __launch_bounds__(kBlock) void dequant_q8_0_staged(const uint8_t *blo
   if constexpr (OUT == LUX3D_F32) {
     Chunk<F32>::store(reinterpret_cast<float *>(y) + g * 8, v);
   } else {
-    uint32_t hb[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      hb[k] = OUT == LUX3D_BF16 ? f32_to_bf16_bits_exact(v[k]) : f32_to_f16_bits_exact(v[k]);
+    // q * d is exact in f32, so every product is finite while the scale is:
+    // the hardware round-to-nearest-even converts (identical to the exact
+    // conversion for non-NaN values) then give the exact result. A block
+    // with an infinite or NaN scale (NaN products carry a payload) takes the
+    // exact software conversion.
     uint4 u;
-    u.x = hb[0] | (hb[1] << 16);
-    u.y = hb[2] | (hb[3] << 16);
-    u.z = hb[4] | (hb[5] << 16);
-    u.w = hb[6] | (hb[7] << 16);
+    if (__builtin_isfinite(d)) {
+      if constexpr (OUT == LUX3D_BF16) {
+        u.x = pack_bf16x2(v[0], v[1]); u.y = pack_bf16x2(v[2], v[3]);
+        u.z = pack_bf16x2(v[4], v[5]); u.w = pack_bf16x2(v[6], v[7]);
+      } else {
+        u.x = pack_f16x2(v[0], v[1]); u.y = pack_f16x2(v[2], v[3]);
+        u.z = pack_f16x2(v[4], v[5]); u.w = pack_f16x2(v[6], v[7]);
+      }
+    } else {
+      uint32_t hb[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        hb[k] = OUT == LUX3D_BF16 ? f32_to_bf16_bits_exact(v[k]) : f32_to_f16_bits_exact(v[k]);
+      u.x = hb[0] | (hb[1] << 16);
+      u.y = hb[2] | (hb[3] << 16);
+      u.z = hb[4] | (hb[5] << 16);
+      u.w = hb[6] | (hb[7] << 16);
+    }
     st16(reinterpret_cast<uint16_t *>(y) + g * 8, u);
   }
 }

@@ -204,15 +204,14 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         float s2 = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
-        const float rr = 1.0f / sqrtf(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
+        const float rr = rsqrt_f32(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = (x[k] * rr) * w[q][k];
       } else if constexpr (NORM == HN_L2) {
         float s2 = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
-        const float nrm = fminf(fmaxf(sqrtf(group_sum<LPR>(s2)), 1e-12f), 1.0e30f);
-        const float rr = 1.0f / nrm;
+        const float rr = l2_rnorm(group_sum<LPR>(s2));
         const float scale = sqrtf((float)D);
         float g[8];
         param8(io.p0, io.p0_dt, (int64_t)hh[r] * D + lane * 8, 1.f, g);
@@ -328,7 +327,7 @@ __global__ __launch_bounds__(256) void head_kernel_any(HeadParams p) {
       const float c = load1<T>(io.x, xo + j) - mean;
       s2 += c * c;
     }
-    rs = 1.0f / sqrtf(wave_sum(s2) * (1.0f / (float)D) + p.eps);
+    rs = rsqrt_f32(wave_sum(s2) * (1.0f / (float)D) + p.eps);
   } else if constexpr (NORM == HN_RMS || NORM == HN_L2) {
     float s2 = 0.f;
     for (int64_t j = lane; j < D; j += 64) {
@@ -336,9 +335,9 @@ __global__ __launch_bounds__(256) void head_kernel_any(HeadParams p) {
       s2 += v * v;
     }
     if constexpr (NORM == HN_RMS) {
-      rs = 1.0f / sqrtf(wave_sum(s2) * (1.0f / (float)D) + p.eps);
+      rs = rsqrt_f32(wave_sum(s2) * (1.0f / (float)D) + p.eps);
     } else {
-      rs = 1.0f / fminf(fmaxf(sqrtf(wave_sum(s2)), 1e-12f), 1.0e30f);
+      rs = l2_rnorm(wave_sum(s2));
     }
   }
   auto normed = [&](int64_t j) -> float {

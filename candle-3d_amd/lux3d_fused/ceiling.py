@@ -1,0 +1,132 @@
+"""Per-op bandwidth ceilings for bench.py: copy kernels that move exactly an
+op's activation bytes with no arithmetic (liblux3d_ceiling.so, built from
+csrc/ceiling.hip), timed like the op itself (graph replay, rotation sets
+larger than the 256 MB Infinity Cache).
+
+Two ceilings per op:
+- `copy`: the same bytes as plain contiguous streams (as many input and
+  output streams as the op has), one 16-byte chunk per thread per stream;
+- `pattern`: the op's own access pattern (the row kernels' rows / threads
+  per row / chunks per thread, or the head kernels' strided [B, H, N, D]
+  views and workgroup shape), also without arithmetic.
+The op's pattern is a dict on its Workload (`Workload.pattern`).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "liblux3d_ceiling.so")
+MALL_BYTES = 256 << 20
+
+
+def _load():
+    import torch  # noqa: F401  (bind to the HIP runtime torch loaded)
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run `make -C candle-3d_amd`")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    PP = ctypes.POINTER(ctypes.c_void_p)
+    lib.lux3d_ceiling_streams.argtypes = [PP, I, PP, I, I64, I64, P]
+    lib.lux3d_ceiling_rows.argtypes = [PP, I, PP, I, I64, I64, I, I, I, P]
+    lib.lux3d_ceiling_heads.argtypes = [P, P, P, P, I64, I64, I64, I64, I, ctypes.POINTER(I64),
+                                        ctypes.POINTER(I64), I, P]
+    for f in (lib.lux3d_ceiling_streams, lib.lux3d_ceiling_rows, lib.lux3d_ceiling_heads):
+        f.restype = ctypes.c_int
+    return lib
+
+
+LIB = _load()
+
+
+def _ptrs(ts):
+    arr = (ctypes.c_void_p * len(ts))()
+    for i, t in enumerate(ts):
+        arr[i] = t.data_ptr()
+    return arr
+
+
+def _sets(bytes_per_set: int) -> int:
+    return int(min(64, max(2, math.ceil(3 * MALL_BYTES / max(bytes_per_set, 1)))))
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: ceiling kernel rejected its arguments (status {rc})")
+
+
+class Copy:
+    """A copy workload: `launch(i)` enqueues one copy on rotation set i % sets
+    on the current stream; `bytes` is what it moves (read + written)."""
+
+    def __init__(self, dev, pattern: dict, same_size: bool):
+        self.dev = dev
+        kind = pattern["kind"]
+        stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+        if kind == "rows" and not same_size:
+            nin, nout, rows, rb = pattern["nin"], pattern["nout"], pattern["rows"], pattern["row_bytes"]
+            per_set = (nin + nout) * rows * rb
+            n = _sets(per_set)
+            bufs = [([torch.empty(rows * rb, dtype=torch.uint8, device=dev).fill_(k + 1) for _ in range(nin)],
+                     [torch.empty(rows * rb, dtype=torch.uint8, device=dev) for _ in range(nout)]) for k in range(n)]
+            args = [(_ptrs(i), _ptrs(o)) for i, o in bufs]
+
+            def launch(i):
+                a = args[i % n]
+                _check(LIB.lux3d_ceiling_rows(a[0], nin, a[1], nout, rows, rb, pattern["eb"], pattern["tpr"],
+                                              int(pattern.get("row_per_block", False)), stream()), "rows")
+            self.bytes = per_set
+        elif kind == "heads" and not same_size:
+            B, H, N, D, eb = pattern["B"], pattern["H"], pattern["N"], pattern["D"], pattern["eb"]
+            ntens = pattern["ntens"]
+            # the input views live in a buffer of `in_numel` elements (e.g. the packed qkv)
+            in_numel, ins, outs = pattern["in_numel"], pattern["in_strides"], pattern["out_strides"]
+            in_off = pattern["in_offsets"]          # element offset of each tensor's view in the buffer
+            per_set = in_numel * eb + ntens * B * H * N * D * eb
+            n = _sets(per_set)
+            bufs = [(torch.empty(in_numel * eb, dtype=torch.uint8, device=dev).fill_(k + 1),
+                     [torch.empty(B * H * N * D * eb, dtype=torch.uint8, device=dev) for _ in range(ntens)])
+                    for k in range(n)]
+            si = (ctypes.c_int64 * 3)(*ins)
+            so = (ctypes.c_int64 * 3)(*outs)
+
+            def launch(i):
+                src, dst = bufs[i % n]
+                q = src.data_ptr() + in_off[0] * eb
+                k = src.data_ptr() + in_off[1] * eb if ntens == 2 else None
+                _check(LIB.lux3d_ceiling_heads(q, k, dst[0].data_ptr(), dst[1].data_ptr() if ntens == 2 else None,
+                                               B, H, N, D, eb, si, so, int(pattern.get("both_in_one", False)),
+                                               stream()), "heads")
+            self.bytes = 2 * ntens * B * H * N * D * eb
+        else:
+            nin, nout = pattern["nin"], pattern["nout"]
+            ib, ob = pattern["in_bytes"], pattern["out_bytes"]
+            per_set = nin * ib + nout * ob
+            n = _sets(per_set)
+            bufs = [([torch.empty(ib, dtype=torch.uint8, device=dev).fill_(k + 1) for _ in range(nin)],
+                     [torch.empty(ob, dtype=torch.uint8, device=dev) for _ in range(nout)]) for k in range(n)]
+            args = [(_ptrs(i), _ptrs(o)) for i, o in bufs]
+
+            def launch(i):
+                a = args[i % n]
+                _check(LIB.lux3d_ceiling_streams(a[0], nin, a[1], nout, ib, ob, stream()), "streams")
+            self.bytes = per_set
+        self.launch = launch
+        self.sets = n
+        self._keep = bufs
+
+
+def same_size_streams(pattern: dict) -> dict:
+    """The op's activation bytes as contiguous streams (same stream counts)."""
+    kind = pattern["kind"]
+    if kind == "rows":
+        b = pattern["rows"] * pattern["row_bytes"]
+        return {"kind": "streams", "nin": pattern["nin"], "nout": pattern["nout"], "in_bytes": b, "out_bytes": b}
+    if kind == "heads":
+        b = pattern["B"] * pattern["H"] * pattern["N"] * pattern["D"] * pattern["eb"]
+        nt = pattern["ntens"]
+        return {"kind": "streams", "nin": nt, "nout": nt, "in_bytes": b, "out_bytes": b}
+    return dict(pattern)

@@ -1,8 +1,20 @@
 """Turn rocprofv3 CSV output into the short text summaries kept in profiles/.
 
   python -m lux3d_fused.rocprof_summary stats <kernel_stats.csv> "<command>" > profiles/<name>.md
+  python -m lux3d_fused.rocprof_summary trace <kernel_stats.csv> <kernel-substring> <bytes> "<command>" \
+        > profiles/kernel_trace_<op>.md
   python -m lux3d_fused.rocprof_summary traffic <fetch.csv> <write.csv> <cal_fetch.csv> <cal_write.csv> \
         <kernel-substring> "<command>" > profiles/<name>.md
+  python -m lux3d_fused.rocprof_summary counters <counter_collection.csv> <kernel-substring> "<command>" \
+        > profiles/<name>.md
+
+`trace` reports the kernels whose name contains <kernel-substring> (the op's
+own kernels; the workload set-up kernels are listed apart), each with its
+average duration and the achieved bandwidth for <bytes> algorithmic bytes
+per launch, in a JSON block that bench.py reads back.
+`counters` reports the median per-dispatch value of every counter in the
+file for the matching kernels, and per-wavefront instruction counts when
+SQ_WAVES was collected.
 
 `traffic` reports the per-dispatch HBM bytes of the kernels whose name
 contains <kernel-substring>, with FETCH_SIZE and WRITE_SIZE (KiB per
@@ -13,6 +25,10 @@ import csv
 import json
 import statistics
 import sys
+
+
+NOTE = ("`$REPO` is the repository root; this file is `python -m lux3d_fused.rocprof_summary` (run from "
+        "`candle-3d_amd/`) of the CSV that command writes.")
 
 
 def _rows(path):
@@ -31,6 +47,64 @@ def stats(path, command):
             name = name[:107] + "..."
         out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
                    f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(out) + "\n"
+
+
+def trace(path, kernel_sub, nbytes, command):
+    rows = _rows(path)
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    mine = [r for r in rows if kernel_sub in r["Name"]]
+    rest = [r for r in rows if kernel_sub not in r["Name"]]
+    nbytes = int(nbytes)
+    res = {"bytes_per_launch": nbytes, "kernels": []}
+    for r in mine:
+        avg = float(r["AverageNs"]) / 1e3
+        res["kernels"].append({"name": r["Name"], "calls": int(r["Calls"]), "avg_us": round(avg, 3),
+                               "min_us": round(float(r["MinNs"]) / 1e3, 3),
+                               "max_us": round(float(r["MaxNs"]) / 1e3, 3),
+                               "gbs": round(nbytes / avg / 1e3, 1), "frac_of_8tbs": round(nbytes / avg / 8e6, 4)})
+    out = ["# rocprofv3 kernel trace", "", f"Command: `{command}`", "", NOTE, "",
+           f"Kernels matching `{kernel_sub}` (the op's own launches, all on cold rotation sets); "
+           f"bandwidth = {nbytes:,} algorithmic bytes per launch / average duration.", "",
+           "| kernel | calls | avg us | min us | max us | GB/s | of 8 TB/s |", "|---|---|---|---|---|---|---|"]
+    for k in res["kernels"]:
+        name = k["name"].replace("|", "/")
+        out.append(f"| `{name[:110]}` | {k['calls']} | {k['avg_us']:.3f} | {k['min_us']:.3f} | {k['max_us']:.3f} | "
+                   f"{k['gbs']:,.1f} | {k['frac_of_8tbs']:.4f} |")
+    if rest:
+        out += ["", "Other kernels in the process (workload set-up):", ""]
+        for r in rest[:6]:
+            out.append(f"- `{r['Name'][:90]}`: {r['Calls']} calls, {float(r['AverageNs']) / 1e3:.3f} us avg")
+    out += ["", "```json", json.dumps(res, indent=1), "```"]
+    return "\n".join(out) + "\n"
+
+
+def counters(path, kernel_sub, command):
+    vals = {}
+    for r in _rows(path):
+        if kernel_sub not in r["Kernel_Name"]:
+            continue
+        vals.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    res = {}
+    for name, cs in vals.items():
+        med = {c: statistics.median(v) for c, v in cs.items()}
+        d = {"dispatches": max(len(v) for v in cs.values()), "median_per_dispatch": med}
+        waves = med.get("SQ_WAVES")
+        if waves:
+            d["per_wavefront"] = {c: round(v / waves, 2) for c, v in med.items() if c.startswith("SQ_INSTS")}
+        if med.get("SQ_BUSY_CYCLES") and med.get("SQ_WAVE_CYCLES"):
+            d["wave_cycles_over_busy_cycles"] = round(med["SQ_WAVE_CYCLES"] / med["SQ_BUSY_CYCLES"], 2)
+        res[name] = d
+    out = ["# rocprofv3 counters (median per dispatch)", "", f"Command: `{command}`", "", NOTE, ""]
+    for name, d in res.items():
+        out += [f"Kernel `{name[:120]}` ({d['dispatches']} dispatches):", "",
+                "| counter | median per dispatch |", "|---|---|"]
+        for c, v in sorted(d["median_per_dispatch"].items()):
+            out.append(f"| {c} | {v:,.0f} |")
+        if "per_wavefront" in d:
+            out += ["", "Per wavefront: " + ", ".join(f"{c} {v}" for c, v in d["per_wavefront"].items())]
+        out.append("")
+    out += ["```json", json.dumps(res, indent=1), "```"]
     return "\n".join(out) + "\n"
 
 
@@ -62,7 +136,7 @@ def traffic(fetch, write, cal_fetch, cal_write, kernel_sub, command):
         res["kernels"][name] = {"read_bytes": int(fk), "write_bytes": int(wk), "hbm_bytes": int(fk + wk),
                                 "dispatches": len(f[name])}
     lines = ["# HBM traffic per dispatch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
-             f"Command: `{command}`", "",
+             f"Command: `{command}`", "", NOTE, "",
              f"Calibration: `{cal_name}` (1 GiB read + 1 GiB written) reads FETCH_SIZE x{f_scale:.4f}, "
              f"WRITE_SIZE x{w_scale:.4f} of the true bytes; the factors below are applied.", "",
              "| kernel | dispatches | read bytes | write bytes | total |", "|---|---|---|---|---|"]
@@ -76,6 +150,10 @@ def traffic(fetch, write, cal_fetch, cal_write, kernel_sub, command):
 def main(argv):
     if argv[0] == "stats":
         sys.stdout.write(stats(argv[1], argv[2]))
+    elif argv[0] == "trace":
+        sys.stdout.write(trace(*argv[1:5]))
+    elif argv[0] == "counters":
+        sys.stdout.write(counters(*argv[1:4]))
     elif argv[0] == "traffic":
         sys.stdout.write(traffic(*argv[1:7]))
     else:

@@ -37,6 +37,10 @@ class Workload:
     flops: int = 0       # matrix-core work per launch (GEMMs); 0 for streaming ops
     reps: int = 0        # launches per timing graph (0: chosen from the byte count)
     peak_tflops: float = 0.0  # matrix peak the flops are priced against (0: dense bf16)
+    # access pattern for the copy ceilings (ceiling.py): the layout the
+    # launcher picks at this shape (rows / threads per row), the head views,
+    # or plain streams; None for latency-bound and matrix-core ops
+    pattern: dict = None
 
 
 def _cur() -> int:
@@ -92,6 +96,9 @@ def cfg0_layer_norm(dev) -> Workload:
         k = i % n
         _lib.call("lux3d_layer_norm", dx[k], dw, db, 1e-6, dy[k], _cur())
     wl = Workload("layer_norm", 0, "row_kernel<F32,LN>", "f32", nbytes, f"[{rows},{d}]", launch, n)
+    # < 2048 rows: one row per workgroup of 128 threads, one 32-byte chunk each
+    wl.pattern = {"kind": "rows", "nin": 1, "nout": 1, "rows": rows, "row_bytes": d * 4, "eb": 4, "tpr": 128,
+                  "row_per_block": True}
     wl._keep = (xs, ys, w, b, dx, dy, dw, db)
     return wl
 
@@ -121,6 +128,10 @@ def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps) -> Workload:
     name = "residual_layer_norm"
     wl = Workload(name, cfg, "row_kernel<RESID_LN>", "bf16" if dt == torch.bfloat16 else "f32", nbytes,
                   str(list(shape)), launch, n)
+    rows = x0.numel() // d
+    # 128 threads per row, one chunk each (d = 1024); a row per workgroup below 2048 rows
+    wl.pattern = {"kind": "rows", "nin": 2, "nout": 2, "rows": rows, "row_bytes": d * esz, "eb": esz, "tpr": 128,
+                  "row_per_block": rows < 2048}
     wl._keep = (xs, as_, hs, ys, g, w, b, D, dg, dw, dbb)
     return wl
 
@@ -169,6 +180,9 @@ def cfg1_qk_layernorm_rope2d(dev, tables: bool = False) -> Workload:
                       _cur())
     name = "qk_layernorm_rope2d" + ("_tables" if tables else "")
     wl = Workload(name, 1, "head_kernel<BF16,64,LN,R1>", "bf16", nbytes, f"q,k [{B},{H},{N},{D}] in qkv", launch, n)
+    wl.pattern = {"kind": "heads", "B": B, "H": H, "N": N, "D": D, "eb": 2, "ntens": 2, "both_in_one": False,
+                  "in_numel": B * N * 3 * H * D, "in_offsets": [0, H * D],
+                  "in_strides": [N * 3 * H * D, D, 3 * H * D], "out_strides": [H * N * D, N * D, D]}
     wl._keep = (qkvs, outs, Ds, qw, qb, kw, kb, pos, emb, dqw, dqb, dkw, dkb, dpos, dc, ds)
     return wl
 
@@ -224,6 +238,10 @@ def _modulate(dev, cfg, rows_per_seg, C, gate_only=False) -> Workload:
     name = ("gated_residual" if gate_only else "adaln_modulate") + ("_ragged" if ragged else "")
     kern = "row_kernel<BF16,GATE>" if gate_only else "row_kernel<BF16,MODULATE>"
     wl = Workload(name, cfg, kern, "bf16", nbytes, f"[{rows},{C}] segs {list(rows_per_seg)}", launch, n)
+    # one wavefront per row; the gate without a base vector on 4 wavefronts when a row is 256 chunks
+    tpr = 256 if gate_only and C // 8 == 256 else 64
+    wl.pattern = {"kind": "rows", "nin": 2 if gate_only else 1, "nout": 1, "rows": rows, "row_bytes": C * 2,
+                  "eb": 2, "tpr": tpr}
     wl._keep = (xs, hs, ys, shift, scale, gate, offs, dx, dh, dy, dsh, dsc, dg, do)
     return wl
 
@@ -288,6 +306,7 @@ def _gated_modulate(dev, cfg, rows_per_seg, C, two_launches=False) -> Workload:
             else "row_kernel<BF16,GATE_MOD>")
     wl = Workload(name, cfg, kern, "bf16", nbytes, f"[{rows},{C}] segs {list(rows_per_seg)}", launch, n,
                   "two launches, priced at the fused op's bytes" if two_launches else "")
+    wl.pattern = {"kind": "rows", "nin": 2, "nout": 2, "rows": rows, "row_bytes": C * 2, "eb": 2, "tpr": 64}
     wl._keep = (xs, hs, xos, ys, t_emb, modulation, pieces, base, offs, D, dg, dsh, dsc, dbg, dbsh, dbsc, do)
     return wl
 
@@ -325,6 +344,9 @@ def cfg2_rms_norm_heads(dev) -> Workload:
         _lib.call("lux3d_rms_norm_heads", dq, dwq, dk, dwk, 1e-6, dqo, dko, _cur())
     wl = Workload("rms_norm_heads", 2, "head_kernel<BF16,128,RMS>", "bf16", nbytes,
                   f"q,k [{B},{H},{L},{D}] in qkv", launch, n)
+    wl.pattern = {"kind": "heads", "B": B, "H": H, "N": L, "D": D, "eb": 2, "ntens": 2, "both_in_one": True,
+                  "in_numel": B * L * H * 3 * D, "in_offsets": [0, D],
+                  "in_strides": [L * H * 3 * D, 3 * D, H * 3 * D], "out_strides": [H * L * D, L * D, D]}
     wl._keep = (qkvs, outs, Ds, wq, wk, dwq, dwk)
     return wl
 
@@ -344,6 +366,7 @@ def _act(dev, name, entry) -> Workload:
         k = i % n
         _lib.call(entry, dx[k], dy[k], _cur())
     wl = Workload(name, 2, f"act_kernel<BF16,{name}>", "bf16", nbytes, str(list(shape)), launch, n)
+    wl.pattern = {"kind": "streams", "nin": 1, "nout": 1, "in_bytes": nbytes // 2, "out_bytes": nbytes // 2}
     wl._keep = (xs, ys, dx, dy)
     return wl
 
@@ -386,6 +409,9 @@ def cfg3_qk_l2norm_rope3d(dev) -> Workload:
         _lib.call("lux3d_qk_l2norm_rope3d", dq, dgq, dk, dgk, None, None, dcd, 10000.0, dqo, dko, _cur())
     wl = Workload("qk_l2norm_rope3d_ragged", 3, "head_kernel<BF16,128,L2,R2>", "bf16", nbytes,
                   f"q,k [1,{N},{H},{D}] in qkv, coords [{N},3]", launch, n)
+    wl.pattern = {"kind": "heads", "B": 1, "H": H, "N": N, "D": D, "eb": 2, "ntens": 2, "both_in_one": True,
+                  "in_numel": N * 3 * H * D, "in_offsets": [0, H * D],
+                  "in_strides": [N * 3 * H * D, D, 3 * H * D], "out_strides": [N * H * D, D, H * D]}
     wl._keep = (qkvs, outs, Ds, gq, gk, cd, dgq, dgk, dcd)
     return wl
 
@@ -406,6 +432,7 @@ def cfg4_dequant_q8_0(dev) -> Workload:
         k = i % n
         _lib.call("lux3d_dequant_q8_0", db[k], dy[k], _cur())
     wl = Workload("dequant_q8_0", 4, "dequant_q8_0_kernel<BF16>", "u8->bf16", nbytes, f"[{rows},{cols}]", launch, n)
+    wl.pattern = {"kind": "streams", "nin": 1, "nout": 1, "in_bytes": nb * 34, "out_bytes": rows * cols * 2}
     wl._keep = (bs, ys, db, dy)
     return wl
 
@@ -431,6 +458,9 @@ def cfg4_dinov3_rope(dev) -> Workload:
         dq, dk, dqo, dko = Ds[i % n]
         _lib.call("lux3d_dinov3_rope", dq, dk, dc, dsn, 5, dqo, dko, _cur())
     wl = Workload("dinov3_rope", 4, "head_kernel<F32,64,R3>", "f32", nbytes, f"q,k [{B},{H},{S},{D}]", launch, n)
+    wl.pattern = {"kind": "heads", "B": B, "H": H, "N": S, "D": D, "eb": 4, "ntens": 2, "both_in_one": False,
+                  "in_numel": 2 * B * S * H * D, "in_offsets": [0, B * S * H * D],
+                  "in_strides": [S * H * D, D, H * D], "out_strides": [H * S * D, S * D, D]}
     wl._keep = (qs, ks, outs, Ds, cos, sin, dc, dsn)
     return wl
 
