@@ -29,14 +29,15 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 //   erfc(z) = t * exp(-z^2 + P(t)),  t = 1 / (1 + z/2),
 // a relative error bound for every z >= 0 (so the GELU tail x*Phi(x) keeps
 // its accuracy). DEG 9: their Chebyshev-fitted coefficients, fractional
-// error below 1.2e-7 in exact arithmetic and 3.6e-7 evaluated in f32 (f32
-// outputs). DEG 7 / 5: lower-degree fits of the same
+// error below 1.2e-7 in exact arithmetic and 3.6e-7 evaluated as below with a
+// two-part exponent argument (f32 outputs). DEG 7 / 5: lower-degree fits of the same
 // form, made here by iteratively reweighted least squares on 20,001
-// Chebyshev nodes of t in (0, 1] against P(t) = log(erfcx(z)) - log(t);
-// evaluated in f32 they keep the relative error of erfc below 2.7e-6 and
-// 5.1e-5 over z in [0, 9] (checked against scipy's erfc), 1/180 and 1/40 of
-// a half-ulp of f16 and bf16, the outputs they serve. One v_rcp_f32, DEG
-// FMAs and one v_exp_f32 per element.
+// Chebyshev nodes of t in (0, 1] against P(t) = log(erfcx(z)) - log(t).
+// Evaluated in f32 as below (the exponent argument rounded to f32 before
+// v_exp_f32) they keep the relative error of erfc below 8.2e-6 (DEG 7) and
+// 5.5e-5 (DEG 5) over z in [0, 9], against scipy's erfc: 1/60 and 1/35 of a
+// half-ulp of f16 and bf16, the outputs they serve. One v_rcp_f32, DEG FMAs
+// and one v_exp_f32 per element (DEG 9 adds the two-part argument).
 template <int DEG>
 __device__ __forceinline__ float erfc_nonneg(float z) {
   const float t = fast_rcp(fmaf(0.5f, z, 1.0f));
@@ -71,6 +72,25 @@ __device__ __forceinline__ float erfc_nonneg(float z) {
     p = fmaf(p, t, -1.26556265f);
   }
   constexpr float log2e = 1.4426950408889634f;
+  if constexpr (DEG == 9) {
+    // f32 outputs: -z^2 + P and its product with log2(e) are carried in two
+    // parts, because rounding an argument near -102 to f32 before the exp2
+    // costs up to 7.5e-6 relative. z^2 = hi + lo exactly (FMA remainder); the
+    // sum P - hi is split by TwoSum; n = rint(a * log2(e)) is taken out and
+    // the small remainder r is formed with FMAs (log2(e) = L2E + L2E_LO), so
+    // erfc = t * 2^r * 2^n keeps the fit's accuracy (3.6e-7).
+    constexpr float L2E_LO = 1.925963033500011e-8f;  // log2(e) - L2E
+    const float hi = z * z, lo = fmaf(z, z, -hi);
+    const float a = p - hi;                          // TwoSum(p, -hi) = a + ae exactly
+    const float bb = a - p;
+    const float ae = (p - (a - bb)) + (-hi - bb);
+    const float a_lo = ae - lo;
+    const float n = __builtin_rintf(a * log2e);
+    float r = fmaf(a, log2e, -n);
+    r = fmaf(a, L2E_LO, r);
+    r = fmaf(a_lo, log2e, r);
+    return t * __builtin_ldexpf(fast_exp2(r), (int)n);
+  }
   return t * fast_exp2(fmaf(-z, z, p) * log2e);
 }
 
@@ -79,17 +99,24 @@ template <typename T> constexpr int erfc_deg() { return T::code == LUX3D_F32 ? 9
 
 template <int ACT, int ERFC_DEG = 9> __device__ __forceinline__ float act(float x) {
   if constexpr (ACT == ACT_GELU_TANH) {
-    // 0.5*x*(1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi)*x*(1 + 0.044715*x^2):
-    // the sigmoid form has no cancellation for x << 0.
-    constexpr float k = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2*sqrt(2/pi)*log2(e)
-    const float u = x * (1.0f + 0.044715f * x * x);
-    return x * fast_rcp(1.0f + fast_exp2(k * u));
+    // candle's f32 Gelu: 0.5*x*(1 + tanh(a)), a = sqrt(2/pi)*x*(1 + 0.044715*x^2).
+    // tanh(a) = sign(a)*(1 - 2/(1 + exp(2|a|))): near |tanh| = 1 the f32
+    // subtraction rounds exactly as the f32 tanh result does, so 1 + tanh(a)
+    // cancels as the reference's does (to exactly 0 for a < -9.01) and the
+    // negative tail matches the reference instead of the true (tiny) value.
+    constexpr float k2 = 2.0f * 1.4426950408889634f;  // 2*log2(e)
+    const float a = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
+    const float m = 1.0f - 2.0f * fast_rcp(1.0f + fast_exp2(k2 * fabsf(a)));  // tanh(|a|)
+    return 0.5f * x * (1.0f + __builtin_copysignf(m, a));
   } else if constexpr (ACT == ACT_GELU_ERF) {
-    // 0.5*x*(1 + erf(x/sqrt2)) evaluated through erfc(|x|/sqrt2), which keeps
-    // full relative accuracy in the negative tail (x*Phi(x) -> 0).
-    const float e = erfc_nonneg<ERFC_DEG>(fabsf(x) * 0.7071067811865476f);
-    const float h = 0.5f * x * e;
-    return x >= 0.f ? x - h : h;
+    // 0.5*x*(1 + erf(x/sqrt2)) through q = erfc(|x|/sqrt2). For x < 0 the
+    // reference forms 1 + erf(z) in f64, where erf(z) = -1 + q is rounded to
+    // the f64 grid near -1 (spacing 2^-53): 1 + erf(z) is q rounded to a
+    // multiple of 2^-53 (a no-op for q >= 2^-30, exactly 0 below 2^-54), which
+    // is applied here so the negative tail matches the reference.
+    const float q = erfc_nonneg<ERFC_DEG>(fabsf(x) * 0.7071067811865476f);
+    if (x >= 0.f) return x - 0.5f * x * q;
+    return x * (__builtin_rintf(q * 0x1p53f) * 0x1p-54f);
   } else {
     constexpr float k = -1.4426950408889634f;  // -log2(e)
     return x * fast_rcp(1.0f + fast_exp2(k * x));

@@ -22,9 +22,54 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (ROCm device); run with -m gpu")
 
 
+# Every comparison made through the helpers below is recorded here: the
+# element count, the worst error, and how many elements passed only through
+# the absolute floor (bf16 / f16: beyond the ulp bound; f32: beyond 1e-5 of
+# |want|). pytest prints the table at the end of the run.
+PARITY_LOG = []
+
+
+def _record(kind, what, n, worst, n_floor):
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    PARITY_LOG.append((test, what, kind, int(n), worst, int(n_floor)))
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    if not PARITY_LOG:
+        return
+    tr = terminalreporter
+    tr.section("parity: elements held to the absolute floor")
+    tot = sum(r[3] for r in PARITY_LOG)
+    fl = sum(r[5] for r in PARITY_LOG)
+    tr.write_line(f"{len(PARITY_LOG)} comparisons, {tot:,} elements, {fl:,} passed only through the floor "
+                  f"({fl / max(tot, 1):.2e} of all)")
+    for test, what, kind, n, worst, n_floor in PARITY_LOG:
+        if n_floor:
+            tr.write_line(f"  {test} [{what}] {kind}: {n_floor} of {n:,} ({n_floor / max(n, 1):.2e}), "
+                          f"worst {worst}")
+
+
 BF16_ULP_TOL = 2
 BF16_ATOL_REL = 2.0 ** -17
 F32_REL_TOL = 1e-5
+# How many elements of one comparison may pass only through the absolute
+# floor: bf16 / f16 beyond the ulp bound, f32 beyond 1e-5 of |want|. Measured
+# on MI355X across the GPU suite: at most 5e-6 of the elements for every
+# bf16 / f16 op (cancellation results n*w + b ~ 0, rotations re*c - im*s ~
+# 0); for f32 LayerNorm-type outputs 1e-3 to 2.7e-3 between the GPU and the
+# oracle and up to 7.9e-3 between the oracle and torch in f64: an output
+# |y| < ~6e-3 of a sum of O(1) terms cannot hold 1e-5 of itself in f32. A
+# comparison may always hold 2 elements to the floor (small edge-case tests).
+BF16_FLOOR_FRAC = 1e-5
+F32_FLOOR_FRAC = 1e-2
+FLOOR_MIN_ALLOW = 2
+
+
+def _check_floor(kind, what, n, n_floor, floor_frac):
+    frac = floor_frac if floor_frac is not None else (F32_FLOOR_FRAC if kind == "f32" else BF16_FLOOR_FRAC)
+    allowed = max(FLOOR_MIN_ALLOW, int(frac * n))
+    assert n_floor <= allowed, (f"{what}: {n_floor} of {n} elements pass only through the absolute floor "
+                                f"(allowed {allowed}: {frac:g} of the elements)")
 
 
 def bf16_ordered(bits: np.ndarray) -> np.ndarray:
@@ -40,7 +85,8 @@ def ulp_distance16(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
     return np.abs(bf16_ordered(a) - bf16_ordered(b))
 
 
-def assert_bf16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL, f16=False):
+def assert_bf16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL, f16=False,
+                      floor_frac=None):
     """bf16/f16 parity: every element within `tol` ulp of the oracle, except
     where the oracle's value is far below bf16's resolution at the tensor's
     scale. There (outputs produced by cancellation, e.g. n*w + b ~ 0 or a
@@ -60,8 +106,11 @@ def assert_bf16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=B
     g, w = got[~nan_g], want[~nan_w]
     d = ulp_distance16(g, w)
     worst = int(d.max()) if d.size else 0
+    n_floor = int((d > tol).sum())
+    _record("f16" if f16 else "bf16", what, got.size, f"{worst} ulp", n_floor)
     if worst <= tol:
         return worst
+    _check_floor("bf16", what, got.size, n_floor, floor_frac)
     bad = d > tol
     gf = _bits_to_f32(g[bad], f16)
     wf = _bits_to_f32(w[bad], f16)
@@ -83,11 +132,11 @@ def _bits_to_f32(b, f16=False):
     return (b.astype(np.uint32) << 16).view(np.float32)
 
 
-def assert_f16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL):
-    return assert_bf16_close(got_bits, want_bits, tol, what, atol_rel, f16=True)
+def assert_f16_close(got_bits, want_bits, tol=BF16_ULP_TOL, what="", atol_rel=BF16_ATOL_REL, floor_frac=None):
+    return assert_bf16_close(got_bits, want_bits, tol, what, atol_rel, f16=True, floor_frac=floor_frac)
 
 
-def assert_f32_close(got, want, rel=F32_REL_TOL, what=""):
+def assert_f32_close(got, want, rel=F32_REL_TOL, what="", floor_frac=None):
     got = np.asarray(got, dtype=np.float32).reshape(-1)
     want = np.asarray(want, dtype=np.float32).reshape(-1)
     assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
@@ -98,7 +147,10 @@ def assert_f32_close(got, want, rel=F32_REL_TOL, what=""):
     err = np.abs(got[ok].astype(np.float64) - want[ok].astype(np.float64))
     bound = rel * np.maximum(np.abs(want[ok].astype(np.float64)), scale)
     worst = float((err / np.maximum(np.abs(want[ok]), scale)).max()) if err.size else 0.0
+    n_floor = int((err > rel * np.abs(want[ok].astype(np.float64))).sum())
+    _record("f32", what, got.size, f"{worst:.2e} rel", n_floor)
     assert np.all(err <= bound), f"{what}: max relative error {worst:.3e} > {rel:g}"
+    _check_floor("f32", what, got.size, n_floor, floor_frac)
     return worst
 
 
@@ -111,7 +163,7 @@ def bf16_bits_from_f64(want) -> np.ndarray:
     return np.where(np.isnan(f), ((u >> 16) | 0x40).astype(np.uint16), r)
 
 
-def assert_vs_f64(got, want64, dt: str, what="", rel=F32_REL_TOL):
+def assert_vs_f64(got, want64, dt: str, what="", rel=F32_REL_TOL, floor_frac=None):
     """Output against a float64 expectation from the golden fixtures: f32
     within `rel` of max(|want|, RMS(want)); bf16 (uint16 bits) within 2 ulp of
     the expectation's bf16 rounding, with the absolute floor of
@@ -124,12 +176,16 @@ def assert_vs_f64(got, want64, dt: str, what="", rel=F32_REL_TOL):
         scale = max(float(np.sqrt(np.mean(w ** 2))) if w.size else 1.0, 1e-30)
         bound = rel * np.maximum(np.abs(w), scale)
         err = np.abs(got - w)
+        n_floor = int((err > rel * np.abs(w)).sum())
+        _record("f32", what, w.size, f"{float((err / np.maximum(np.abs(w), scale)).max()) if w.size else 0:.2e} rel",
+                n_floor)
+        _check_floor("f32", what, w.size, n_floor, floor_frac)
         assert np.all(err <= bound), (
             f"{what}: max error {float((err / np.maximum(np.abs(w), scale)).max()):.3e} > {rel:g} (relative)")
         return
     if dt == "bf16":
-        return assert_bf16_close(got, bf16_bits_from_f64(want64), what=what)
+        return assert_bf16_close(got, bf16_bits_from_f64(want64), what=what, floor_frac=floor_frac)
     if dt == "f16":
         want_bits = np.asarray(want64, dtype=np.float16).view(np.uint16)
-        return assert_f16_close(got, want_bits, what=what)
+        return assert_f16_close(got, want_bits, what=what, floor_frac=floor_frac)
     raise ValueError(dt)

@@ -128,7 +128,9 @@ def test_rope2d_dinov3(dev, ops):
 def test_activations(dev, ops, name, fn):
     g = load("activations")
     y = getattr(ops, fn)(to_dev(g["x"], dev))
-    assert_vs_f64(host(y), g[name], "f32", name)
+    # the fixture is the exact f64 GELU; the kernel follows candle's f32 tanh
+    # form, which cancels for x < -3 (those tail elements hold only the floor)
+    assert_vs_f64(host(y), g[name], "f32", name, floor_frac=0.3 if name == "gelu_tanh" else None)
 
 
 @pytest.mark.parametrize("dim", [4, 256, 2048])

@@ -448,10 +448,14 @@ def test_activations_match_torch_f64(act):
     tf = {"gelu_erf": lambda t: F.gelu(t), "gelu_tanh": lambda t: F.gelu(t, approximate="tanh"),
           "silu": F.silu}[act]
     ref = tf(f64(x)).numpy()
-    assert_f32_close(fn(x), ref, what=act)
+    # candle's f32 Gelu 0.5*x*(1 + tanh(u)) cancels for x < -3 (1 + tanh(u)
+    # loses relative accuracy, and is exactly 0 below x = -5.3): against the
+    # exact f64 GELU those tail elements hold only the absolute floor
+    tail = 0.3 if act == "gelu_tanh" else None
+    assert_f32_close(fn(x), ref, what=act, floor_frac=tail)
     xb = orc.bf16_bits(x)
     refb = tf(f64(orc.bf16_to_f32(xb))).numpy()
-    assert_bf16_close(fn(xb, dt=orc.BF16), to_bf16_bits(refb), tol=1, what=act + " bf16")
+    assert_bf16_close(fn(xb, dt=orc.BF16), to_bf16_bits(refb), tol=1, what=act + " bf16", floor_frac=tail)
 
 
 # ---------------------------------------------------------------------------
