@@ -2,7 +2,7 @@
 
   python -m lux3d_fused.rocprof_summary stats <kernel_stats.csv> "<command>" > profiles/<name>.md
   python -m lux3d_fused.rocprof_summary trace <kernel_stats.csv> <kernel-substring> <bytes> "<command>" \
-        > profiles/kernel_trace_<op>.md
+        [<stdout of the profiled command>] > profiles/kernel_trace_<op>.md
   python -m lux3d_fused.rocprof_summary traffic <fetch.csv> <write.csv> <cal_fetch.csv> <cal_write.csv> \
         <kernel-substring> "<command>" > profiles/<name>.md
   python -m lux3d_fused.rocprof_summary counters <counter_collection.csv> <kernel-substring> "<command>" \
@@ -50,7 +50,18 @@ def stats(path, command):
     return "\n".join(out) + "\n"
 
 
-def trace(path, kernel_sub, nbytes, command):
+def _profiled_events(log_path):
+    """The HIP-event time per launch that `bench.py --profile` printed while
+    it ran under the profiler (its JSON line), or None."""
+    if not log_path:
+        return None
+    for line in open(log_path):
+        if line.startswith("{") and '"us_per_launch_graph"' in line:
+            return json.loads(line)["us_per_launch_graph"]
+    return None
+
+
+def trace(path, kernel_sub, nbytes, command, log_path=None):
     rows = _rows(path)
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
     mine = [r for r in rows if kernel_sub in r["Name"]]
@@ -71,6 +82,12 @@ def trace(path, kernel_sub, nbytes, command):
         name = k["name"].replace("|", "/")
         out.append(f"| `{name[:110]}` | {k['calls']} | {k['avg_us']:.3f} | {k['min_us']:.3f} | {k['max_us']:.3f} | "
                    f"{k['gbs']:,.1f} | {k['frac_of_8tbs']:.4f} |")
+    ev = _profiled_events(log_path)
+    if ev is not None:
+        res["events_us_under_profiler"] = ev
+        out += ["", f"The same launches timed with HIP events around the graph replays, inside the profiled run: "
+                    f"{ev:.3f} us per launch. Each traced dispatch carries the profiler's own per-dispatch cost; "
+                    f"bench.py's unprofiled graph timing of the same launches (its ops[].us) is lower by that cost."]
     if rest:
         out += ["", "Other kernels in the process (workload set-up):", ""]
         for r in rest[:6]:
@@ -151,7 +168,7 @@ def main(argv):
     if argv[0] == "stats":
         sys.stdout.write(stats(argv[1], argv[2]))
     elif argv[0] == "trace":
-        sys.stdout.write(trace(*argv[1:5]))
+        sys.stdout.write(trace(*argv[1:6]))
     elif argv[0] == "counters":
         sys.stdout.write(counters(*argv[1:4]))
     elif argv[0] == "traffic":
