@@ -501,13 +501,14 @@ int qk_rope2d_common(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor
     if (k->dtype != q->dtype) return fail(LUX3D_ERR_DTYPE, "%s: `k` dtype differs from `q`", fn);
     p.ntens = 2;
   }
-  const bool qn = p.io[0].p0_dt >= 0 || p.io[0].p1_dt >= 0;
-  const bool kn = p.ntens == 2 && (p.io[1].p0_dt >= 0 || p.io[1].p1_dt >= 0);
+  // LayerNorm when the weight is given; its bias is optional (a candle
+  // LayerNorm without bias); a bias without a weight is an error
+  const bool qn = p.io[0].p0_dt >= 0;
+  const bool kn = p.ntens == 2 && p.io[1].p0_dt >= 0;
   if (p.ntens == 2 && qn != kn) return fail(LUX3D_ERR_NULL, "%s: q and k must both be normalised or both not", fn);
-  if (qn && (p.io[0].p0_dt < 0 || p.io[0].p1_dt < 0))
-    return fail(LUX3D_ERR_NULL, "%s: LayerNorm needs both weight and bias", fn);
-  if (kn && (p.io[1].p0_dt < 0 || p.io[1].p1_dt < 0))
-    return fail(LUX3D_ERR_NULL, "%s: LayerNorm needs both weight and bias", fn);
+  if (p.io[0].p1_dt >= 0 && !qn) return fail(LUX3D_ERR_NULL, "%s: LayerNorm bias given without a weight", fn);
+  if (p.ntens == 2 && p.io[1].p1_dt >= 0 && !kn)
+    return fail(LUX3D_ERR_NULL, "%s: LayerNorm bias given without a weight", fn);
   if (qn && !(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
   norm = qn ? HN_LN : HN_NONE;
   p.B = qv.B; p.H = qv.H; p.N = qv.N; p.D = qv.D; p.eps = eps;
@@ -909,7 +910,7 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
   AttnParams p;
   int r;
   if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
-  if (!q_w || !q_b) return fail(LUX3D_ERR_NULL, "%s: LayerNorm needs both weight and bias", fn);
+  if (!q_w) return fail(LUX3D_ERR_NULL, "%s: LayerNorm needs a weight (the bias may be NULL)", fn);
   const void *wp, *bp;
   int wdt, bdt;
   if ((r = param_vec(q_w, p.D, fn, "q_w", wp, wdt)) || (r = param_vec(q_b, p.D, fn, "q_b", bp, bdt))) return r;
@@ -922,7 +923,8 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
     return fail(LUX3D_ERR_LAYOUT, "%s: cos_full and sin_alt_full must share layout and dtype", fn);
   // fused: the matrix-core path, and 16-byte aligned parameters and table rows
   const int tb = elem_bytes(cos_full->dtype);
-  const bool fused = p.mfma && q->dtype != LUX3D_F32 && (p.D == 64 || p.D == 128) && aligned16(wp) && aligned16(bp) &&
+  const bool fused = p.mfma && q->dtype != LUX3D_F32 && (p.D == 64 || p.D == 128) && aligned16(wp) &&
+                     (bdt < 0 || aligned16(bp)) &&
                      aligned16(cos_full->data) && aligned16(sin_alt_full->data) && (cN * tb) % 16 == 0 &&
                      (cB * tb) % 16 == 0;
   if (!fused) {
@@ -1003,12 +1005,14 @@ int contiguous_of(const lux3d_tensor_t *t, const char *fn, const char *name, int
 }  // namespace
 
 int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *keys, const lux3d_tensor_t *vals,
-                           const lux3d_tensor_t *nbr, lux3d_stream_t stream) {
+                           const lux3d_tensor_t *nbr, const lux3d_tensor_t *bad_coords, lux3d_stream_t stream) {
   const char *fn = "lux3d_sparse_neighbors";
   int r;
   if ((r = contiguous_of(coords, fn, "coords", LUX3D_I32, 2)) || (r = contiguous_of(keys, fn, "keys", LUX3D_I64, -1)) ||
       (r = contiguous_of(vals, fn, "vals", LUX3D_I32, -1)) || (r = contiguous_of(nbr, fn, "nbr", LUX3D_I32, 2)))
     return r;
+  if (bad_coords && ((r = contiguous_of(bad_coords, fn, "bad_coords", LUX3D_I32, -1)) || numel(bad_coords) < 1))
+    return r ? r : fail(LUX3D_ERR_SHAPE, "%s: bad_coords must hold one int32", fn);
   const int64_t n = coords->shape[0], cap = numel(keys);
   if (coords->shape[1] != 3) return fail(LUX3D_ERR_SHAPE, "%s: coords must be [N, 3]", fn);
   if (nbr->shape[0] != n || nbr->shape[1] != 27) return fail(LUX3D_ERR_SHAPE, "%s: nbr must be [%lld, 27]", fn,
@@ -1020,7 +1024,9 @@ int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *k
   if (n > INT32_MAX / 27) return fail(LUX3D_ERR_SHAPE, "%s: too many voxels", fn);
   return hip_status(launch_sparse_map(static_cast<const int32_t *>(coords->data), n,
                                       static_cast<unsigned long long *>(keys->data), static_cast<int32_t *>(vals->data),
-                                      cap, static_cast<int32_t *>(nbr->data), stream_of(stream)),
+                                      cap, static_cast<int32_t *>(nbr->data),
+                                      bad_coords ? static_cast<int32_t *>(bad_coords->data) : nullptr,
+                                      stream_of(stream)),
                     fn);
 }
 
@@ -1114,12 +1120,14 @@ int lux3d_sparse_conv3d_rulebook(const lux3d_tensor_t *x, const lux3d_tensor_t *
 }
 
 int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids, const lux3d_tensor_t *out,
-                            lux3d_stream_t stream) {
+                            const lux3d_tensor_t *bad_ids, lux3d_stream_t stream) {
   const char *fn = "lux3d_index_select_rows";
   int r;
   if ((r = contiguous_of(src, fn, "src", -1, -1)) || (r = contiguous_of(ids, fn, "ids", -1, 1)) ||
       (r = contiguous_of(out, fn, "out", src->dtype, src->rank)))
     return r;
+  if (bad_ids && ((r = contiguous_of(bad_ids, fn, "bad_ids", LUX3D_I32, -1)) || numel(bad_ids) < 1))
+    return r ? r : fail(LUX3D_ERR_SHAPE, "%s: bad_ids must hold one int32", fn);
   if (ids->dtype != LUX3D_I32 && ids->dtype != LUX3D_I64)
     return fail(LUX3D_ERR_DTYPE, "%s: ids must be int32 or int64", fn);
   if (out->shape[0] != ids->shape[0]) return fail(LUX3D_ERR_SHAPE, "%s: out must have one row per id", fn);
@@ -1129,7 +1137,8 @@ int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids
     row *= src->shape[i];
   }
   return hip_status(launch_gather_rows(src->data, src->shape[0], ids->data, ids->dtype == LUX3D_I64, ids->shape[0],
-                                       nullptr, out->data, row * elem_bytes(src->dtype), stream_of(stream)),
+                                       nullptr, out->data, row * elem_bytes(src->dtype),
+                                       bad_ids ? static_cast<int32_t *>(bad_ids->data) : nullptr, stream_of(stream)),
                     fn);
 }
 

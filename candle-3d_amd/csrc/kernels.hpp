@@ -146,7 +146,7 @@ hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
 // TRELLIS.2 sparse voxel ops.
 // Coordinate hash (cap: a power of two >= 2n) and neighbour table nbr [n, 27].
 hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
-                             int32_t *nbr, hipStream_t s);
+                             int32_t *nbr, int32_t *bad, hipStream_t s);
 struct SparseConvParams {
   const float *x = nullptr;       // [n, cin]
   const int32_t *nbr = nullptr;   // [n, 27]
@@ -165,7 +165,7 @@ hipError_t launch_sparse_conv_rulebook(const SparseConvParams &p, const int32_t 
 // out[m] = src[ids[m]] for m < rows (and m < *count when count is given);
 // rows of row_bytes bytes; ids out of range give zero rows.
 hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bool ids64, int64_t rows,
-                              const int32_t *count, void *out, int64_t row_bytes, hipStream_t s);
+                              const int32_t *count, void *out, int64_t row_bytes, int32_t *bad, hipStream_t s);
 struct C2SParams {
   const int32_t *coords = nullptr;  // [n, 3]
   const void *feats = nullptr;      // [n, C], rows of 8 children x child_row_bytes

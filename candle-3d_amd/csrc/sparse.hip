@@ -47,20 +47,27 @@ __device__ __forceinline__ uint64_t hash_key(unsigned long long k) {
   return h ^ (h >> 29);
 }
 
-__global__ __launch_bounds__(256) void map_clear_kernel(unsigned long long *keys, int32_t *vals, int64_t cap) {
+// bad (optional): the count of coordinates outside the packable range,
+// zeroed here and incremented by map_insert_kernel (the next launch).
+__global__ __launch_bounds__(256) void map_clear_kernel(unsigned long long *keys, int32_t *vals, int64_t cap,
+                                                        int32_t *bad) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < cap) {
     keys[i] = kEmptyKey;
     vals[i] = -1;
   }
+  if (bad && i == 0) *bad = 0;
 }
 
 __global__ __launch_bounds__(256) void map_insert_kernel(const int32_t *coords, int64_t n, unsigned long long *keys,
-                                                         int32_t *vals, int64_t cap) {
+                                                         int32_t *vals, int64_t cap, int32_t *bad) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const int32_t x = coords[3 * i], y = coords[3 * i + 1], z = coords[3 * i + 2];
-  if (!coord_ok(x, y, z)) return;
+  if (!coord_ok(x, y, z)) {  // neither inserted nor found: counted
+    if (bad) atomicAdd(bad, 1);
+    return;
+  }
   const unsigned long long key = pack_coord(x, y, z);
   uint64_t slot = hash_key(key) & (uint64_t)(cap - 1);
   for (int64_t probe = 0; probe < cap; ++probe) {  // cap >= 2n: a free slot exists
@@ -448,14 +455,18 @@ __global__ __launch_bounds__(256) void sparse_conv_generic_kernel(SparseConvPara
 // out[m, :] = src[ids[m], :] for m < rows (rows read from `count` when given);
 // ids out of range give zero rows. VEC: 16-byte aligned rows.
 template <typename IDX, bool VEC>
+// bad (optional): incremented once per id outside [0, nsrc) (its row is
+// written as zeros); zeroed beforehand by zero_counter_kernel.
 __global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64_t nsrc, const IDX *ids, int64_t rows,
-                                                          const int32_t *count, char *out, int64_t row_bytes) {
+                                                          const int32_t *count, char *out, int64_t row_bytes,
+                                                          int32_t *bad) {
   const int64_t lim = count ? (int64_t)*count : rows;
   const int64_t units = VEC ? row_bytes / 16 : row_bytes;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t m = t / units, u = t % units;
   if (m >= lim || m >= rows) return;
   const int64_t id = (int64_t)ids[m];
+  if (bad && u == 0 && !(id >= 0 && id < nsrc)) atomicAdd(bad, 1);
   if (VEC) {
     uint4 v = make_uint4(0, 0, 0, 0);
     if (id >= 0 && id < nsrc) v = *reinterpret_cast<const uint4 *>(src + id * row_bytes + u * 16);
@@ -463,6 +474,10 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64
   } else {
     out[m * row_bytes + u] = (id >= 0 && id < nsrc) ? src[id * row_bytes + u] : 0;
   }
+}
+
+__global__ __launch_bounds__(64) void zero_counter_kernel(int32_t *c) {
+  if (threadIdx.x == 0) *c = 0;
 }
 
 // ---- C2S ----------------------------------------------------------------------------
@@ -630,12 +645,12 @@ unsigned grid_of(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 }  // namespace
 
 hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
-                             int32_t *nbr, hipStream_t s) {
+                             int32_t *nbr, int32_t *bad, hipStream_t s) {
   if (cap <= 0 || (cap & (cap - 1)) || cap < 2 * n) return hipErrorInvalidValue;
   if (grid_of(cap) == 0 || (cap + 255) / 256 > INT32_MAX || (n * 27 + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(map_clear_kernel, dim3(grid_of(cap)), dim3(256), 0, s, keys, vals, cap);
+  hipLaunchKernelGGL(map_clear_kernel, dim3(grid_of(cap)), dim3(256), 0, s, keys, vals, cap, bad);
   if (n == 0) return hipGetLastError();
-  hipLaunchKernelGGL(map_insert_kernel, dim3(grid_of(n)), dim3(256), 0, s, coords, n, keys, vals, cap);
+  hipLaunchKernelGGL(map_insert_kernel, dim3(grid_of(n)), dim3(256), 0, s, coords, n, keys, vals, cap, bad);
   hipLaunchKernelGGL(map_neighbors_kernel, dim3(grid_of(n * 27)), dim3(256), 0, s, coords, n, keys, vals, cap, nbr);
   return hipGetLastError();
 }
@@ -684,8 +699,9 @@ hipError_t launch_sparse_conv_rulebook(const SparseConvParams &p, const int32_t 
 }
 
 hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bool ids64, int64_t rows,
-                              const int32_t *count, void *out, int64_t row_bytes, hipStream_t s) {
-  if (rows <= 0 || row_bytes <= 0) return hipSuccess;
+                              const int32_t *count, void *out, int64_t row_bytes, int32_t *bad, hipStream_t s) {
+  if (bad) hipLaunchKernelGGL(zero_counter_kernel, dim3(1), dim3(64), 0, s, bad);
+  if (rows <= 0 || row_bytes <= 0) return hipGetLastError();
   const bool vec = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const int64_t units = vec ? row_bytes / 16 : row_bytes;
@@ -695,14 +711,14 @@ hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bo
   char *op = static_cast<char *>(out);
   if (ids64) {
     if (vec) hipLaunchKernelGGL((gather_rows_kernel<int64_t, true>), grid, block, 0, s, sp, nsrc,
-                                static_cast<const int64_t *>(ids), rows, count, op, row_bytes);
+                                static_cast<const int64_t *>(ids), rows, count, op, row_bytes, bad);
     else hipLaunchKernelGGL((gather_rows_kernel<int64_t, false>), grid, block, 0, s, sp, nsrc,
-                            static_cast<const int64_t *>(ids), rows, count, op, row_bytes);
+                            static_cast<const int64_t *>(ids), rows, count, op, row_bytes, bad);
   } else {
     if (vec) hipLaunchKernelGGL((gather_rows_kernel<int32_t, true>), grid, block, 0, s, sp, nsrc,
-                                static_cast<const int32_t *>(ids), rows, count, op, row_bytes);
+                                static_cast<const int32_t *>(ids), rows, count, op, row_bytes, bad);
     else hipLaunchKernelGGL((gather_rows_kernel<int32_t, false>), grid, block, 0, s, sp, nsrc,
-                            static_cast<const int32_t *>(ids), rows, count, op, row_bytes);
+                            static_cast<const int32_t *>(ids), rows, count, op, row_bytes, bad);
   }
   return hipGetLastError();
 }
@@ -758,7 +774,8 @@ hipError_t launch_c2s(const C2SParams &p, hipStream_t s) {
       break;
   }
   // child features: rows src_rows[j] of feats viewed as [n * 8, C / 8]
-  return launch_gather_rows(p.feats, p.n * 8, p.src_rows, false, p.n * 8, p.count, p.out_feats, p.child_row_bytes, s);
+  return launch_gather_rows(p.feats, p.n * 8, p.src_rows, false, p.n * 8, p.count, p.out_feats, p.child_row_bytes,
+                            nullptr, s);
 }
 
 }  // namespace lux3d

@@ -497,18 +497,10 @@ RopeEmbeddings Rope2d::embeddings(const Tensor &positions, size_t token_dim) con
   return e;
 }
 
-namespace {
-// The ABI's LayerNorm takes weight and bias; a bias-free LayerNorm uses zeros.
-Tensor bias_or_zeros(const LayerNorm &n) {
-  if (n.bias()) return *n.bias();
-  return Tensor::zeros(n.weight().dims(), DType::F32, n.weight().device());
-}
-}  // namespace
-
 Tensor apply_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeEmbeddings &embeddings) {
   Tensor out = empty_like(q);
-  const Tensor b = bias_or_zeros(q_norm);
-  abi_check(lux3d_qk_layernorm_rope2d(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(b).p(), nullptr, nullptr, nullptr,
+  abi_check(lux3d_qk_layernorm_rope2d(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(q_norm.bias()).p(), nullptr,
+                                      nullptr, nullptr,
                                       (float)q_norm.eps(), Desc(embeddings.cos_full).p(),
                                       Desc(embeddings.sin_alt_full).p(), Desc(out).p(), nullptr, q.device().stream()));
   return out;
@@ -525,9 +517,9 @@ Tensor apply_rope(const Tensor &tokens, const RopeEmbeddings &embeddings) {
 std::pair<Tensor, Tensor> qk_layernorm_rope2d(const Tensor &q, const Tensor &k, const LayerNorm &q_norm,
                                               const LayerNorm &k_norm, const Tensor &positions, float base) {
   Tensor qo = empty_like(q), ko = empty_like(k);
-  const Tensor qb = bias_or_zeros(q_norm), kb = bias_or_zeros(k_norm);
-  abi_check(lux3d_qk_layernorm_rope2d_pos(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(qb).p(), Desc(k).p(),
-                                          Desc(k_norm.weight()).p(), Desc(kb).p(), (float)q_norm.eps(),
+  abi_check(lux3d_qk_layernorm_rope2d_pos(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(q_norm.bias()).p(),
+                                          Desc(k).p(), Desc(k_norm.weight()).p(), Desc(k_norm.bias()).p(),
+                                          (float)q_norm.eps(),
                                           Desc(positions).p(), base, Desc(qo).p(), Desc(ko).p(), q.device().stream()));
   return {qo, ko};
 }
@@ -696,8 +688,8 @@ Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float
 Tensor sdpa_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeEmbeddings &embeddings,
                            const Tensor &k, const Tensor &v, float scale) {
   Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
-  const Tensor b = bias_or_zeros(q_norm);
-  abi_check(lux3d_sdpa_layernorm_rope2d(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(b).p(), (float)q_norm.eps(),
+  abi_check(lux3d_sdpa_layernorm_rope2d(Desc(q).p(), Desc(q_norm.weight()).p(), Desc(q_norm.bias()).p(),
+                                        (float)q_norm.eps(),
                                         Desc(embeddings.cos_full).p(), Desc(embeddings.sin_alt_full).p(), Desc(k).p(),
                                         Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
   return out;
@@ -746,14 +738,43 @@ Tensor coords_tensor(const std::vector<Coord> &coords, const Device &dev) {
 }  // namespace
 
 Tensor sparse_neighbors(const std::vector<Coord> &coords, const Device &dev) {
+  // the coordinates are on the host here: check the hash key's range before any device work
+  for (const Coord &c : coords)
+    for (int a = 0; a < 3; ++a)
+      if (c[a] < -(1 << 20) || c[a] >= (1 << 20) - 1)
+        fail(LUX3D_ERR_VALUE, "sparse_neighbors: coord [" + std::to_string(c[0]) + ", " + std::to_string(c[1]) + ", " +
+                                  std::to_string(c[2]) + "] outside the table's [-2^20, 2^20 - 1) range");
   const int64_t n = (int64_t)coords.size();
   int64_t cap = 16;
   while (cap < 2 * n) cap *= 2;
   const Tensor keys = Tensor::empty({cap}, DType::I64, dev), vals = Tensor::empty({cap}, DType::I32, dev);
   Tensor nbr = Tensor::empty({n, 27}, DType::I32, dev);
   abi_check(lux3d_sparse_neighbors(Desc(coords_tensor(coords, dev)).p(), Desc(keys).p(), Desc(vals).p(), Desc(nbr).p(),
-                                   dev.stream()));
+                                   nullptr, dev.stream()));
   return nbr;
+}
+
+SlatTokens slat_prepare(const Shape &feats_dims, int64_t in_channels, const std::vector<Coord> &coords,
+                        int64_t resolution, const Trellis2Rope3d &rope, const Device &dev) {
+  if (feats_dims.size() != 2) fail(LUX3D_ERR_SHAPE, "SLAT DiT features must be [rows, channels], got " + dims_str(feats_dims));
+  const int64_t rows = feats_dims[0], channels = feats_dims[1];
+  if (channels != in_channels)
+    fail(LUX3D_ERR_SHAPE, "SLAT DiT expects " + std::to_string(in_channels) + " token channels, got " +
+                              std::to_string(channels));
+  if (rows != (int64_t)coords.size())
+    fail(LUX3D_ERR_SHAPE, "SLAT DiT coords/features mismatch: " + std::to_string(coords.size()) + " coords vs " +
+                              std::to_string(rows) + " rows");
+  std::vector<int64_t> flat;
+  flat.reserve(coords.size() * 3);
+  for (const Coord &c : coords)
+    for (int a = 0; a < 3; ++a) {
+      if (c[a] < 0 || c[a] >= resolution)
+        fail(LUX3D_ERR_VALUE, "SLAT coord [" + std::to_string(c[0]) + ", " + std::to_string(c[1]) + ", " +
+                                  std::to_string(c[2]) + "] outside the 0.." + std::to_string(resolution) + " grid");
+      flat.push_back(c[a]);
+    }
+  auto [cos, sin] = rope.cos_sin(flat, dev);
+  return {coords_tensor(coords, dev), cos, sin};
 }
 
 Tensor index_select_rows(const Tensor &feats, const Tensor &ids) {
@@ -761,7 +782,15 @@ Tensor index_select_rows(const Tensor &feats, const Tensor &ids) {
   if (shape.empty()) fail(LUX3D_ERR_SHAPE, "index_select_rows: scalar input");
   shape[0] = ids.elem_count();
   Tensor out = Tensor::empty(shape, feats.dtype(), feats.device());
-  abi_check(lux3d_index_select_rows(Desc(feats).p(), Desc(ids).p(), Desc(out).p(), feats.device().stream()));
+  // candle's index_select fails on an id outside the rows: count them on the
+  // device and read the count back (this op returns after a stream sync)
+  Tensor bad = Tensor::empty({1}, DType::I32, feats.device());
+  abi_check(lux3d_index_select_rows(Desc(feats).p(), Desc(ids).p(), Desc(out).p(), Desc(bad).p(),
+                                    feats.device().stream()));
+  const int64_t nbad = bad.to_vec_i32()[0];
+  if (nbad)
+    fail(LUX3D_ERR_VALUE, "index_select_rows: " + std::to_string(nbad) + " of " + std::to_string(ids.elem_count()) +
+                              " ids outside 0.." + std::to_string(feats.dim(0)));
   return out;
 }
 

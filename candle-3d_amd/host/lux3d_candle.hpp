@@ -328,8 +328,22 @@ using Coord = std::array<int32_t, 3>;
 Coord kernel_offset_delta(size_t k);
 // CoordMap + the per-offset lookups, on the device: nbr int32 [N, 27]
 Tensor sparse_neighbors(const std::vector<Coord> &coords, const Device &dev);
-// index_select_rows (trellis2_sparse.rs:117-131)
+// index_select_rows (trellis2_sparse.rs:117-131); throws, as candle's
+// index_select does, when an id is outside the rows (counted on the device,
+// read back after a stream sync)
 Tensor index_select_rows(const Tensor &feats, const Tensor &ids);
+
+// Trellis2SlatDit::prepare (runtime/trellis2_dit.rs:511-544): checks the
+// token features (their dims, [rows, in_channels]) against the host coords
+// ([rows] x (x, y, z), each coordinate within 0..resolution) with the
+// reference's messages, then builds the RoPE tables. Also returns the coords
+// as a device int32 [rows, 3] tensor: the source lux3d_qk_l2norm_rope3d can
+// rotate from in-kernel instead of reading the tables.
+struct SlatTokens {
+  Tensor coords, cos, sin;
+};
+SlatTokens slat_prepare(const Shape &feats_dims, int64_t in_channels, const std::vector<Coord> &coords,
+                        int64_t resolution, const Trellis2Rope3d &rope, const Device &dev);
 
 class SparseConv3d {
  public:

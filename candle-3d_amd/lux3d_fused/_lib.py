@@ -66,11 +66,11 @@ SIGNATURES = {
     "lux3d_q8_0_linear": [TP, TP, TP, TP, TP, S],
     "lux3d_sdpa": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_layernorm_rope2d": [TP, TP, TP, ctypes.c_float, TP, TP, TP, TP, ctypes.c_float, TP, S],
-    "lux3d_sparse_neighbors": [TP, TP, TP, TP, S],
+    "lux3d_sparse_neighbors": [TP, TP, TP, TP, TP, S],
     "lux3d_sparse_conv3d": [TP, TP, TP, TP, TP, S],
     "lux3d_sparse_rulebook": [TP, TP, TP, S],
     "lux3d_sparse_conv3d_rulebook": [TP, TP, TP, TP, TP, TP, S],
-    "lux3d_index_select_rows": [TP, TP, TP, S],
+    "lux3d_index_select_rows": [TP, TP, TP, TP, S],
     "lux3d_channel_to_spatial": [TP, TP, TP, TP, TP, TP, TP, TP, TP, S],
 }
 

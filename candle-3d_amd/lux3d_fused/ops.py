@@ -440,9 +440,10 @@ def kernel_offset_delta(k: int):
     return (k // 9 - 1, (k % 9) // 3 - 1, k % 3 - 1)
 
 
-def sparse_neighbors(coords: torch.Tensor) -> torch.Tensor:
+def sparse_neighbors(coords: torch.Tensor, bad_coords: Optional[torch.Tensor] = None) -> torch.Tensor:
     """CoordMap + per-offset lookups on the device: coords int32 [N, 3] ->
-    nbr int32 [N, 27] (-1: missing)."""
+    nbr int32 [N, 27] (-1: missing). `bad_coords` (int32 [1]) receives the
+    number of coordinates outside the table's [-2^20, 2^20 - 1) range."""
     n = coords.shape[0]
     cap = 16
     while cap < 2 * n:
@@ -450,7 +451,8 @@ def sparse_neighbors(coords: torch.Tensor) -> torch.Tensor:
     keys = torch.empty(cap, dtype=torch.int64, device=coords.device)
     vals = torch.empty(cap, dtype=torch.int32, device=coords.device)
     nbr = torch.empty((n, 27), dtype=torch.int32, device=coords.device)
-    _lib.call("lux3d_sparse_neighbors", desc(coords), desc(keys), desc(vals), desc(nbr), _stream(coords))
+    _lib.call("lux3d_sparse_neighbors", desc(coords), desc(keys), desc(vals), desc(nbr), desc(bad_coords),
+              _stream(coords))
     return nbr
 
 
@@ -492,10 +494,11 @@ class SparseRulebook:
         _lib.call("lux3d_sparse_rulebook", desc(nbr), desc(self.pairs), desc(self.counts), _stream(nbr))
 
 
-def index_select_rows(feats: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
-    """index_select_rows (trellis2_sparse.rs:117-131): feats[ids] along dim 0."""
+def index_select_rows(feats: torch.Tensor, ids: torch.Tensor, bad_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """index_select_rows (trellis2_sparse.rs:117-131): feats[ids] along dim 0.
+    `bad_ids` (int32 [1]) receives the number of ids outside [0, rows)."""
     out = torch.empty((ids.shape[0],) + tuple(feats.shape[1:]), dtype=feats.dtype, device=feats.device)
-    _lib.call("lux3d_index_select_rows", desc(feats), desc(ids), desc(out), _stream(feats))
+    _lib.call("lux3d_index_select_rows", desc(feats), desc(ids), desc(out), desc(bad_ids), _stream(feats))
     return out
 
 

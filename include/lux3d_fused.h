@@ -21,8 +21,16 @@
  *  - Return value: LUX3D_OK (0) or a negative lux3d_status; the message is
  *    available from lux3d_last_error() on the calling thread. Argument errors
  *    are detected before anything is enqueued.
+ *  - Launches: the fused transformer-layer entries (LayerNorm to Q8_0
+ *    dequant below) enqueue exactly one kernel. Some next-row entries
+ *    enqueue a short fixed sequence on the same stream; each says so.
+ *  - Device-side preconditions that only the data can violate (coordinates
+ *    out of range, gather ids out of range) are counted into an optional
+ *    int32 error counter the entry sets, since checking them on the host
+ *    would need a device-to-host copy and a sync.
  *  - Thread safety: no global mutable state besides the thread-local error
- *    message; results are deterministic (no atomics, fixed reduction order).
+ *    message; results are deterministic (no floating-point atomics, fixed
+ *    reduction order; the error counters use integer atomics).
  */
 #ifndef LUX3D_FUSED_H
 #define LUX3D_FUSED_H
@@ -33,7 +41,7 @@
 extern "C" {
 #endif
 
-#define LUX3D_ABI_VERSION 1
+#define LUX3D_ABI_VERSION 2
 #define LUX3D_MAX_RANK 5
 
 typedef enum {
@@ -169,7 +177,9 @@ int lux3d_gated_residual_adaln_modulate(const lux3d_tensor_t *x, const lux3d_ten
  *     [B, N, 3, H, D] qkv buffer), D a multiple of 4 (as Rope2d requires);
  *     k may be NULL. D = 64 or 128 with 16-byte aligned rows takes the
  *     vectorised kernel, other head dims and alignments a generic one.
- *   q_w/q_b (k_w/k_b): [D] LayerNorm affine, or all NULL for RoPE only.
+ *   q_w/q_b (k_w/k_b): [D] LayerNorm affine, or all NULL for RoPE only; the
+ *     bias may be NULL with the weight given (a LayerNorm without bias:
+ *     out = n*w), a bias without its weight is rejected.
  *   cos_full, sin_alt_full: [B, N, D] or [B, 1, N, D] f32 tables as built by
  *     Rope2d::embeddings (sin table with the rotate-half negation folded in).
  *   q_out, k_out: contiguous [B, H, N, D].
@@ -333,8 +343,12 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
 
 /* ---- TRELLIS.2 sparse voxel ops (runtime/trellis2_sparse.rs) ----------------
  * lux3d_sparse_neighbors: CoordMap::new + the per-offset lookups of
- * SparseConv3d::forward (trellis2_sparse.rs:62-91, 205-222), on the device.
- *   coords: int32 [N, 3] contiguous (x, y, z), each within (-2^20, 2^20 - 1);
+ * SparseConv3d::forward (trellis2_sparse.rs:62-91, 205-222), on the device;
+ * three kernels (clear the table, insert, look up).
+ *   coords: int32 [N, 3] contiguous (x, y, z), each in [-2^20, 2^20 - 1)
+ *     (the packed hash key); a coordinate outside is neither inserted nor
+ *     found, and is counted into bad_coords;
+ *   bad_coords: int32 [1] or NULL: set to the number of such coordinates;
  *   keys: int64 [cap], vals: int32 [cap] -- a workspace, cap a power of two
  *         >= 2 N (the hash table; cleared here);
  *   nbr: int32 [N, 27] out: nbr[i][k] = row of coords[i] + (kd-1, kh-1, kw-1),
@@ -353,8 +367,10 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
  *
  * lux3d_index_select_rows: index_select_rows (trellis2_sparse.rs:117-131):
  *   out[m, ...] = src[ids[m], ...]; src [R, ...] and out [M, ...] contiguous,
- *   same dtype and row shape; ids int32 or int64 [M]. Ids outside [0, R)
- *   give zero rows (no error: checking would need a device sync).
+ *   same dtype and row shape; ids int32 or int64 [M]. An id outside [0, R)
+ *   gives a zero row and is counted: bad_ids (int32 [1] or NULL) is set to
+ *   the number of such ids (candle's index_select errors on them; the C++
+ *   mirror reads the count back and throws).
  *
  * lux3d_channel_to_spatial: channel_to_spatial (trellis2_sparse.rs:269-338):
  *   coords int32 [N, 3]; feats [N, C] (any dtype, C % 8 == 0, contiguous);
@@ -367,7 +383,7 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
  *   count stays in device memory (read it after a stream sync).            */
 int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *keys,
                            const lux3d_tensor_t *vals, const lux3d_tensor_t *nbr,
-                           lux3d_stream_t stream);
+                           const lux3d_tensor_t *bad_coords, lux3d_stream_t stream);
 int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
                         const lux3d_tensor_t *weight, const lux3d_tensor_t *bias,
                         const lux3d_tensor_t *out, lux3d_stream_t stream);
@@ -389,7 +405,8 @@ int lux3d_sparse_conv3d_rulebook(const lux3d_tensor_t *x, const lux3d_tensor_t *
                                  const lux3d_tensor_t *bias, const lux3d_tensor_t *out,
                                  lux3d_stream_t stream);
 int lux3d_index_select_rows(const lux3d_tensor_t *src, const lux3d_tensor_t *ids,
-                            const lux3d_tensor_t *out, lux3d_stream_t stream);
+                            const lux3d_tensor_t *out, const lux3d_tensor_t *bad_ids,
+                            lux3d_stream_t stream);
 int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t *feats,
                              const lux3d_tensor_t *logits, const lux3d_tensor_t *workspace,
                              const lux3d_tensor_t *out_coords, const lux3d_tensor_t *src_rows,
@@ -421,7 +438,7 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
  * scale), with q's LayerNorm + 2D RoPE (attention_math.rs:127-150) applied
  * inside the attention kernel's Q load: the normalised q never goes through
  * HBM. q is the raw [B, H, N, D] head view (bf16 / f16); q_w, q_b the
- * LayerNorm affine ([D], any float dtype); cos_full / sin_alt_full the Rope2d
+ * LayerNorm affine ([D], any float dtype; q_b may be NULL); cos_full / sin_alt_full the Rope2d
  * tables as lux3d_qk_layernorm_rope2d takes them; k the already normalised
  * and rotated keys (lux3d_qk_layernorm_rope2d on k alone); v, scale and out
  * as lux3d_sdpa (out [B, H, N, D]; it may be the view the caller transposes

@@ -643,7 +643,11 @@ static void r1_rows(const void *p, int64_t r0, int64_t r1) {
     if (c->norm) {
       float mean;
       float den = slow_ln_stats(c->dt, c->t, base, d, c->eps, &mean);
-      for (int64_t k = 0; k < d; ++k) v[k] = ((ld(c->dt, c->t, base + k) - mean) / den) * c->w[k] + c->b[k];
+      /* a LayerNorm without bias (candle_nn::LayerNorm, bias None) stops at n * w */
+      for (int64_t k = 0; k < d; ++k) {
+        v[k] = ((ld(c->dt, c->t, base + k) - mean) / den) * c->w[k];
+        if (c->b) v[k] = v[k] + c->b[k];
+      }
     } else {
       for (int64_t k = 0; k < d; ++k) v[k] = ld(c->dt, c->t, base + k);
     }

@@ -591,11 +591,38 @@ void errors_on_host(const Device &dev) {
   CHECK(throws_with([&] { Trellis2Rope3d(4).cos_sin({1, 2, 3}, dev); }, "is too small for 3-axis RoPE"));
   CHECK(throws_with([&] { Trellis2Rope3d(13).cos_sin({1, 2, 3}, dev); }, "must be divisible by 2"));
   CHECK(throws_with([&] { dinov3_rope_cos_sin(10, 100.0f, 2, 2, dev); }, "is not divisible by 4"));
+  // Trellis2SlatDit::prepare's checks (trellis2_dit.rs:516-541), before any device work
+  const Trellis2Rope3d rope128(128);
+  CHECK(throws_with([&] { slat_prepare({2, 8}, 16, {{0, 0, 0}, {1, 2, 3}}, 64, rope128, dev); },
+                    "SLAT DiT expects 16 token channels, got 8"));
+  CHECK(throws_with([&] { slat_prepare({3, 8}, 8, {{0, 0, 0}, {1, 2, 3}}, 64, rope128, dev); },
+                    "SLAT DiT coords/features mismatch: 2 coords vs 3 rows"));
+  CHECK(throws_with([&] { slat_prepare({2, 8}, 8, {{0, 0, 0}, {1, 64, 3}}, 64, rope128, dev); },
+                    "SLAT coord [1, 64, 3] outside the 0..64 grid"));
+  CHECK(throws_with([&] { slat_prepare({1, 8}, 8, {{-1, 0, 0}}, 64, rope128, dev); }, "outside the 0..64 grid"));
+  CHECK(throws_with([&] { sparse_neighbors({{0, 0, 0}, {1 << 20, 0, 0}}, dev); }, "outside the table's"));
   CHECK(throws_with([&] { QMatMul::from_q8_0(Tensor(), 4, 48); }, "needs k % 32 == 0"));
   CHECK(throws_with([&] { GgufFile::open(g_fixture_dir + "/missing.gguf"); }, "cannot open"));
   CHECK(throws_with([&] { SafetensorsFile::open(g_fixture_dir + "/tiny_q8.gguf"); }, "safetensors"));
   const GgufFile f = GgufFile::open(g_fixture_dir + "/tiny_q8.gguf");
   CHECK(f.version() == 3 && f.names().size() == 3 && f.contains("blocks.0.norm.weight"));
+}
+
+// slat_prepare on valid coords: the tables equal Trellis2Rope3d::cos_sin's and
+// the device coords round-trip; index_select_rows throws on an id past the rows.
+void slat_prepare_and_gather_checks(const Device &dev) {
+  const Trellis2Rope3d rope(12);
+  const std::vector<Coord> coords = {{0, 0, 0}, {3, 1, 2}, {63, 63, 63}};
+  const SlatTokens t = slat_prepare({3, 4}, 4, coords, 64, rope, dev);
+  auto [cos, sin] = rope.cos_sin({0, 0, 0, 3, 1, 2, 63, 63, 63}, dev);
+  CHECK(t.cos.to_vec_f32() == cos.to_vec_f32() && t.sin.to_vec_f32() == sin.to_vec_f32());
+  const std::vector<int32_t> c = t.coords.to_vec_i32();
+  CHECK(c.size() == 9 && c[3] == 3 && c[4] == 1 && c[5] == 2 && c[8] == 63);
+  const Tensor feats = Tensor::from_f32({1, 2, 3, 4, 5, 6}, {3, 2}, DType::F32, dev);
+  const std::vector<float> g = index_select_rows(feats, Tensor::from_i32({2, 0}, {2}, dev)).to_vec_f32();
+  CHECK(g == std::vector<float>({5, 6, 1, 2}));
+  CHECK(throws_with([&] { index_select_rows(feats, Tensor::from_i32({2, 3, -1}, {3}, dev)); },
+                    "index_select_rows: 2 of 3 ids outside 0..3"));
 }
 
 void errors_on_device(const Device &dev) {
@@ -654,6 +681,7 @@ int main(int argc, char **argv) {
       {"sparse_conv_loader_transposes_flex_gemm_layout", sparse_conv_loader_transposes_flex_gemm_layout, true},
       {"sparse_conv_rulebook_identity_and_shift", sparse_conv_rulebook_identity_and_shift, true},
       {"c2s_order_and_feature_selection", c2s_order_and_feature_selection, true},
+      {"slat_prepare_and_gather_checks", slat_prepare_and_gather_checks, true},
       {"errors_on_device", errors_on_device, true},
   };
   Device dev;  // ordinal 0, null stream; Device::hip() is only called when a GPU is needed

@@ -41,8 +41,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.LIB.lux3d_abi_version() == 1
-    assert _lib.ABI_VERSION == 1
+    assert _lib.LIB.lux3d_abi_version() == 2
+    assert _lib.ABI_VERSION == 2
 
 
 FAKE = 0x100000  # 16-byte aligned fake device address; never dereferenced
@@ -148,10 +148,15 @@ def test_head_op_errors():
     rc, msg = status("lux3d_qk_layernorm_rope2d", q, None, None, None, None, None, 1e-5, T([2, 11, 64], _lib.F32),
                      tab, out, None, None)
     assert rc == _lib.ERR_SHAPE
-    # LayerNorm needs both w and b
-    rc, msg = status("lux3d_qk_layernorm_rope2d", q, T([64], _lib.F32), None, None, None, None, 1e-5, tab, tab, out,
+    # a LayerNorm bias without its weight (a weight without bias is a bias-free LayerNorm)
+    rc, msg = status("lux3d_qk_layernorm_rope2d", q, None, T([64], _lib.F32), None, None, None, 1e-5, tab, tab, out,
                      None, None)
-    assert rc == _lib.ERR_NULL
+    assert rc == _lib.ERR_NULL and "bias given without a weight" in msg
+    # q normalised, k not
+    k = T([2, 16, 10, 64], strides=[10 * 3 * 16 * 64, 64, 3 * 16 * 64, 1], data=FAKE + 128)
+    rc, msg = status("lux3d_qk_layernorm_rope2d", q, T([64], _lib.F32), None, k, None, None, 1e-5, tab, tab, out,
+                     out, None)
+    assert rc == _lib.ERR_NULL and "both be normalised" in msg
     # a non-unit innermost stride
     rc, msg = status("lux3d_qk_layernorm_rope2d", T([2, 16, 10, 64], strides=[20480, 1280, 128, 2]), None, None,
                      None, None, None, 1e-5, tab, tab, out, None, None)
@@ -283,12 +288,14 @@ def test_sdpa_argument_errors():
 
 def test_sparse_argument_errors():
     co, nbr = T([100, 3], _lib.I32), T([100, 27], _lib.I32)
-    rc, msg = status("lux3d_sparse_neighbors", co, T([128], _lib.I64), T([128], _lib.I32), nbr, None)
+    rc, msg = status("lux3d_sparse_neighbors", co, T([128], _lib.I64), T([128], _lib.I32), nbr, None, None)
     assert rc == _lib.ERR_SHAPE and "power-of-two" in msg        # 128 < 2 N
-    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I64), T([255], _lib.I32), nbr, None)
+    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I64), T([255], _lib.I32), nbr, None, None)
     assert rc == _lib.ERR_SHAPE
-    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I32), T([256], _lib.I32), nbr, None)
+    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I32), T([256], _lib.I32), nbr, None, None)
     assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I64), T([256], _lib.I32), nbr, T([1], _lib.F32), None)
+    assert rc == _lib.ERR_DTYPE and "bad_coords" in msg
     x, w, out = T([100, 64], _lib.F32), T([27, 32, 64], _lib.F32), T([100, 32], _lib.F32)
     rc, msg = status("lux3d_sparse_conv3d", x, nbr, T([27, 32, 48], _lib.F32), None, out, None)
     assert rc == _lib.ERR_SHAPE and "SparseConv3d expects" in msg
@@ -296,10 +303,12 @@ def test_sparse_argument_errors():
     assert rc == _lib.ERR_DTYPE
     rc, msg = status("lux3d_sparse_conv3d", x, nbr, w, T([31], _lib.F32), out, None)
     assert rc == _lib.ERR_SHAPE
-    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.F32), T([5, 4]), None)
+    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.F32), T([5, 4]), None, None)
     assert rc == _lib.ERR_DTYPE
-    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.I32), T([5, 3]), None)
+    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.I32), T([5, 3]), None, None)
     assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_index_select_rows", T([10, 4]), T([5], _lib.I32), T([5, 4]), T([0], _lib.I32), None)
+    assert rc == _lib.ERR_SHAPE and "bad_ids" in msg
     f, lg = T([100, 12], _lib.F32), T([100, 8], _lib.F32)
     args = [T([108], _lib.I32), T([800, 3], _lib.I32), T([800], _lib.I32), T([800, 1], _lib.F32),
             T([100, 8], _lib.F32), T([1], _lib.I32), None]
@@ -316,7 +325,7 @@ def test_sdpa_layernorm_rope2d_argument_errors():
     w, b = T([64], _lib.F32), T([64], _lib.F32)
     cs, sn = T([2, 33, 64], _lib.F32), T([2, 33, 64], _lib.F32)
     rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, None, b, 1e-5, cs, sn, k, v, 0.125, o, None)
-    assert rc == _lib.ERR_NULL and "weight and bias" in msg
+    assert rc == _lib.ERR_NULL and "needs a weight" in msg
     rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, T([63], _lib.F32), b, 1e-5, cs, sn, k, v, 0.125, o, None)
     assert rc == _lib.ERR_SHAPE
     rc, msg = status("lux3d_sdpa_layernorm_rope2d", q, w, b, 1e-5, T([2, 34, 64], _lib.F32), sn, k, v, 0.125, o, None)

@@ -232,7 +232,8 @@ def test_sdpa_graph_replay_matches_eager(dev, ops):
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("d,case", [(64, "fused"), (128, "fused"), (64, "unaligned_q"), (64, "bf16_tables")])
+@pytest.mark.parametrize("d,case", [(64, "fused"), (128, "fused"), (64, "unaligned_q"), (64, "bf16_tables"),
+                                    (64, "no_bias")])
 def test_sdpa_layernorm_rope2d_equals_the_two_launches(dev, ops, orc, d, case):
     """VGGT attention with q's LayerNorm + 2D RoPE in the Q load
     (vggt.rs:170-183) equals lux3d_qk_layernorm_rope2d followed by lux3d_sdpa
@@ -248,7 +249,7 @@ def test_sdpa_layernorm_rope2d_equals_the_two_launches(dev, ops, orc, d, case):
     qkv = (torch.randn((b, n, 3, h, width), generator=g) * 2 + 0.5).to(dev).to(torch.bfloat16).permute(2, 0, 3, 1, 4)
     q_raw, k_raw, v = qkv[0][..., -d:], qkv[1][..., :d], qkv[2][..., :d]
     qw = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
-    qb = (0.1 * torch.randn(d, generator=g)).to(dev)
+    qb = (0.1 * torch.randn(d, generator=g)).to(dev) if case != "no_bias" else None
     kw = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
     kb = (0.1 * torch.randn(d, generator=g)).to(dev)
     emb = ops.Rope2d(100.0).embeddings(torch.from_numpy(pos).to(dev), d)

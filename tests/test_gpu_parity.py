@@ -332,7 +332,7 @@ def test_rope2d_tables(dev, ops, orc, synth, dt):
                                        ("f32", "positions")])
 def test_qk_layernorm_rope2d_cfg1(dev, ops, orc, synth, dt, source):
     print(f"\n[case] qk_layernorm_rope2d configs[1] dt={dt} source={source}", flush=True)
-    B = 8 if dt == "bf16" else 2
+    B = 8
     q, k, pos, N = _vggt_qkv(synth, dev, dt, B=B)
     D = 64
     qw, qb = synth.normal(21, D, 1.0, 0.02), synth.normal(22, D, 0.0, 0.02)
@@ -352,6 +352,27 @@ def test_qk_layernorm_rope2d_cfg1(dev, ops, orc, synth, dt, source):
     kh = np.ascontiguousarray(host_view(k, dt))
     check(qo, orc.layernorm_rope2d(qh, qw, qb, 1e-5, cos, sin, dt=odt), dt, "q")
     check(ko, orc.layernorm_rope2d(kh, kw, kb, 1e-5, cos, sin, dt=odt), dt, "k")
+
+
+@pytest.mark.parametrize("dt,source", [("bf16", "positions"), ("f32", "tables")])
+def test_qk_layernorm_rope2d_without_bias(dev, ops, orc, synth, dt, source):
+    """A LayerNorm without bias (candle_nn::LayerNorm, bias None: n * w) on the
+    q / k heads: the bias is NULL at the C ABI."""
+    print(f"\n[case] qk_layernorm_rope2d without bias dt={dt} source={source}", flush=True)
+    q, k, pos, N = _vggt_qkv(synth, dev, dt, B=2, ph=13, pw=11)
+    D = 64
+    qw, kw = synth.normal(25, D, 1.0, 0.1), synth.normal(26, D, 1.0, 0.1)
+    T = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    cos, sin = orc.rope2d_tables(pos, D, 100.0)
+    if source == "tables":
+        emb = ops.RopeEmbeddings(T(cos).unsqueeze(1), T(sin).unsqueeze(1))
+        qo, ko = ops.qk_layernorm_rope2d(q, k, (T(qw), None, 1e-5), (T(kw), None, 1e-5), emb)
+    else:
+        qo, ko = ops.qk_layernorm_rope2d(q, k, (T(qw), None, 1e-5), (T(kw), None, 1e-5), positions=T(pos), base=100.0)
+    sync()
+    odt = oracle_dt(orc, dt)
+    check(qo, orc.layernorm_rope2d(np.ascontiguousarray(host_view(q, dt)), qw, None, 1e-5, cos, sin, dt=odt), dt, "q")
+    check(ko, orc.layernorm_rope2d(np.ascontiguousarray(host_view(k, dt)), kw, None, 1e-5, cos, sin, dt=odt), dt, "k")
 
 
 def test_rope_fused_and_single_tensor(dev, ops, orc, synth):

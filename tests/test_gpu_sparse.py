@@ -146,11 +146,31 @@ def test_index_select_rows(dev, ops, dt, ids_dt, row):
     ids[::97] = 1000   # out of range: zero rows
     ids[1::89] = -1
     ids = ids.to(torch.int64 if ids_dt == "i64" else torch.int32)
-    got = ops.index_select_rows(src.to(dev), ids.to(dev)).cpu()
+    bad = torch.full((1,), 12345, dtype=torch.int32, device=dev)   # the entry sets it
+    got = ops.index_select_rows(src.to(dev), ids.to(dev), bad_ids=bad).cpu()
     valid = (ids >= 0) & (ids < 1000)
     want = torch.zeros((4321,) + row, dtype=tdt)
     want[valid] = src[ids[valid].long()]
     assert torch.equal(got, want)
+    assert int(bad.item()) == int((~valid).sum())
+    # all ids valid: the count is zero
+    ops.index_select_rows(src.to(dev), ids[valid].to(dev), bad_ids=bad)
+    assert int(bad.item()) == 0
+
+
+def test_sparse_neighbors_counts_unpackable_coords(dev, ops, orc):
+    """Coordinates outside [-2^20, 2^20 - 1) are neither inserted nor found
+    and are counted into bad_coords; the others keep their neighbours."""
+    _case(op="neighbors", case="out of range")
+    c = random_coords(400, 8, 7)
+    far = np.array([[1 << 20, 0, 0], [0, -(1 << 20) - 1, 0], [3, 3, 2 ** 30]], dtype=np.int32)
+    allc = np.concatenate([c, far])
+    bad = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    nbr = ops.sparse_neighbors(torch.from_numpy(allc).to(dev), bad_coords=bad).cpu().numpy()
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 3
+    assert np.array_equal(nbr[:400], orc.sparse_neighbors(c))
+    assert (nbr[400:] == -1).all()
 
 
 @pytest.mark.parametrize("n,c,fdt,ldt", [(3, 16, "f32", "f32"), (5000, 64, "f32", "f32"), (3000, 128, "bf16", "bf16"),

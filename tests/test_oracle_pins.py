@@ -338,6 +338,11 @@ def test_layernorm_rope2d_is_ln_then_rope():
     fused = orc.layernorm_rope2d(q, w, b, 1e-5, c, s)
     ln = F.layer_norm(f64(q), (64,), f64(w), f64(b), eps=1e-5).numpy().astype(np.float32)
     assert_f32_close(fused, orc.rope2d_apply(ln, c, s), what="L2+R1")
+    # a LayerNorm without bias (candle_nn::LayerNorm, bias None) stops at n * w
+    nob = orc.layernorm_rope2d(q, w, None, 1e-5, c, s)
+    ln0 = F.layer_norm(f64(q), (64,), f64(w), None, eps=1e-5).numpy().astype(np.float32)
+    assert_f32_close(nob, orc.rope2d_apply(ln0, c, s), what="L2 (no bias)+R1")
+    assert np.array_equal(nob, orc.layernorm_rope2d(q, w, np.zeros(64, np.float32), 1e-5, c, s))
 
 
 # ---------------------------------------------------------------------------
