@@ -1030,6 +1030,28 @@ int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *k
                     fn);
 }
 
+int lux3d_sparse_neighbors_noalloc(const lux3d_tensor_t *coords, const lux3d_tensor_t *nbr,
+                                   const lux3d_tensor_t *bad_coords, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sparse_neighbors_noalloc";
+  int r;
+  if ((r = contiguous_of(coords, fn, "coords", LUX3D_I32, 2)) || (r = contiguous_of(nbr, fn, "nbr", LUX3D_I32, 2)))
+    return r;
+  if (bad_coords && ((r = contiguous_of(bad_coords, fn, "bad_coords", LUX3D_I32, -1)) || numel(bad_coords) < 1))
+    return r ? r : fail(LUX3D_ERR_SHAPE, "%s: bad_coords must hold one int32", fn);
+  const int64_t n = coords->shape[0];
+  if (coords->shape[1] != 3) return fail(LUX3D_ERR_SHAPE, "%s: coords must be [N, 3]", fn);
+  if (nbr->shape[0] != n || nbr->shape[1] != 27) return fail(LUX3D_ERR_SHAPE, "%s: nbr must be [%lld, 27]", fn,
+                                                              (long long)n);
+  if (n > kNoAllocMaxVoxels)
+    return fail(LUX3D_ERR_SHAPE, "%s: %lld voxels exceed the allocation-free table's limit of %lld (use "
+                "lux3d_sparse_neighbors with a caller-provided table)", fn, (long long)n, (long long)kNoAllocMaxVoxels);
+  return hip_status(launch_sparse_map_noalloc(static_cast<const int32_t *>(coords->data), n,
+                                              static_cast<int32_t *>(nbr->data),
+                                              bad_coords ? static_cast<int32_t *>(bad_coords->data) : nullptr,
+                                              stream_of(stream)),
+                    fn);
+}
+
 int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr, const lux3d_tensor_t *weight,
                         const lux3d_tensor_t *bias, const lux3d_tensor_t *out, lux3d_stream_t stream) {
   const char *fn = "lux3d_sparse_conv3d";

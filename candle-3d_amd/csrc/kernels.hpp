@@ -147,6 +147,12 @@ hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
 // Coordinate hash (cap: a power of two >= 2n) and neighbour table nbr [n, 27].
 hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
                              int32_t *nbr, int32_t *bad, hipStream_t s);
+// The same with the hash table in a per-device static array (no allocation):
+// n <= kNoAllocMaxVoxels; the table holds kNoAllocCap slots.
+constexpr int64_t kNoAllocMaxVoxels = int64_t(1) << 20;
+constexpr int64_t kNoAllocCap = 2 * kNoAllocMaxVoxels;
+constexpr int64_t kNoAllocTableBytes = kNoAllocCap * (8 + 4);  // 24 MiB
+hipError_t launch_sparse_map_noalloc(const int32_t *coords, int64_t n, int32_t *nbr, int32_t *bad, hipStream_t s);
 struct SparseConvParams {
   const float *x = nullptr;       // [n, cin]
   const int32_t *nbr = nullptr;   // [n, 27]

@@ -23,10 +23,19 @@
 // thread per (parent, subidx) writes the child coordinate and source row in
 // the reference order (parent order, ascending subidx), and a row gather
 // copies the child features. The child count is written to device memory.
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace lux3d {
+
+// Coordinate hash table of the allocation-free neighbour entry
+// (lux3d_sparse_neighbors_noalloc): keys u64 [kNoAllocCap] then vals int32
+// [kNoAllocCap], one copy per device, held until the process ends. Device
+// code only: host code uses the address hipGetSymbolAddress returns for the
+// current device (noalloc_table below), never this name.
+static __device__ __align__(256) unsigned char scratch[kNoAllocTableBytes];
 
 namespace {
 
@@ -643,6 +652,44 @@ __global__ __launch_bounds__(256) void c2s_emit_kernel(const int32_t *coords, co
 unsigned grid_of(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 
 }  // namespace
+
+namespace {
+// Per-device address of `scratch`, looked up once per device (with that
+// device current) on the first allocation-free call.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t noalloc_table(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_sparse_map_noalloc(const int32_t *coords, int64_t n, int32_t *nbr, int32_t *bad, hipStream_t s) {
+  if (n > kNoAllocMaxVoxels) return hipErrorInvalidValue;
+  int64_t cap = 16;
+  while (cap < 2 * n) cap *= 2;
+  if (cap > kNoAllocCap) return hipErrorInvalidValue;  // the table's slots
+  void *table = nullptr;
+  const hipError_t e = noalloc_table(&table);
+  if (e != hipSuccess) return e;
+  // the table is cleared by the first kernel of the sequence (no memset)
+  auto *keys = static_cast<unsigned long long *>(table);
+  auto *vals = reinterpret_cast<int32_t *>(static_cast<unsigned char *>(table) + kNoAllocCap * sizeof(unsigned long long));
+  return launch_sparse_map(coords, n, keys, vals, cap, nbr, bad, s);
+}
 
 hipError_t launch_sparse_map(const int32_t *coords, int64_t n, unsigned long long *keys, int32_t *vals, int64_t cap,
                              int32_t *nbr, int32_t *bad, hipStream_t s) {

@@ -67,6 +67,7 @@ SIGNATURES = {
     "lux3d_sdpa": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_layernorm_rope2d": [TP, TP, TP, ctypes.c_float, TP, TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sparse_neighbors": [TP, TP, TP, TP, TP, S],
+    "lux3d_sparse_neighbors_noalloc": [TP, TP, TP, S],
     "lux3d_sparse_conv3d": [TP, TP, TP, TP, TP, S],
     "lux3d_sparse_rulebook": [TP, TP, TP, S],
     "lux3d_sparse_conv3d_rulebook": [TP, TP, TP, TP, TP, TP, S],

@@ -456,6 +456,15 @@ def sparse_neighbors(coords: torch.Tensor, bad_coords: Optional[torch.Tensor] = 
     return nbr
 
 
+def sparse_neighbors_noalloc(coords: torch.Tensor, nbr: torch.Tensor,
+                             bad_coords: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sparse_neighbors into a caller-provided `nbr` (int32 [N, 27]) with the
+    hash table in the library's per-device static array: the library
+    allocates nothing. N <= 2^20; calls that overlap on one GPU race."""
+    _lib.call("lux3d_sparse_neighbors_noalloc", desc(coords), desc(nbr), desc(bad_coords), _stream(coords))
+    return nbr
+
+
 class SparseConv3d:
     """Submanifold 3x3x3 sparse convolution (trellis2_sparse.rs:135-243).
     `weight` is the checkpoint's flex_gemm layout [Cout, 3, 3, 3, Cin] (or

@@ -384,6 +384,17 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
 int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *keys,
                            const lux3d_tensor_t *vals, const lux3d_tensor_t *nbr,
                            const lux3d_tensor_t *bad_coords, lux3d_stream_t stream);
+/* lux3d_sparse_neighbors_noalloc: lux3d_sparse_neighbors without the `keys` /
+ * `vals` workspace and without any allocation. This entry has no counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops). The hash table lives in
+ * a per-device static array of the library (24 MiB, held until the process
+ * ends), so N is limited to 2^20 voxels (LUX3D_ERR_SHAPE beyond). Every call
+ * on a GPU uses that GPU's one table: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. Same
+ * kernels and outputs as lux3d_sparse_neighbors.                           */
+int lux3d_sparse_neighbors_noalloc(const lux3d_tensor_t *coords, const lux3d_tensor_t *nbr,
+                                   const lux3d_tensor_t *bad_coords, lux3d_stream_t stream);
 int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
                         const lux3d_tensor_t *weight, const lux3d_tensor_t *bias,
                         const lux3d_tensor_t *out, lux3d_stream_t stream);

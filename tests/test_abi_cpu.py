@@ -296,6 +296,16 @@ def test_sparse_argument_errors():
     assert rc == _lib.ERR_DTYPE
     rc, msg = status("lux3d_sparse_neighbors", co, T([256], _lib.I64), T([256], _lib.I32), nbr, T([1], _lib.F32), None)
     assert rc == _lib.ERR_DTYPE and "bad_coords" in msg
+    # the allocation-free variant: same shapes, and at most 2^20 voxels
+    big = (1 << 20) + 1
+    rc, msg = status("lux3d_sparse_neighbors_noalloc", T([big, 3], _lib.I32), T([big, 27], _lib.I32), None, None)
+    assert rc == _lib.ERR_SHAPE and "limit of 1048576" in msg
+    rc, msg = status("lux3d_sparse_neighbors_noalloc", co, T([100, 26], _lib.I32), None, None)
+    assert rc == _lib.ERR_SHAPE and "[100, 27]" in msg
+    rc, msg = status("lux3d_sparse_neighbors_noalloc", co, nbr, T([1], _lib.F32), None)
+    assert rc == _lib.ERR_DTYPE and "bad_coords" in msg
+    rc, msg = status("lux3d_sparse_neighbors_noalloc", T([100, 3], _lib.I64), nbr, None, None)
+    assert rc == _lib.ERR_DTYPE
     x, w, out = T([100, 64], _lib.F32), T([27, 32, 64], _lib.F32), T([100, 32], _lib.F32)
     rc, msg = status("lux3d_sparse_conv3d", x, nbr, T([27, 32, 48], _lib.F32), None, out, None)
     assert rc == _lib.ERR_SHAPE and "SparseConv3d expects" in msg
