@@ -888,9 +888,10 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
 
 namespace {
 // Validates q, k, v, out for attention and fills the strides; `mfma` tells
-// whether every row is 16-byte aligned with D 64 / 128 in a 2-byte type.
+// whether every row is 16-byte aligned with D 64 / 128. `f32_out_ok`: out
+// may also be f32 when q, k, v are 2-byte.
 int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v,
-                float scale, const lux3d_tensor_t *out, AttnParams &p);
+                float scale, const lux3d_tensor_t *out, AttnParams &p, bool f32_out_ok = false);
 }  // namespace
 
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
@@ -899,6 +900,17 @@ int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_ten
   AttnParams p;
   int r;
   if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+int lux3d_sdpa_heads_f32(const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                         const lux3d_tensor_t *out, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa_heads_f32";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p, true))) return r;
+  p.exact_p = true;
+  p.out_f32 = out->dtype == LUX3D_F32;
   return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
 }
 
@@ -944,7 +956,7 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
 
 namespace {
 int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k, const lux3d_tensor_t *v,
-                float scale, const lux3d_tensor_t *out, AttnParams &p) {
+                float scale, const lux3d_tensor_t *out, AttnParams &p, bool f32_out_ok) {
   int r;
   const lux3d_tensor_t *ts[4] = {q, k, v, out};
   const char *names[4] = {"q", "k", "v", "out"};
@@ -952,7 +964,9 @@ int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k
     if ((r = check_desc(ts[i], fn, names[i]))) return r;
     if (ts[i]->rank != 4)
       return fail(LUX3D_ERR_SHAPE, "%s: `%s` must be [B, H, L, D] (rank %d given)", fn, names[i], ts[i]->rank);
-    if (ts[i]->dtype != q->dtype) return fail(LUX3D_ERR_DTYPE, "%s: q, k, v and out must share one dtype", fn);
+    if (ts[i]->dtype != q->dtype && !(i == 3 && f32_out_ok && ts[i]->dtype == LUX3D_F32))
+      return fail(LUX3D_ERR_DTYPE, f32_out_ok ? "%s: q, k and v must share one dtype; out has it or is f32"
+                                              : "%s: q, k, v and out must share one dtype", fn);
     if (ts[i]->shape[3] > 1 && ts[i]->stride[3] != 1)
       return fail(LUX3D_ERR_LAYOUT, "%s: `%s` must have a unit innermost stride", fn, names[i]);
   }
@@ -979,9 +993,9 @@ int attn_params(const char *fn, const lux3d_tensor_t *q, const lux3d_tensor_t *k
   p.scale = scale;
   // matrix cores: D 64 / 128, every row start 16-byte aligned
   bool mfma = D == 64 || D == 128;
-  const int64_t align_el = 16 / elem_bytes(q->dtype);
   for (int i = 0; i < 4 && mfma; ++i) {
     const lux3d_tensor_t *t = ts[i];
+    const int64_t align_el = 16 / elem_bytes(t->dtype);
     mfma = aligned16(t->data);
     for (int a = 0; a < 3 && mfma; ++a)
       if (t->shape[a] > 1 && t->stride[a] % align_el) mfma = false;

@@ -33,6 +33,16 @@
 // XCD (hardware places workgroup i on XCD i % 8) and share its L2 copy of K
 // and V.
 //
+// Exact-probability form (EXACTP, bf16 only; exact_sdpa_heads): the
+// probabilities stay f32 and enter P v as three bf16 terms p = p1 + p2 + p3
+// (p1 = bf16(p), p2 = bf16(p - p1), p3 = p - p1 - p2), which sum to the f32
+// value exactly: p has 24 significant bits and each RNE step leaves a
+// remainder of at most 16, then 8 of them. bf16 x bf16 products are exact in
+// f32, so scores and P v are f32 products with f32 accumulation -- the
+// reference's widen-to-f32 arithmetic up to the order of the sums -- on the
+// bf16 matrix cores; the row sum adds the f32 probabilities. The output is
+// rounded once, to bf16 or (p.out_f32) stored as f32.
+//
 // f32 matrix-core kernel (attn_mfma_f32_kernel): the same scheme on
 // v_mfma_f32_32x32x2_f32 for f32 inputs with D 64 / 128, f32 throughout.
 //
@@ -113,9 +123,11 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
 // QLN: q arrives raw; its LayerNorm and 2D RoPE (the QK kernel's arithmetic
 // and lane mapping, bit for bit) are applied while the Q fragments are
 // loaded, so the normalised q never goes through HBM.
+// EXACTP: f32 probabilities as three bf16 terms (see the file header).
 template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool QLN = false,
-          bool DMA = false>
+          bool DMA = false, bool EXACTP = false>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+  static_assert(!EXACTP || (std::is_same<T, BF16>::value && !DOT && !QLN), "exact probabilities: bf16, f32 sums");
   using M = Mma<T>;
   using op_t = typename M::op_t;
   constexpr int BQ = 4 * 32 * QT;
@@ -136,7 +148,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   const char *qbase = reinterpret_cast<const char *>(p.q) + (bi * p.q_sb + hi * p.q_sh) * 2;
   const char *kbase = reinterpret_cast<const char *>(p.k) + (bi * p.k_sb + hi * p.k_sh) * 2;
   const char *vbase = reinterpret_cast<const char *>(p.v) + (bi * p.v_sb + hi * p.v_sh) * 2;
-  char *obase = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh) * 2;
+  const int ob = EXACTP && p.out_f32 ? 4 : 2;  // output element bytes
+  char *obase = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh) * ob;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
@@ -353,6 +366,21 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       alpha_q[qt] = __builtin_amdgcn_exp2f(m[qt] - mn);
       m[qt] = mn;
       float ls = 0.f;
+      if constexpr (EXACTP) {
+        // f32 probabilities stay in s; split into bf16 terms at the P v product
+#pragma unroll
+        for (int kt = k0; kt < k1; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][i], c2, -mn));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][i + 1], c2, -mn));
+            s[qt][kt][i] = p0;
+            s[qt][kt][i + 1] = p1;
+            ls += p0 + p1;
+          }
+        l[qt] = l[qt] * alpha_q[qt] + ls;
+        return;
+      }
 #pragma unroll
       for (int kt = k0; kt < k1; ++kt)
 #pragma unroll
@@ -397,7 +425,39 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       const s16x4_t hi2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr + 8 * KROW));
       return __builtin_bit_cast(op_t, __builtin_shufflevector(lo, hi2, 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    if constexpr (PHASED && QT == 2) {
+    // EXACTP: O^T += V^T (P1 + P2 + P3)^T, the three bf16 terms of each f32
+    // probability pair built per 16-key step (one A fragment per dim tile)
+    auto pv_exact = [&](int qt) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          u32x4_t p1, p2, p3;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = s[qt][kt][8 * jj + 2 * e], b = s[qt][kt][8 * jj + 2 * e + 1];
+            p1[e] = pack_bf16x2(a, b);
+            const float ra = a - __uint_as_float(p1[e] << 16), rb = b - __uint_as_float(p1[e] & 0xffff0000u);
+            p2[e] = pack_bf16x2(ra, rb);
+            p3[e] = pack_bf16x2(ra - __uint_as_float(p2[e] << 16), rb - __uint_as_float(p2[e] & 0xffff0000u));
+          }
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const op_t a = vfrag(dt, kt, jj);
+            o[qt][dt] = M::run(a, __builtin_bit_cast(op_t, p1), o[qt][dt]);
+            o[qt][dt] = M::run(a, __builtin_bit_cast(op_t, p2), o[qt][dt]);
+            o[qt][dt] = M::run(a, __builtin_bit_cast(op_t, p3), o[qt][dt]);
+          }
+        }
+    };
+    if constexpr (EXACTP) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        softmax(qt, 0, NKT);
+        rescale(qt);
+        pv_exact(qt);
+      }
+    } else if constexpr (PHASED && QT == 2) {
       // P v of query tile 0 has no dependence on the softmax of tile 1:
       // issued together, the matrix cores and the VALU overlap in one wavefront
       softmax(0, 0, NKT);
@@ -448,7 +508,17 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     const int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
     const float inv = 1.f / half_swap_sum(l[qt]);
     if (qr >= Lq) continue;
-    char *orow = obase + qr * p.o_st * 2;
+    char *orow = obase + qr * p.o_st * ob;
+    if (EXACTP && p.out_f32) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(orow + (dt * 32 + 8 * g + 4 * hh) * 4) =
+              make_float4(o[qt][dt][4 * g] * inv, o[qt][dt][4 * g + 1] * inv, o[qt][dt][4 * g + 2] * inv,
+                          o[qt][dt][4 * g + 3] * inv);
+      continue;
+    }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -704,7 +774,7 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
   const char *qrow = reinterpret_cast<const char *>(p.q) + (bi * p.q_sb + hi * p.q_sh + qi * p.q_st) * EB;
   const char *kbase = reinterpret_cast<const char *>(p.k) + (bi * p.k_sb + hi * p.k_sh) * EB;
   const char *vbase = reinterpret_cast<const char *>(p.v) + (bi * p.v_sb + hi * p.v_sh) * EB;
-  char *orow = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh + qi * p.o_st) * EB;
+  char *orow = reinterpret_cast<char *>(p.o) + (bi * p.o_sb + hi * p.o_sh + qi * p.o_st) * (p.out_f32 ? 4 : EB);
   const int64_t D = p.D, Lk = p.Lk;
 
   float qv[DPL], o[DPL];
@@ -750,17 +820,24 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
 #pragma unroll
   for (int u = 0; u < DPL; ++u) {
     const int64_t d = lane + 64 * u;
-    if (d < D) store1<T>(orow, d, o[u] * inv);
+    if (d < D) {
+      if (p.out_f32) store1<F32>(orow, d, o[u] * inv);
+      else store1<T>(orow, d, o[u] * inv);
+    }
   }
 }
 
-template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool DMA>
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool DMA,
+          bool EXACTP = false>
 hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
   constexpr int BQ = 4 * 32 * QT;
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  if (p.qln)
+  if constexpr (EXACTP)
+    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, false, DMA, true>),
+                       dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  else if (p.qln)
     hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, true, DMA>), dim3((unsigned)nwg),
                        dim3(256), 0, s, p, nqb, nwg);
   else
@@ -816,6 +893,23 @@ constexpr int64_t kShortQ = 4096;
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if (p.qln && !(T::code != LUX3D_F32 && p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
+  if (p.qln && p.exact_p) return hipErrorInvalidValue;
+  if (p.out_f32 && !p.exact_p && T::code != LUX3D_F32) return hipErrorInvalidValue;
+  if (p.exact_p && T::code != LUX3D_F32) {
+    // f32 probabilities: the bf16 matrix-core kernel with three-term P, else
+    // the generic kernel (f32 throughout)
+    if constexpr (T::code == LUX3D_BF16) {
+      if (p.mfma && p.D == 64) {
+        if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, false, false, false, true>(p, s);
+        return launch_mfma<T, 64, 2, 64, 2, true, false, false, false, true>(p, s);
+      }
+      if (p.mfma && p.D == 128) {
+        if (dma_fits(p, 2)) return launch_mfma<T, 128, 1, 64, 2, true, false, false, true, true>(p, s);
+        return launch_mfma<T, 128, 1, 64, 2, true, false, false, false, true>(p, s);
+      }
+    }
+    return launch_generic<T>(p, s);
+  }
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {

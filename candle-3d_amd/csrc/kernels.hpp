@@ -130,6 +130,9 @@ struct AttnParams {
   int64_t o_sb = 0, o_sh = 0, o_st = 0;
   float scale = 0.f;
   bool mfma = false;
+  // exact_p: f32 probabilities and sums whatever the input type (the
+  // reference's exact_sdpa_heads); out_f32: out is f32 (exact_p or f32 inputs)
+  bool exact_p = false, out_f32 = false;
   // q LayerNorm + 2D RoPE applied in the Q load (matrix-core path): q is the
   // raw head view; qw / qb the LayerNorm affine (D elements); tables the
   // Rope2d cos_full / sin_alt_full, element (b, n, j) at b*tab_sB + n*tab_sN + j.

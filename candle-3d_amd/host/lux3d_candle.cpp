@@ -681,7 +681,7 @@ Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out) {
 Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float scale) {
   if (q.rank() != 4) fail(LUX3D_ERR_SHAPE, "sdpa: q must be [B, H, L, D], got " + dims_str(q.dims()));
   Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
-  abi_check(lux3d_sdpa(Desc(q).p(), Desc(k).p(), Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
+  abi_check(lux3d_sdpa_heads_f32(Desc(q).p(), Desc(k).p(), Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
   return out;
 }
 
@@ -696,7 +696,10 @@ Tensor sdpa_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeE
 }
 
 Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale, size_t) {
-  return exact_sdpa_heads(q, k, v, scale);
+  if (q.rank() != 4) fail(LUX3D_ERR_SHAPE, "sdpa: q must be [B, H, L, D], got " + dims_str(q.dims()));
+  Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
+  abi_check(lux3d_sdpa(Desc(q).p(), Desc(k).p(), Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
+  return out;
 }
 
 QMatMul QMatMul::from_q8_0(const Tensor &blocks, int64_t n, int64_t k) {

@@ -288,7 +288,8 @@ Tensor dequantize_q8_0(const Tensor &blocks, const Shape &shape, DType out);
 // Attention over [B, H, L, D] views: softmax(q k^T * scale) v, one kernel,
 // no scores buffer. exact_query_chunked_sdpa (attention_math.rs:199-241; the
 // chunk size only bounded the reference's scores buffer and is ignored) and
-// exact_sdpa_heads (attention_math.rs:244-259). Returns a contiguous
+// exact_sdpa_heads (attention_math.rs:244-259; f32 arithmetic whatever the
+// input dtype, lux3d_sdpa_heads_f32). Both return a contiguous
 // [B, H, Lq, D] tensor in q's dtype.
 Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale,
                                 size_t chunk_size = SIZE_MAX);

@@ -426,9 +426,13 @@ def exact_query_chunked_sdpa(q, k, v, scale: float, chunk_size: int = 0) -> torc
     return sdpa(q, k, v, scale)
 
 
-def exact_sdpa_heads(q, k, v, scale: float) -> torch.Tensor:
-    """attention_math.rs:244-259 (f32 arithmetic, output in q's dtype)."""
-    return sdpa(q, k, v, scale)
+def exact_sdpa_heads(q, k, v, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """attention_math.rs:244-259: f32 arithmetic whatever q's dtype, output
+    in q's dtype (default) or in `out`, which may also be f32."""
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _lib.call("lux3d_sdpa_heads_f32", desc(q), desc(k), desc(v), float(scale), desc(out), _stream(q))
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -515,9 +515,10 @@ def cfg2_q8_0_linear_f32(dev) -> Workload:
     return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection", torch.float32)
 
 
-def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16) -> Workload:
+def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16, heads_f32=False) -> Workload:
     """Attention over q, k, v taken as the permuted views of a fused
-    [B, N, 3, H, D] qkv buffer (vggt.rs:161-168), output [B, H, N, D]."""
+    [B, N, 3, H, D] qkv buffer (vggt.rs:161-168), output [B, H, N, D].
+    heads_f32: the exact_sdpa_heads entry (f32 arithmetic for any input)."""
     from . import _lib
     s = synth.config_seed(cfg) + 700
     esz = torch.empty((), dtype=dt).element_size()
@@ -531,13 +532,20 @@ def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16) -> Workl
         descs.append((ops.desc(v[0]), ops.desc(v[1]), ops.desc(v[2]), ops.desc(o)))
     scale = 1.0 / float(d) ** 0.5
 
+    entry = "lux3d_sdpa_heads_f32" if heads_f32 else "lux3d_sdpa"
+
     def launch(i):
         dq, dk, dv, do = descs[i % n_sets]
-        _lib.call("lux3d_sdpa", dq, dk, dv, scale, do, _cur())
+        _lib.call(entry, dq, dk, dv, scale, do, _cur())
     nbytes = 4 * b * h * n * d * esz
     f32 = dt == torch.float32
-    wl = Workload(name, cfg, f"attn_mfma_f32_kernel<{d}>" if f32 else f"attn_mfma_kernel<BF16,{d}>",
-                  "f32 (f32 matrix cores)" if f32 else "bf16 -> f32 acc", nbytes,
+    if f32:
+        kern, arith = f"attn_mfma_f32_kernel<{d}>", "f32 (f32 matrix cores)"
+    elif heads_f32:
+        kern, arith = f"attn_mfma_kernel<BF16,{d},...,EXACTP>", "bf16 in, f32 probabilities (3 bf16 terms), bf16 out"
+    else:
+        kern, arith = f"attn_mfma_kernel<BF16,{d}>", "bf16 -> f32 acc"
+    wl = Workload(name, cfg, kern, arith, nbytes,
                   f"q,k,v [{b},{h},{n},{d}] from qkv [{b},{n},3,{h},{d}] ({what})", launch, n_sets,
                   flops=4 * b * h * n * n * d, reps=reps, peak_tflops=157.3 if f32 else 0.0)
     wl._keep = (qkvs, outs, descs)
@@ -597,8 +605,16 @@ def cfg1_sdpa_global(dev) -> Workload:
 
 
 def cfg4_sdpa_dinov3(dev) -> Workload:
-    # the DINOv3 encoder's attention over its 1029 tokens (TRELLIS.2 image conditioning)
-    return _sdpa(dev, "sdpa_dinov3", 4, 1, 1029, 16, 64, "DINOv3 self-attention, 1029 tokens")
+    # the DINOv3 encoder's attention over its 1029 tokens (TRELLIS.2 image
+    # conditioning); the reference calls exact_sdpa_heads there (trellis2_dino.rs:392)
+    return _sdpa(dev, "sdpa_dinov3", 4, 1, 1029, 16, 64, "DINOv3 self-attention, 1029 tokens, exact_sdpa_heads",
+                 heads_f32=True)
+
+
+def cfg4_sdpa_dinov3_f32(dev) -> Workload:
+    # the same with f32 activations (the encoder run in f32)
+    return _sdpa(dev, "sdpa_dinov3_f32", 4, 1, 1029, 16, 64, "DINOv3 self-attention, 1029 tokens, f32",
+                 dt=torch.float32, heads_f32=True)
 
 
 def cfg2_sdpa(dev) -> Workload:
@@ -754,6 +770,7 @@ EXTRAS: List[Callable] = [
     cfg2_sdpa,
     cfg3_sdpa,
     cfg4_sdpa_dinov3,
+    cfg4_sdpa_dinov3_f32,
     cfg3_sparse_conv_c1024,
     cfg3_sparse_conv_c256,
     cfg3_sparse_conv_c256_output_stationary,

@@ -428,7 +428,8 @@ int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t 
  * lux3d_sdpa: out = softmax(q k^T * scale) v, replacing
  * exact_query_chunked_sdpa (runtime/attention_math.rs:199-241; its
  * chunk_size only bounds the scores buffer, which this kernel never
- * materialises) and exact_sdpa_heads (attention_math.rs:244-259).
+ * materialises), and exact_sdpa_heads (attention_math.rs:244-259) for f32
+ * inputs (for 2-byte inputs see lux3d_sdpa_heads_f32).
  *   q: [B, H, Lq, D]; k, v: [B, H, Lk, D]; out: [B, H, Lq, D];
  *   one dtype for all four (f32, bf16 or f16); any batch / head / token
  *   strides (the permuted views of a fused qkv buffer pass as they are),
@@ -443,6 +444,20 @@ int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t 
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
                lux3d_stream_t stream);
+
+/* lux3d_sdpa_heads_f32: exact_sdpa_heads (attention_math.rs:244-259), which
+ * widens q, k and v to f32, computes scores, softmax and P v in f32 and
+ * narrows the result to the input dtype. Arguments as lux3d_sdpa, except that
+ * out may be f32 as well as q's dtype (then the f32 result is stored, not
+ * narrowed). f32 inputs run as lux3d_sdpa. bf16 with D 64 / 128 and 16-byte
+ * aligned rows runs on the bf16 matrix cores: bf16 products are exact in f32,
+ * and the f32 probabilities enter P v as three bf16 terms whose sum is the
+ * f32 value exactly, so the arithmetic is f32 products with f32 accumulation.
+ * Other 2-byte cases run the generic kernel (f32 throughout). out must not
+ * overlap q, k or v.                                                          */
+int lux3d_sdpa_heads_f32(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
+                         const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
+                         lux3d_stream_t stream);
 
 /* lux3d_sdpa_layernorm_rope2d: the VGGT / Pi3 attention of vggt.rs:170-183,
  * exact_query_chunked_sdpa(apply_layernorm_rope(q, q_norm, rope), k, v,

@@ -403,6 +403,31 @@ void sparse_attention_matches_naive(const Device &dev) {
   }
 }
 
+// exact_sdpa_heads (attention_math.rs:244-259) on bf16 q, k, v: f32
+// arithmetic, the result narrowed to bf16 once. Against the naive f32
+// attention of the same (bf16-valued) inputs, each output is within one half
+// bf16 unit of the f32 value plus the f32 error of the naive sums. D 64 with
+// 16-byte rows runs the matrix-core kernel.
+void exact_sdpa_heads_bf16_is_f32_arithmetic(const Device &dev) {
+  const size_t H = 2, T = 70, TKV = 130, HD = 64;
+  auto pat = [&](size_t n, size_t seed) {
+    std::vector<float> x(H * n * HD);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = pattern_f32(i * 7 + seed * 3) * 3.0f;
+    return x;
+  };
+  const Tensor q = Tensor::from_f32(pat(T, 1), {1, (int64_t)H, (int64_t)T, (int64_t)HD}, DType::BF16, dev);
+  const Tensor k = Tensor::from_f32(pat(TKV, 2), {1, (int64_t)H, (int64_t)TKV, (int64_t)HD}, DType::BF16, dev);
+  const Tensor v = Tensor::from_f32(pat(TKV, 3), {1, (int64_t)H, (int64_t)TKV, (int64_t)HD}, DType::BF16, dev);
+  const Tensor out = exact_sdpa_heads(q, k, v, 1.0f / std::sqrt((float)HD));
+  CHECK(out.dtype() == DType::BF16);
+  const std::vector<float> got = out.to_vec_f32();
+  const std::vector<float> want = naive_attention(q.to_vec_f32(), k.to_vec_f32(), v.to_vec_f32(), H, T, TKV, HD);
+  size_t bad = 0;
+  for (size_t i = 0; i < got.size(); ++i)
+    if (std::fabs(got[i] - want[i]) > std::ldexp(std::fabs(want[i]), -8) + 1e-5f) ++bad;
+  CHECK(bad == 0);
+}
+
 // tests/trellis2_sparse.rs: kernel offsets, the coordinate map, the sparse
 // conv against a dense loop reference, identity / shift kernels, the loader
 // transpose and the C2S order.
@@ -672,6 +697,7 @@ int main(int argc, char **argv) {
       {"dequantize_q8_0_exact", dequantize_q8_0_exact, true},
       {"q8_0_linear_closed_form", q8_0_linear_closed_form, true},
       {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
+      {"exact_sdpa_heads_bf16_is_f32_arithmetic", exact_sdpa_heads_bf16_is_f32_arithmetic, true},
       {"vggt_attention_fused_equals_two_calls", vggt_attention_fused_equals_two_calls, true},
       {"gguf_q8_linear_from_file", gguf_q8_linear_from_file, true},
       {"kernel_offset_deltas_cover_the_3x3x3_kernel", kernel_offset_deltas_cover_the_3x3x3_kernel, false},

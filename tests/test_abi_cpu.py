@@ -284,6 +284,16 @@ def test_sdpa_argument_errors():
     assert rc == _lib.ERR_LAYOUT
     rc, msg = status("lux3d_sdpa", None, k, v, 0.125, o, None)
     assert rc == _lib.ERR_NULL
+    # exact_sdpa_heads: out has q's dtype or is f32; q, k, v share one dtype
+    rc, msg = status("lux3d_sdpa", q, k, v, 0.125, T([2, 4, 33, 64], _lib.F32), None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_sdpa_heads_f32", q, k, v, 0.125, T([2, 4, 33, 64], _lib.F16), None)
+    assert rc == _lib.ERR_DTYPE and "out has it or is f32" in msg
+    rc, msg = status("lux3d_sdpa_heads_f32", q, T([2, 4, 50, 64], _lib.F32), v, 0.125, T([2, 4, 33, 64], _lib.F32),
+                     None)
+    assert rc == _lib.ERR_DTYPE
+    rc, msg = status("lux3d_sdpa_heads_f32", q, k, v, -1.0, o, None)
+    assert rc == _lib.ERR_VALUE
 
 
 def test_sparse_argument_errors():
