@@ -251,13 +251,14 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) 
 // running on one XCD share x rows and weight columns in its L2.
 template <typename OUT, int GM, int BM, int NW = 8>
 __global__ __launch_bounds__(64 * NW, 1) void q8_0_gemm_ring_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
-  // NW wavefronts, each owning 32 columns: BN = 32 NW (256 or 128)
+  // NW wavefronts, each owning 32 columns: BN = 32 NW (256 or 128); BM a multiple of 32 up to 256
   constexpr int BN = 32 * NW, BK = 64, TM = BM / 32, NS = kRingStages;
   constexpr int RW = BN * 64, RS = BN * 8;          // weights and scales per stage
   constexpr int kRingA = BM * 128, kRingStage = kRingA + RW + RS;  // 51,200 / 34,816 / 25,600 bytes
   constexpr int SEGW = BM / (8 * NW);              // x segments (1 KB = 8 rows) per wavefront
   constexpr int kRingOps = SEGW + 2 + 1;           // direct loads per wavefront per stage
-  static_assert((BM == 128 || BM == 256) && (NW == 4 || NW == 8) && SEGW >= 1, "tile shape");
+  static_assert(BM % 32 == 0 && BM <= 256 && BM % (8 * NW) == 0 && (NW == 4 || NW == 8) && SEGW >= 1,
+                "tile shape");
   __shared__ __align__(16) char ring[NS * kRingStage];
 
   const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
@@ -382,8 +383,13 @@ __global__ __launch_bounds__(64 * NW, 1) void q8_0_gemm_ring_kernel(Q8GemmParams
     // stage the wavefront's BM x 32 block through the ring, RP rows per
     // pass (rows padded by 16 bytes), and store whole 16-byte row pieces
     constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB;
-    constexpr int RP = NW * 128 * LROW <= NS * kRingStage ? 128 : 64, REGION = RP * LROW;
-    static_assert(NW * REGION <= NS * kRingStage, "epilogue staging fits the ring");
+    // RP rows per pass: a multiple of 32 that divides BM and fits the ring
+    constexpr int CAP = NS * kRingStage;
+    constexpr int RP = NW * BM * LROW <= CAP ? BM
+                       : (BM % 128 == 0 && NW * 128 * LROW <= CAP) ? 128
+                       : (BM % 64 == 0 && NW * 64 * LROW <= CAP) ? 64 : 32;
+    constexpr int REGION = RP * LROW;
+    static_assert(NW * REGION <= CAP && BM % RP == 0, "epilogue staging fits the ring");
     __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
     char *reg = ring + wave * REGION;
     const int64_t c0w = c0 + wave * 32;
@@ -641,9 +647,11 @@ bool ring_fits(const Q8GemmParams &p) {
 // the ring kernel whenever K % 64 == 0 (every shape of the models): 256-row
 // tiles when they cover every CU at least once (1,018 TFLOP/s at
 // 4096x2048x8192, 512 tiles), else 128-row tiles of 8 wavefronts when those
-// do, else 128 x 128 tiles of 4 wavefronts (1029x1024x4096: 9 x 32 tiles,
-// 24.0 us against 26.8 us for 9 x 16 tiles of 8 wavefronts). The 128 x 128
-// kernel with 32-deep k-steps covers K % 64 == 32.
+// do, else tiles of 4 wavefronts: 160 x 128 when 128 x 128 ones would
+// outnumber the CUs but 160-row ones do not (1029x1024x4096: 7 x 32 tiles in
+// 19.2 us, against 23.5 us for 9 x 32 of 128 x 128, 26.8 us for 9 x 16 tiles
+// of 8 wavefronts, 22.4 us for 5 x 32 of 256 x 128), else 128 x 128. The
+// 128 x 128 kernel with 32-deep k-steps covers K % 64 == 32.
 constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
 
 template <typename OUT>
@@ -665,6 +673,15 @@ hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
       const int64_t tiles_m = (p.M + 127) / 128;
       hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 128>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0,
                          s, p, (int)tiles_m, (int)tiles_n);
+    } else if ((p.M + 127) / 128 * ((p.N + 127) / 128) > kRingMinTiles &&
+               (p.M + 159) / 160 * ((p.N + 127) / 128) <= kRingMinTiles) {
+      // fewer 128 x 256 tiles than CUs, more 128 x 128 ones: 160 x 128 tiles
+      // of four wavefronts, one per CU (the 128-row tiles would leave some CUs
+      // two; 1029 x 1024 -> 4096: 7 x 32 tiles in 19.2 us against 9 x 32 in
+      // 23.5 us)
+      const int64_t tiles_m = (p.M + 159) / 160, tiles_n128 = (p.N + 127) / 128;
+      hipLaunchKernelGGL((q8_0_gemm_ring_kernel<OUT, 8, 160, 4>), dim3((unsigned)(tiles_m * tiles_n128)), dim3(256), 0,
+                         s, p, (int)tiles_m, (int)tiles_n128);
     } else {
       // fewer 128 x 256 tiles than CUs: 128 x 128 tiles of four wavefronts
       // (two workgroups per CU by LDS) spread the same wavefronts over more CUs

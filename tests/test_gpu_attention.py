@@ -92,6 +92,8 @@ def _print_case(**kw):
 
 @pytest.mark.parametrize("b,n,h,d,dt,kscale,rising", [
     (2, 1374, 4, 64, "bf16", 1.0, False),     # VGGT frame-attention tokens (37 x 37 + 5)
+    (1, 2100, 16, 64, "bf16", 1.0, True),     # 16 heads, 17 query blocks each
+    (2, 2100, 16, 64, "bf16", 2.0, False),
     (1, 517, 3, 128, "bf16", 2.0, True),     # TRELLIS.2 head dim, peaky and moving maxima
     (2, 300, 2, 64, "f16", 3.0, True),
     (1, 129, 2, 128, "f16", 1.0, False),
@@ -108,7 +110,8 @@ def test_sdpa_self_attention_mfma(dev, ops, orc, b, n, h, d, dt, kscale, rising)
     assert_attn_close(out, want, wabs, dt, True, f"self {b}x{h}x{n}x{d} {dt}")
 
 
-@pytest.mark.parametrize("lq,lk,d", [(300, 517, 128), (1, 1, 64), (5, 1, 64), (1, 200, 128), (257, 64, 64)])
+@pytest.mark.parametrize("lq,lk,d", [(300, 517, 128), (1, 1, 64), (5, 1, 64), (1, 200, 128), (257, 64, 64),
+                                     (40, 129, 64), (100, 200, 64), (33, 4000, 64)])
 def test_sdpa_cross_attention_and_edges(dev, ops, orc, lq, lk, d):
     _print_case(lq=lq, lk=lk, d=d)
     g = torch.Generator(device="cpu").manual_seed(lq * 7 + lk)

@@ -74,10 +74,12 @@ def make_problem(synth, orc, dev, m, k, n, seed, bias=True):
     return xd, blocks, b
 
 
-# K % 64 == 0 takes the LDS-ring kernel with 128-row tiles at these sizes
-# (fewer than 256 tiles of 256 rows); (77, 96, 100) takes the 128 x 128
-# kernel with 32-deep k-steps. The 256-row ring tiles: the ring-kernel test
-# and the large sampled test below.
+# K % 64 == 0 takes the LDS-ring kernel: at these sizes (fewer than 256
+# tiles of 256 rows) 160 x 128 tiles when 128 x 128 ones would exceed the CUs
+# (1029 x 1024 -> 4096: 7 x 32 tiles), 128 x 128 tiles of four wavefronts
+# otherwise; (77, 96, 100) takes the 128 x 128 kernel with 32-deep k-steps.
+# The 256-row ring tiles: the ring-kernel test and the large sampled test
+# below.
 @pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136), (77, 96, 100),
                                    (64, 128, 100)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
@@ -232,12 +234,12 @@ def test_q8_0_linear_f32_strided_and_rejects_k96(dev, ops, orc, synth):
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 @pytest.mark.parametrize("extra", [0, 3])
 def test_q8_0_linear_four_wavefront_tiles(dev, ops, orc, synth, out, extra):
-    """x [300, 256] -> [300, 200]: 3 x 1 tiles of 128 x 256 cannot fill the
-    CUs, so the ring kernel runs 3 x 2 tiles of 128 x 128 with four
-    wavefronts (the last column tile holds 72 columns, the last row tile 44
-    rows). y is a view of a buffer `extra` columns wider: aligned rows take
-    the staged epilogue, unaligned rows the per-element stores."""
-    m, k, n = 300, 256, 200
+    """x [300, 192] -> [300, 200]: 3 x 1 tiles of 128 x 256 cannot fill the
+    CUs, so the ring kernel runs 3 x 2 tiles of 128 x 128
+    with four wavefronts (the last column tile holds 72 columns, the last row
+    tile 44 rows). y is a view of a buffer `extra` columns wider: aligned
+    rows take the staged epilogue, unaligned rows the per-element stores."""
+    m, k, n = 300, 192, 200
     print(f"\n[case] q8_0_linear four-wavefront tiles out={out} ldy={n + extra}", flush=True)
     xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 820 + extra)
     ywide = torch.zeros((m, n + extra), dtype=TDT[out], device=dev)
@@ -249,5 +251,30 @@ def test_q8_0_linear_four_wavefront_tiles(dev, ops, orc, synth, out, extra):
     want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, b, orc.F32 if out == "f32" else orc.BF16,
                                     with_abs=True)
     assert_gemm_close(host(ywide[:, :n], out), want, abs_sum, out, "four-wavefront tiles")
+    if extra:
+        assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"
+
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("extra", [0, 3])
+@pytest.mark.parametrize("m", [1029, 1001])
+def test_q8_0_linear_160_row_tiles(dev, ops, orc, synth, out, extra, m):
+    """[m, 1024] -> 4096 (the configs[4] weight): 9 x 32 tiles of 128 x 128
+    would exceed the 256 CUs, 7 x 32 of 160 x 128 do not, so those run (one
+    per CU). The last row tile holds 69 (m 1029) or 41 (m 1001) rows; y rows
+    aligned (staged epilogue) or not (per-element stores)."""
+    k, n = 1024, 4096
+    print(f"\n[case] q8_0_linear 160-row tiles m={m} out={out} ldy={n + extra}", flush=True)
+    xd, blocks, b = make_problem(synth, orc, dev, m, k, n, 900 + m + extra)
+    ywide = torch.zeros((m, n + extra), dtype=TDT[out], device=dev)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(blocks).to(dev), n, k)
+    from lux3d_fused import _lib
+    _lib.call("lux3d_q8_0_linear", ops.desc(xd), ops.desc(qs), ops.desc(scales), ops.desc(torch.from_numpy(b).to(dev)),
+              ops.desc(ywide[:, :n]), None)
+    torch.cuda.synchronize()
+    odt = {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}[out]
+    want, abs_sum = orc.q8_0_linear(host(xd, "bf16"), blocks, n, b, odt, with_abs=True)
+    assert_gemm_close(host(ywide[:, :n], out), want, abs_sum, out, f"160-row tiles m={m}")
     if extra:
         assert torch.all(ywide[:, n:] == 0), "columns past n must stay untouched"

@@ -99,6 +99,7 @@ def _check(ops, orc, q, k, v, scale, dt, what):
     (2, 129, 2, 128, 1.0, False, 3),      # one full block + one key
     (1, 65, 1, 64, 4.0, False, 4),
     (1, 4200, 2, 64, 1.0, True, 5),       # > 4096 queries: two query tiles per wavefront
+    (1, 2100, 16, 64, 1.0, False, 6),
 ])
 def test_sdpa_heads_f32_bf16_matrix_cores(dev, ops, orc, b, n, h, d, kscale, rising, seed):
     _case(b=b, n=n, h=h, d=d, seed=seed)
@@ -106,7 +107,8 @@ def test_sdpa_heads_f32_bf16_matrix_cores(dev, ops, orc, b, n, h, d, kscale, ris
     _check(ops, orc, q, k, v, 1.0 / np.sqrt(d), "bf16", f"bf16 {b}x{h}x{n}x{d}")
 
 
-@pytest.mark.parametrize("lq,lk,d", [(300, 517, 128), (1, 1, 64), (5, 1, 64), (257, 64, 64), (77, 200, 128)])
+@pytest.mark.parametrize("lq,lk,d", [(300, 517, 128), (1, 1, 64), (5, 1, 64), (257, 64, 64), (77, 200, 128),
+                                     (40, 129, 64), (100, 200, 64)])
 def test_sdpa_heads_f32_cross_attention(dev, ops, orc, lq, lk, d):
     """Cross-attention shapes (TripoSG's exact_sdpa_heads call sits on the
     encoder's keys), including single keys and partial key blocks."""
