@@ -144,8 +144,10 @@ def committed_trace(tag):
     if not os.path.exists(path):
         return None
     try:
-        k = _json_block(path)["kernels"][0]
-        return k["name"], k["avg_us"], k["calls"]
+        blk = _json_block(path)
+        k = blk["kernels"][0]
+        # several kernels per op launch: their summed time per op launch
+        return k["name"], blk.get("op_us_per_launch", k["avg_us"]), k["calls"]
     except (IndexError, ValueError, KeyError):
         return None
 
@@ -332,6 +334,8 @@ def main():
                 us = time_graph(torch, wl.launch, args.iters)
                 print(json.dumps({"op": tag, "us_per_launch_graph": round(us, 3),
                                   "gbs": round(wl.bytes / us / 1e3, 1), "bytes": wl.bytes,
+                                  "flops": wl.flops or 0, "peak_tflops": (wl.peak_tflops or PEAK_BF16_TFLOPS)
+                                  if wl.flops else 0, "kernel": wl.kernel,
                                   "launches": 3 + 6 * args.iters}), flush=True)
                 return
             del wl
@@ -429,6 +433,9 @@ def main():
         if tr:
             row.update({"trace_us": tr[1], "trace_frac_peak": round(nbytes / tr[1] / 1e3 / PEAK_GBS, 4),
                         "trace_kernel": tr[0]})
+            if flops:
+                row.update({"trace_tflops": round(flops / tr[1] / 1e6, 1),
+                            "trace_frac_mfma_peak": round(flops / tr[1] / 1e6 / peak_tf, 4)})
         tb = committed_traffic(tag)
         if tb:
             row["traffic_bytes"] = tb

@@ -2,16 +2,18 @@
 
   python -m lux3d_fused.rocprof_summary stats <kernel_stats.csv> "<command>" > profiles/<name>.md
   python -m lux3d_fused.rocprof_summary trace <kernel_stats.csv> <kernel-substring> <bytes> "<command>" \
-        [<stdout of the profiled command>] > profiles/kernel_trace_<op>.md
+        [<stdout of the profiled command> [<flops per launch> <peak TFLOP/s>]] > profiles/kernel_trace_<op>.md
   python -m lux3d_fused.rocprof_summary traffic <fetch.csv> <write.csv> <cal_fetch.csv> <cal_write.csv> \
         <kernel-substring> "<command>" > profiles/<name>.md
   python -m lux3d_fused.rocprof_summary counters <counter_collection.csv> <kernel-substring> "<command>" \
         > profiles/<name>.md
 
 `trace` reports the kernels whose name contains <kernel-substring> (the op's
-own kernels; the workload set-up kernels are listed apart), each with its
+own kernels, alternatives separated by `|`; the workload set-up kernels are
+listed apart), each with its
 average duration and the achieved bandwidth for <bytes> algorithmic bytes
-per launch, in a JSON block that bench.py reads back.
+per launch (and, for matrix-core ops, the achieved TFLOP/s for <flops> per
+launch against <peak>), in a JSON block that bench.py reads back.
 `counters` reports the median per-dispatch value of every counter in the
 file for the matching kernels, and per-wavefront instruction counts when
 SQ_WAVES was collected.
@@ -50,39 +52,67 @@ def stats(path, command):
     return "\n".join(out) + "\n"
 
 
-def _profiled_events(log_path):
-    """The HIP-event time per launch that `bench.py --profile` printed while
-    it ran under the profiler (its JSON line), or None."""
+def _profiled_line(log_path):
+    """The JSON line `bench.py --profile` printed while it ran under the
+    profiler (HIP-event time per launch, op launches, bytes, flops), or {}."""
     if not log_path:
-        return None
+        return {}
     for line in open(log_path):
         if line.startswith("{") and '"us_per_launch_graph"' in line:
-            return json.loads(line)["us_per_launch_graph"]
-    return None
+            return json.loads(line)
+    return {}
 
 
-def trace(path, kernel_sub, nbytes, command, log_path=None):
+def trace(path, kernel_sub, nbytes, command, log_path=None, flops=None, peak_tflops=None):
     rows = _rows(path)
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    mine = [r for r in rows if kernel_sub in r["Name"]]
-    rest = [r for r in rows if kernel_sub not in r["Name"]]
+    subs = kernel_sub.split("|")
+    mine = [r for r in rows if any(s in r["Name"] for s in subs)]
+    rest = [r for r in rows if r not in mine]
     nbytes = int(nbytes)
+    flops = int(flops) if flops else None
+    peak = float(peak_tflops) if peak_tflops else None
     res = {"bytes_per_launch": nbytes, "kernels": []}
+    if flops:
+        res.update({"flops_per_launch": flops, "peak_tflops": peak})
+    single = len(mine) == 1  # per-kernel rates only when one kernel is the whole op
     for r in mine:
         avg = float(r["AverageNs"]) / 1e3
-        res["kernels"].append({"name": r["Name"], "calls": int(r["Calls"]), "avg_us": round(avg, 3),
-                               "min_us": round(float(r["MinNs"]) / 1e3, 3),
-                               "max_us": round(float(r["MaxNs"]) / 1e3, 3),
-                               "gbs": round(nbytes / avg / 1e3, 1), "frac_of_8tbs": round(nbytes / avg / 8e6, 4)})
+        k = {"name": r["Name"], "calls": int(r["Calls"]), "avg_us": round(avg, 3),
+             "min_us": round(float(r["MinNs"]) / 1e3, 3), "max_us": round(float(r["MaxNs"]) / 1e3, 3)}
+        if single:
+            k.update({"gbs": round(nbytes / avg / 1e3, 1), "frac_of_8tbs": round(nbytes / avg / 8e6, 4)})
+            if flops:
+                k.update({"tflops": round(flops / avg / 1e6, 1),
+                          "frac_of_peak_tflops": round(flops / avg / 1e6 / peak, 4)})
+        res["kernels"].append(k)
+    what = (f"bandwidth = {nbytes:,} algorithmic bytes per launch / average duration" +
+            (f"; rate = {flops:,} flops per launch / average duration, against {peak} TFLOP/s" if flops else ""))
     out = ["# rocprofv3 kernel trace", "", f"Command: `{command}`", "", NOTE, "",
-           f"Kernels matching `{kernel_sub}` (the op's own launches, all on cold rotation sets); "
-           f"bandwidth = {nbytes:,} algorithmic bytes per launch / average duration.", "",
-           "| kernel | calls | avg us | min us | max us | GB/s | of 8 TB/s |", "|---|---|---|---|---|---|---|"]
+           f"Kernels matching `{kernel_sub}` (the op's own launches, all on cold rotation sets); {what}.", ""]
+    if flops:
+        out += ["| kernel | calls | avg us | min us | max us | GB/s | TFLOP/s | of peak |",
+                "|---|---|---|---|---|---|---|---|"]
+    else:
+        out += ["| kernel | calls | avg us | min us | max us | GB/s | of 8 TB/s |", "|---|---|---|---|---|---|---|"]
     for k in res["kernels"]:
         name = k["name"].replace("|", "/")
+        if single:
+            rates = f"{k['gbs']:,.1f} | " + (f"{k['tflops']:,.1f} | {k['frac_of_peak_tflops']:.4f} |" if flops
+                                              else f"{k['frac_of_8tbs']:.4f} |")
+        else:
+            rates = "- | - | - |" if flops else "- | - |"
         out.append(f"| `{name[:110]}` | {k['calls']} | {k['avg_us']:.3f} | {k['min_us']:.3f} | {k['max_us']:.3f} | "
-                   f"{k['gbs']:,.1f} | {k['frac_of_8tbs']:.4f} |")
-    ev = _profiled_events(log_path)
+                   + rates)
+    run = _profiled_line(log_path)
+    if run.get("launches") and len(res["kernels"]) > 1:
+        # several kernels per op launch: the op's time is their summed durations per launch
+        op_us = sum(float(r["TotalDurationNs"]) for r in mine) / 1e3 / run["launches"]
+        res["op_us_per_launch"] = round(op_us, 3)
+        out += ["", f"Op time per launch (the matching kernels' summed durations / {run['launches']} op launches): "
+                    f"{op_us:.3f} us" + (f", {flops / op_us / 1e6:,.1f} TFLOP/s ({flops / op_us / 1e6 / peak:.4f} of "
+                                         f"{peak} TFLOP/s)" if flops else f", {nbytes / op_us / 1e3:,.1f} GB/s") + "."]
+    ev = run.get("us_per_launch_graph")
     if ev is not None:
         res["events_us_under_profiler"] = ev
         out += ["", f"The same launches timed with HIP events around the graph replays, inside the profiled run: "
@@ -168,7 +198,7 @@ def main(argv):
     if argv[0] == "stats":
         sys.stdout.write(stats(argv[1], argv[2]))
     elif argv[0] == "trace":
-        sys.stdout.write(trace(*argv[1:6]))
+        sys.stdout.write(trace(*argv[1:8]))
     elif argv[0] == "counters":
         sys.stdout.write(counters(*argv[1:4]))
     elif argv[0] == "traffic":
