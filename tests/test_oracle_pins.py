@@ -683,6 +683,28 @@ def test_sdpa_bf16_inputs_round_once():
     assert np.allclose(wabs, p @ np.abs(v64), rtol=1e-6)
 
 
+def test_sdpa_f32_bar_rejects_bf16_probabilities():
+    """The bar the GPU exact_sdpa_heads path is held to (attention_math.rs:
+    244-259: f32 scores, softmax and P v), |err| <= 1e-5 * wabs +
+    2^-23 |want| against the oracle's f32 output, at the DINOv3 length (1029
+    tokens, D 64, 4 heads): the exact f64 attention passes it everywhere,
+    and the same attention with the probabilities rounded to bf16 before
+    P v (the exact_query_chunked_sdpa path's rounding) fails it on most
+    outputs, so the bar can tell the two arithmetics apart."""
+    rng = np.random.default_rng(13)
+    q, k, v = (orc.bf16_bits(rng.standard_normal((4, 1029, 64))) for _ in range(3))
+    want, wabs = orc.sdpa(q, k, v, 0.125, dt=orc.BF16, out_dt=orc.F32, with_abs=True)
+    q64, k64, v64 = (torch.from_numpy(orc.bf16_to_f32(a).astype(np.float64)) for a in (q, k, v))
+    s = (q64 @ k64.transpose(1, 2)) * 0.125
+    p = torch.exp(s - s.amax(-1, keepdim=True))
+    bound = 1e-5 * wabs.astype(np.float64) + 2.0 ** -23 * np.abs(want.astype(np.float64))
+    exact = ((p @ v64) / p.sum(-1, keepdim=True)).numpy()
+    assert np.all(np.abs(exact - want) <= bound)
+    pb = p.to(torch.float32).to(torch.bfloat16).to(torch.float64)
+    rounded = ((pb @ v64) / pb.sum(-1, keepdim=True)).numpy()
+    assert np.mean(np.abs(rounded - want) > bound) > 0.5
+
+
 # ---- TRELLIS.2 sparse ops ---------------------------------------------------
 
 def _delta(k):
