@@ -43,8 +43,10 @@
 // bf16 matrix cores; the row sum adds the f32 probabilities. The output is
 // rounded once, to bf16 or (p.out_f32) stored as f32.
 //
-// f32 matrix-core kernel (attn_mfma_f32_kernel): the same scheme on
-// v_mfma_f32_32x32x2_f32 for f32 inputs with D 64 / 128, f32 throughout.
+// f32 inputs (attn_f32x3_kernel, D 64 / 128): the same scheme on the bf16
+// matrix cores, with q, k, v and the probabilities split exactly into three
+// bf16 terms each and the six significant cross products per MFMA step;
+// f32-class arithmetic at 6 / 16 of the f32 MFMA's matrix-core cycles.
 //
 // Generic kernel (attn_generic_kernel): one wavefront per query row, f32
 // arithmetic throughout (lanes over keys for the scores, over head dims for
@@ -90,6 +92,29 @@ template <> struct Mma<F16> {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), one, acc, false);
   }
 };
+
+// Exact three-term bf16 split of two f32 values a, b (packed pairs, low half
+// = a): a = a1 + a2 + a3 exactly. a has 24 significant bits; a1 = RNE_bf16(a)
+// leaves a remainder of at most 16 significant bits, a2 = RNE_bf16 of that
+// one of at most 8, which bf16 holds exactly (bf16 has f32's exponent range).
+struct Split3 {
+  uint32_t t1, t2, t3;
+};
+__device__ __forceinline__ Split3 split3_bf16(float a, float b) {
+  Split3 r;
+  r.t1 = pack_bf16x2(a, b);
+  const float ra = a - __uint_as_float(r.t1 << 16), rb = b - __uint_as_float(r.t1 & 0xffff0000u);
+  r.t2 = pack_bf16x2(ra, rb);
+  r.t3 = pack_bf16x2(ra - __uint_as_float(r.t2 << 16), rb - __uint_as_float(r.t2 & 0xffff0000u));
+  return r;
+}
+// the same into element e of three packed operand vectors
+__device__ __forceinline__ void split3_into(float a, float b, u32x4_t &x1, u32x4_t &x2, u32x4_t &x3, int e) {
+  const Split3 r = split3_bf16(a, b);
+  x1[e] = r.t1;
+  x2[e] = r.t2;
+  x3[e] = r.t3;
+}
 
 // The value the partner lane (lane ^ 32) holds, paired with this lane's own:
 // v_permlane32_swap exchanges the two 32-lane halves.
@@ -434,13 +459,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         for (int jj = 0; jj < 2; ++jj) {
           u32x4_t p1, p2, p3;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = s[qt][kt][8 * jj + 2 * e], b = s[qt][kt][8 * jj + 2 * e + 1];
-            p1[e] = pack_bf16x2(a, b);
-            const float ra = a - __uint_as_float(p1[e] << 16), rb = b - __uint_as_float(p1[e] & 0xffff0000u);
-            p2[e] = pack_bf16x2(ra, rb);
-            p3[e] = pack_bf16x2(ra - __uint_as_float(p2[e] << 16), rb - __uint_as_float(p2[e] & 0xffff0000u));
-          }
+          for (int e = 0; e < 4; ++e)
+            split3_into(s[qt][kt][8 * jj + 2 * e], s[qt][kt][8 * jj + 2 * e + 1], p1, p2, p3, e);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             const op_t a = vfrag(dt, kt, jj);
@@ -530,36 +550,33 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   }
 }
 
-// ---- f32 matrix-core kernel ----------------------------------------------------
+// ---- f32 inputs on the bf16 matrix cores (three-term split) --------------------
 //
-// v_mfma_f32_32x32x2_f32 keeps everything in f32: scores, probabilities (not
-// rounded) and output sums; that is exact_sdpa_heads (attention_math.rs:
-// 244-259) up to the order of the sums. A workgroup of 4 wavefronts owns 128
-// queries (32 per wavefront) of one (batch, head); K and V blocks of BKV keys
-// are double-buffered in LDS, as in the 2-byte kernel.
-//   S^T = K Q^T   k-step c covers dims {c, D/2 + c}: lane half hh supplies
-//                 dim hh * D/2 + c, so each lane's K and Q values are
-//                 contiguous (four k-steps per 16-byte LDS read; Q held in
-//                 registers).
-//   O^T += V^T P^T  k-step i of a 32-key tile pairs the two keys the lane
-//                 halves hold in S^T's i-th accumulator, 8 (i/4) + 4 hh +
-//                 i % 4: each lane passes its own probability, and V is read
-//                 in its natural [key][dim] layout (no transpose).
-template <int D, int BKV, int MINW, bool DMA = false>
-__global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+// f32 q, k and v are split exactly into three bf16 terms each (x = x1 + x2 +
+// x3, split3_bf16). A product x y is then the sum of nine bf16 x bf16
+// products, each exact in f32; the three smallest (x2 y3, x3 y2, x3 y3)
+// together stay below 2^-25 |x y|, under half an f32 ulp of the product, and
+// are dropped. Each MFMA step of S = K Q^T and of O^T += V^T P^T becomes six
+// bf16 MFMAs (smallest terms first) accumulating in f32; the probabilities
+// are f32 and split the same way, the row sum adds them in f32. That is the
+// f32 arithmetic of exact_sdpa_heads (attention_math.rs:244-259) up to the
+// order of the sums and that sub-half-ulp truncation per product, at 6 / 16
+// of the matrix-core cycles of v_mfma_f32_32x32x2_f32 (which runs at 1/16
+// of the bf16 rate). Layout as attn_mfma_kernel with QT = 1: K and V blocks
+// of BKV keys are loaded as f32 (keys past Lk clamped to Lk - 1, their scores
+// masked), split in registers and stored as three bf16 planes each, [key][dim]
+// rows padded by 16 bytes, double-buffered.
+template <int D, int BKV, int MINW>
+__global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
+  using op_t = bf16x8_t;
+  using M = Mma<BF16>;
   constexpr int BQ = 128;
-  // Padded rows: K + 4 floats (16-byte fragment reads conflict-free), V + 8
-  // (the lane halves' rows, 4 apart, 32 banks apart). DMA: unpadded rows,
-  // 16-byte chunk c of row r in slot c ^ sw(r), sw(r) = (r & 3) | 8 ((r >> 2) & 1),
-  // which keeps both reads conflict-free.
-  constexpr int KROW = DMA ? D : D + 4;
-  constexpr int VROW = DMA ? D : D + 8;
-  constexpr int KCH = BKV * D / 4 / 256;   // 16-byte chunks of K (and of V) per thread per block
-  constexpr int NKT = BKV / 32, NDT = D / 32, HD = D / 2;
+  constexpr int KROW = D + 8;              // bf16 per plane row
+  constexpr int PL = BKV * KROW;           // one plane of one block
+  constexpr int KCH = BKV * D / 4 / 256;   // 16-byte f32 chunks of K (and of V) per thread per block
+  constexpr int NKT = BKV / 32, NDT = D / 32;
   static_assert(KCH >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
-  __shared__ __align__(16) float smem[2 * BKV * KROW + 2 * BKV * VROW];
-  float(*Ks)[BKV * KROW] = reinterpret_cast<float(*)[BKV * KROW]>(smem);
-  float(*Vs)[BKV * VROW] = reinterpret_cast<float(*)[BKV * VROW]>(smem + 2 * BKV * KROW);
+  __shared__ __align__(16) uint16_t smem[2 * 6 * PL];  // [buffer][K planes 0..2, V planes 0..2]
 
   const int64_t lid = xcd_logical_id(blockIdx.x, nwg);
   const int64_t bh = lid / nqb, qb = lid % nqb;
@@ -572,70 +589,57 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
   const int l32 = lane & 31, hh = lane >> 5;
   const int64_t Lq = p.Lq, Lk = p.Lk;
 
-  // Q as the B operand: lane holds Q[query l32][hh * D/2 + c], c < D/2
-  float qf[HD];
+  // Q as the B operand, three terms: lane holds Q[query l32][c * 16 + 8 * hh + e]
+  op_t q1[D / 16], q2[D / 16], q3[D / 16];
   {
     int64_t qr = qb * BQ + wave * 32 + l32;
     qr = qr < Lq ? qr : Lq - 1;
+    const float *qrow = qbase + qr * p.q_st;
 #pragma unroll
-    for (int c4 = 0; c4 < HD / 4; ++c4) {
-      const float4 v4 = *reinterpret_cast<const float4 *>(qbase + qr * p.q_st + hh * HD + c4 * 4);
-      qf[c4 * 4] = v4.x; qf[c4 * 4 + 1] = v4.y; qf[c4 * 4 + 2] = v4.z; qf[c4 * 4 + 3] = v4.w;
+    for (int c = 0; c < D / 16; ++c) {
+      const float4 a = *reinterpret_cast<const float4 *>(qrow + c * 16 + 8 * hh);
+      const float4 b = *reinterpret_cast<const float4 *>(qrow + c * 16 + 8 * hh + 4);
+      u32x4_t x1, x2, x3;
+      split3_into(a.x, a.y, x1, x2, x3, 0);
+      split3_into(a.z, a.w, x1, x2, x3, 1);
+      split3_into(b.x, b.y, x1, x2, x3, 2);
+      split3_into(b.z, b.w, x1, x2, x3, 3);
+      q1[c] = __builtin_bit_cast(op_t, x1);
+      q2[c] = __builtin_bit_cast(op_t, x2);
+      q3[c] = __builtin_bit_cast(op_t, x3);
     }
   }
   // staging: chunk c = t + 256 i holds K / V row c / (D/4), floats 4 (c % (D/4)) ..
-  int s_row[KCH], s_part[KCH];
+  int s_row[KCH], s_c4[KCH];
 #pragma unroll
   for (int i = 0; i < KCH; ++i) {
     const int c = t + i * 256;
     s_row[i] = c / (D / 4);
-    s_part[i] = c % (D / 4);
+    s_c4[i] = c % (D / 4);
   }
   float4 rk[KCH], rv[KCH];
-  auto sw = [](int r) { return (r & 3) | (((r >> 2) & 1) << 3); };
-  // DMA: load i of a wavefront fills LDS bytes [seg * 1024, + 1024) of a
-  // buffer (seg = wave * KCH + i) in lane order. Per block, the descriptors
-  // start at the block's first key and the range-checked per-lane offset
-  // holds the in-block offset (the scalar offset is not range-checked), so
-  // keys past Lk fall outside and read as zeros (finite; their scores are
-  // masked)
-  uint32_t dk_off[KCH], dv_off[KCH];
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
-    const int byte = (wave * KCH + i) * 1024 + lane * 16, r = byte / (4 * D), c = ((byte % (4 * D)) / 16) ^ sw(r);
-    dk_off[i] = (uint32_t)((r * p.k_st + c * 4) * 4);
-    dv_off[i] = (uint32_t)((r * p.v_st + c * 4) * 4);
-  }
-  const int64_t kbytes = ((Lk - 1) * p.k_st + D) * 4, vbytes = ((Lk - 1) * p.v_st + D) * 4;
-  const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)smem;
-  const uint32_t lds_v = lds_k + 2 * BKV * KROW * 4;
-  auto dma_kv = [&](int64_t j, int buf) {
-    const int64_t sk = j * BKV * p.k_st * 4, sv = j * BKV * p.v_st * 4;
-    const i32x4_t krs = buffer_rsrc(reinterpret_cast<const char *>(kbase) + sk, kbytes - sk);
-    const i32x4_t vrs = buffer_rsrc(reinterpret_cast<const char *>(vbase) + sv, vbytes - sv);
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const uint32_t off = (uint32_t)((wave * KCH + i) * 1024);
-      lds_load16(krs, dk_off[i], 0, __builtin_amdgcn_readfirstlane(lds_k + off + buf * BKV * KROW * 4));
-      lds_load16(vrs, dv_off[i], 0, __builtin_amdgcn_readfirstlane(lds_v + off + buf * BKV * VROW * 4));
-    }
-  };
-  // keys past Lk read row Lk - 1 (finite data; their scores are masked)
   auto load_kv = [&](int64_t j) {
     const int64_t key0 = j * BKV;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       int64_t key = key0 + s_row[i];
       key = key < Lk ? key : Lk - 1;
-      rk[i] = *reinterpret_cast<const float4 *>(kbase + key * p.k_st + s_part[i] * 4);
-      rv[i] = *reinterpret_cast<const float4 *>(vbase + key * p.v_st + s_part[i] * 4);
+      rk[i] = *reinterpret_cast<const float4 *>(kbase + key * p.k_st + s_c4[i] * 4);
+      rv[i] = *reinterpret_cast<const float4 *>(vbase + key * p.v_st + s_c4[i] * 4);
     }
   };
   auto store_kv = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      *reinterpret_cast<float4 *>(&Ks[buf][s_row[i] * KROW + s_part[i] * 4]) = rk[i];
-      *reinterpret_cast<float4 *>(&Vs[buf][s_row[i] * VROW + s_part[i] * 4]) = rv[i];
+      const int off = s_row[i] * KROW + s_c4[i] * 4;
+      const Split3 ka = split3_bf16(rk[i].x, rk[i].y), kb = split3_bf16(rk[i].z, rk[i].w);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 0) * PL + off) = make_uint2(ka.t1, kb.t1);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 1) * PL + off) = make_uint2(ka.t2, kb.t2);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 2) * PL + off) = make_uint2(ka.t3, kb.t3);
+      const Split3 va = split3_bf16(rv[i].x, rv[i].y), vb = split3_bf16(rv[i].z, rv[i].w);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 3) * PL + off) = make_uint2(va.t1, vb.t1);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 4) * PL + off) = make_uint2(va.t2, vb.t2);
+      *reinterpret_cast<uint2 *>(smem + (buf * 6 + 5) * PL + off) = make_uint2(va.t3, vb.t3);
     }
   };
 
@@ -647,35 +651,35 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
   const int64_t nkv = (Lk + BKV - 1) / BKV;
   const bool tail = (Lk % BKV) != 0;
 
-  if constexpr (DMA) {
-    dma_kv(0, 0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  } else {
-    load_kv(0);
-    store_kv(0);
-  }
+  load_kv(0);
+  store_kv(0);
   lds_barrier();
 
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   auto step = [&](int64_t j, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
     const int buf = (int)(j & 1);
-    if constexpr (DMA) {
-      if (j + 1 < nkv) dma_kv(j + 1, buf ^ 1);
-    } else {
-      if (j + 1 < nkv) load_kv(j + 1);
-    }
+    if (j + 1 < nkv) load_kv(j + 1);
+    const uint16_t *K1 = smem + (buf * 6 + 0) * PL, *K2 = smem + (buf * 6 + 1) * PL, *K3 = smem + (buf * 6 + 2) * PL;
+
+    // S^T = K Q^T: lane holds key 8 * (i / 4) + 4 * hh + i % 4 of each 32-key tile, query l32
     f32x16_t s[NKT];
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
       s[kt] = f32x16_t{};
 #pragma unroll
-      for (int c4 = 0; c4 < HD / 4; ++c4) {
-        const int krow = kt * 32 + l32, kch = DMA ? ((hh * (HD / 4) + c4) ^ sw(krow)) : hh * (HD / 4) + c4;
-        const float4 a4 = *reinterpret_cast<const float4 *>(&Ks[buf][krow * KROW + kch * 4]);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, qf[c4 * 4], s[kt], 0, 0, 0);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, qf[c4 * 4 + 1], s[kt], 0, 0, 0);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, qf[c4 * 4 + 2], s[kt], 0, 0, 0);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, qf[c4 * 4 + 3], s[kt], 0, 0, 0);
+      for (int c = 0; c < D / 16; ++c) {
+        const int off = (kt * 32 + l32) * KROW + (2 * c + hh) * 8;
+        const op_t a1 = *reinterpret_cast<const op_t *>(K1 + off);
+        const op_t a2 = *reinterpret_cast<const op_t *>(K2 + off);
+        const op_t a3 = *reinterpret_cast<const op_t *>(K3 + off);
+        s[kt] = M::run(a3, q1[c], s[kt]);
+        s[kt] = M::run(a2, q2[c], s[kt]);
+        s[kt] = M::run(a1, q3[c], s[kt]);
+        s[kt] = M::run(a2, q1[c], s[kt]);
+        s[kt] = M::run(a1, q2[c], s[kt]);
+        s[kt] = M::run(a1, q1[c], s[kt]);
       }
     }
     if constexpr (MASK) {
@@ -686,8 +690,8 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
         for (int i = 0; i < 16; ++i)
           if (kt * 32 + 8 * (i >> 2) + (i & 3) >= lim) s[kt][i] = -INFINITY;
     }
-    // online softmax; the reference maximum moves only when a block's maximum
-    // exceeds it by 2^8 (probabilities stay <= 256), as in the 2-byte kernel
+    // online softmax in f32; the reference maximum moves only when a block's
+    // maximum exceeds it by 2^8 (probabilities stay <= 256)
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt)
@@ -702,37 +706,57 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_f32_kernel(AttnParams p, 
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][i], c2, -mn));
-        ls += s[kt][i];
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][i], c2, -mn));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][i + 1], c2, -mn));
+        s[kt][i] = p0;
+        s[kt][i + 1] = p1;
+        ls += p0 + p1;
       }
     l = l * alpha + ls;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
     }
-    // O^T += V^T P^T
+    // O^T += V^T P^T with three-term V and P: A = V^T fragments of each plane
+    // (ds_read_b64_tr_b16 from V's [key][dim] rows, as in attn_mfma_kernel)
+    auto vfrag = [&](int pl, int dt, int kt, int jj) {
+      const int g16 = lane & 15;
+      const int vrow = kt * 32 + 16 * jj + 4 * hh + (g16 >> 2);
+      const int vcol = dt * 32 + 16 * ((lane >> 4) & 1) + 4 * (g16 & 3);
+      const uint16_t *vr = smem + (buf * 6 + 3 + pl) * PL + vrow * KROW + vcol;
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr));
+      const s16x4_t hi2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vr + 8 * KROW));
+      return __builtin_bit_cast(op_t, __builtin_shufflevector(lo, hi2, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int vrow = kt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-        const float *vr = &Vs[buf][vrow * VROW];
+      for (int jj = 0; jj < 2; ++jj) {
+        u32x4_t x1, x2, x3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) split3_into(s[kt][8 * jj + 2 * e], s[kt][8 * jj + 2 * e + 1], x1, x2, x3, e);
+        const op_t P1 = __builtin_bit_cast(op_t, x1), P2 = __builtin_bit_cast(op_t, x2);
+        const op_t P3 = __builtin_bit_cast(op_t, x3);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          const int vcol = dt * 32 + l32, vc = DMA ? (((vcol >> 2) ^ sw(vrow)) << 2) | (vcol & 3) : vcol;
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[vc], s[kt][i], o[dt], 0, 0, 0);
+          const op_t v1 = vfrag(0, dt, kt, jj), v2 = vfrag(1, dt, kt, jj), v3 = vfrag(2, dt, kt, jj);
+          o[dt] = M::run(v3, P1, o[dt]);
+          o[dt] = M::run(v2, P2, o[dt]);
+          o[dt] = M::run(v1, P3, o[dt]);
+          o[dt] = M::run(v2, P1, o[dt]);
+          o[dt] = M::run(v1, P2, o[dt]);
+          o[dt] = M::run(v1, P1, o[dt]);
         }
       }
-    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wavefront's block j + 1 landed
-    else if (j + 1 < nkv) store_kv(buf ^ 1);
+    if (j + 1 < nkv) store_kv(buf ^ 1);
     lds_barrier();
   };
   const int64_t nfull = tail ? nkv - 1 : nkv;
   for (int64_t j = 0; j < nfull; ++j) step(j, std::false_type{});
   if (tail) step(nkv - 1, std::true_type{});
 
-  // out[query][dim]: lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
+  // out[query][dim] (f32): lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
   const int64_t qr = qb * BQ + wave * 32 + l32;
   const float inv = 1.f / half_swap_sum(l);
   if (qr < Lq) {
@@ -867,18 +891,12 @@ bool dma_fits(const AttnParams &p, int eb) {
   return p.k_st >= 0 && p.v_st >= 0 && ((p.Lk + 64) * st + p.D) * eb < (int64_t(1) << 31);
 }
 
-// K / V as direct global -> LDS loads when every key offset of a head fits
-// the 32-bit buffer offsets (bit-identical; VGGT frame attention 537 against
-// 568 us, TripoSG 519 against 676 us), else register-staged.
 template <int D, int BKV, int MINW>
-hipError_t launch_mfma_f32(const AttnParams &p, hipStream_t s) {
+hipError_t launch_f32x3(const AttnParams &p, hipStream_t s) {
   const int64_t nqb = (p.Lq + 127) / 128;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  if (dma_fits(p, 4))
-    hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW, true>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
-  else
-    hipLaunchKernelGGL((attn_mfma_f32_kernel<D, BKV, MINW, false>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  hipLaunchKernelGGL((attn_f32x3_kernel<D, BKV, MINW>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
   return hipGetLastError();
 }
 
@@ -923,11 +941,13 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
     }
   } else {
     if (p.mfma) {
-      // 32-key blocks at D 64: 127 VGPRs and 36 KB of LDS, four wavefronts
-      // per SIMD (VGGT frame attention in f32: 572 against 670 us for 64-key
-      // blocks at two)
-      if (p.D == 64) return launch_mfma_f32<64, 32, 2>(p, s);
-      if (p.D == 128) return launch_mfma_f32<128, 32, 2>(p, s);
+      // f32 on the bf16 matrix cores (three-term splits), 32-key blocks: at
+      // D 64 55 KB of LDS and 173 VGPRs, two workgroups per CU; at D 128
+      // 104 KB, one. Against the f32 MFMA kernel this replaced (same box,
+      // graph-timed): VGGT frame 342 against 541 us, TripoSG 401 against 523,
+      // DINOv3 52.5 against 86.0
+      if (p.D == 64) return launch_f32x3<64, 32, 2>(p, s);
+      if (p.D == 128) return launch_f32x3<128, 32, 1>(p, s);
     }
   }
   return launch_generic<T>(p, s);

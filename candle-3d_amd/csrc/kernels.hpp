@@ -118,7 +118,7 @@ hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s);
 
 // Scaled dot-product attention over [B, H, L, D] views (element strides per
 // batch, head and token; unit inner stride). out = softmax(q k^T * scale) v.
-// `mfma` selects the matrix-core kernel (bf16 / f16, D 64 or 128, every row
+// `mfma` selects the matrix-core kernels (D 64 or 128, every row
 // 16-byte aligned); otherwise the generic kernel (any float dtype, D <= 512).
 struct AttnParams {
   const void *q = nullptr, *k = nullptr, *v = nullptr;

@@ -540,14 +540,17 @@ def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16, heads_f3
     nbytes = 4 * b * h * n * d * esz
     f32 = dt == torch.float32
     if f32:
-        kern, arith = f"attn_mfma_f32_kernel<{d}>", "f32 (f32 matrix cores)"
+        kern, arith = f"attn_f32x3_kernel<{d}>", "f32 (bf16 matrix cores, three-term splits)"
     elif heads_f32:
         kern, arith = f"attn_mfma_kernel<BF16,{d},...,EXACTP>", "bf16 in, f32 probabilities (3 bf16 terms), bf16 out"
     else:
         kern, arith = f"attn_mfma_kernel<BF16,{d}>", "bf16 -> f32 acc"
     wl = Workload(name, cfg, kern, arith, nbytes,
                   f"q,k,v [{b},{h},{n},{d}] from qkv [{b},{n},3,{h},{d}] ({what})", launch, n_sets,
-                  flops=4 * b * h * n * n * d, reps=reps, peak_tflops=157.3 if f32 else 0.0)
+                  flops=4 * b * h * n * n * d, reps=reps,
+                  # f32 runs six bf16 MFMAs per product step (three-term splits):
+                  # its matrix-core ceiling is the dense bf16 peak / 6
+                  peak_tflops=2500.0 / 6 if f32 else 0.0)
     wl._keep = (qkvs, outs, descs)
     return wl
 

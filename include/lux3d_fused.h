@@ -437,9 +437,12 @@ int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t 
  * D = 64 or 128 with every row 16-byte aligned runs on the matrix cores:
  * bf16 / f16 with f32 scores, f32 softmax, the probabilities rounded to the
  * input type for P v (f32 accumulation) and one rounding of the output; f32
- * on the f32 matrix cores with scores, probabilities and sums all in f32.
- * Other cases run a generic kernel in f32 throughout. The f32 paths are the
- * arithmetic of exact_sdpa_heads up to the order of the sums. out must not
+ * on the bf16 matrix cores with q, k, v and the probabilities split exactly
+ * into three bf16 terms each and the six significant cross products per
+ * step (each product within half an f32 ulp), scores, probabilities and sums
+ * in f32. Other cases run a generic kernel in f32 throughout. The f32 paths
+ * are the arithmetic of exact_sdpa_heads up to the order of the sums (and,
+ * on the matrix cores, that sub-half-ulp product truncation). out must not
  * overlap q, k or v.                                                         */
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,

@@ -185,10 +185,11 @@ def test_sdpa_generic_kernel(dev, ops, orc, case):
 @pytest.mark.parametrize("b,n,h,d,lk", [(2, 300, 3, 64, None), (1, 257, 2, 128, None), (1, 77, 2, 128, 130),
                                          (1, 1, 1, 64, 1), (1, 33, 2, 64, 1000)])
 def test_sdpa_f32_matrix_cores(dev, ops, orc, b, n, h, d, lk):
-    """f32 q, k, v with D 64 / 128 take the f32 matrix-core kernel
-    (v_mfma_f32_32x32x2_f32, f32 scores and probabilities): self-attention on
-    the permuted views of a fused qkv buffer, and cross-attention with key
-    counts that leave a partial block."""
+    """f32 q, k, v with D 64 / 128 take the matrix-core kernel for f32
+    (attn_f32x3_kernel: three-term bf16 splits, f32 scores and
+    probabilities), held to the f32 bar: self-attention on the permuted views
+    of a fused qkv buffer, and cross-attention with key counts that leave a
+    partial block."""
     _print_case(op="sdpa f32 mfma", b=b, n=n, h=h, d=d, lk=lk)
     if lk is None:
         q, k, v = qkv_views(dev, b, n, h, d, "f32", 17 + n)
@@ -284,8 +285,7 @@ def test_sdpa_keys_past_lk_are_not_read(dev, ops, orc, dt, d, lk):
     every head hold NaN: every read stays inside the allocation, and a kernel
     that fetched a key past Lk would turn the masked 0 * V into NaN outputs.
     Lk leaves a partial last block on every path (32-key f32 blocks, 64-key
-    bf16 / f16 blocks), including the direct-load ones (f32 D 64 / 128,
-    bf16 / f16 D 128)."""
+    bf16 / f16 blocks), including the direct-load ones (bf16 / f16 D 128)."""
     _print_case(op="sdpa nan tail", dt=dt, d=d, lk=lk)
     b, h, lq = 2, 3, 96
     g = torch.Generator(device="cpu").manual_seed(lk * 3 + d)
@@ -319,7 +319,8 @@ def test_sdpa_register_staged_path_matches_direct_loads(dev, ops, dt, d, lk):
     address a head's keys (a negative token stride here). Keys and values
     read backwards through a negative stride, and the same keys flipped into
     a contiguous buffer, are the same logical sequence: the two paths must
-    agree bit for bit."""
+    agree bit for bit. (f32 has only the register-staged kernel, which must
+    take the negative stride the same way.)"""
     from lux3d_fused import _lib
     _print_case(op="sdpa register path", dt=dt, d=d, lk=lk)
     b, h, lq = 1, 2, 130

@@ -123,7 +123,7 @@ def test_sdpa_heads_f32_cross_attention(dev, ops, orc, lq, lk, d):
 @pytest.mark.parametrize("case", ["f16_d64", "bf16_d80", "bf16_unaligned", "f32_d64"])
 def test_sdpa_heads_f32_other_paths(dev, ops, orc, case):
     """f16 (generic kernel), bf16 with D 80 or unaligned rows (generic
-    kernel), f32 (the f32 matrix cores)."""
+    kernel), f32 (the three-term split kernel for f32 inputs)."""
     _case(case=case)
     dt = case.split("_")[0]
     d = 80 if case.endswith("d80") else 64
