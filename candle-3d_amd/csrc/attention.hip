@@ -93,21 +93,6 @@ template <> struct Mma<F16> {
   }
 };
 
-// Exact three-term bf16 split of two f32 values a, b (packed pairs, low half
-// = a): a = a1 + a2 + a3 exactly. a has 24 significant bits; a1 = RNE_bf16(a)
-// leaves a remainder of at most 16 significant bits, a2 = RNE_bf16 of that
-// one of at most 8, which bf16 holds exactly (bf16 has f32's exponent range).
-struct Split3 {
-  uint32_t t1, t2, t3;
-};
-__device__ __forceinline__ Split3 split3_bf16(float a, float b) {
-  Split3 r;
-  r.t1 = pack_bf16x2(a, b);
-  const float ra = a - __uint_as_float(r.t1 << 16), rb = b - __uint_as_float(r.t1 & 0xffff0000u);
-  r.t2 = pack_bf16x2(ra, rb);
-  r.t3 = pack_bf16x2(ra - __uint_as_float(r.t2 << 16), rb - __uint_as_float(r.t2 & 0xffff0000u));
-  return r;
-}
 // the same into element e of three packed operand vectors
 __device__ __forceinline__ void split3_into(float a, float b, u32x4_t &x1, u32x4_t &x2, u32x4_t &x3, int e) {
   const Split3 r = split3_bf16(a, b);

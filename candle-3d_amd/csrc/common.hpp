@@ -40,6 +40,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Exact three-term bf16 split of two f32 values a, b (packed pairs, low half
+// = a): a = a1 + a2 + a3. a has 24 significant bits; a1 = RNE_bf16(a) leaves
+// a remainder of at most 16 significant bits, a2 = RNE_bf16 of that one of at
+// most 8, which bf16 holds exactly (bf16 has f32's exponent range). Exact
+// while a3 stays a normal number, i.e. for |a| above about 2^-110; below, the
+// lost part is under 2^-126 in absolute terms.
+struct Split3 {
+  uint32_t t1, t2, t3;
+};
+__device__ __forceinline__ Split3 split3_bf16(float a, float b) {
+  Split3 r;
+  r.t1 = pack_bf16x2(a, b);
+  const float ra = a - __uint_as_float(r.t1 << 16), rb = b - __uint_as_float(r.t1 & 0xffff0000u);
+  r.t2 = pack_bf16x2(ra, rb);
+  r.t3 = pack_bf16x2(ra - __uint_as_float(r.t2 << 16), rb - __uint_as_float(r.t2 & 0xffff0000u));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
   typedef float f32x2_t __attribute__((ext_vector_type(2)));

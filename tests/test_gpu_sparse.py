@@ -113,6 +113,7 @@ def test_sparse_conv3d_reference_cases(dev, ops, orc):
     (5000, 128, 128, 64, True),
     (777, 32, 40, 16, False),
     (20000, 256, 256, 64, True),
+    (1500, 48, 40, 16, False),
 ])
 @pytest.mark.parametrize("path", ["output_stationary", "rulebook"])
 def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface, path):
