@@ -9,8 +9,8 @@
 //    outputs may differ in size (Q8_0 dequant reads 34-byte blocks and writes
 //    twice as many bytes);
 //  - rows: the row kernels' layout -- a row of `row_bytes` owned by TPR
-//    threads, thread t holding chunks c*TPR + t (c < NC) of 8 elements
-//    (16 bytes for 2-byte types, 32 for f32), 256-thread workgroups of whole
+//    threads, thread t holding units c*TPR + t (c < NC) of 16 bytes (or 32
+//    with elem_bytes 4: 8 f32 in a row), 256-thread workgroups of whole
 //    rows (or one row per workgroup when TPR is 128 / 256 and the op runs a
 //    row per workgroup);
 //  - heads: the head kernels' layout -- [B, H, N, D] views with any outer

@@ -5,9 +5,10 @@
 //
 // Mapping. A row of D elements is owned by TPR threads (one wavefront for
 // TPR = 64, or 2 / 4 wavefronts reducing through LDS for short row counts).
-// Thread t holds chunks c = 0..NC-1 of 8 elements at element
-// (c*TPR + t)*8, so each load instruction of a wavefront reads 1 KiB (bf16)
-// or 2 KiB (f32) of contiguous row data. The whole row stays in registers:
+// Thread t holds chunks c = 0..NC-1 of 8 elements: for 2-byte types the 8
+// elements at (c*TPR + t)*8, for f32 the 4 at (2c*TPR + t)*4 and the 4 at
+// ((2c+1)*TPR + t)*4 (chunk_at), so each 16-byte load or store instruction
+// of a wavefront covers 1 KiB of contiguous row data. The whole row stays in registers:
 // HBM traffic is exactly one read of every input and one write of every
 // output. Statistics are two-pass over the registers (mean, then centred sum
 // of squares), reduced with DPP + permlane swaps (no LDS for TPR = 64).
@@ -98,6 +99,88 @@ __device__ __forceinline__ void lds8(const float *src, int64_t idx, float (&v)[8
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Element offsets of chunk c of lane t in a row: its two 4-element halves.
+// 2-byte types: 8 consecutive elements (one 16-byte access). f32: the halves
+// lie TPR * 4 elements apart, so that every 16-byte access instruction of a
+// wavefront covers 1 KiB of contiguous row (32 consecutive bytes per lane
+// would make each instruction touch 2 KiB with half of it used; the copy
+// of that layout measured 12-16% slower than the interleaved one at the
+// configs' f32 rows). The row's statistics do not depend on which elements a
+// lane holds, and every operand of an element uses the same offsets.
+struct ChunkAt {
+  int64_t o0, o1;
+};
+template <typename T, int TPR>
+__device__ __forceinline__ ChunkAt chunk_at(int c, int t) {
+  if constexpr (T::bytes == 4) return {(int64_t)(2 * c * TPR + t) * 4, (int64_t)((2 * c + 1) * TPR + t) * 4};
+  else return {(int64_t)(c * TPR + t) * 8, (int64_t)(c * TPR + t) * 8 + 4};
+}
+template <typename T>
+__device__ __forceinline__ void ld_row(const char *row, ChunkAt a, float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    const uint4 x = ld16<LUX3D_NT_STREAMS != 0>(row + a.o0 * 4), y = ld16<LUX3D_NT_STREAMS != 0>(row + a.o1 * 4);
+    v[0] = __uint_as_float(x.x); v[1] = __uint_as_float(x.y); v[2] = __uint_as_float(x.z); v[3] = __uint_as_float(x.w);
+    v[4] = __uint_as_float(y.x); v[5] = __uint_as_float(y.y); v[6] = __uint_as_float(y.z); v[7] = __uint_as_float(y.w);
+  } else {
+    Chunk<T>::load(row + a.o0 * T::bytes, v);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st_row(char *row, ChunkAt a, const float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    st16(row + a.o0 * 4, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                    __float_as_uint(v[3])));
+    st16(row + a.o1 * 4, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                    __float_as_uint(v[7])));
+  } else {
+    Chunk<T>::store(row + a.o0 * T::bytes, v);
+  }
+}
+// 4 parameters of dtype dt at element i (cached loads), or dflt
+__device__ __forceinline__ void param4(const void *p, int dt, int64_t i, float dflt, float *v) {
+  if (dt == LUX3D_F32) {
+    const float4 a = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(p) + i);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  } else if (dt == LUX3D_BF16 || dt == LUX3D_F16) {
+    const uint2 a = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p) + i);
+    const uint32_t w[2] = {a.x, a.y};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t h = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      v[k] = dt == LUX3D_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = dflt;
+  }
+}
+// the parameters of chunk a (offset by off elements)
+template <typename T>
+__device__ __forceinline__ void param_at(const void *p, int dt, int64_t off, ChunkAt a, float dflt, float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    param4(p, dt, off + a.o0, dflt, v);
+    param4(p, dt, off + a.o1, dflt, v + 4);
+  } else {
+    param8(p, dt, off + a.o0, dflt, v);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void mod_at(const ModPiece &m, int64_t seg, ChunkAt a, float dflt, float (&v)[8]) {
+  param_at<T>(m.p, m.dt, seg * m.ld, a, dflt, v);
+  if (m.base_dt >= 0) {
+    float b[8];
+    param_at<T>(m.base, m.base_dt, 0, a, 0.f, b);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = b[k] + v[k];
+  }
+}
+__device__ __forceinline__ void lds_at(const float *src, ChunkAt a, float (&v)[8]) {
+  const float4 x = *reinterpret_cast<const float4 *>(src + a.o0);
+  const float4 y = *reinterpret_cast<const float4 *>(src + a.o1);
+  v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+}
+
 template <typename T, int TPR, int NC, int MODE, int BLOCK = kBlock, bool STAGE = false>
 __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   static_assert(BLOCK % TPR == 0, "a block holds whole rows");
@@ -118,14 +201,14 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   float v[NC][8];
   const char *xr = reinterpret_cast<const char *>(p.x) + row * p.x_rs * EB;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) Chunk<T>::load(xr + (int64_t)(c * TPR + t) * 8 * EB, v[c]);
+  for (int c = 0; c < NC; ++c) ld_row<T>(xr, chunk_at<T, TPR>(c, t), v[c]);
   // GATE_MOD: the branch rows are loaded with x, ahead of the segment lookup
   // and the staging barrier, so both streams are in flight together
   float hb[MODE == ROW_GATE_MOD ? NC : 1][8];
   if constexpr (MODE == ROW_GATE_MOD) {
     const char *ar = reinterpret_cast<const char *>(p.a) + row * p.a_rs * EB;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) Chunk<T>::load(ar + (int64_t)(c * TPR + t) * 8 * EB, hb[c]);
+    for (int c = 0; c < NC; ++c) ld_row<T>(ar, chunk_at<T, TPR>(c, t), hb[c]);
   }
 
   // segment of this row; with STAGE, whether the workgroup shares one
@@ -150,14 +233,14 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
     char *yr = reinterpret_cast<char *>(p.y) + row * p.y_rs * EB;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
       float hv[8], g[8];
-      Chunk<T>::load(ar + idx * EB, hv);
-      if (staged) lds8(st.gate, idx, g);
-      else mod8(p.gate, seg, idx, 1.f, g);
+      ld_row<T>(ar, at, hv);
+      if (staged) lds_at(st.gate, at, g);
+      else mod_at<T>(p.gate, seg, at, 1.f, g);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[c][k] = add_rn(v[c][k], mul_rn(hv[k], g[k]));
-      if (live) Chunk<T>::store(yr + idx * EB, v[c]);
+      if (live) st_row<T>(yr, at, v[c]);
     }
     return;
   }
@@ -170,19 +253,19 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
     const bool gated = p.gate.dt >= 0;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
       float g[8];
       if (!gated) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) g[k] = 1.f;
       } else if (staged) {
-        lds8(st.gate, idx, g);
+        lds_at(st.gate, at, g);
       } else {
-        mod8(p.gate, seg, idx, 1.f, g);
+        mod_at<T>(p.gate, seg, at, 1.f, g);
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[c][k] = Chunk<T>::round_trip(add_rn(v[c][k], mul_rn(hb[c][k], g[k])));
-      if (live) Chunk<T>::store(hr + idx * EB, v[c]);
+      if (live) st_row<T>(hr, at, v[c]);
     }
   }
 
@@ -191,10 +274,10 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
     char *hr = reinterpret_cast<char *>(p.h) + row * p.h_rs * EB;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
       float av[8], g[8];
-      Chunk<T>::load(ar + idx * EB, av);
-      param8(p.g, p.g_dt, idx, 1.f, g);
+      ld_row<T>(ar, at, av);
+      param_at<T>(p.g, p.g_dt, 0, at, 1.f, g);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         // LayerScale product and residual add as two roundings (no FMA
@@ -202,7 +285,7 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
         const float ls = p.g_dt >= 0 ? mul_rn(av[k], g[k]) : av[k];
         v[c][k] = Chunk<T>::round_trip(add_rn(ls, v[c][k]));  // the norm reads the stored h
       }
-      if (live) Chunk<T>::store(hr + idx * EB, v[c]);
+      if (live) st_row<T>(hr, at, v[c]);
     }
   }
 
@@ -229,14 +312,14 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
       float sh[8], sc1[8], out[8];
       if (staged) {
-        lds8(st.shift, idx, sh);
-        lds8(st.scale1, idx, sc1);
+        lds_at(st.shift, at, sh);
+        lds_at(st.scale1, at, sc1);
       } else {
-        mod8(p.shift, seg, idx, 0.f, sh);
-        mod8(p.scale, seg, idx, 0.f, sc1);
+        mod_at<T>(p.shift, seg, at, 0.f, sh);
+        mod_at<T>(p.scale, seg, at, 0.f, sc1);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sc1[k] = sc1[k] + 1.0f;
       }
@@ -244,23 +327,23 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * sc1[k] + sh[k];
       if (MODE == ROW_MODULATE && p.gate.dt >= 0) {  // M1' output gate (GATE_MOD's gate is the residual's)
         float g[8];
-        if (staged) lds8(st.gate, idx, g);
-        else mod8(p.gate, seg, idx, 1.f, g);
+        if (staged) lds_at(st.gate, at, g);
+        else mod_at<T>(p.gate, seg, at, 1.f, g);
 #pragma unroll
         for (int k = 0; k < 8; ++k) out[k] = g[k] * out[k] + v[c][k];
       }
-      if (live) Chunk<T>::store(yr + idx * EB, out);
+      if (live) st_row<T>(yr, at, out);
     }
   } else {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t idx = (int64_t)(c * TPR + t) * 8;
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
       float w[8], b[8], out[8];
-      param8(p.w, p.w_dt, idx, 1.f, w);
-      param8(p.b, p.b_dt, idx, 0.f, b);
+      param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
+      param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);
 #pragma unroll
       for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * w[k] + b[k];
-      if (live) Chunk<T>::store(yr + idx * EB, out);
+      if (live) st_row<T>(yr, at, out);
     }
   }
 }

@@ -76,7 +76,9 @@ class Copy:
 
             def launch(i):
                 a = args[i % n]
-                _check(LIB.lux3d_ceiling_rows(a[0], nin, a[1], nout, rows, rb, pattern["eb"], pattern["tpr"],
+                # the row kernels move 16-byte units for every dtype (8 bf16 /
+                # f16 elements, or half of an f32 chunk): the 2-byte form of the copy
+                _check(LIB.lux3d_ceiling_rows(a[0], nin, a[1], nout, rows, rb, 2, pattern["tpr"],
                                               int(pattern.get("row_per_block", False)), stream()), "rows")
             self.bytes = per_set
         elif kind == "heads" and not same_size:

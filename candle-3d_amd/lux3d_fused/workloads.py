@@ -103,7 +103,7 @@ def cfg0_layer_norm(dev) -> Workload:
     return wl
 
 
-def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps) -> Workload:
+def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps, name="residual_layer_norm") -> Workload:
     from . import _lib
     s = synth.config_seed(cfg)
     d = shape[-1]
@@ -125,7 +125,6 @@ def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps) -> Workload:
     def launch(i):
         dx, da, dh, dy = D[i % n]
         _lib.call("lux3d_residual_layer_norm", dx, da, dg, dw, dbb, eps, dh, dy, _cur())
-    name = "residual_layer_norm"
     wl = Workload(name, cfg, "row_kernel<RESID_LN>", "bf16" if dt == torch.bfloat16 else "f32", nbytes,
                   str(list(shape)), launch, n)
     rows = x0.numel() // d
@@ -140,15 +139,25 @@ def cfg1_residual_layer_norm(dev) -> Workload:
     return _residual_ln(dev, 1, (8, 1374, 1024), torch.bfloat16, (1.0, 0.02), 1e-5)
 
 
+def cfg1_residual_layer_norm_f32(dev) -> Workload:
+    # the configs[1] pre-block in f32, VGGT's precision in the reference (vggt.rs:571-574)
+    return _residual_ln(dev, 1, (8, 1374, 1024), torch.float32, (1.0, 0.02), 1e-5, name="residual_layer_norm_f32")
+
+
 def cfg4_residual_layer_norm(dev) -> Workload:
     return _residual_ln(dev, 4, (1, 1029, 1024), torch.float32, (1e-5, 1e-6), 1e-5)
 
 
-def cfg1_qk_layernorm_rope2d(dev, tables: bool = False) -> Workload:
+def cfg1_qk_layernorm_rope2d_f32(dev) -> Workload:
+    return cfg1_qk_layernorm_rope2d(dev, dt=torch.float32)
+
+
+def cfg1_qk_layernorm_rope2d(dev, tables: bool = False, dt=torch.bfloat16) -> Workload:
     from . import _lib
     B, N, H, D = 8, 1374, 16, 64
     s = synth.config_seed(1)
-    qkv0 = _normal(s + 7, (B, N, 3, H, D), dev, torch.bfloat16)
+    esz = torch.empty((), dtype=dt).element_size()
+    qkv0 = _normal(s + 7, (B, N, 3, H, D), dev, dt)
     qw = _normal(s + 21, (D,), dev, torch.float32, 1.0, 0.02)
     qb = _normal(s + 22, (D,), dev, torch.float32, 0.0, 0.02)
     kw = _normal(s + 23, (D,), dev, torch.float32, 1.0, 0.02)
@@ -156,12 +165,12 @@ def cfg1_qk_layernorm_rope2d(dev, tables: bool = False) -> Workload:
     pos = _t(synth.vggt_positions(B, 37, 37), dev)
     emb = ops.Rope2d(100.0).embeddings(pos, D) if tables else None
     qk_elems = B * N * H * D
-    nbytes = 2 * qk_elems * 2 * 2 + 4 * D * 4
+    nbytes = 2 * qk_elems * esz * 2 + 4 * D * 4
     nbytes += (2 * B * N * D * 4) if tables else (B * N * 2 * 4)
-    n = _n_sets(nbytes + qk_elems * 2)  # + the v third that shares the qkv buffer
+    n = _n_sets(nbytes + qk_elems * esz)  # + the v third that shares the qkv buffer
     qkvs = [_fill_like(qkv0, k) for k in range(n)]
-    outs = [(torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev),
-             torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev)) for _ in range(n)]
+    outs = [(torch.empty((B, H, N, D), dtype=dt, device=dev),
+             torch.empty((B, H, N, D), dtype=dt, device=dev)) for _ in range(n)]
     Ds = []
     for k in range(n):
         perm = qkvs[k].permute(2, 0, 3, 1, 4)
@@ -178,9 +187,11 @@ def cfg1_qk_layernorm_rope2d(dev, tables: bool = False) -> Workload:
         else:
             _lib.call("lux3d_qk_layernorm_rope2d_pos", dq, dqw, dqb, dk, dkw, dkb, 1e-5, dpos, 100.0, dqo, dko,
                       _cur())
-    name = "qk_layernorm_rope2d" + ("_tables" if tables else "")
-    wl = Workload(name, 1, "head_kernel<BF16,64,LN,R1>", "bf16", nbytes, f"q,k [{B},{H},{N},{D}] in qkv", launch, n)
-    wl.pattern = {"kind": "heads", "B": B, "H": H, "N": N, "D": D, "eb": 2, "ntens": 2, "both_in_one": False,
+    f32 = dt == torch.float32
+    name = "qk_layernorm_rope2d" + ("_tables" if tables else "") + ("_f32" if f32 else "")
+    wl = Workload(name, 1, f"head_kernel<{'F32' if f32 else 'BF16'},64,LN,R1>", "f32" if f32 else "bf16", nbytes,
+                  f"q,k [{B},{H},{N},{D}] in qkv", launch, n)
+    wl.pattern = {"kind": "heads", "B": B, "H": H, "N": N, "D": D, "eb": esz, "ntens": 2, "both_in_one": False,
                   "in_numel": B * N * 3 * H * D, "in_offsets": [0, H * D],
                   "in_strides": [N * 3 * H * D, D, 3 * H * D], "out_strides": [H * N * D, N * D, D]}
     wl._keep = (qkvs, outs, Ds, qw, qb, kw, kb, pos, emb, dqw, dqb, dkw, dkb, dpos, dc, ds)
@@ -755,6 +766,8 @@ TARGETS: List[Callable] = [
 ]
 EXTRAS: List[Callable] = [
     cfg0_layer_norm,
+    cfg1_residual_layer_norm_f32,
+    cfg1_qk_layernorm_rope2d_f32,
     cfg2_timestep_embedding,
     lambda dev: cfg1_qk_layernorm_rope2d(dev, tables=True),
     cfg2_gelu_erf,
