@@ -65,3 +65,67 @@ def test_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         for got, want in zip((h, y, qo, ko, act_out), eager):
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep} differs from eager"
+
+
+def test_graph_replays_of_the_newer_entries(dev):
+    """The same check for the fused gated residual + modulate, exact_sdpa_heads
+    on bf16 (three-term probabilities), f32 attention (three-term splits) and
+    the allocation-free coordinate map (its static table is cleared by its
+    own first kernel on every replay, and the bad-coordinate counter by the
+    same kernel)."""
+    print("\n[case] graph replay of gated_residual_adaln_modulate + sdpa_heads_f32 + f32 sdpa + neighbors_noalloc",
+          flush=True)
+    from lux3d_fused import ops, synth, _lib
+    T = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dt or torch.float32)  # noqa: E731
+    rows, C = 3000, 1536
+    x = T(synth.normal(11, rows * C).reshape(rows, C), torch.bfloat16)
+    hh = T(synth.normal(12, rows * C).reshape(rows, C), torch.bfloat16)
+    te = T(synth.normal(13, 2 * 6 * C, 0.0, 0.1).reshape(2, 6 * C))
+    pieces = ops.chunk_modulation(te)
+    so = torch.tensor([0, 1200, rows], dtype=torch.int64, device=dev)
+    x_out, y_mod = torch.empty_like(x), torch.empty_like(x)
+    qkv = T(synth.normal(14, 300 * 3 * 4 * 64).reshape(1, 300, 3, 4, 64), torch.bfloat16).permute(2, 0, 3, 1, 4)
+    o_ex = torch.empty((1, 4, 300, 64), dtype=torch.bfloat16, device=dev)
+    qkv32 = T(synth.normal(15, 260 * 3 * 4 * 64).reshape(1, 260, 3, 4, 64)).permute(2, 0, 3, 1, 4)
+    o32 = torch.empty((1, 4, 260, 64), dtype=torch.float32, device=dev)
+    rng = np.random.default_rng(16)
+    flat = rng.choice(48 ** 3, size=5000, replace=False)
+    c = np.stack([flat // 2304, (flat // 48) % 48, flat % 48], axis=1).astype(np.int32) - 24
+    c[7, 0] = (1 << 20) + 3  # one coordinate outside the packable range
+    coords = torch.from_numpy(c).to(dev)
+    nbr = torch.empty((5000, 27), dtype=torch.int32, device=dev)
+    bad = torch.empty((1,), dtype=torch.int32, device=dev)
+    d = ops.desc
+
+    def run():
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("lux3d_gated_residual_adaln_modulate", d(x), d(hh), d(so), d(pieces[2]), None, d(pieces[3]), None,
+                  d(pieces[4]), None, 1e-6, d(x_out), d(y_mod), s)
+        _lib.call("lux3d_sdpa_heads_f32", d(qkv[0]), d(qkv[1]), d(qkv[2]), 0.125, d(o_ex), s)
+        _lib.call("lux3d_sdpa", d(qkv32[0]), d(qkv32[1]), d(qkv32[2]), 0.125, d(o32), s)
+        _lib.call("lux3d_sparse_neighbors_noalloc", d(coords), d(nbr), d(bad), s)
+
+    outs = (x_out, y_mod, o_ex, o32, nbr, bad)
+    run()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in outs]
+    assert int(bad.item()) == 1
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run()
+    for rep in range(4):
+        for t in outs:
+            t.fill_(-7 if t.dtype == torch.int32 else float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(outs, eager):
+            a = got.view(torch.int16) if got.dtype == torch.bfloat16 else got
+            b = want.view(torch.int16) if want.dtype == torch.bfloat16 else want
+            assert torch.equal(a, b), f"replay {rep} differs from eager"
