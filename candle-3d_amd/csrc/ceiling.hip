@@ -14,8 +14,8 @@
 //    rows (or one row per workgroup when TPR is 128 / 256 and the op runs a
 //    row per workgroup);
 //  - heads: the head kernels' layout -- [B, H, N, D] views with any outer
-//    strides, D / 8 lanes per head row, two rows per thread (one for f32),
-//    workgroups of `tb` consecutive tokens x all heads, q and k in
+//    strides, D / 8 lanes per head row, two rows per thread (one for f32,
+//    whose lane l holds 16 bytes at 16 l of each half row), workgroups of `tb` consecutive tokens x all heads, q and k in
 //    grid.y (or both in one workgroup, as the D = 128 kernels do).
 // Every output word is the XOR of the loaded words that map to it, so no
 // load can be dropped by the compiler.
@@ -99,7 +99,9 @@ struct Heads {
 // EB: element bytes; D: head dim; R: rows per thread; NTB: tensors per workgroup
 template <int EB, int D, int R, int NTB>
 __global__ __launch_bounds__(256) void heads_kernel(Heads p) {
-  constexpr int LPR = D / 8, CB = 8 * EB;
+  // CB: bytes per lane per row; f32 rows in two halves of D / 2 elements,
+  // lane l holding the 16 bytes at 16 l of each (HS apart)
+  constexpr int LPR = D / 8, CB = 8 * EB, HS = D * 2;
   const int lane = threadIdx.x % LPR, ipp = blockDim.x / LPR;
   // token and head counts below 2^31 (checked on the host): 32-bit indices
   const uint32_t H = (uint32_t)p.H, N = (uint32_t)p.N, ntok = (uint32_t)(p.B * p.N);
@@ -113,8 +115,8 @@ __global__ __launch_bounds__(256) void heads_kernel(Heads p) {
     live[r] = it < items && tok < ntok;
     if (!live[r]) { h = 0; tok = tok0; }
     const uint32_t b = tok / N, n = tok - b * N;
-    xo[r] = ((int64_t)b * p.sB + (int64_t)h * p.sH + (int64_t)n * p.sN) * EB + lane * CB;
-    yo[r] = ((int64_t)b * p.oB + (int64_t)h * p.oH + (int64_t)n * p.oN) * EB + lane * CB;
+    xo[r] = ((int64_t)b * p.sB + (int64_t)h * p.sH + (int64_t)n * p.sN) * EB + lane * 16;
+    yo[r] = ((int64_t)b * p.oB + (int64_t)h * p.oH + (int64_t)n * p.oN) * EB + lane * 16;
   }
   u32x4 v[NTB][R][CB / 16];
 #pragma unroll
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(256) void heads_kernel(Heads p) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int h = 0; h < CB / 16; ++h) v[q][r][h] = ld(x + xo[r] + h * 16);
+      for (int h = 0; h < CB / 16; ++h) v[q][r][h] = ld(x + xo[r] + h * HS);
   }
 #pragma unroll
   for (int q = 0; q < NTB; ++q) {
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(256) void heads_kernel(Heads p) {
     for (int r = 0; r < R; ++r)
       if (live[r])
 #pragma unroll
-        for (int h = 0; h < CB / 16; ++h) st(y + yo[r] + h * 16, v[q][r][h]);
+        for (int h = 0; h < CB / 16; ++h) st(y + yo[r] + h * HS, v[q][r][h]);
   }
 }
 

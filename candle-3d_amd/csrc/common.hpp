@@ -251,6 +251,25 @@ __device__ __forceinline__ void param8(const void *p, int dt, int64_t i, float d
   }
 }
 
+// 4 consecutive parameters starting at element i (i a multiple of 4, the
+// base 16-byte aligned), cached loads, or dflt.
+__device__ __forceinline__ void param4(const void *p, int dt, int64_t i, float dflt, float *v) {
+  if (dt == LUX3D_F32) {
+    const float4 a = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(p) + i);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  } else if (dt == LUX3D_BF16 || dt == LUX3D_F16) {
+    const uint2 a = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p) + i);
+    const uint32_t w[2] = {a.x, a.y};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t h = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      v[k] = dt == LUX3D_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = dflt;
+  }
+}
 template <typename T> __device__ __forceinline__ const char *cptr(const void *p) {
   return reinterpret_cast<const char *>(p);
 }
@@ -260,8 +279,9 @@ template <typename T> __device__ __forceinline__ const char *cptr(const void *p)
 // ---------------------------------------------------------------------------
 
 // DPP controls: quad_perm [1,0,3,2] = xor 1, quad_perm [2,3,0,1] = xor 2,
-// row_half_mirror (lane i of 8 <- 7-i), row_mirror (lane i of 16 <- 15-i).
-enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+// quad_perm [3,2,1,0] = xor 3, row_half_mirror (lane i of 8 <- 7-i = i^7),
+// row_mirror (lane i of 16 <- 15-i = i^15).
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_XOR3 = 0x1B, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
 
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -298,10 +318,13 @@ template <int LANES> __device__ __forceinline__ float group_sum(float v) {
   else return wave_sum(v);
 }
 
-// Value held by lane (lane ^ M).
+// Value held by lane (lane ^ M). xor 4 = xor 3, then xor 7 (two DPP moves);
+// xor 8 = xor 7, then xor 15.
 template <int M> __device__ __forceinline__ float lane_xor(float v) {
   if constexpr (M == 1) return dpp<DPP_XOR1>(v);
   else if constexpr (M == 2) return dpp<DPP_XOR2>(v);
+  else if constexpr (M == 4) return dpp<DPP_HALF_MIRROR>(dpp<DPP_XOR3>(v));
+  else if constexpr (M == 8) return dpp<DPP_MIRROR>(dpp<DPP_HALF_MIRROR>(v));
   else return __shfl_xor(v, M, 64);
 }
 

@@ -136,24 +136,6 @@ __device__ __forceinline__ void st_row(char *row, ChunkAt a, const float (&v)[8]
     Chunk<T>::store(row + a.o0 * T::bytes, v);
   }
 }
-// 4 parameters of dtype dt at element i (cached loads), or dflt
-__device__ __forceinline__ void param4(const void *p, int dt, int64_t i, float dflt, float *v) {
-  if (dt == LUX3D_F32) {
-    const float4 a = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(p) + i);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  } else if (dt == LUX3D_BF16 || dt == LUX3D_F16) {
-    const uint2 a = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p) + i);
-    const uint32_t w[2] = {a.x, a.y};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t h = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-      v[k] = dt == LUX3D_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = dflt;
-  }
-}
 // the parameters of chunk a (offset by off elements)
 template <typename T>
 __device__ __forceinline__ void param_at(const void *p, int dt, int64_t off, ChunkAt a, float dflt, float (&v)[8]) {

@@ -3,9 +3,11 @@
 // TripoSG per-head RMSNorm, TRELLIS.2 L2 norm + 3D RoPE, DINOv3 2D RoPE.
 //
 // Mapping. One workgroup per token (b, n) processes every head of q and k
-// for that token: LPR = D/8 lanes own one head row (8 elements each, one
-// 16-byte load for bf16), so a wavefront covers 8 (D=64) or 4 (D=128) head
-// rows. The token's rotation phases are computed (or read from the caller's
+// for that token: LPR = D/8 lanes own one head row, 8 elements each, so a
+// wavefront covers 8 (D=64) or 4 (D=128) head rows. 2-byte types: lane l
+// holds elements 8l..8l+7 (one 16-byte load); f32: elements 4l..4l+3 and
+// D/2+4l..D/2+4l+3, so each 16-byte load instruction of the wavefront covers
+// whole 64-byte runs of the row instead of every other 16 bytes. The token's rotation phases are computed (or read from the caller's
 // tables) once into LDS and shared by all 2H head rows; head statistics are
 // reduced in-register with DPP over the LPR lanes. Every rotation in the
 // reference has the form out[j] = y[j]*C[j] + y[j ^ M]*S[j] for a fixed
@@ -25,6 +27,43 @@ template <int D> struct RotPartner<HR_R1_POS, D> { static constexpr int M = D / 
 template <int D> struct RotPartner<HR_R2_TAB, D> { static constexpr int M = 1; };
 template <int D> struct RotPartner<HR_R2_COORD, D> { static constexpr int M = 1; };
 template <int D> struct RotPartner<HR_R3_TAB, D> { static constexpr int M = D / 2; };
+
+// Element of the head row that a lane's x[k] holds (see Mapping above).
+template <typename T, int D> __device__ __forceinline__ int head_elem(int lane, int k) {
+  if constexpr (T::bytes == 4) return (k >> 2) * (D / 2) + lane * 4 + (k & 3);
+  else return lane * 8 + k;
+}
+// A lane's 8 elements of the row at `row` (byte address of element 0).
+template <typename T, int D> __device__ __forceinline__ void head_load(const char *row, int lane, float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    const uint4 a = ld16<LUX3D_NT_STREAMS != 0>(row + lane * 16);
+    const uint4 b = ld16<LUX3D_NT_STREAMS != 0>(row + D * 2 + lane * 16);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+  } else {
+    Chunk<T>::load(row + lane * 16, v);
+  }
+}
+template <typename T, int D> __device__ __forceinline__ void head_store(char *row, int lane, const float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    st16(row + lane * 16, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                     __float_as_uint(v[3])));
+    st16(row + D * 2 + lane * 16, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                             __float_as_uint(v[7])));
+  } else {
+    Chunk<T>::store(row + lane * 16, v);
+  }
+}
+// Per-channel parameters of the lane's 8 elements, channel 0 at element `off`.
+template <typename T, int D>
+__device__ __forceinline__ void head_param(const void *p, int dt, int64_t off, int lane, float dflt, float (&v)[8]) {
+  if constexpr (T::bytes == 4) {
+    param4(p, dt, off + lane * 4, dflt, v);
+    param4(p, dt, off + D / 2 + lane * 4, dflt, v + 4);
+  } else {
+    param8(p, dt, off + lane * 8, dflt, v);
+  }
+}
 
 // x / d for x < 2^31 from the launcher's (m, s) = (ceil(2^s / d), 31 +
 // ceil(log2 d)): x m / 2^s exceeds x / d by less than 2^31 / 2^s <= 1 / d,
@@ -178,11 +217,11 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const char *xp = reinterpret_cast<const char *>(io.x) +
-                       view_off<O32>(bb[r], hh[r], nn[r], io.sB, io.sH, io.sN, lane * 8) * EB;
-      Chunk<T>::load(xp, v[q][r]);
+                       view_off<O32>(bb[r], hh[r], nn[r], io.sB, io.sH, io.sN, 0) * EB;
+      head_load<T, D>(xp, lane, v[q][r]);
     }
-    if constexpr (NORM == HN_LN || NORM == HN_RMS) param8(io.p0, io.p0_dt, lane * 8, 1.f, w[q]);
-    if constexpr (NORM == HN_LN) param8(io.p1, io.p1_dt, lane * 8, 0.f, bias[q]);
+    if constexpr (NORM == HN_LN || NORM == HN_RMS) head_param<T, D>(io.p0, io.p0_dt, 0, lane, 1.f, w[q]);
+    if constexpr (NORM == HN_LN) head_param<T, D>(io.p1, io.p1_dt, 0, lane, 0.f, bias[q]);
   }
 
   if constexpr (ROT != HR_NONE) {
@@ -214,7 +253,7 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         const float rr = l2_rnorm(group_sum<LPR>(s2));
         const float scale = sqrtf((float)D);
         float g[8];
-        param8(io.p0, io.p0_dt, (int64_t)hh[r] * D + lane * 8, 1.f, g);
+        head_param<T, D>(io.p0, io.p0_dt, (int64_t)hh[r] * D, lane, 1.f, g);
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = ((x[k] * rr) * g[k]) * scale;
       }
@@ -222,23 +261,34 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         bool rotate = true;
         if constexpr (ROT == HR_R3_TAB) rotate = nn[r] >= (uint32_t)p.prefix;  // prefix tokens pass through
         if (rotate) {
+          // partner of element j = head_elem(lane, k): j ^ M
           float pv[8];
-          if constexpr (M < 8) {
+          if constexpr (EB == 4 && (M < 4 || M == D / 2)) {
+            constexpr int KM = M == D / 2 ? 4 : M;  // in the lane: the other half, or the same 4
+#pragma unroll
+            for (int k = 0; k < 8; ++k) pv[k] = x[k ^ KM];
+          } else if constexpr (EB == 4) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 4>(x[k]);
+          } else if constexpr (M < 8) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) pv[k] = x[k ^ M];
           } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) pv[k] = lane_xor<M / 8>(x[k]);
           }
-          const float *C = Cs + tt[r] * D + lane * 8;
-          const float *S = Ss + tt[r] * D + lane * 8;
+          const float *C = Cs + tt[r] * D;
+          const float *S = Ss + tt[r] * D;
 #pragma unroll
-          for (int k = 0; k < 8; ++k) x[k] = rotate1(x[k], C[k], pv[k], S[k]);
+          for (int k = 0; k < 8; ++k) {
+            const int j = head_elem<T, D>(lane, k);
+            x[k] = rotate1(x[k], C[j], pv[k], S[j]);
+          }
         }
       }
       if (live[r]) {
-        char *yp = reinterpret_cast<char *>(io.y) + view_off<O32>(bb[r], hh[r], nn[r], io.oB, io.oH, io.oN, lane * 8) * EB;
-        Chunk<T>::store(yp, v[q][r]);
+        char *yp = reinterpret_cast<char *>(io.y) + view_off<O32>(bb[r], hh[r], nn[r], io.oB, io.oH, io.oN, 0) * EB;
+        head_store<T, D>(yp, lane, v[q][r]);
       }
     }
   }
