@@ -539,13 +539,13 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 //
 // f32 q, k and v are split exactly into three bf16 terms each (x = x1 + x2 +
 // x3, split3_bf16). A product x y is then the sum of nine bf16 x bf16
-// products, each exact in f32; the three smallest (x2 y3, x3 y2, x3 y3)
-// together stay below 2^-25 |x y|, under half an f32 ulp of the product, and
-// are dropped. Each MFMA step of S = K Q^T and of O^T += V^T P^T becomes six
+// products, each exact in f32; with |x2| <= 2^-8 |x| and |x3| <= 2^-17 |x|
+// the three smallest (x2 y3, x3 y2, x3 y3) together stay below 2^-24 |x y|,
+// under one f32 ulp of the product, and are dropped. Each MFMA step of S = K Q^T and of O^T += V^T P^T becomes six
 // bf16 MFMAs (smallest terms first) accumulating in f32; the probabilities
 // are f32 and split the same way, the row sum adds them in f32. That is the
 // f32 arithmetic of exact_sdpa_heads (attention_math.rs:244-259) up to the
-// order of the sums and that sub-half-ulp truncation per product, at 6 / 16
+// order of the sums and that sub-ulp truncation per product, at 6 / 16
 // of the matrix-core cycles of v_mfma_f32_32x32x2_f32 (which runs at 1/16
 // of the bf16 rate). Layout as attn_mfma_kernel with QT = 1: K and V blocks
 // of BKV keys are loaded as f32 (keys past Lk clamped to Lk - 1, their scores
