@@ -114,6 +114,8 @@ def test_sparse_conv3d_reference_cases(dev, ops, orc):
     (777, 32, 40, 16, False),
     (20000, 256, 256, 64, True),
     (1500, 48, 40, 16, False),
+    (1500, 512, 600, 24, True),
+    (700, 640, 512, 16, False),
 ])
 @pytest.mark.parametrize("path", ["output_stationary", "rulebook"])
 def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface, path):
@@ -218,17 +220,19 @@ def test_sparse_rulebook_pairs(dev, ops, orc, n):
         assert counts[k] == len(want) and got == want, k
 
 
-def test_sparse_conv3d_rulebook_matches_reference_order(dev, ops, orc):
+@pytest.mark.parametrize("cin,cout", [(32, 48), (512, 520)])
+def test_sparse_conv3d_rulebook_matches_reference_order(dev, ops, orc, cin, cout):
     """The rulebook path adds the taps in the reference's order; on inputs
     whose products and partial sums are exact in f32 it equals the oracle
-    bit for bit."""
+    bit for bit (64- and 128-wide tap tiles)."""
+    _case(op="conv3d exact", cin=cin, cout=cout)
     coords = random_coords(2000, 24, 22, True)
     rng = np.random.default_rng(23)
-    x = rng.integers(-4, 5, (len(coords), 32)).astype(np.float32)
-    w27 = (rng.integers(-3, 4, (27, 48, 32)) * 0.25).astype(np.float32)
-    bias = (rng.integers(-8, 9, 48) * 0.5).astype(np.float32)
+    x = rng.integers(-4, 5, (len(coords), cin)).astype(np.float32)
+    w27 = (rng.integers(-3, 4, (27, cout, cin)) * 0.25).astype(np.float32)
+    bias = (rng.integers(-8, 9, cout) * 0.5).astype(np.float32)
     conv = ops.SparseConv3d(torch.from_numpy(w27).permute(1, 0, 2).contiguous().to(dev), torch.from_numpy(bias).to(dev),
-                            32, 48)
+                            cin, cout)
     nbr = ops.sparse_neighbors(torch.from_numpy(coords).to(dev))
     got = conv.forward(ops.SparseRulebook(nbr), torch.from_numpy(x).to(dev)).cpu().numpy()
     want = orc.sparse_conv3d(x, orc.sparse_neighbors(coords), w27, bias)
