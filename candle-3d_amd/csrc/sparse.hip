@@ -14,9 +14,11 @@
 // rows are gathered through the neighbour table (missing neighbours load
 // zeros). The reference's 27 gather + GEMM + index_add passes become one
 // kernel, and every output element is written once: no scatter, no atomics,
-// a fixed summation order. f32 in, f32 accumulation on the matrix cores
-// (v_mfma_f32_32x32x2_f32), as the reference computes sparse features in F32.
-// Taps that no row of a tile uses are skipped.
+// a fixed summation order. f32 arithmetic, as the reference computes sparse
+// features in F32, on the bf16 matrix cores: each staged f32 operand is split
+// exactly into three bf16 terms and a product keeps the six largest of the
+// nine term products (split3_bf16; the rulebook tap kernel below states the
+// bound). Taps that no row of a tile uses are skipped.
 //
 // C2S: per parent the leaf mask (logits > 0) and its popcount, an exclusive
 // scan of the counts (block scans + one scan of the block totals), then one
@@ -117,17 +119,20 @@ __global__ __launch_bounds__(256) void map_neighbors_kernel(const int32_t *coord
 // ---- sparse convolution -------------------------------------------------------
 
 // A 256-thread workgroup computes BM rows x BN output channels; its 4
-// wavefronts (2 x 2) each own (BM/2) x (BN/2) as 32 x 32 f32 MFMA tiles. The
-// K loop runs over the used taps and Cin in steps of BK = 16.
+// wavefronts (2 x 2) each own (BM/2) x (BN/2) as 32 x 32 MFMA tiles. The K
+// loop runs over the used taps and Cin in steps of BK = 16; each step stages
+// x and W_k as three bf16 planes (the layout of sparse_tap_x3_kernel) and
+// runs six bf16 MFMAs per tile.
 template <int BM, int BN>
-__global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams p) {
+__global__ __launch_bounds__(256) void sparse_conv_x3_kernel(SparseConvParams p) {
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   constexpr int BK = 16;
-  constexpr int ROW = BK + 1;  // floats per LDS row (odd: conflict-free column reads)
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int ACH = BM * BK / 4 / 256, BCH = BN * BK / 4 / 256;  // float4 per thread per step
   static_assert(ACH >= 1 && BCH >= 1, "tile");
-  __shared__ float As[2][BM * ROW];
-  __shared__ float Bs[2][BN * ROW];
+  constexpr int PA = BM * BK * 2, PB = BN * BK * 2;  // bytes of one bf16 plane
+  constexpr int STAGE = 3 * (PA + PB);
+  __shared__ __align__(16) char lds[2 * STAGE];
   __shared__ int32_t nb[BM * 27];
   __shared__ uint32_t tap_mask;
 
@@ -183,18 +188,19 @@ __global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams 
       rb[i] = *reinterpret_cast<const float4 *>(p.w + ((int64_t)k * Cout + o) * Cin + c0 + b_part[i] * 4);
     }
   };
+  auto put = [](char *plane0, int pbytes, int off, float4 v) {
+    const Split3 lo = split3_bf16(v.x, v.y), hi = split3_bf16(v.z, v.w);
+    *reinterpret_cast<uint2 *>(plane0 + off) = make_uint2(lo.t1, hi.t1);
+    *reinterpret_cast<uint2 *>(plane0 + pbytes + off) = make_uint2(lo.t2, hi.t2);
+    *reinterpret_cast<uint2 *>(plane0 + 2 * pbytes + off) = make_uint2(lo.t3, hi.t3);
+  };
   auto store_step = [&](int buf) {
+    char *st = lds + buf * STAGE;
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      float *d = &As[buf][a_row[i] * ROW + a_part[i] * 4];
-      const float4 v = aok[i] ? ra[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-    }
+    for (int i = 0; i < ACH; ++i)
+      put(st, PA, a_row[i] * 32 + a_part[i] * 8, aok[i] ? ra[i] : make_float4(0.f, 0.f, 0.f, 0.f));
 #pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      float *d = &Bs[buf][b_row[i] * ROW + b_part[i] * 4];
-      d[0] = rb[i].x; d[1] = rb[i].y; d[2] = rb[i].z; d[3] = rb[i].w;
-    }
+    for (int i = 0; i < BCH; ++i) put(st + 3 * PA, PB, b_row[i] * 32 + b_part[i] * 8, rb[i]);
   };
 
   f32x16_t acc[TM][TN];
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams 
     store_step(0);
   }
   lds_barrier();
-  const int lrow = lane & 31, lk = lane >> 5;
+  const int frag = (lane & 31) * 32 + (lane >> 5) * 16;
   int cur_k;
   int64_t cur_c0;
   if (nsteps > 0) step_at(0, cur_k, cur_c0);
@@ -235,17 +241,27 @@ __global__ __launch_bounds__(256) void sparse_conv_mfma_kernel(SparseConvParams 
       nk = rest ? __builtin_ctz(rest) : cur_k;
     }
     if (st + 1 < nsteps) load_step(nk, nc0);
+    {
+      const char *sa = lds + buf * STAGE, *sb = sa + 3 * PA;
+      bf16x8_t a[3][TM], b[3][TN];
 #pragma unroll
-    for (int s2 = 0; s2 < BK / 2; ++s2) {
-      float a[TM], b[TN];
+      for (int q = 0; q < 3; ++q) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = As[buf][(wm * (BM / 2) + i * 32 + lrow) * ROW + s2 * 2 + lk];
+        for (int i = 0; i < TM; ++i)
+          a[q][i] = *reinterpret_cast<const bf16x8_t *>(sa + q * PA + (wm * (BM / 2) + i * 32) * 32 + frag);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = Bs[buf][(wn * (BN / 2) + j * 32 + lrow) * ROW + s2 * 2 + lk];
+        for (int j = 0; j < TN; ++j)
+          b[q][j] = *reinterpret_cast<const bf16x8_t *>(sb + q * PB + (wn * (BN / 2) + j * 32) * 32 + frag);
+      }
+      // smallest terms first: (x3 w1, x2 w2, x1 w3), (x2 w1, x1 w2), x1 w1
+      constexpr int ta[6] = {2, 1, 0, 1, 0, 0}, tb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int u = 0; u < 6; ++u)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ta[u]][i], b[tb[u]][j], acc[i][j], 0, 0, 0);
     }
     if (st + 1 < nsteps) store_step(buf ^ 1);
     lds_barrier();
@@ -756,11 +772,11 @@ hipError_t launch_sparse_conv(const SparseConvParams &p, hipStream_t s) {
     const int64_t gy = (p.n + 63) / 64;
     if (gy > 65535) {
       if ((p.n + 127) / 128 > 65535) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((sparse_conv_mfma_kernel<128, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)((p.n + 127) / 128)),
+      hipLaunchKernelGGL((sparse_conv_x3_kernel<128, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)((p.n + 127) / 128)),
                          dim3(256), 0, s, p);
       return hipGetLastError();
     }
-    hipLaunchKernelGGL((sparse_conv_mfma_kernel<64, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)gy), dim3(256), 0,
+    hipLaunchKernelGGL((sparse_conv_x3_kernel<64, 64>), dim3((unsigned)((p.cout + 63) / 64), (unsigned)gy), dim3(256), 0,
                        s, p);
     return hipGetLastError();
   }

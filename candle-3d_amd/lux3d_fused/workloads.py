@@ -674,14 +674,15 @@ def _sparse_conv(dev, name, n, ch, res, reps, rulebook=True):
         else:
             _lib.call("lux3d_sparse_conv3d", dx[i % 2], dn, dw, db, do[i % 2], _cur())
     nbytes = n * ch * 4 * 2 + n * 27 * 4 + 27 * ch * ch * 4
+    # f32 arithmetic on the bf16 matrix cores: six bf16 MFMAs per f32 step,
+    # so the ceiling is the bf16 peak / 6
     if rulebook:
-        # f32 arithmetic on the bf16 matrix cores: six bf16 MFMAs per f32
-        # step, so the ceiling is the bf16 peak / 6
         tile = 128 if ch >= 512 else 64
         kern, arith, peak = (f"sparse_tap_x3_kernel<{tile},{tile}> x 27 taps",
                              "f32 (bf16 matrix cores, three-term splits)", 2500.0 / 6)
     else:
-        kern, arith, peak = "sparse_conv_mfma_kernel<64,64>", "f32 -> f32 acc (MFMA f32)", 157.3
+        kern, arith, peak = ("sparse_conv_x3_kernel<64,64>", "f32 (bf16 matrix cores, three-term splits)",
+                             2500.0 / 6)
     wl = Workload(name, 3, kern, arith, nbytes,
                   f"{n} shell voxels in {res}^3, C {ch} -> {ch}, {used / n:.1f} active taps per voxel", launch, 2,
                   flops=2 * used * ch * ch, reps=reps, peak_tflops=peak)
