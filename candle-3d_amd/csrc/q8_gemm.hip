@@ -13,7 +13,7 @@
 // are only 2-byte aligned, into int8 [N, K] row-major plus f32 scales
 // [N, K/32], so the GEMM streams them with 16-byte loads.
 //
-// Two GEMM kernels (both one rounding of the f32 sum per output):
+// Three GEMM kernels (each one rounding of the f32 sum per output):
 // - q8_0_gemm_ring_kernel (K % 64 == 0, the common case): a workgroup of NW
 //   wavefronts (8, or 4 for small shapes) computes a BM x 32 NW tile; x, the
 //   int8 weights and the scales stream through a 3-stage LDS ring by direct
@@ -22,8 +22,9 @@
 // - q8_0_gemm_kernel (K % 64 == 32): a 256-thread workgroup computes a
 //   128 x 128 tile; x and the dequantised W are staged as bf16 in LDS,
 //   double-buffered, through registers.
-// - q8_0_gemm_ring_f32_kernel (f32 x, K % 64 == 0): the ring scheme with the
-//   exact f32 weights q * d and f32 products on v_mfma_f32_32x32x2_f32.
+// - q8_0_gemm_x3_kernel (f32 x, K % 64 == 0): f32 arithmetic on the bf16
+//   matrix cores, x split exactly into three bf16 terms, the int8 weights
+//   exact in bf16 and each Q8_0 block's scale applied to its block sum.
 // Within a k-step the kernels assign k to MFMA sub-steps differently, so
 // their outputs can differ in the last bit of the f32 sum; each is
 // deterministic.
@@ -227,7 +228,6 @@ __global__ __launch_bounds__(kGemmThreads, MINW) void q8_0_gemm_kernel(Q8GemmPar
 
 constexpr int kRingStages = 3;
 constexpr int kRingThreads = 512;
-constexpr int kRingW = 256 * 64, kRingS = 256 * 8;  // weights and scales per stage (256 columns)
 
 // 8 int8 (two dwords) -> bf16(f32(q) * d), RNE; q * d is exact in f32
 __device__ __forceinline__ bf16x8_t dequant8(uint32_t lo, uint32_t hi, float d) {
@@ -441,25 +441,42 @@ __global__ __launch_bounds__(64 * NW, 1) void q8_0_gemm_ring_kernel(Q8GemmParams
   }
 }
 
-// ---- f32 activations ------------------------------------------------------------
+// ---- f32 activations on the bf16 matrix cores -------------------------------------
 //
-// The ring scheme with f32 x: each weight is the exact f32 product q * d (the
-// reference's own Q8_0 dequant target, nn_blocks.rs:140), products and sums
-// in f32 on v_mfma_f32_32x32x2_f32. 128-row tiles keep a stage at 51,200
-// bytes: x 128 rows x 256 bytes, 16-byte chunk c of row r in slot c ^ (r & 15)
-// (conflict-free fragment reads), then the weights and scales exactly as in
-// the bf16 kernel. MFMA k-step (c4, e) of a 64-deep k-step pairs k = c and
-// k = 32 + c (c = 4 c4 + e): lane half hh supplies k = 32 hh + c, so its x
-// values are contiguous (one 16-byte read per four k-steps) and its weight
-// bytes are the same 32 int8 of one Q8_0 block the bf16 kernel uses.
+// y = sum over Q8_0 blocks b of d_b * (sum_{k in b} x_k q_k): each int8 q is
+// exact in bf16, each f32 x is split exactly into three bf16 terms (x = x1 +
+// x2 + x3, split3_bf16), so x q = x1 q + x2 q + x3 q with every product
+// exact in f32. A 32-deep block of a 32 x 32 tile is six bf16 MFMAs (three
+// terms x two 16-deep sub-steps) into a zeroed f32 block sum, which one FMA
+// per element scales by the column's d and adds to the accumulator. That is
+// the reference's f32 dequantize-then-matmul (w = q d exact in f32, f32
+// products and sums, nn_blocks.rs:140) up to the order of the sums, at 6/16
+// of the matrix-core cycles of v_mfma_f32_32x32x2_f32 per block. It replaced
+// a ring kernel on v_mfma_f32_32x32x2_f32 (4096 x 2048 -> 8192: 994 -> 430
+// us, same-box A/B).
+//
+// 128 x 256 tiles, 8 wavefronts as 2 (rows) x 4 (columns), 64 x 64 each.
+// 32-deep k-steps through a 4-stage LDS ring filled by direct global -> LDS
+// loads: x (128 rows x 128 bytes, row-major), the int8 weights (32 columns x
+// 32 bytes per 1 KB segment; lane l holds column l % 32, bytes 16 (l / 32)
+// .. + 15) and the scales (32 columns per wavefront, both lane halves). Each
+// step one cooperative pass splits the next stage's x into three bf16 planes
+// (double-buffered; 64-byte rows, 16-byte chunk c of row r in slot c ^ ((r
+// >> 2) & 3), so fragment reads are conflict-free). k order: in sub-step s,
+// lane half h holds k = 16 h + 8 s + e on both operands. One barrier per
+// step: wait for stage kt + 1, barrier, issue stage kt + 3, split stage
+// kt + 1, compute stage kt.
+constexpr int kX3Stages = 4, kX3Threads = 512;
+constexpr int kX3XL = 128 * 128, kX3WB = 256 * 32, kX3SB = 8 * 256;
+constexpr int kX3Stage = kX3XL + kX3WB + kX3SB;  // 26,624 bytes
+constexpr int kX3Plane = 128 * 64;               // one bf16 plane of 128 rows x 32 k
+constexpr int kX3Ops = 4;                        // direct loads per wavefront per stage
+
 template <typename OUT, int GM>
-__global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_f32_kernel(Q8GemmParams p, int tiles_m,
-                                                                              int tiles_n) {
-  constexpr int BM = 128, BN = 256, BK = 64, TM = BM / 32, NS = kRingStages;
-  constexpr int kRingA = BM * 256, kRingStage = kRingA + kRingW + kRingS;  // 51,200 bytes
-  constexpr int SEGW = kRingA / 1024 / 8;          // x segments (1 KB = 4 rows) per wavefront
-  constexpr int kRingOps = SEGW + 2 + 1;
-  __shared__ __align__(16) char ring[NS * kRingStage];
+__global__ __launch_bounds__(kX3Threads, 1) void q8_0_gemm_x3_kernel(Q8GemmParams p, int tiles_m, int tiles_n) {
+  constexpr int BM = 128, BN = 256, BK = 32, NS = kX3Stages;
+  __shared__ __align__(16) char lds[NS * kX3Stage + 2 * 3 * kX3Plane];
+  char *const planes = lds + NS * kX3Stage;
 
   const int G = tiles_m * tiles_n, bid = (int)blockIdx.x;
   const int per = G / 8, rem = G % 8, xcd = bid % 8, pos = bid / 8;
@@ -470,141 +487,164 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_f32_kernel(Q8G
   const int tm = first_m + in_group % gsize, tn = in_group / gsize;
 
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5, lrow = lane & 31;
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5, l32 = lane & 31;
+  const int wm = wave >> 2, wn = wave & 3;
   const int64_t m0 = (int64_t)tm * BM, c0 = (int64_t)tn * BN;
-  const int64_t ncol = c0 + wave * 32 + lrow, nc = ncol < p.N ? ncol : p.N - 1;
   const int64_t nblk = p.K / 32;
-  const int nk = (int)(p.K / BK);
+  const int nk = (int)nblk;
 
-  uint32_t xoff[SEGW];
+  // direct-load offsets (rows and columns past the matrix clamp to the last)
+  uint32_t xoff[2];
 #pragma unroll
-  for (int i = 0; i < SEGW; ++i) {
-    const int g = wave * SEGW + i;
-    const int r = 4 * g + (lane >> 4), c = (lane & 15) ^ (r & 15);
+  for (int i = 0; i < 2; ++i) {
+    const int r = 8 * (2 * wave + i) + (lane >> 3);
     const int64_t gr = m0 + r < p.M ? m0 + r : p.M - 1;
-    xoff[i] = (uint32_t)(((gr - m0) * p.ldx + 4 * c) * 4);
+    xoff[i] = (uint32_t)(((gr - m0) * p.ldx + 4 * (lane & 7)) * 4);
   }
   const int64_t last_row = p.M - 1 - m0 < BM - 1 ? p.M - 1 - m0 : BM - 1;
   const int64_t ncols = p.N - c0 < BN ? p.N - c0 : BN;
+  const int64_t wcol = c0 + 32 * wave + l32, wc = wcol < p.N ? wcol : p.N - 1;
   const i32x4_t xr = buffer_rsrc(reinterpret_cast<const char *>(p.x) + m0 * p.ldx * 4, (last_row * p.ldx + p.K) * 4);
   const i32x4_t wr = buffer_rsrc(p.qs + c0 * p.K, ncols * p.K);
   const i32x4_t sr = buffer_rsrc(p.scales + c0 * nblk, ncols * nblk * 4);
-  const uint32_t woff = (uint32_t)((nc - c0) * p.K + 32 * h);
-  const uint32_t soff = (uint32_t)(((nc - c0) * nblk + h) * 4);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring;
-  auto issue = [&](int kt, int buf) {
-    const uint32_t st = lds0 + buf * kRingStage;
+  const uint32_t woff = (uint32_t)((wc - c0) * p.K + 16 * h);
+  const uint32_t soff = (uint32_t)((wc - c0) * nblk * 4);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds0 + slot * kX3Stage;
 #pragma unroll
-    for (int i = 0; i < SEGW; ++i)
-      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 4, __builtin_amdgcn_readfirstlane(st + (wave * SEGW + i) * 1024));
-    lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048));
-    lds_load16(wr, woff, (uint32_t)kt * BK + 16, __builtin_amdgcn_readfirstlane(st + kRingA + wave * 2048 + 1024));
-    lds_load4(sr, soff, (uint32_t)kt * 8, __builtin_amdgcn_readfirstlane(st + kRingA + kRingW + wave * 256));
+    for (int i = 0; i < 2; ++i)
+      lds_load16(xr, xoff[i], (uint32_t)kt * BK * 4, __builtin_amdgcn_readfirstlane(st + (2 * wave + i) * 1024));
+    lds_load16(wr, woff, (uint32_t)kt * BK, __builtin_amdgcn_readfirstlane(st + kX3XL + wave * 1024));
+    lds_load4(sr, soff, (uint32_t)kt * 4, __builtin_amdgcn_readfirstlane(st + kX3XL + kX3WB + wave * 256));
   };
-  // x fragment of M-tile i, four k-steps c4: row i * 32 + lrow, logical
-  // chunk 8 h + c4 (the swizzle only depends on the row within the tile)
-  int fbase[8];
+  // the split pass: thread t takes 16-byte chunks t and t + 512 of the stage's
+  // x (row q / 8, k 4 (q % 8) .. + 3)
+  auto split = [&](int slot, int pb) {
+    const char *xs = lds + slot * kX3Stage;
+    char *pl = planes + pb * 3 * kX3Plane;
 #pragma unroll
-  for (int c4 = 0; c4 < 8; ++c4) fbase[c4] = lrow * 256 + (((8 * h + c4) ^ (lrow & 15)) << 4);
-  uint4 w0, w1;
-  float sc;
-  auto read_w = [&](const char *st) {
-    w0 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + lane * 16);
-    w1 = *reinterpret_cast<const uint4 *>(st + kRingA + wave * 2048 + 1024 + lane * 16);
-    sc = *reinterpret_cast<const float *>(st + kRingA + kRingW + wave * 256 + lane * 4);
-  };
-  // the four exact weights of k-steps 4 c4 .. 4 c4 + 3 (bytes of w0 / w1)
-  auto make_w = [&](int c4, float (&wv)[4]) {
-    const uint4 &v = c4 < 4 ? w0 : w1;
-    const uint32_t word = (c4 & 3) == 0 ? v.x : (c4 & 3) == 1 ? v.y : (c4 & 3) == 2 ? v.z : v.w;
-    wv[0] = (float)(int8_t)(word & 0xFFu) * sc;
-    wv[1] = (float)(int8_t)((word >> 8) & 0xFFu) * sc;
-    wv[2] = (float)(int8_t)((word >> 16) & 0xFFu) * sc;
-    wv[3] = (float)(int8_t)(word >> 24) * sc;
-  };
-  auto read_a = [&](const char *st, int c4, float4 (&a)[TM]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const float4 *>(st + fbase[c4] + i * 32 * 256);
-  };
-  f32x16_t acc[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) acc[i] = f32x16_t{};
-  auto mfmas = [&](const float4 (&a)[TM], const float (&wv)[4]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, wv[0], acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, wv[1], acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, wv[2], acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, wv[3], acc[i], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      const int q = t + i * 512, r = q >> 3, c = q & 7;
+      const float4 v = *reinterpret_cast<const float4 *>(xs + q * 16);
+      const Split3 lo = split3_bf16(v.x, v.y), hi = split3_bf16(v.z, v.w);
+      const int off = r * 64 + (((c >> 1) ^ ((r >> 2) & 3)) << 4) + (c & 1) * 8;
+      *reinterpret_cast<uint2 *>(pl + off) = make_uint2(lo.t1, hi.t1);
+      *reinterpret_cast<uint2 *>(pl + kX3Plane + off) = make_uint2(lo.t2, hi.t2);
+      *reinterpret_cast<uint2 *>(pl + 2 * kX3Plane + off) = make_uint2(lo.t3, hi.t3);
     }
   };
-
+  // fragment offsets: A rows wm * 64 + i * 32 + l32, chunk 2 h + s
+  int aoff[2][2];
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st) issue(st < nk ? st : nk - 1, st);
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kRingOps));
-  __builtin_amdgcn_s_barrier();
-
-  float4 a0[TM], a1[TM];
-  float b0[4], b1[4];
-  read_w(ring);
-  read_a(ring, 0, a0);
-  make_w(0, b0);
-  for (int kt = 0; kt < nk; ++kt) {
-    issue(kt + NS - 1 < nk ? kt + NS - 1 : nk - 1, (kt + NS - 1) % NS);
-    __builtin_amdgcn_sched_barrier(0);
-    const char *st = ring + (kt % NS) * kRingStage;
+  for (int i = 0; i < 2; ++i) {
+    const int r = wm * 64 + i * 32 + l32;
 #pragma unroll
-    for (int c4 = 0; c4 < 7; c4 += 2) {
-      read_a(st, c4 + 1, a1);
-      make_w(c4 + 1, b1);
-      mfmas(a0, b0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (c4 + 2 < 8) {
-        read_a(st, c4 + 2, a0);
-        make_w(c4 + 2, b0);
-        mfmas(a1, b1);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int s2 = 0; s2 < 2; ++s2) aoff[i][s2] = r * 64 + (((2 * h + s2) ^ ((r >> 2) & 3)) << 4);
+  }
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+  auto compute = [&](int slot, int pb) {
+    const char *st = lds + slot * kX3Stage;
+    const char *pl = planes + pb * 3 * kX3Plane;
+    // weights of columns wn * 64 + j * 32 + l32: 16 int8 -> two bf16x8 (sub-steps)
+    bf16x8_t b[2][2];
+    float d[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(st + kX3XL + (2 * wn + j) * 1024 + lane * 16);
+      d[j] = *reinterpret_cast<const float *>(st + kX3XL + kX3WB + (2 * wn + j) * 256 + l32 * 4);
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t v = wv[2 * s2 + u];
+          pk[2 * u] = pack_bf16x2((float)(int8_t)(v & 0xFFu), (float)(int8_t)((v >> 8) & 0xFFu));
+          pk[2 * u + 1] = pack_bf16x2((float)(int8_t)((v >> 16) & 0xFFu), (float)(int8_t)(v >> 24));
+        }
+        b[j][s2] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
       }
     }
-    // a1 / b1 hold k-steps 28..31; stage kt + 1 landed and this wavefront's
-    // reads of stage kt are done; then every wavefront's
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0((NS - 2) * kRingOps));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      bf16x8_t a[3][2];
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) a[q][s2] = *reinterpret_cast<const bf16x8_t *>(pl + q * kX3Plane + aoff[i][s2]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // block sum, smallest terms first, then scaled by the column's d
+        f32x16_t blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2][0], b[j][0], f32x16_t{}, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2][1], b[j][1], blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][0], b[j][0], blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][1], b[j][1], blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][0], b[j][0], blk, 0, 0, 0);
+        blk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][1], b[j][1], blk, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(blk[e], d[j], acc[i][j][e]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s2 = 0; s2 < NS - 1; ++s2) issue(s2 < nk ? s2 : nk - 1, s2);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kX3Ops));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  split(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt + 1 landed (kt + 2 may be in flight); every wavefront is done
+    // with compute(kt - 1) and split(kt)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(kX3Ops));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    const char *nx = ring + ((kt + 1) % NS) * kRingStage;
-    read_w(nx);
-    read_a(nx, 0, a0);
-    mfmas(a1, b1);
-    make_w(0, b0);
+    issue(kt + NS - 1 < nk ? kt + NS - 1 : nk - 1, (kt + NS - 1) % NS);
     __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) split((kt + 1) % NS, (kt + 1) & 1);
+    compute(kt % NS, kt & 1);
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring and the planes
 
+  // epilogue: each wavefront's 64 x 64 block through LDS, bias added, one
+  // rounding, 16-byte row pieces
   char *ybase = reinterpret_cast<char *>(p.y);
-  const float bias = (p.bias && ncol < p.N) ? p.bias[ncol] : 0.f;
   constexpr int EB = OUT::code == LUX3D_F32 ? 4 : 2;
+  float bias[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = c0 + wn * 64 + j * 32 + l32;
+    bias[j] = (p.bias && col < p.N) ? p.bias[col] : 0.f;
+  }
   if (((uintptr_t)p.y % 16 == 0) && ((p.ldy * EB) % 16 == 0)) {
-    constexpr int ROW_B = 32 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB, RP = 128;
-    constexpr int REGION = RP * LROW;
-    static_assert(8 * REGION <= NS * kRingStage, "epilogue staging fits the ring");
-    __builtin_amdgcn_s_barrier();  // every wavefront is done with the ring
-    char *reg = ring + wave * REGION;
-    const int64_t c0w = c0 + wave * 32;
+    constexpr int ROW_B = 64 * EB, LROW = ROW_B + 16, CPR = ROW_B / 16, EPC = 16 / EB;
+    constexpr int REGION = 64 * LROW;
+    static_assert(8 * REGION <= (int)sizeof(lds), "epilogue staging fits");
+    char *reg = lds + wave * REGION;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        const float v = acc[i][e] + bias;
-        if constexpr (EB == 4) *reinterpret_cast<float *>(reg + r * LROW + lrow * 4) = v;
-        else if constexpr (OUT::code == LUX3D_BF16)
-          *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
-        else *reinterpret_cast<uint16_t *>(reg + r * LROW + lrow * 2) = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
-      }
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int it = 0; it < RP * CPR / 64; ++it) {
+        for (int e = 0; e < 16; ++e) {
+          const int r = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3), cl = j * 32 + l32;
+          const float v = acc[i][j][e] + bias[j];
+          if constexpr (EB == 4) *reinterpret_cast<float *>(reg + r * LROW + cl * 4) = v;
+          else if constexpr (OUT::code == LUX3D_BF16)
+            *reinterpret_cast<uint16_t *>(reg + r * LROW + cl * 2) = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+          else *reinterpret_cast<uint16_t *>(reg + r * LROW + cl * 2) = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFFu);
+        }
+    const int64_t r0 = m0 + wm * 64, cw = c0 + wn * 64;
+#pragma unroll
+    for (int it = 0; it < 64 * CPR / 64; ++it) {
       const int q = it * 64 + lane, r = q / CPR, part = q % CPR;
-      const int64_t row = m0 + r, col = c0w + part * EPC;
+      const int64_t row = r0 + r, col = cw + part * EPC;
       if (row >= p.M || col >= p.N) continue;
       const uint4 v = *reinterpret_cast<const uint4 *>(reg + r * LROW + part * 16);
       char *dst = ybase + (row * p.ldy + col) * EB;
@@ -622,14 +662,18 @@ __global__ __launch_bounds__(kRingThreads, 1) void q8_0_gemm_ring_f32_kernel(Q8G
     }
     return;
   }
-  if (ncol < p.N) {
+  // y rows not 16-byte aligned: one element per store
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = c0 + wn * 64 + j * 32 + l32;
+    if (col >= p.N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
         if (row >= p.M) continue;
-        store1<OUT>(ybase, row * p.ldy + ncol, acc[i][e] + bias);
+        store1<OUT>(ybase, row * p.ldy + col, acc[i][j][e] + bias[j]);
       }
   }
 }
@@ -657,11 +701,11 @@ constexpr int64_t kRingMinTiles = 256;  // MI355X compute units
 template <typename OUT>
 hipError_t launch_tiles(const Q8GemmParams &p, hipStream_t s) {
   if (p.x_f32) {
-    // f32 activations: the f32 ring kernel (K % 64 == 0, checked by the caller)
+    // f32 activations (K % 64 == 0, checked by the caller)
     const int64_t tiles_m = (p.M + 127) / 128, tiles_n = (p.N + 255) / 256;
     if (tiles_m * tiles_n > 0x7FFFFFFF) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((q8_0_gemm_ring_f32_kernel<OUT, 8>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kRingThreads), 0,
-                       s, p, (int)tiles_m, (int)tiles_n);
+    hipLaunchKernelGGL((q8_0_gemm_x3_kernel<OUT, 8>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kX3Threads), 0, s, p,
+                       (int)tiles_m, (int)tiles_n);
     return hipGetLastError();
   }
   if (ring_fits(p)) {

@@ -501,9 +501,13 @@ def _q8_linear(dev, cfg, m, k, n, what, xdt=torch.bfloat16) -> Workload:
         j = i % n_sets
         _lib.call("lux3d_q8_0_linear", dx[j], dq, dsc, db, dy[j], _cur())
     if xe == 4:
-        wl = Workload("q8_0_linear_f32", cfg, "q8_0_gemm_ring_f32_kernel<BF16>", "f32 x f32(Q8_0) -> f32 acc",
-                      nbytes, f"x[{m},{k}] f32 @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n,
-                      peak_tflops=157.3)
+        # f32 arithmetic on the bf16 matrix cores: x in three bf16 terms, the
+        # int8 weights exact, three bf16 MFMAs per f32 step (ceiling: the
+        # bf16 peak / 3)
+        wl = Workload("q8_0_linear_f32", cfg, "q8_0_gemm_x3_kernel<BF16>",
+                      "f32 x f32(Q8_0) (bf16 matrix cores, three-term x)", nbytes,
+                      f"x[{m},{k}] f32 @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n,
+                      peak_tflops=2500.0 / 3)
     else:
         wl = Workload("q8_0_linear", cfg, "q8_0_gemm_ring_kernel<BF16,...>", "bf16 x int8(Q8_0) -> f32 acc", nbytes,
                       f"x[{m},{k}] @ W[{n},{k}]^T ({what})", launch, n_sets, flops=2 * m * k * n)
