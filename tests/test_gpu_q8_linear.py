@@ -181,9 +181,10 @@ def test_q8_0_linear_large_sampled_rows(dev, ops, orc, synth):
     assert_gemm_close(host(y, "bf16")[rows], want, abs_sum, "bf16", "sampled rows")
 
 
-# f32 activations: the weights are dequantized exactly to f32 (q * d) and the
-# products summed in f32 on the f32 matrix cores; the same f32 accumulation
-# tolerance as above. (4353, 128, 3700) has 35 x 15 = 525 tiles of 128 rows,
+# f32 activations: the reference dequantizes the weights exactly to f32
+# (q * d) and sums f32 products; the kernel forms each Q8_0 block's sum of
+# x q exactly-split products on the bf16 matrix cores and scales it by d, the
+# same sum up to its order. The same f32 accumulation tolerance as above. (4353, 128, 3700) has 35 x 15 = 525 tiles of 128 rows,
 # the last holding one row, the last column piece 116 columns.
 @pytest.mark.parametrize("m,k,n", [(1029, 1024, 4096), (300, 256, 200), (1, 64, 32), (129, 2048, 136),
                                    (4353, 128, 3700)])
