@@ -330,7 +330,10 @@ int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y,
  *   y: [..., n] rows, bf16 / f16 / f32.
  * Each weight is dequantized exactly as lux3d_dequant_q8_0 does, to x's
  * dtype (bf16: RNE of the exact product; f32: the exact product), products
- * accumulate in f32 (MFMA), the bias is added in f32 and y is rounded once.
+ * accumulate in f32 on the matrix cores, the bias is added in f32 and y is
+ * rounded once. For f32 x the sum of each Q8_0 block is formed from exactly
+ * split bf16 terms of x times the exact int8 values and then scaled by the
+ * block's d: the f32 arithmetic up to the order of the sums.
  * This is the dequantize-then-matmul path of candle's GPU backends; candle's
  * CPU path instead quantizes x to Q8_0 blocks and takes integer dot
  * products.                                                                 */
@@ -361,9 +364,11 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
  *   x: f32 [N, Cin], nbr: int32 [N, 27] (from lux3d_sparse_neighbors),
  *   weight: f32 [27, Cout, Cin] (the loader's transposed kernel, weight27),
  *   bias: f32 [Cout] or NULL, out: f32 [N, Cout]; all contiguous.
- * One output-stationary implicit GEMM on the matrix cores (f32 MFMA) when
- * Cin % 16 == 0 and x, weight are 16-byte aligned; otherwise a generic
- * kernel. f32 accumulation; no scatter.
+ * One output-stationary implicit GEMM on the bf16 matrix cores when
+ * Cin % 16 == 0 and x, weight are 16-byte aligned (f32 arithmetic: operands
+ * split exactly into three bf16 terms, the six significant cross products
+ * per step, each product within one f32 ulp); otherwise a generic kernel.
+ * f32 accumulation; no scatter.
  *
  * lux3d_index_select_rows: index_select_rows (trellis2_sparse.rs:117-131):
  *   out[m, ...] = src[ids[m], ...]; src [R, ...] and out [M, ...] contiguous,
@@ -405,8 +410,9 @@ int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
  * out = 0; out[dst] += x[src] W_k^T for k = 0..26 in order; out += bias --
  * the zeros / index_add / broadcast_add sequence of SparseConv3d::forward
  * (trellis2_sparse.rs:205-242). Only present neighbours reach the matrix
- * cores (f32 MFMA), so sparse sets run several times faster than the
- * output-stationary kernel. Cin % 16 == 0 and 16-byte aligned x and weight
+ * cores (f32 arithmetic on the bf16 matrix cores, as lux3d_sparse_conv3d),
+ * so sparse sets run several times faster than the output-stationary
+ * kernel. Cin % 16 == 0 and 16-byte aligned x and weight
  * are required (else LUX3D_ERR_SHAPE / LUX3D_ERR_LAYOUT: use
  * lux3d_sparse_conv3d). */
 int lux3d_sparse_rulebook(const lux3d_tensor_t *nbr, const lux3d_tensor_t *pairs,
@@ -439,10 +445,10 @@ int lux3d_channel_to_spatial(const lux3d_tensor_t *coords, const lux3d_tensor_t 
  * input type for P v (f32 accumulation) and one rounding of the output; f32
  * on the bf16 matrix cores with q, k, v and the probabilities split exactly
  * into three bf16 terms each and the six significant cross products per
- * step (each product within half an f32 ulp), scores, probabilities and sums
+ * step (each product within one f32 ulp), scores, probabilities and sums
  * in f32. Other cases run a generic kernel in f32 throughout. The f32 paths
  * are the arithmetic of exact_sdpa_heads up to the order of the sums (and,
- * on the matrix cores, that sub-half-ulp product truncation). out must not
+ * on the matrix cores, that sub-ulp product truncation). out must not
  * overlap q, k or v.                                                         */
 int lux3d_sdpa(const lux3d_tensor_t *q, const lux3d_tensor_t *k,
                const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
