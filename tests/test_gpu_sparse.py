@@ -138,6 +138,29 @@ def test_sparse_conv3d_mfma(dev, ops, orc, n, cin, cout, res, surface, path):
     _conv_check(out.cpu().numpy()[rows], want, a)
 
 
+def test_sparse_conv3d_output_stationary_128_row_tiles(dev, ops, orc):
+    """More than 65535 * 64 voxels: the output-stationary conv takes 128-row
+    tiles (the 64-row grid would exceed the launch's y limit); 4.3M random
+    voxels in 256^3, 16 -> 16 channels, checked on sampled rows."""
+    n, cin, cout = 4_300_000, 16, 16
+    _case(op="conv3d", n=n, cin=cin, cout=cout, path="output_stationary 128-row tiles")
+    coords = random_coords(n, 256, 77)
+    rng = np.random.default_rng(78)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    w27 = (rng.standard_normal((27, cout, cin)) / np.sqrt(27 * cin)).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    wt = torch.from_numpy(w27).permute(1, 0, 2).contiguous()
+    conv = ops.SparseConv3d(wt.to(dev), torch.from_numpy(bias).to(dev), cin, cout)
+    nbr_d = ops.sparse_neighbors(torch.from_numpy(coords).to(dev))
+    out = conv.forward(nbr_d, torch.from_numpy(x).to(dev))
+    torch.cuda.synchronize()
+    rows = np.sort(np.concatenate([np.arange(64), np.arange(n - 200, n),
+                                   np.random.default_rng(3).choice(n, 400, replace=False)]))
+    nbr = orc.sparse_neighbors(coords)
+    want, a = orc.sparse_conv3d(x, nbr[rows], w27, bias, with_abs=True)
+    _conv_check(out[torch.from_numpy(rows).to(dev)].cpu().numpy(), want, a)
+
+
 @pytest.mark.parametrize("dt,ids_dt,row", [("f32", "i64", (64,)), ("bf16", "i32", (6, 8)), ("f32", "i32", (3,)),
                                            ("bf16", "i64", (5,))])
 def test_index_select_rows(dev, ops, dt, ids_dt, row):
