@@ -391,16 +391,21 @@ __device__ __forceinline__ void tap_epilogue(float *out, int64_t Cout, int64_t n
 // cycles of v_mfma_f32_32x32x2_f32. Plane rows are 16 bf16 (32 bytes) with no
 // padding: a fragment read (lane l: row l % 32, k half l / 32) covers 1 KB
 // contiguously, and each thread's 8-byte plane writes of 4 consecutive k
-// cover 512 contiguous bytes per wavefront. Two stages, one barrier per step;
+// cover 512 contiguous bytes per wavefront (at 32-deep steps, rows of 64
+// bytes, chunk c in slot c ^ ((r >> 2) & 3)). Two stages, one barrier per step;
 // the next step's global loads are issued before the current step's MFMAs.
 // This replaced a tap kernel on v_mfma_f32_32x32x2_f32 (64 x 64 tiles):
 // 7.52 -> 5.13 ms (C 1024 over 24k voxels), 1.76 -> 1.54 ms (C 256 over
 // 150k), same-box A/B.
-template <int BM, int BN>
+template <int BM, int BN, int BK = 16>
 __global__ __launch_bounds__(256) void sparse_tap_x3_kernel(SparseConvParams p, const int32_t *pairs,
                                                             const int32_t *counts, int k) {
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-  constexpr int BK = 16;
+  static_assert(BK == 16 || BK == 32, "k-step");
+  constexpr int RB = 2 * BK;  // bytes of one plane row
+  // 16-byte chunk c8 of plane row r: slot c8 at BK = 16 (a fragment read
+  // covers 1 KB contiguously), c8 ^ ((r >> 2) & 3) at BK = 32
+  auto slot = [](int c8, int r) { return BK == 16 ? c8 : c8 ^ ((r >> 2) & 3); };
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int ACH = BM * BK / 4 / 256, BCH = BN * BK / 4 / 256;
   static_assert(ACH >= 1 && BCH >= 1, "tile");
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(256) void sparse_tap_x3_kernel(SparseConvParams p, 
   }
   __syncthreads();
 
-  // chunk c = 4 consecutive k of row c / 4 at k offset 4 (c % 4)
+  // chunk c = 4 consecutive k of row c / (BK / 4) at k offset 4 (c % (BK / 4))
   const float *wk = p.w + (int64_t)k * Cout * Cin;
   // Rows without a source (past the tap's pairs) load row 0 and are zeroed
   // after the load: a branch around the load would make the compiler wait
@@ -434,19 +439,19 @@ __global__ __launch_bounds__(256) void sparse_tap_x3_kernel(SparseConvParams p, 
   bool aok[ACH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
-    const int c = t + i * 256, row = c >> 2;
+    const int c = t + i * 256, row = c / (BK / 4), part = c % (BK / 4);
     const int32_t s = src[row];
     aok[i] = s >= 0;
-    arow[i] = p.x + (int64_t)(s >= 0 ? s : 0) * Cin + (c & 3) * 4;
-    aoff[i] = row * 32 + (c & 3) * 8;
+    arow[i] = p.x + (int64_t)(s >= 0 ? s : 0) * Cin + part * 4;
+    aoff[i] = row * RB + slot(part >> 1, row) * 16 + (part & 1) * 8;
   }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) {
-    const int c = t + i * 256, row = c >> 2;
+    const int c = t + i * 256, row = c / (BK / 4), part = c % (BK / 4);
     int64_t o = n0 + row;
     o = o < Cout ? o : Cout - 1;
-    brow[i] = wk + o * Cin + (c & 3) * 4;
-    boff[i] = row * 32 + (c & 3) * 8;
+    brow[i] = wk + o * Cin + part * 4;
+    boff[i] = row * RB + slot(part >> 1, row) * 16 + (part & 1) * 8;
   }
   float4 ra[ACH], rb[BCH];
   auto load_step = [&](int64_t c0) {
@@ -477,30 +482,46 @@ __global__ __launch_bounds__(256) void sparse_tap_x3_kernel(SparseConvParams p, 
   load_step(0);
   store_step(0);
   lds_barrier();
-  const int frag = (lane & 31) * 32 + (lane >> 5) * 16;
+  // fragment rows: row (lane % 32) of each 32-row tile, 16-byte chunk
+  // 2 s + lane / 32 in sub-step s
+  int afr[TM][BK / 16], bfr[TN][BK / 16];
+#pragma unroll
+  for (int s2 = 0; s2 < BK / 16; ++s2) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * (BM / 2) + i * 32 + (lane & 31);
+      afr[i][s2] = r * RB + slot(2 * s2 + (lane >> 5), r) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * (BN / 2) + j * 32 + (lane & 31);
+      bfr[j][s2] = r * RB + slot(2 * s2 + (lane >> 5), r) * 16;
+    }
+  }
   for (int64_t st = 0; st < nsteps; ++st) {
     const int buf = (int)(st & 1);
     if (st + 1 < nsteps) load_step((st + 1) * BK);
     const char *sa = lds + buf * STAGE, *sb = sa + 3 * PA;
-    bf16x8_t a[3][TM], b[3][TN];
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
+    for (int s2 = 0; s2 < BK / 16; ++s2) {
+      bf16x8_t a[3][TM], b[3][TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        a[q][i] = *reinterpret_cast<const bf16x8_t *>(sa + q * PA + (wm * (BM / 2) + i * 32) * 32 + frag);
+      for (int q = 0; q < 3; ++q) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        b[q][j] = *reinterpret_cast<const bf16x8_t *>(sb + q * PB + (wn * (BN / 2) + j * 32) * 32 + frag);
+        for (int i = 0; i < TM; ++i) a[q][i] = *reinterpret_cast<const bf16x8_t *>(sa + q * PA + afr[i][s2]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[q][j] = *reinterpret_cast<const bf16x8_t *>(sb + q * PB + bfr[j][s2]);
+      }
+      // smallest terms first: (x3 w1, x2 w2, x1 w3), (x2 w1, x1 w2), x1 w1
+      constexpr int ta[6] = {2, 1, 0, 1, 0, 0}, tb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+      for (int u = 0; u < 6; ++u)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ta[u]][i], b[tb[u]][j], acc[i][j], 0, 0, 0);
     }
-    // smallest terms first: (x3 w1, x2 w2, x1 w3), (x2 w1, x1 w2), x1 w1
-    constexpr int ta[6] = {2, 1, 0, 1, 0, 0}, tb[6] = {0, 1, 2, 0, 1, 0};
-#pragma unroll
-    for (int u = 0; u < 6; ++u)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ta[u]][i], b[tb[u]][j], acc[i][j], 0, 0, 0);
     if (st + 1 < nsteps) store_step(buf ^ 1);
     lds_barrier();
   }
@@ -809,8 +830,12 @@ hipError_t launch_sparse_conv_rulebook(const SparseConvParams &p, const int32_t 
       hipLaunchKernelGGL((sparse_tap_x3_kernel<128, 128>), grid, dim3(256), 0, s, p, pairs, counts, k);
   } else {
     const dim3 grid((unsigned)((p.cout + 63) / 64), (unsigned)((p.n + 63) / 64));
-    for (int k = 0; k < 27; ++k)
-      hipLaunchKernelGGL((sparse_tap_x3_kernel<64, 64>), grid, dim3(256), 0, s, p, pairs, counts, k);
+    for (int k = 0; k < 27; ++k) {
+      if (p.cin % 32 == 0)  // 32-deep steps: half the barriers (1.434 against 1.468 ms, C 256)
+        hipLaunchKernelGGL((sparse_tap_x3_kernel<64, 64, 32>), grid, dim3(256), 0, s, p, pairs, counts, k);
+      else
+        hipLaunchKernelGGL((sparse_tap_x3_kernel<64, 64>), grid, dim3(256), 0, s, p, pairs, counts, k);
+    }
   }
   if (p.bias)
     hipLaunchKernelGGL(fill_rows_kernel, dim3(grid_of(p.n * p.cout)), dim3(256), 0, s, p.out, p.n, p.cout, p.bias,
