@@ -3,7 +3,8 @@
  * for candle-3d (Lux3D). This is the drop-in boundary: a Rust CustomOp (or any
  * FFI caller) passes borrowed device buffers described by lux3d_tensor_t and a
  * HIP stream; every entry point validates its arguments on the host, enqueues
- * exactly one kernel on that stream, never synchronises and never allocates.
+ * its kernels on that stream (one for each fused transformer-layer entry; see
+ * Launches below), never synchronises and never allocates.
  *
  * Each entry names the reference function(s) it replaces (paths relative to
  * crates/lux3d-core/src/ of the candle-3d tree; "candle" = the candle fork the
