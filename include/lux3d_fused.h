@@ -334,7 +334,9 @@ int lux3d_dequant_q8_0(const lux3d_tensor_t *blocks, const lux3d_tensor_t *y,
  * accumulate in f32 on the matrix cores, the bias is added in f32 and y is
  * rounded once. For f32 x the sum of each Q8_0 block is formed from exactly
  * split bf16 terms of x times the exact int8 values and then scaled by the
- * block's d: the f32 arithmetic up to the order of the sums.
+ * block's d: the f32 arithmetic up to the order of the sums (a non-finite d
+ * makes the output non-finite as in the reference, though it can be +-inf
+ * where the reference's per-weight 0 * inf gives NaN).
  * This is the dequantize-then-matmul path of candle's GPU backends; candle's
  * CPU path instead quantizes x to Q8_0 blocks and takes integer dot
  * products.                                                                 */
