@@ -44,8 +44,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // = a): a = a1 + a2 + a3. a has 24 significant bits; a1 = RNE_bf16(a) leaves
 // a remainder of at most 16 significant bits, a2 = RNE_bf16 of that one of at
 // most 8, which bf16 holds exactly (bf16 has f32's exponent range). Exact
-// while a3 stays a normal number, i.e. for |a| above about 2^-110; below, the
-// lost part is under 2^-126 in absolute terms.
+// while a3 stays a normal number, i.e. for |a| above about 2^-110 (below, the
+// lost part is under 2^-126 in absolute terms), and while a1 does not round
+// to infinity, i.e. for |a| below 2^128 (1 - 2^-9) ~ 3.39e38. An infinite or
+// NaN a gives NaN terms.
 struct Split3 {
   uint32_t t1, t2, t3;
 };
