@@ -20,6 +20,13 @@ namespace lux3d {
 namespace {
 
 constexpr int kBlock = 256;
+// Workgroup of the staged modulate rows (one row per wavefront): 8 rows
+// share one staging of the segment pieces. Same-box A/B against 256 / 1024
+// threads: configs[2] gated residual + modulate 12.9 against 13.9 / 13.0 us,
+// configs[3] 135.1 against 138.5 / 141.4 us, configs[2] modulate 7.37
+// against 7.46 / 7.45 us, configs[3] modulate 66.2 against 66.2 / 77.2 us
+// (1024-thread workgroups straddle more segment boundaries).
+constexpr int kStagedBlock = 512;
 
 template <int TPR, int BLOCK = kBlock>
 __device__ __forceinline__ float row_total(float s, float *red) {
@@ -399,8 +406,8 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   // wavefront with NC chunks per lane (configs[2] modulate: 7.1 us vs 9.4 us),
   // and so does the gated residual + modulate (configs[2]: 13.1 us against
   // 19.2 us on 2 wavefronts and 18.9 us on 4).
-  // 256-thread workgroups of several rows let modulate / gate share the
-  // staged segment pieces.
+  // Workgroups of several rows let modulate / gate share the staged segment
+  // pieces (256 threads; 512 for the one-wavefront modulate rows).
   int tpr = 0, nc = 0;
   bool row_per_block = false;
   if (vec) {
@@ -429,7 +436,10 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
     hipLaunchKernelGGL((row_kernel_any<T, MODE>), dim3((unsigned)p.rows), dim3(kBlock), 0, s, p);
     return hipGetLastError();
   }
-  const int block = row_per_block ? tpr : kBlock;
+  int block = row_per_block ? tpr : kBlock;
+  // staged segment pieces: larger workgroups stage them for more rows
+  if ((MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) && !row_per_block && tpr == 64 && kStagedBlock > kBlock)
+    block = kStagedBlock;
   const int64_t rpb = block / tpr;
   const dim3 grid((unsigned)((p.rows + rpb - 1) / rpb));
   // Stage the segment pieces in LDS when a workgroup holds several rows.
@@ -453,6 +463,10 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   LUX3D_ROW_CASE(128, 1, 256) LUX3D_ROW_CASE(128, 2, 256) LUX3D_ROW_CASE(128, 3, 256) LUX3D_ROW_CASE(128, 4, 256)
   LUX3D_ROW_CASE(128, 1, 128) LUX3D_ROW_CASE(128, 2, 128) LUX3D_ROW_CASE(128, 3, 128) LUX3D_ROW_CASE(128, 4, 128)
   LUX3D_ROW_CASE(256, 1, 256) LUX3D_ROW_CASE(256, 2, 256) LUX3D_ROW_CASE(256, 3, 256) LUX3D_ROW_CASE(256, 4, 256)
+  if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) {
+    LUX3D_ROW_CASE(64, 1, kStagedBlock) LUX3D_ROW_CASE(64, 2, kStagedBlock) LUX3D_ROW_CASE(64, 3, kStagedBlock)
+    LUX3D_ROW_CASE(64, 4, kStagedBlock) LUX3D_ROW_CASE(64, 8, kStagedBlock)
+  }
 #undef LUX3D_ROW_CASE
   return hipErrorInvalidValue;
 }
