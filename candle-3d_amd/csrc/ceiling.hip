@@ -14,8 +14,9 @@
 //    rows (or one row per workgroup when TPR is 128 / 256 and the op runs a
 //    row per workgroup);
 //  - heads: the head kernels' layout -- [B, H, N, D] views with any outer
-//    strides, D / 8 lanes per head row, two rows per thread (one for f32,
-//    whose lane l holds 16 bytes at 16 l of each half row), workgroups of `tb` consecutive tokens x all heads, q and k in
+//    strides, D / 8 lanes per head row, R rows per thread as the kernel
+//    runs them (f32: 1, its lane l holding 16 bytes at 16 l of each half
+//    row; 2-byte types: 2, or 4 for unrotated D = 128 rows), workgroups of `tb` consecutive tokens x all heads, q and k in
 //    grid.y (or both in one workgroup, as the D = 128 kernels do).
 // Every output word is the XOR of the loaded words that map to it, so no
 // load can be dropped by the compiler.
@@ -210,15 +211,19 @@ int lux3d_ceiling_rows(const void *const *in, int nin, void *const *out, int nou
 
 // q, k: [B, H, N, D] views (element strides in_s = {sB, sH, sN}, unit inner
 // stride) -> contiguous-or-strided outputs (out_s); k / ko may be NULL.
-// D 64 / 128; elem_bytes 2 / 4; both_in_one: q and k in one workgroup.
+// D 64 / 128; elem_bytes 2 / 4; both_in_one: q and k in one workgroup;
+// rows_per_thread: the head kernel's R (0: 1 for f32, 2 for 2-byte types;
+// 4 for the 2-byte D = 128 rows without a rotation).
 // Workgroup shape as the head kernels: whole heads per pass, tb tokens.
 int lux3d_ceiling_heads(const void *q, const void *k, void *qo, void *ko, int64_t B, int64_t H, int64_t N, int64_t D,
-                        int elem_bytes, const int64_t *in_s, const int64_t *out_s, int both_in_one, void *stream) {
+                        int elem_bytes, const int64_t *in_s, const int64_t *out_s, int both_in_one,
+                        int rows_per_thread, void *stream) {
   if (B * N <= 0 || H <= 0) return 0;
   if ((D != 64 && D != 128) || (elem_bytes != 2 && elem_bytes != 4)) return -6;
   if (B * N >= (int64_t(1) << 31) || H > 4096) return -6;
   const int ntens = k ? 2 : 1;
-  const int lpr = (int)(D / 8), r = elem_bytes == 4 ? 1 : 2;
+  const int lpr = (int)(D / 8), r = rows_per_thread > 0 ? rows_per_thread : (elem_bytes == 4 ? 1 : 2);
+  if (r != 1 && r != 2 && r != 4) return -6;
   const int64_t hl = H * lpr;
   const int64_t kk = hl >= 256 ? 1 : 256 / hl;
   int64_t threads = ((kk * hl + 63) / 64) * 64;
@@ -237,12 +242,13 @@ int lux3d_ceiling_heads(const void *q, const void *k, void *qo, void *ko, int64_
   const dim3 grid((unsigned)((B * N + tb - 1) / tb), two ? 1u : (unsigned)ntens), block((unsigned)threads);
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define LUX3D_HEADS(EB, D_, R_, NTB)                                                         \
-  if (elem_bytes == EB && D == D_ && (two ? 2 : 1) == NTB) {                               \
+  if (elem_bytes == EB && D == D_ && r == R_ && (two ? 2 : 1) == NTB) {                    \
     hipLaunchKernelGGL((heads_kernel<EB, D_, R_, NTB>), grid, block, 0, st, p);            \
     return status(hipGetLastError());                                                      \
   }
   LUX3D_HEADS(2, 64, 2, 1) LUX3D_HEADS(2, 64, 2, 2) LUX3D_HEADS(2, 128, 2, 1) LUX3D_HEADS(2, 128, 2, 2)
   LUX3D_HEADS(4, 64, 1, 1) LUX3D_HEADS(4, 64, 1, 2) LUX3D_HEADS(4, 128, 1, 1) LUX3D_HEADS(4, 128, 1, 2)
+  LUX3D_HEADS(2, 128, 4, 1) LUX3D_HEADS(2, 128, 4, 2)
 #undef LUX3D_HEADS
   return -6;
 }

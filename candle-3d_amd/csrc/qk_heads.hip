@@ -460,10 +460,9 @@ bool offsets_fit_32(const HeadParams &p, int eb) {
   return true;
 }
 
-template <typename T, int D, int NTB, bool O32>
+template <typename T, int D, int NTB, int R, bool O32>
 hipError_t launch_cases(int norm, int rot, const HeadParams &p, int tb, const dim3 &grid, const dim3 &block, size_t lds,
                         hipStream_t s) {
-  constexpr int R = T::bytes == 4 ? 1 : 2;
 #define LUX3D_HEAD_CASE(NORM_, ROT_)                                                                          \
   if (norm == NORM_ && rot == ROT_) {                                                                         \
     hipLaunchKernelGGL((head_kernel<T, D, NORM_, ROT_, R, NTB, O32>), grid, block, lds, s, p, tb);            \
@@ -481,11 +480,10 @@ hipError_t launch_cases(int norm, int rot, const HeadParams &p, int tb, const di
   return hipErrorInvalidValue;
 }
 
-template <typename T, int D, int NTB>
+template <typename T, int D, int NTB, int R>
 hipError_t launch_dn(int norm, int rot, const HeadParams &p0, hipStream_t s) {
   const int64_t tokens = p0.B * p0.N;
   constexpr int LPR = D / 8;
-  constexpr int R = T::bytes == 4 ? 1 : 2;
   // Whole heads per pass: threads = k*H*LPR rounded to wavefronts, <= 256.
   const int64_t hl = p0.H * LPR;
   int64_t k = hl >= 256 ? 1 : 256 / hl;
@@ -499,20 +497,30 @@ hipError_t launch_dn(int norm, int rot, const HeadParams &p0, hipStream_t s) {
   div_magic(p.N, p.div_n_m, p.div_n_s);
   const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
   const dim3 grid((unsigned)((tokens + tb - 1) / tb), NTB == 2 ? 1u : (unsigned)p.ntens), block((unsigned)threads);
-  if (offsets_fit_32(p, T::bytes)) return launch_cases<T, D, NTB, true>(norm, rot, p, (int)tb, grid, block, lds, s);
-  return launch_cases<T, D, NTB, false>(norm, rot, p, (int)tb, grid, block, lds, s);
+  if (offsets_fit_32(p, T::bytes)) return launch_cases<T, D, NTB, R, true>(norm, rot, p, (int)tb, grid, block, lds, s);
+  return launch_cases<T, D, NTB, R, false>(norm, rot, p, (int)tb, grid, block, lds, s);
 }
 
 // q and k share a workgroup for D = 128 (measured: configs[2] RMS and
 // configs[3] L2+RoPE gain 7-9%); for D = 64 one tensor per workgroup is
-// faster.
+// faster. Rows per thread R: 1 for f32, 2 for 2-byte types,
+// and 4 for 2-byte D = 128 rows without a rotation (configs[2] RMS heads:
+// 13.0 against 14.0 us with R = 2; with a rotation the phase staging grows
+// with R, and configs[3] L2 + 3D RoPE takes 140.7 against 133.3 us).
 template <typename T, int D>
 hipError_t launch_d(int norm, int rot, const HeadParams &p, hipStream_t s) {
   const int64_t tokens = p.B * p.N;
   if (tokens <= 0 || p.H <= 0) return hipSuccess;
   if (tokens > INT32_MAX || p.H > 4096) return hipErrorInvalidValue;
-  if (D == 128 && p.ntens == 2) return launch_dn<T, D, 2>(norm, rot, p, s);
-  return launch_dn<T, D, 1>(norm, rot, p, s);
+  constexpr int R = T::bytes == 4 ? 1 : 2;
+  if constexpr (T::bytes == 2 && D == 128) {
+    if (rot == HR_NONE) {
+      if (p.ntens == 2) return launch_dn<T, D, 2, 4>(norm, rot, p, s);
+      return launch_dn<T, D, 1, 4>(norm, rot, p, s);
+    }
+  }
+  if (D == 128 && p.ntens == 2) return launch_dn<T, D, 2, R>(norm, rot, p, s);
+  return launch_dn<T, D, 1, R>(norm, rot, p, s);
 }
 
 template <typename T>

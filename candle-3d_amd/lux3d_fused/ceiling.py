@@ -33,7 +33,7 @@ def _load():
     lib.lux3d_ceiling_streams.argtypes = [PP, I, PP, I, I64, I64, P]
     lib.lux3d_ceiling_rows.argtypes = [PP, I, PP, I, I64, I64, I, I, I, P]
     lib.lux3d_ceiling_heads.argtypes = [P, P, P, P, I64, I64, I64, I64, I, ctypes.POINTER(I64),
-                                        ctypes.POINTER(I64), I, P]
+                                        ctypes.POINTER(I64), I, I, P]
     for f in (lib.lux3d_ceiling_streams, lib.lux3d_ceiling_rows, lib.lux3d_ceiling_heads):
         f.restype = ctypes.c_int
     return lib
@@ -101,7 +101,7 @@ class Copy:
                 k = src.data_ptr() + in_off[1] * eb if ntens == 2 else None
                 _check(LIB.lux3d_ceiling_heads(q, k, dst[0].data_ptr(), dst[1].data_ptr() if ntens == 2 else None,
                                                B, H, N, D, eb, si, so, int(pattern.get("both_in_one", False)),
-                                               stream()), "heads")
+                                               int(pattern.get("rows_per_thread", 0)), stream()), "heads")
             self.bytes = 2 * ntens * B * H * N * D * eb
         else:
             nin, nout = pattern["nin"], pattern["nout"]

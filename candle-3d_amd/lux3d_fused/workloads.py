@@ -355,8 +355,9 @@ def cfg2_rms_norm_heads(dev) -> Workload:
         _lib.call("lux3d_rms_norm_heads", dq, dwq, dk, dwk, 1e-6, dqo, dko, _cur())
     wl = Workload("rms_norm_heads", 2, "head_kernel<BF16,128,RMS>", "bf16", nbytes,
                   f"q,k [{B},{H},{L},{D}] in qkv", launch, n)
+    # the unrotated D = 128 rows run four rows per thread
     wl.pattern = {"kind": "heads", "B": B, "H": H, "N": L, "D": D, "eb": 2, "ntens": 2, "both_in_one": True,
-                  "in_numel": B * L * H * 3 * D, "in_offsets": [0, D],
+                  "rows_per_thread": 4, "in_numel": B * L * H * 3 * D, "in_offsets": [0, D],
                   "in_strides": [L * H * 3 * D, 3 * D, H * 3 * D], "out_strides": [H * L * D, L * D, D]}
     wl._keep = (qkvs, outs, Ds, wq, wk, dwq, dwk)
     return wl
