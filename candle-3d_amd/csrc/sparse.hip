@@ -570,6 +570,43 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64
   }
 }
 
+// Rows of at least 512 bytes (16-byte aligned): one wavefront per row, four
+// rows per workgroup; each lane keeps up to four 16-byte chunks in flight
+// (4 KB of the row per pass) before storing them. The row count and the row
+// id are read once per wavefront.
+template <typename IDX>
+__global__ __launch_bounds__(256) void gather_rows_wave_kernel(const char *src, int64_t nsrc, const IDX *ids,
+                                                               int64_t rows, const int32_t *count, char *out,
+                                                               int64_t row_bytes, int32_t *bad) {
+  const int64_t lim = count ? (int64_t)*count : rows;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= lim || m >= rows) return;  // wave-uniform
+  const int64_t id = (int64_t)ids[m];
+  const bool ok = id >= 0 && id < nsrc;
+  if (bad && lane == 0 && !ok) atomicAdd(bad, 1);
+  char *dr = out + m * row_bytes;
+  const int64_t units = row_bytes / 16;
+  if (!ok) {  // wave-uniform: the row is written as zeros, src is not read
+    for (int64_t u = lane; u < units; u += 64) *reinterpret_cast<uint4 *>(dr + u * 16) = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const char *sr = src + id * row_bytes;
+  for (int64_t u0 = 0; u0 < units; u0 += 256) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t u = u0 + i * 64 + lane;
+      v[i] = u < units ? *reinterpret_cast<const uint4 *>(sr + u * 16) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t u = u0 + i * 64 + lane;
+      if (u < units) *reinterpret_cast<uint4 *>(dr + u * 16) = v[i];
+    }
+  }
+}
+
 __global__ __launch_bounds__(64) void zero_counter_kernel(int32_t *c) {
   if (threadIdx.x == 0) *c = 0;
 }
@@ -854,6 +891,17 @@ hipError_t launch_gather_rows(const void *src, int64_t nsrc, const void *ids, bo
   const dim3 grid(grid_of(rows * units)), block(256);
   const char *sp = static_cast<const char *>(src);
   char *op = static_cast<char *>(out);
+  if (vec && units >= 32) {  // configs[3] C2S (2 KB child rows): 90.0 against 91.8 us
+    const dim3 wgrid((unsigned)((rows + 3) / 4));
+    if ((rows + 3) / 4 > INT32_MAX) return hipErrorInvalidValue;
+    if (ids64)
+      hipLaunchKernelGGL((gather_rows_wave_kernel<int64_t>), wgrid, block, 0, s, sp, nsrc,
+                         static_cast<const int64_t *>(ids), rows, count, op, row_bytes, bad);
+    else
+      hipLaunchKernelGGL((gather_rows_wave_kernel<int32_t>), wgrid, block, 0, s, sp, nsrc,
+                         static_cast<const int32_t *>(ids), rows, count, op, row_bytes, bad);
+    return hipGetLastError();
+  }
   if (ids64) {
     if (vec) hipLaunchKernelGGL((gather_rows_kernel<int64_t, true>), grid, block, 0, s, sp, nsrc,
                                 static_cast<const int64_t *>(ids), rows, count, op, row_bytes, bad);

@@ -162,7 +162,8 @@ def test_sparse_conv3d_output_stationary_128_row_tiles(dev, ops, orc):
 
 
 @pytest.mark.parametrize("dt,ids_dt,row", [("f32", "i64", (64,)), ("bf16", "i32", (6, 8)), ("f32", "i32", (3,)),
-                                           ("bf16", "i64", (5,))])
+                                           ("bf16", "i64", (5,)), ("f32", "i64", (128,)), ("f32", "i32", (1028,)),
+                                           ("bf16", "i32", (16, 64))])
 def test_index_select_rows(dev, ops, dt, ids_dt, row):
     _case(op="index_select", dt=dt, ids=ids_dt, row=row)
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16}[dt]
@@ -200,7 +201,7 @@ def test_sparse_neighbors_counts_unpackable_coords(dev, ops, orc):
 
 
 @pytest.mark.parametrize("n,c,fdt,ldt", [(3, 16, "f32", "f32"), (5000, 64, "f32", "f32"), (3000, 128, "bf16", "bf16"),
-                                         (1025, 8, "f32", "f16"), (0, 8, "f32", "f32")])
+                                         (1025, 8, "f32", "f16"), (0, 8, "f32", "f32"), (2000, 2048, "f32", "f32")])
 def test_channel_to_spatial(dev, ops, orc, n, c, fdt, ldt):
     _case(op="c2s", n=n, c=c, feats=fdt, logits=ldt)
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
