@@ -482,6 +482,21 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) o[1][dt] = M::run(vfrag(dt, kt, jj), pf[1][kt * 2 + jj], o[1][dt]);
     } else {
+      // DMA (the D = 128 kernels): every V fragment of the block is read
+      // before the softmax, so the LDS latency hides behind the VALU work
+      // (TRELLIS.2 40k 10.42 -> 9.91 ms, TripoSG 83.0 -> 81.6 us; D = 64 and
+      // the register-staged D = 128 kernel do not gain or would spill).
+      constexpr int NVF = DMA ? NDT * NKT * 2 : 1;
+      op_t vf[NVF];
+      if constexpr (DMA) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) vf[(dt * NKT + kt) * 2 + jj] = vfrag(dt, kt, jj);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         softmax(qt, 0, NKT);
@@ -493,7 +508,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
-            const op_t a = vfrag(dt, kt, jj);
+            const op_t a = DMA ? vf[(dt * NKT + kt) * 2 + jj] : vfrag(dt, kt, jj);
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) o[qt][dt] = M::run(a, pf[qt][kt * 2 + jj], o[qt][dt]);
           }
