@@ -618,7 +618,23 @@ __global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int
     s_c4[i] = c % (D / 4);
   }
   float4 rk[KCH], rv[KCH];
-  auto load_kv = [&](int64_t j) {
+  // element offsets of this thread's chunks from a block's first key
+  int64_t k_off[KCH], v_off[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    k_off[i] = (int64_t)s_row[i] * p.k_st + s_c4[i] * 4;
+    v_off[i] = (int64_t)s_row[i] * p.v_st + s_c4[i] * 4;
+  }
+  // `clamp` (the tail block only): keys past Lk read row Lk - 1
+  auto load_kv = [&](int64_t j, bool clamp) {
+    if (!clamp) {
+      const float *kb = kbase + j * BKV * p.k_st, *vb = vbase + j * BKV * p.v_st;
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) rk[i] = *reinterpret_cast<const float4 *>(kb + k_off[i]);
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) rv[i] = *reinterpret_cast<const float4 *>(vb + v_off[i]);
+      return;
+    }
     const int64_t key0 = j * BKV;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
@@ -651,7 +667,7 @@ __global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int
   const int64_t nkv = (Lk + BKV - 1) / BKV;
   const bool tail = (Lk % BKV) != 0;
 
-  load_kv(0);
+  load_kv(0, nkv == 1 && tail);
   store_kv(0);
   lds_barrier();
 
@@ -660,7 +676,7 @@ __global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int
   auto step = [&](int64_t j, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
     const int buf = (int)(j & 1);
-    if (j + 1 < nkv) load_kv(j + 1);
+    if (j + 1 < nkv) load_kv(j + 1, tail && j + 2 == nkv);
     const uint16_t *K1 = smem + (buf * 6 + 0) * PL, *K2 = smem + (buf * 6 + 1) * PL, *K3 = smem + (buf * 6 + 2) * PL;
 
     // S^T = K Q^T: lane holds key 8 * (i / 4) + 4 * hh + i % 4 of each 32-key tile, query l32
