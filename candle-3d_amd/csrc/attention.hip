@@ -355,13 +355,17 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
           }
     }
 
-    // online softmax of query tile qt; P packed as the B operand of O^T += V^T P^T
+    // online softmax of query tile qt in two parts. smax moves the reference
+    // maximum; after it one wave-uniform branch rescales O (rescale_all);
+    // sexp then forms the probabilities (P packed as the B operand of
+    // O^T += V^T P^T). Issued after that branch, the exponentials share one
+    // basic block with the P v MFMAs, so the two can interleave.
     op_t pf[QT][NKT * 2];
     float alpha_q[QT];
-    auto softmax = [&](int qt, int k0, int k1) {  // over key tiles [k0, k1)
+    auto smax = [&](int qt) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int kt = k0; kt < k1; ++kt)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
       const float cand = half_swap_max(mx) * c2;
@@ -375,11 +379,31 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       }
       alpha_q[qt] = __builtin_amdgcn_exp2f(m[qt] - mn);
       m[qt] = mn;
+    };
+    auto rescale = [&](int qt) {
+      if (!LAZY || __builtin_amdgcn_ballot_w64(alpha_q[qt] != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha_q[qt];
+      }
+    };
+    auto rescale_all = [&]() {
+      bool any = false;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) any = any || alpha_q[qt] != 1.f;
+      if (!LAZY || __builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha_q[qt];
+      }
+    };
+    auto sexp = [&](int qt) {
+      const float mn = m[qt];
       float ls = 0.f;
       if constexpr (EXACTP) {
         // f32 probabilities stay in s; split into bf16 terms at the P v product
 #pragma unroll
-        for (int kt = k0; kt < k1; ++kt)
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int i = 0; i < 16; i += 2) {
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][i], c2, -mn));
@@ -392,7 +416,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         return;
       }
 #pragma unroll
-      for (int kt = k0; kt < k1; ++kt)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           u32x4_t pk;
@@ -409,13 +433,6 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         }
       l[qt] = l[qt] * alpha_q[qt] + ls;
     };
-    auto rescale = [&](int qt) {
-      if (!LAZY || __builtin_amdgcn_ballot_w64(alpha_q[qt] != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[qt][dt] *= alpha_q[qt];
-      }
-    };
-    // A = V^T[dim l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of tile kt
     // A = V^T[dim dt * 32 + l32][keys 16 * jj + 4 * hh + {0..3, 8..11}] of
     // tile kt (the accumulator order of the probabilities), read from V's
     // [key][dim] rows: ds_read_b64_tr_b16 hands lane i of each 16-lane group
@@ -457,24 +474,28 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     };
     if constexpr (EXACTP) {
 #pragma unroll
+      // one query tile at a time: with both tiles' exponentials in one basic
+      // block the two-tile kernel spills
       for (int qt = 0; qt < QT; ++qt) {
-        softmax(qt, 0, NKT);
+        smax(qt);
         rescale(qt);
+        sexp(qt);
         pv_exact(qt);
       }
     } else if constexpr (PHASED && QT == 2) {
       // P v of query tile 0 has no dependence on the softmax of tile 1:
       // issued together, the matrix cores and the VALU overlap in one wavefront
-      softmax(0, 0, NKT);
-      rescale(0);
+      smax(0);
+      smax(1);
+      rescale_all();
+      sexp(0);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) o[0][dt] = M::run(vfrag(dt, kt, jj), pf[0][kt * 2 + jj], o[0][dt]);
-      softmax(1, 0, NKT);
-      rescale(1);
+      sexp(1);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -498,10 +519,10 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        softmax(qt, 0, NKT);
-        rescale(qt);
-      }
+      for (int qt = 0; qt < QT; ++qt) smax(qt);
+      rescale_all();
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) sexp(qt);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll

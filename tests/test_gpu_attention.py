@@ -183,13 +183,14 @@ def test_sdpa_generic_kernel(dev, ops, orc, case):
 
 
 @pytest.mark.parametrize("b,n,h,d,lk", [(2, 300, 3, 64, None), (1, 257, 2, 128, None), (1, 77, 2, 128, 130),
-                                         (1, 1, 1, 64, 1), (1, 33, 2, 64, 1000)])
+                                         (1, 1, 1, 64, 1), (1, 33, 2, 64, 1000), (1, 40, 2, 64, 96),
+                                         (1, 64, 1, 128, 32)])
 def test_sdpa_f32_matrix_cores(dev, ops, orc, b, n, h, d, lk):
     """f32 q, k, v with D 64 / 128 take the matrix-core kernel for f32
     (attn_f32x3_kernel: three-term bf16 splits, f32 scores and
     probabilities), held to the f32 bar: self-attention on the permuted views
     of a fused qkv buffer, and cross-attention with key counts that leave a
-    partial block."""
+    partial block or fill whole blocks (no key clamp at all)."""
     _print_case(op="sdpa f32 mfma", b=b, n=n, h=h, d=d, lk=lk)
     if lk is None:
         q, k, v = qkv_views(dev, b, n, h, d, "f32", 17 + n)
