@@ -942,8 +942,12 @@ hipError_t launch_f32x3(const AttnParams &p, hipStream_t s) {
 // TRELLIS.2 40k voxels 10.3 against 11.2 ms, bit-identical). D 64 stays
 // register-staged (with rotating inputs DMA gained nothing there):
 // 128-query workgroups for short sequences, which fill the CUs in more,
-// shorter rounds, and 256-query ones (the phased form) for long ones.
+// shorter rounds, and 256-query ones (the phased form) for long ones or
+// when even 256-query workgroups number kPhasedMinWg or more (VGGT frame
+// attention, 768 of them: 89.6 against 91.6 us; with q's LayerNorm fused the
+// 128-query form stays ahead, 91.4 against 92.2 us).
 constexpr int64_t kShortQ = 4096;
+constexpr int64_t kPhasedMinWg = 512;
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
@@ -968,7 +972,9 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {
-        if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
+        const int64_t nwg2 = p.B * p.H * ((p.Lq + 255) / 256);
+        if (p.Lq <= kShortQ && (p.qln || nwg2 < kPhasedMinWg))
+          return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
         return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);
       }
       if (p.D == 128) {
@@ -979,7 +985,7 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   } else {
     if (p.mfma) {
       // f32 on the bf16 matrix cores (three-term splits), 32-key blocks: at
-      // D 64 55 KB of LDS and 173 VGPRs, two workgroups per CU; at D 128
+      // D 64 55 KB of LDS and 181 VGPRs, two workgroups per CU; at D 128
       // 104 KB, one. Against the f32 MFMA kernel this replaced (same box,
       // graph-timed): VGGT frame 342 against 541 us, TripoSG 401 against 523,
       // DINOv3 52.5 against 86.0
