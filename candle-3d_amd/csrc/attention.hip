@@ -941,13 +941,29 @@ hipError_t launch_f32x3(const AttnParams &p, hipStream_t s) {
 // a head fits the 32-bit buffer offsets (TripoSG 87.2 against 92.3 us,
 // TRELLIS.2 40k voxels 10.3 against 11.2 ms, bit-identical). D 64 stays
 // register-staged (with rotating inputs DMA gained nothing there):
-// 128-query workgroups for short sequences, which fill the CUs in more,
-// shorter rounds, and 256-query ones (the phased form) for long ones or
-// when even 256-query workgroups number kPhasedMinWg or more (VGGT frame
-// attention, 768 of them: 89.6 against 91.6 us; with q's LayerNorm fused the
-// 128-query form stays ahead, 91.4 against 92.2 us).
+// 128-query workgroups (three per CU) or 256-query ones (the phased form,
+// two per CU), whichever leaves the busiest CU less work (below); with q's
+// LayerNorm fused, 128-query ones up to 4096 queries (VGGT frame 91.4
+// against 92.2 us).
 constexpr int64_t kShortQ = 4096;
-constexpr int64_t kPhasedMinWg = 512;
+constexpr int64_t kCus = 256;  // MI355X
+
+// Time of the busiest CU when nwg workgroups spread evenly over the CUs and
+// per_cu of them run at once; t[k] is the time of k resident workgroups.
+int64_t busiest_cu_time(int64_t nwg, int per_cu, const int *t) {
+  const int64_t m = (nwg + kCus - 1) / kCus;
+  return (m / per_cu) * t[per_cu] + t[m % per_cu];
+}
+// t: VGGT frames (1374 keys, D 64) timed with k workgroups resident per CU,
+// in 0.1 us: 128-query 20.4 / 32.5 / 45.4 us (k = 1 / 2 / 3), 256-query
+// 32.0 / 54.7 us (k = 1 / 2). The 256-query form must win by 3%; so set,
+// the rule picks the faster form at each of 2 to 8 frames, 1 / 2 / 4 x 2048
+// tokens and DINOv3's 1029 (both forms timed at each).
+bool use_256_query(const AttnParams &p) {
+  static const int t1[4] = {0, 204, 325, 454}, t2[3] = {0, 320, 547};
+  const int64_t n1 = p.B * p.H * ((p.Lq + 127) / 128), n2 = p.B * p.H * ((p.Lq + 255) / 256);
+  return 100 * busiest_cu_time(n2, 2, t2) < 97 * busiest_cu_time(n1, 3, t1);
+}
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
@@ -972,8 +988,7 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {
-        const int64_t nwg2 = p.B * p.H * ((p.Lq + 255) / 256);
-        if (p.Lq <= kShortQ && (p.qln || nwg2 < kPhasedMinWg))
+        if (p.qln ? p.Lq <= kShortQ : !use_256_query(p))
           return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
         return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);
       }
