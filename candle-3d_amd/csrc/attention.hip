@@ -190,8 +190,11 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     float w8[8], b8[8];
     param8(p.qw, p.qw_dt, ch * 8, 1.f, w8);
     param8(p.qb, p.qb_dt, ch * 8, 0.f, b8);
-#pragma unroll 1
-    for (int row = lane / LPR; row < QT * 32; row += RPP) {
+    // the passes unrolled: their row loads are all in flight together
+    static_assert((QT * 32) % RPP == 0, "whole passes");
+#pragma unroll
+    for (int it = 0; it < QT * 32 / RPP; ++it) {
+      const int row = lane / LPR + it * RPP;
       int64_t qr = qb * BQ + wave * QT * 32 + row;
       qr = qr < Lq ? qr : Lq - 1;
       float x[8];
