@@ -206,6 +206,24 @@ def test_sdpa_f32_matrix_cores(dev, ops, orc, b, n, h, d, lk):
     assert_attn_close(out, want, wabs, "f32", False, f"f32 mfma {b}x{h}x{n}x{d} lk={lk}")
 
 
+@pytest.mark.parametrize("b", [5, 6, 8])
+def test_sdpa_vggt_frames_sampled(dev, ops, orc, b):
+    """VGGT frame attention over b frames (1374 tokens, 16 heads, D 64):
+    the launcher runs 256-query workgroups for 5 and 8 frames and 128-query
+    ones for 6 (whichever leaves the busiest CU less work); the oracle checks
+    32 sampled queries of every head."""
+    n, h, d = 1374, 16, 64
+    _print_case(op="sdpa frames sampled", b=b, n=n, h=h, d=d)
+    q, k, v = qkv_views(dev, b, n, h, d, "bf16", 40 + b)
+    out = ops.sdpa(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(b).choice(n, 32, replace=False))
+    qs = np.ascontiguousarray(host(q, "bf16")[:, :, rows])
+    want, wabs = orc.sdpa(qs, host(k, "bf16"), host(v, "bf16"), 0.125, dt=orc.BF16, with_abs=True)
+    got = out[:, :, torch.from_numpy(rows).to(dev)]
+    assert_attn_close(got, want, wabs, "bf16", True, f"{b} frames sampled")
+
+
 def test_sdpa_vggt_global_attention_sampled(dev, ops, orc):
     """VGGT global attention (8 frames x 1374 tokens = 10992 per head, 16
     heads, D 64); the oracle checks 64 sampled queries of every head."""
