@@ -961,9 +961,9 @@ hipError_t launch_f32x3(const AttnParams &p, hipStream_t s) {
 // TRELLIS.2 40k voxels 10.3 against 11.2 ms, bit-identical). D 64 stays
 // register-staged (with rotating inputs DMA gained nothing there):
 // 128-query workgroups (three per CU) or 256-query ones (the phased form,
-// two per CU), whichever leaves the busiest CU less work (below); with q's
-// LayerNorm fused, 128-query ones up to 4096 queries (VGGT frame 91.4
-// against 92.2 us).
+// two per CU), whichever leaves the busiest CU less work (below), also with
+// q's LayerNorm fused (VGGT frame 92.8 against 96.0 us); the exact-
+// probability kernel takes 128-query ones up to kShortQ queries.
 constexpr int64_t kShortQ = 4096;
 constexpr int64_t kCus = 256;  // MI355X
 
@@ -1007,7 +1007,7 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {
-        if (p.qln ? p.Lq <= kShortQ : !use_256_query(p))
+        if (!use_256_query(p))
           return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
         return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);
       }
