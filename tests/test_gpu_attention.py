@@ -206,22 +206,23 @@ def test_sdpa_f32_matrix_cores(dev, ops, orc, b, n, h, d, lk):
     assert_attn_close(out, want, wabs, "f32", False, f"f32 mfma {b}x{h}x{n}x{d} lk={lk}")
 
 
-@pytest.mark.parametrize("b", [5, 6, 8])
-def test_sdpa_vggt_frames_sampled(dev, ops, orc, b):
+@pytest.mark.parametrize("b,dt", [(5, "bf16"), (6, "bf16"), (8, "bf16"), (8, "f16")])
+def test_sdpa_vggt_frames_sampled(dev, ops, orc, b, dt):
     """VGGT frame attention over b frames (1374 tokens, 16 heads, D 64):
     the launcher runs 256-query workgroups for 5 and 8 frames and 128-query
     ones for 6 (whichever leaves the busiest CU less work); the oracle checks
     32 sampled queries of every head."""
     n, h, d = 1374, 16, 64
-    _print_case(op="sdpa frames sampled", b=b, n=n, h=h, d=d)
-    q, k, v = qkv_views(dev, b, n, h, d, "bf16", 40 + b)
+    _print_case(op="sdpa frames sampled", b=b, n=n, h=h, d=d, dt=dt)
+    q, k, v = qkv_views(dev, b, n, h, d, dt, 40 + b)
     out = ops.sdpa(q, k, v, 0.125)
     torch.cuda.synchronize()
     rows = np.sort(np.random.default_rng(b).choice(n, 32, replace=False))
-    qs = np.ascontiguousarray(host(q, "bf16")[:, :, rows])
-    want, wabs = orc.sdpa(qs, host(k, "bf16"), host(v, "bf16"), 0.125, dt=orc.BF16, with_abs=True)
+    qs = np.ascontiguousarray(host(q, dt)[:, :, rows])
+    odt = orc.BF16 if dt == "bf16" else orc.F16
+    want, wabs = orc.sdpa(qs, host(k, dt), host(v, dt), 0.125, dt=odt, with_abs=True)
     got = out[:, :, torch.from_numpy(rows).to(dev)]
-    assert_attn_close(got, want, wabs, "bf16", True, f"{b} frames sampled")
+    assert_attn_close(got, want, wabs, dt, True, f"{b} frames sampled {dt}")
 
 
 def test_sdpa_vggt_global_attention_sampled(dev, ops, orc):
