@@ -418,7 +418,13 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, int64_t bytes) 
                  __builtin_amdgcn_readfirstlane(n), 0x00020000};
 }
 // Each lane reads 16 (4) bytes at voff + soff of the buffer; the wavefront
-// writes them in lane order at LDS byte address lds.
+// writes them in lane order at LDS byte address lds. Inline assembly rather
+// than the compiler's buffer-load-to-LDS builtin: the compiler then does not
+// know the LDS is written and inserts no vmcnt waits of its own (the callers
+// wait explicitly), which kept the Q8_0 ring 2% faster. hipcc warns that m0 is
+// a reserved register in the clobber list; the kernels of this library make
+// no m0 use of their own (their assembly holds m0 only in these pairs), so
+// nothing live is overwritten.
 __device__ __forceinline__ void lds_load16(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
                : "memory", "m0");
