@@ -298,6 +298,29 @@ def test_sdpa_layernorm_rope2d_equals_the_two_launches(dev, ops, orc, d, case):
         assert np.all(np.abs(g64 - w64) <= bound)
 
 
+def test_sdpa_layernorm_rope2d_vggt_frames_equals_the_two_launches(dev, ops):
+    """The configs[1] shape (8 frames, 16 heads, D 64), where both the fused
+    q LayerNorm + RoPE attention and lux3d_sdpa run 256-query workgroups:
+    the fused result equals the two launches bit for bit."""
+    from lux3d_fused import synth
+    b, h, d = 8, 16, 64
+    _print_case(op="sdpa_layernorm_rope2d frames", b=b, h=h, d=d)
+    pos = synth.vggt_positions(b, 37, 37)
+    n = pos.shape[1]
+    g = torch.Generator(device="cpu").manual_seed(77)
+    qkv = (torch.randn((b, n, 3, h, d), generator=g) * 2 + 0.5).to(dev).to(torch.bfloat16).permute(2, 0, 3, 1, 4)
+    q_raw, k_raw, v = qkv[0], qkv[1], qkv[2]
+    qw, qb = (1 + 0.1 * torch.randn(d, generator=g)).to(dev), (0.1 * torch.randn(d, generator=g)).to(dev)
+    kw, kb = (1 + 0.1 * torch.randn(d, generator=g)).to(dev), (0.1 * torch.randn(d, generator=g)).to(dev)
+    emb = ops.Rope2d(100.0).embeddings(torch.from_numpy(pos).to(dev), d)
+    k_n = ops.apply_layernorm_rope(k_raw, (kw, kb, 1e-6), emb)
+    fused = ops.sdpa_layernorm_rope2d(q_raw, (qw, qb, 1e-6), emb, k_n, v, 0.125)
+    two = ops.sdpa(ops.apply_layernorm_rope(q_raw, (qw, qb, 1e-6), emb), k_n, v, 0.125)
+    torch.cuda.synchronize()
+    assert torch.isfinite(fused.float()).all()
+    assert torch.equal(fused, two)
+
+
 @pytest.mark.parametrize("dt,d,lk", [("f32", 64, 200), ("f32", 128, 77), ("bf16", 128, 200), ("bf16", 64, 130),
                                      ("f16", 128, 33)])
 def test_sdpa_keys_past_lk_are_not_read(dev, ops, orc, dt, d, lk):
