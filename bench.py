@@ -16,6 +16,10 @@ op is timed the same way and reported under "ops", each with:
     bytes with no arithmetic, as contiguous streams and in the op's own access
     pattern (csrc/ceiling.hip), timed the same way: the achievable bandwidth
     at that size and layout on this chip;
+  - `best_copy_us`: the fastest of a family of plain copies of the op's
+    streams (one-shot and persistent grids, 1-8 chunks per thread, 256-1024
+    threads per workgroup), the bound the op's fraction of peak is read
+    against (the full size sweep: `bench.py --ceiling-sweep`);
   - `trace_us`: the kernel's average duration in the committed rocprofv3
     kernel trace of `bench.py --profile <op>` (profiles/kernel_trace_<op>.md),
     and `traffic_bytes` from the committed FETCH_SIZE / WRITE_SIZE summary
@@ -24,8 +28,13 @@ op is timed the same way and reported under "ops", each with:
     sample of the same op, on all threads of the box's CPU share and on one
     thread (median of 20 runs after 3 warm-ups).
 
+The last stdout line is the headline JSON (a few KB: the step, its roofline
+and CPU baseline, and one short entry per target op); the full per-op table
+is printed to stderr as `[bench] table [...]` and, with --table-out, to a file.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
        python bench.py --profile NAME [--iters K]   (one op, for rocprofv3)
+       python bench.py --ceiling-sweep [--sweep-variants all|best] [--iters K]
 """
 import argparse
 import json
@@ -53,6 +62,13 @@ def parse():
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-runs", type=int, default=20)
+    ap.add_argument("--table-out", default=None, help="also write the full per-op table (JSON) to this file")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the copy ceilings (quick A/B runs)")
+    ap.add_argument("--ceiling-sweep", action="store_true",
+                    help="time the plain-copy family (lux3d_fused.ceiling) over copy sizes instead of the ops")
+    ap.add_argument("--sweep-mb", type=int, nargs="*", default=None, help="--ceiling-sweep: these sizes only")
+    ap.add_argument("--sweep-variants", default="all", choices=["all", "best", "throttle"],
+                    help="--ceiling-sweep: every variant, or the subset the per-op table uses (for rocprofv3)")
     return ap.parse_args()
 
 
@@ -116,6 +132,58 @@ def ceilings(torch, dev, pattern, n):
     del pat
     torch.cuda.empty_cache()
     return cu, pu, nbytes
+
+
+# copy sizes of the sweep, in MB moved per launch (half read, half written):
+# the configs' op sizes (11-787 MB) and the points between them
+SWEEP_MB = [8, 11, 13, 17, 24, 34, 50, 67, 90, 134, 180, 270, 393, 512, 787, 1024]
+
+
+def ceiling_sweep(torch, dev, which, iters, sizes=None):
+    """Time the plain-copy family at every SWEEP_MB size (one input stream,
+    one output stream, rotation sets beyond the Infinity Cache, graph-timed
+    like the ops). Prints one JSON line per size, the manifest of launches
+    in order (for the rocprofv3 trace summary), and a summary line."""
+    from lux3d_fused import ceiling as C
+    variants = {"all": C.sweep_variants, "throttle": C.throttle_variants, "best": lambda: C.BEST_VARIANTS}[which]()
+    manifest, best = [], {}
+    for mb in sizes or SWEEP_MB:
+        half = mb * 1000 * 1000 // 2 // 16 * 16
+        base = C.BestCopy(dev, 1, 1, half, half, variants[0])
+        res = {}
+        for v in variants:
+            cp = C.BestCopy(dev, 1, 1, half, half, v, bufs=base.bufs)
+            us = time_graph(torch, cp.launch, iters)
+            name = C.variant_name(v)
+            res[name] = round(us, 3)
+            manifest.append({"mb": mb, "variant": name, "dispatches": 3 + 6 * iters})
+        k = min(res, key=res.get)
+        best[mb] = {"variant": k, "us": res[k], "gbs": round(2 * half / res[k] / 1e3, 1),
+                    "frac_peak": round(2 * half / res[k] / 1e3 / PEAK_GBS, 4),
+                    "oneshot_c1_b256_us": res.get("oneshot_c1_b256")}
+        print(json.dumps({"sweep_mb": mb, "bytes": 2 * half, "sets": base.sets, "us": res}), flush=True)
+        print(f"[sweep] {mb} MB: best {k} {res[k]:.2f} us = {best[mb]['gbs']} GB/s ({best[mb]['frac_peak']:.3f})",
+              file=sys.stderr, flush=True)
+        del base
+        torch.cuda.empty_cache()
+    print(json.dumps({"manifest": manifest}), flush=True)
+    print(json.dumps({"sweep_best": best, "iters": iters, "variants": which}), flush=True)
+
+
+def best_copy(torch, dev, pattern, n):
+    """(us, variant) of the fastest plain copy (ceiling.BEST_VARIANTS) of the
+    op's activation streams, graph-timed like the op."""
+    from lux3d_fused import ceiling as C
+    nin, nout, ib, ob = C.stream_shape(pattern)
+    base = C.BestCopy(dev, nin, nout, ib, ob, C.BEST_VARIANTS[0])
+    res = {}
+    for v in C.BEST_VARIANTS:
+        cp = C.BestCopy(dev, nin, nout, ib, ob, v, bufs=base.bufs)
+        res[C.variant_name(v)] = time_graph(torch, cp.launch, n)
+    del base
+    torch.cuda.empty_cache()
+    k = min(res, key=res.get)
+    return res[k], k
 
 
 def _json_block(path):
@@ -310,6 +378,9 @@ def main():
     dev = torch.device("cuda:0")
     from lux3d_fused import workloads as W
 
+    if args.ceiling_sweep:
+        ceiling_sweep(torch, dev, args.sweep_variants, args.iters if args.iters != 100 else 20, args.sweep_mb)
+        return
     if args.profile == "copy_1gib":
         # calibration kernel of known traffic for the FETCH_SIZE / WRITE_SIZE
         # counters: 1 GiB read + 1 GiB written per launch
@@ -423,12 +494,17 @@ def main():
         if flops:
             row.update({"bound": "mfma", "tflops": round(flops / us / 1e6, 1), "mfma_peak_tflops": peak_tf,
                         "frac_mfma_peak": round(flops / us / 1e6 / peak_tf, 4)})
-        else:
+        elif not args.no_ceilings:
             row["runtime_copy_us"] = round(runtime_copy_us(torch, dev, nbytes, n), 3)
-        if pattern:
+        if pattern and not args.no_ceilings:
             cu, pu, cbytes = ceilings(torch, dev, pattern, n)
             row.update({"copy_us": round(cu, 3), "pattern_us": round(pu, 3), "copy_bytes": cbytes,
                         "frac_of_pattern": round(pu / us, 4)})
+            if not flops:
+                bu, bv = best_copy(torch, dev, pattern, n)
+                row.update({"best_copy_us": round(bu, 3), "best_copy_variant": bv,
+                            "best_copy_frac_peak": round(cbytes / bu / 1e3 / PEAK_GBS, 4),
+                            "frac_of_best_copy": round(bu / us, 4)})
         tr = committed_trace(tag)
         if tr:
             row.update({"trace_us": tr[1], "trace_frac_peak": round(nbytes / tr[1] / 1e3 / PEAK_GBS, 4),
@@ -440,7 +516,8 @@ def main():
         if tb:
             row["traffic_bytes"] = tb
         print(f"[bench] {tag}: {us:.2f} us (warm {us_warm:.2f}"
-              + (f", copy {row['copy_us']:.2f}, pattern {row['pattern_us']:.2f}" if pattern else "") + ")",
+              + (f", copy {row['copy_us']:.2f}, pattern {row['pattern_us']:.2f}" if "copy_us" in row else "")
+              + (f", best copy {row['best_copy_us']:.2f}" if "best_copy_us" in row else "") + ")",
               file=sys.stderr, flush=True)
         table.append(row)
 
@@ -484,9 +561,19 @@ def main():
                    "step_bytes": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "ops": table,
     }
-    print(json.dumps(out), flush=True)
+    # The full table (every op with its ceilings, traces and CPU rows) goes to
+    # stderr and, on request, a file; the stdout line keeps the headline plus
+    # one short entry per op so that it stays a few KB.
+    print("[bench] table " + json.dumps(table), file=sys.stderr, flush=True)
+    if args.table_out:
+        with open(args.table_out, "w") as f:
+            json.dump({**out, "ops": table}, f, indent=1)
+    out["ops"] = [{"op": r["op"], "us": r["us"], "frac": r["frac_peak"],
+                   **({"best_copy_us": r["best_copy_us"]} if "best_copy_us" in r else {}),
+                   **({"frac_mfma": r["frac_mfma_peak"]} if "frac_mfma_peak" in r else {})}
+                  for r in table if r["target_70pct"] or "frac_mfma_peak" in r]
+    print(json.dumps(out, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":
