@@ -10,6 +10,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <cstdlib>
+
 #include "lux3d_fused.h"
 
 namespace lux3d {
@@ -272,6 +275,113 @@ __device__ __forceinline__ void param4(const void *p, int dt, int64_t i, float d
     for (int k = 0; k < 4; ++k) v[k] = dflt;
   }
 }
+// Dynamic LDS bytes for a launch whose kernel uses `used` bytes, raised so
+// that at most `wg_per_cu` of its workgroups are resident on a CU (the extra
+// bytes are a reservation the kernel never touches). Some streaming kernels
+// run fastest with fewer resident workgroups than their registers allow:
+// past that point more loads in flight only queue at the memory controllers
+// (sweeps of the reservation in one process: configs[1] F1 18.04 -> 17.67 us
+// at 6 workgroups of 256 threads per CU, configs[3] modulate 66.0 -> 64.4 us
+// at 2 of 512; the launchers state each cap they set). The CU's LDS size comes
+// from the device attribute, looked up once per device; if the lookup fails
+// no reservation is added. LUX3D_OCCUPANCY_CAP=0 in the environment turns
+// the reservations off (read at every launch, for A/B timing in one process).
+inline size_t lds_for_occupancy(hipStream_t s, int wg_per_cu, size_t used) {
+  static std::atomic<int> lds_per_cu[64];  // 0: not looked up yet, -1: unknown
+  const char *off = getenv("LUX3D_OCCUPANCY_CAP");
+  if (off && off[0] == '0') return used;
+  int dev = hipGetStreamDeviceId(s);
+  if (dev < 0 || dev >= 64) return used;
+  int lds = lds_per_cu[dev].load(std::memory_order_relaxed);
+  if (lds == 0) {
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+        lds <= 0)
+      lds = -1;
+    lds_per_cu[dev].store(lds, std::memory_order_relaxed);
+  }
+  if (lds < 0 || wg_per_cu < 1) return used;
+  const size_t want = (size_t)lds / (size_t)(wg_per_cu + 1) + 1;  // wg_per_cu + 1 of them do not fit
+  return used > want ? used : want;
+}
+
+// Keeps the machine scheduler from moving instructions across this point:
+// it orders loads for latency and register pressure, not for vmcnt, and so
+// would sink a small early load (a position, a parameter) below the row
+// loads that a wait for it must then also wait for.
+__device__ __forceinline__ void issue_fence() {
+#ifndef LUX3D_XP_NOFENCE
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
+// Per-channel parameters in two steps, for the kernels whose activation
+// loads must stay in flight. vmcnt counts loads and stores together in issue
+// order, so a parameter load inside a branch on its dtype whose data the
+// branch converts at once (param8) makes the wavefront wait there for every
+// earlier load and store. `pissue` issues the raw bytes of 8 parameters --
+// elements i..i+3 and j..j+3 -- with no branch on the dtype, through
+// bounds-checked buffer loads (bytes past the vector read as 0, an absent
+// vector has a zero-size descriptor and reads nothing), and `pdecode`
+// converts them where they are used, after the kernel's one wait.
+#ifdef LUX3D_XP_GLOBAL
+struct rsrc_t { const char *p; };
+__device__ __forceinline__ rsrc_t param_rsrc(const void *p, int dt, int64_t n) {
+  return rsrc_t{(dt < 0 || n <= 0) ? nullptr : reinterpret_cast<const char *>(p)};
+}
+struct PRaw {
+  u32x4_t a, b;
+};
+__device__ __forceinline__ PRaw pissue(rsrc_t r, int dt, int64_t i, int64_t j) {
+  const int sh = dt == LUX3D_F32 ? 2 : 1;
+  PRaw q;
+  if (r.p) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(r.p + (i << sh));
+    const uint4 b = *reinterpret_cast<const uint4 *>(r.p + (j << sh));
+    q.a = u32x4_t{a.x, a.y, a.z, a.w};
+    q.b = u32x4_t{b.x, b.y, b.z, b.w};
+  } else {
+    q.a = u32x4_t{0u, 0u, 0u, 0u};
+    q.b = q.a;
+  }
+  return q;
+}
+#else
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t param_rsrc(const void *p, int dt, int64_t n) {
+  int64_t bytes = (dt < 0 || !p) ? 0 : n * (dt == LUX3D_F32 ? 4 : 2);
+  if (bytes > 0x7FFFFFFF) bytes = 0x7FFFFFFF;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+struct PRaw {
+  u32x4_t a, b;
+};
+__device__ __forceinline__ PRaw pissue(rsrc_t r, int dt, int64_t i, int64_t j) {
+  const int sh = dt == LUX3D_F32 ? 2 : 1;
+  PRaw q;
+  q.a = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(i << sh), 0, 0);
+  q.b = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(j << sh), 0, 0);
+  return q;
+}
+#endif
+__device__ __forceinline__ void pdecode(const PRaw &q, int dt, float dflt, float (&v)[8]) {
+  if (dt == LUX3D_F32) {
+    v[0] = __uint_as_float(q.a.x); v[1] = __uint_as_float(q.a.y);
+    v[2] = __uint_as_float(q.a.z); v[3] = __uint_as_float(q.a.w);
+    v[4] = __uint_as_float(q.b.x); v[5] = __uint_as_float(q.b.y);
+    v[6] = __uint_as_float(q.b.z); v[7] = __uint_as_float(q.b.w);
+  } else if (dt == LUX3D_BF16 || dt == LUX3D_F16) {
+    const uint32_t w[4] = {q.a.x, q.a.y, q.b.x, q.b.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t h = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      v[k] = dt == LUX3D_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = dflt;
+  }
+}
+
 template <typename T> __device__ __forceinline__ const char *cptr(const void *p) {
   return reinterpret_cast<const char *>(p);
 }
@@ -395,10 +505,15 @@ __device__ __forceinline__ int64_t segment_of(const int64_t *off, int64_t nseg, 
     int64_t s = r / rows_per_seg;
     return s < nseg ? s : nseg - 1;
   }
+  // read through the constant address space: with r uniform over the
+  // wavefront (every caller) these are scalar loads, counted by lgkmcnt, so
+  // the search does not wait on the wavefront's outstanding vector loads
+  typedef const __attribute__((address_space(4))) int64_t *coff_t;
+  const coff_t c = (coff_t)off;
   int64_t lo = 0, hi = nseg - 1;
   while (lo < hi) {
     int64_t mid = (lo + hi + 1) >> 1;
-    if (off[mid] <= r) lo = mid; else hi = mid - 1;
+    if (c[mid] <= r) lo = mid; else hi = mid - 1;
   }
   return lo;
 }

@@ -191,6 +191,23 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   const char *xr = reinterpret_cast<const char *>(p.x) + row * p.x_rs * EB;
 #pragma unroll
   for (int c = 0; c < NC; ++c) ld_row<T>(xr, chunk_at<T, TPR>(c, t), v[c]);
+  // LN (one stream in, one out): w and b are issued with the row as raw
+  // bytes (pissue) and decoded after the statistics, so their latency hides
+  // under the row's (configs[0]: 3.69 against 3.87 us, same-box A/B). The
+  // other modes keep their parameters where they are used: issuing them all
+  // with the rows measured slower for the two-stream rows (configs[1] F1
+  // 18.7 against 18.5 us).
+  constexpr bool LN_UPFRONT = MODE == ROW_LN && NC <= 2;
+  PRaw q_w[LN_UPFRONT ? NC : 1], q_b[LN_UPFRONT ? NC : 1];
+  if constexpr (LN_UPFRONT) {
+    const rsrc_t r_w = param_rsrc(p.w, p.w_dt, p.d), r_b = param_rsrc(p.b, p.b_dt, p.d);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
+      q_w[c] = pissue(r_w, p.w_dt, at.o0, at.o1);
+      q_b[c] = pissue(r_b, p.b_dt, at.o0, at.o1);
+    }
+  }
   // GATE_MOD: the branch rows are loaded with x, ahead of the segment lookup
   // and the staging barrier, so both streams are in flight together
   float hb[MODE == ROW_GATE_MOD ? NC : 1][8];
@@ -328,8 +345,13 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
     for (int c = 0; c < NC; ++c) {
       const ChunkAt at = chunk_at<T, TPR>(c, t);
       float w[8], b[8], out[8];
-      param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
-      param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);
+      if constexpr (LN_UPFRONT) {
+        pdecode(q_w[c], p.w_dt, 1.f, w);
+        pdecode(q_b[c], p.b_dt, 0.f, b);
+      } else {
+        param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
+        param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);
+      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) out[k] = (v[c][k] - mean) * rstd * w[k] + b[k];
       if (live) st_row<T>(yr, at, out);
@@ -445,17 +467,29 @@ hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
   // Stage the segment pieces in LDS when a workgroup holds several rows.
   const int npieces = (MODE == ROW_MODULATE || MODE == ROW_GATE_MOD) ? 2 + (p.gate.dt >= 0 ? 1 : 0)
                                                                       : (MODE == ROW_GATE ? 1 : 0);
-  const size_t lds = (size_t)npieces * (size_t)p.d * sizeof(float);
+  size_t lds = (size_t)npieces * (size_t)p.d * sizeof(float);
   const bool stage = npieces > 0 && rpb > 1 && lds <= 64 * 1024;
+  // resident-workgroup caps (lds_for_occupancy), each measured in one
+  // process with the cap on and off: the two-wavefront 2-byte residual rows
+  // at 6 per CU (configs[1] F1: 17.67 against 18.04 us; the f32 rows are
+  // not faster capped: 31.5 against 31.3), the 512-thread staged modulate
+  // rows at 2 (configs[3] modulate 64.4 against 66.0 us, configs[2] even).
+  // The ragged gated residual + modulate rows are slower capped (139.1
+  // against 134.6 us at 2) and run uncapped.
+  size_t lds_launch = stage ? lds : 0;
+  if (MODE == ROW_RESID_LN && T::bytes == 2 && !row_per_block && block == 256 && tpr == 128)
+    lds_launch = lds_for_occupancy(s, 6, lds_launch);
+  if (MODE == ROW_MODULATE && stage && block == 512) lds_launch = lds_for_occupancy(s, 2, lds_launch);
 #define LUX3D_ROW_CASE(TPR_, NC_, BLK_)                                                                 \
   if (tpr == TPR_ && nc == NC_ && block == BLK_) {                                                      \
     if constexpr (MODE == ROW_MODULATE || MODE == ROW_GATE || MODE == ROW_GATE_MOD) {                   \
       if (stage && BLK_ > TPR_) {                                                                       \
-        hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_, (BLK_ > TPR_)>), grid, dim3(BLK_), lds, s, p); \
+        hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_, (BLK_ > TPR_)>), grid, dim3(BLK_), lds_launch, \
+                           s, p);                                                                       \
         return hipGetLastError();                                                                       \
       }                                                                                                 \
     }                                                                                                   \
-    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_>), grid, dim3(BLK_), 0, s, p);              \
+    hipLaunchKernelGGL((row_kernel<T, TPR_, NC_, MODE, BLK_>), grid, dim3(BLK_), lds_launch, s, p);     \
     return hipGetLastError();                                                                           \
   }
   LUX3D_ROW_CASE(64, 1, 256) LUX3D_ROW_CASE(64, 2, 256) LUX3D_ROW_CASE(64, 3, 256)

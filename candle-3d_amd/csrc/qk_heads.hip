@@ -172,16 +172,82 @@ __device__ __forceinline__ void stage_phases(const HeadParams &p, uint32_t tok0,
   }
 }
 
+// Phase sources of one angle item e < tb * D/2 (R1_POS: a position and a
+// frequency; R2_COORD: a coordinate and a frequency), issued as plain loads
+// with no branch on loaded data (an item past the tile reads item 0's
+// sources), so that the head rows issued after them stay in flight while
+// the phases are computed; phase_finish then writes the two LDS entries the
+// angle feeds, exactly as stage_phases does.
+struct PhaseSrc {
+  uint32_t v;  // position / coordinate bits
+  float f;     // frequency
+};
+template <int ROT, int D>
+__device__ __forceinline__ PhaseSrc phase_issue(const HeadParams &p, uint32_t tok0, int tb, uint32_t ntok, uint32_t N,
+                                                int e) {
+  constexpr int half = D / 2, quarter = D / 4;
+  if (e >= tb * half) e = 0;
+  const int t = e / half, a = e % half;
+  uint32_t tok = tok0 + t;
+  tok = tok < ntok ? tok : ntok - 1;
+  const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s), n = tok - b * N;
+  PhaseSrc s;
+  if constexpr (ROT == HR_R1_POS) {
+    const int axis = a / quarter, k = a % quarter;
+    const int64_t idx = (int64_t)b * p.pos_sB + (int64_t)n * p.pos_sN + axis * p.pos_sC;
+    // the low 32 bits of an int64 position (little-endian), or the int32
+    s.v = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(p.pos) +
+                                              (idx << (p.pos_dt == LUX3D_I64 ? 3 : 2)));
+    s.f = p.freq[k];
+  } else {
+    const int axis = a < 3 * p.nfreq ? a / p.nfreq : 0;
+    s.v = (uint32_t)reinterpret_cast<const int32_t *>(p.pos)[(int64_t)n * p.pos_sN + axis * p.pos_sC];
+    s.f = p.freq[a < 3 * p.nfreq ? a % p.nfreq : 0];
+  }
+  return s;
+}
+// The angle is evaluated for every thread (an item past the tile evaluates
+// item 0's) and only the LDS writes are conditional: a use of the loaded
+// sources under a branch let the compiler sink their loads into it, behind
+// the row loads.
+template <int ROT, int D>
+__device__ __forceinline__ void phase_finish(const HeadParams &p, int tb, int e, PhaseSrc s, float *Cs, float *Ss) {
+  constexpr int half = D / 2, quarter = D / 4;
+  const bool in_tile = e < tb * half;
+  const int ec = in_tile ? e : 0;
+  const int t = ec / half, a = ec % half;
+  float cv, sv;
+  int j0, j1;
+  if constexpr (ROT == HR_R1_POS) {
+    const int axis = a / quarter, k = a % quarter;
+    sincosf((float)s.v * s.f, &sv, &cv);
+    j0 = axis * half + k;
+    j1 = j0 + quarter;
+  } else {
+    const float ang = a < 3 * p.nfreq ? (float)(int32_t)s.v * s.f : 0.f;
+    sincosf(ang, &sv, &cv);
+    j0 = 2 * a;
+    j1 = 2 * a + 1;
+  }
+  if (in_tile) {
+    Cs[t * D + j0] = cv;
+    Ss[t * D + j0] = -sv;
+    Cs[t * D + j1] = cv;
+    Ss[t * D + j1] = sv;
+  }
+}
+
 // Grid: x = tiles of `tb` consecutive tokens; y = tensor (q, k) when NTB = 1,
 // or 1 when NTB = 2 (each workgroup then handles q and k of its tokens, whose
 // rows lie side by side in a packed qkv buffer, and stages the phases once).
 // Work items are (token, head) rows of LPR lanes; each thread owns R of the
-// tile's rows per tensor. Order of work per workgroup: issue every row load
-// (and the per-channel parameters), then stage the tile's rotation phases in
-// LDS while those loads are in flight, one LDS barrier, then normalise /
-// rotate / store. Each workgroup therefore waits on one HBM round trip. Rows
-// of one head are adjacent in the [B, H, N, D] output across the tile's
-// tokens, so a head's stores form contiguous runs of tb*D elements.
+// tile's rows per tensor. Order of work per workgroup: issue the phase
+// sources, every row load and the per-channel parameters, then stage the
+// tile's rotation phases in LDS while the rows are in flight, one LDS
+// barrier, then normalise / rotate / store. Each workgroup therefore waits
+// on one HBM round trip. Rows of one head are adjacent in the [B, H, N, D]
+// output across the tile's tokens, so a head's stores form contiguous runs
+// of tb*D elements.
 template <typename T, int D, int NORM, int ROT, int R, int NTB, bool O32>
 __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   constexpr int LPR = D / 8;
@@ -209,8 +275,28 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
     const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s);
     tt[r] = t; hh[r] = h; nn[r] = tok - imul<O32>(b, N); bb[r] = b;
   }
+  // Order of the loads (vmcnt counts loads and stores in issue order, so a
+  // wait for one load waits for all issued before it): (1) this thread's
+  // phase sources, (2) the head rows, (3) the per-channel parameters as raw
+  // bytes (pissue). The phases are then computed and staged while the rows
+  // are in flight (their wait leaves (2) and (3) outstanding), and one
+  // barrier and one wait later every row is normalised, rotated and stored.
+  // Unrotated rows (HR_NONE) keep the plain order -- each tensor's rows, then
+  // its parameters read where they are converted -- which measured faster
+  // for them (configs[2] RMS heads 13.0 against 14.1 us, same-box A/B at
+  // equal occupancy) than issuing every load first.
+  constexpr bool SRC = ROT == HR_R1_POS || ROT == HR_R2_COORD;
+  constexpr bool EARLY = ROT != HR_NONE;
+  const int e0 = threadIdx.x;
+  PhaseSrc ps{};
+  if constexpr (SRC) ps = phase_issue<ROT, D>(p, tok0, tb, ntok, N, e0);
+  issue_fence();
+
   float v[NTB][R][8];
   float w[NTB][8], bias[NTB][8];
+  PRaw qw[NTB], qb[NTB], qg[NORM == HN_L2 && EARLY ? NTB : 1][NORM == HN_L2 && EARLY ? R : 1];
+  // lane's elements of a head row: i..i+3 and j..j+3 (see head_elem)
+  const int pi = EB == 4 ? lane * 4 : lane * 8, pj = EB == 4 ? D / 2 + lane * 4 : lane * 8 + 4;
 #pragma unroll
   for (int q = 0; q < NTB; ++q) {
     const HeadIO &io = p.io[NTB == 1 ? blockIdx.y : q];
@@ -220,13 +306,45 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
                        view_off<O32>(bb[r], hh[r], nn[r], io.sB, io.sH, io.sN, 0) * EB;
       head_load<T, D>(xp, lane, v[q][r]);
     }
-    if constexpr (NORM == HN_LN || NORM == HN_RMS) head_param<T, D>(io.p0, io.p0_dt, 0, lane, 1.f, w[q]);
-    if constexpr (NORM == HN_LN) head_param<T, D>(io.p1, io.p1_dt, 0, lane, 0.f, bias[q]);
+    if constexpr (!EARLY) {
+      if constexpr (NORM == HN_LN || NORM == HN_RMS) head_param<T, D>(io.p0, io.p0_dt, 0, lane, 1.f, w[q]);
+      if constexpr (NORM == HN_LN) head_param<T, D>(io.p1, io.p1_dt, 0, lane, 0.f, bias[q]);
+    }
+  }
+  if constexpr (EARLY) {
+    issue_fence();
+#pragma unroll
+    for (int q = 0; q < NTB; ++q) {
+      const HeadIO &io = p.io[NTB == 1 ? blockIdx.y : q];
+      if constexpr (NORM == HN_LN || NORM == HN_RMS) qw[q] = pissue(param_rsrc(io.p0, io.p0_dt, D), io.p0_dt, pi, pj);
+      if constexpr (NORM == HN_LN) qb[q] = pissue(param_rsrc(io.p1, io.p1_dt, D), io.p1_dt, pi, pj);
+      if constexpr (NORM == HN_L2) {
+        const rsrc_t rg = param_rsrc(io.p0, io.p0_dt, (int64_t)H * D);
+#pragma unroll
+        for (int r = 0; r < R; ++r) qg[q][r] = pissue(rg, io.p0_dt, (int64_t)hh[r] * D + pi, (int64_t)hh[r] * D + pj);
+      }
+    }
+    issue_fence();
   }
 
   if constexpr (ROT != HR_NONE) {
-    stage_phases<ROT, D>(p, tok0, tb, ntok, N, Cs, Ss);
+    if constexpr (SRC) {
+      phase_finish<ROT, D>(p, tb, e0, ps, Cs, Ss);
+      // tiles with more angles than threads: the rest the plain way
+      for (int e = e0 + (int)blockDim.x; e < tb * (D / 2); e += blockDim.x)
+        phase_finish<ROT, D>(p, tb, e, phase_issue<ROT, D>(p, tok0, tb, ntok, N, e), Cs, Ss);
+    } else {
+      stage_phases<ROT, D>(p, tok0, tb, ntok, N, Cs, Ss);
+    }
     lds_barrier();
+  }
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int q = 0; q < NTB; ++q) {
+      const HeadIO &io = p.io[NTB == 1 ? blockIdx.y : q];
+      if constexpr (NORM == HN_LN || NORM == HN_RMS) pdecode(qw[q], io.p0_dt, 1.f, w[q]);
+      if constexpr (NORM == HN_LN) pdecode(qb[q], io.p1_dt, 0.f, bias[q]);
+    }
   }
 
 #pragma unroll
@@ -253,7 +371,8 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         const float rr = l2_rnorm(group_sum<LPR>(s2));
         const float scale = sqrtf((float)D);
         float g[8];
-        head_param<T, D>(io.p0, io.p0_dt, (int64_t)hh[r] * D, lane, 1.f, g);
+        if constexpr (EARLY) pdecode(qg[q][r], io.p0_dt, 1.f, g);
+        else head_param<T, D>(io.p0, io.p0_dt, (int64_t)hh[r] * D, lane, 1.f, g);
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = ((x[k] * rr) * g[k]) * scale;
       }
@@ -495,7 +614,13 @@ hipError_t launch_dn(int norm, int rot, const HeadParams &p0, hipStream_t s) {
   HeadParams p = p0;
   div_magic(p.H, p.div_h_m, p.div_h_s);
   div_magic(p.N, p.div_n_m, p.div_n_s);
-  const size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
+  size_t lds = rot != HR_NONE ? (size_t)2 * tb * D * sizeof(float) : 0;
+  // resident-workgroup cap (lds_for_occupancy), measured in one process with
+  // the cap on and off: the VGGT D = 64 f32 rotation from positions at 6
+  // per CU (configs[1] QK LayerNorm + RoPE in f32: 30.1 against 30.5 us);
+  // the 2-byte form is faster uncapped (17.13 against 17.36 us), and the
+  // unrotated D = 128 rows measure even.
+  if (D == 64 && T::bytes == 4 && threads == 256 && rot == HR_R1_POS) lds = lds_for_occupancy(s, 6, lds);
   const dim3 grid((unsigned)((tokens + tb - 1) / tb), NTB == 2 ? 1u : (unsigned)p.ntens), block((unsigned)threads);
   if (offsets_fit_32(p, T::bytes)) return launch_cases<T, D, NTB, R, true>(norm, rot, p, (int)tb, grid, block, lds, s);
   return launch_cases<T, D, NTB, R, false>(norm, rot, p, (int)tb, grid, block, lds, s);

@@ -10,7 +10,10 @@ import ctypes
 import os
 
 LIB_NAME = "liblux3d_fused.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
+# LUX3D_FUSED_LIB names another build of the same library (A/B timing of
+# kernel variants); it must exist, like the default
+LIB_PATH = os.environ.get("LUX3D_FUSED_LIB") or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
 
 MAX_RANK = 5
 
