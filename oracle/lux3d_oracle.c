@@ -33,6 +33,12 @@
  *                            weight; tiny brute force (tests/test_oracle_pins.py)
  *   or_q8_0_linear_f32       numpy f64 matmul of the f32-dequantized weight; identity
  *                            weight returns x; tiny brute force
+ *   or_quantize_q8_0         brute force per block against an independent Python
+ *                            restatement; amax / round-half-away / saturation / NaN
+ *                            special cases; a round trip within d / 2 per value
+ *   or_q8_0_linear_int8      the integer block dot exact against numpy int64;
+ *                            brute force on tiny shapes (Python loop in the same
+ *                            f32 order); a one-block case in closed form
  *   or_sparse_neighbors      reference KATs (tests/trellis2_sparse.rs:67-93) + brute
  *                            force over all pairs
  *   or_sparse_conv3d         torch conv3d (f64) on the densified grid; the
@@ -849,6 +855,23 @@ void or_timestep_embedding_sin_first(const float *t, int64_t n, int64_t dim, flo
     }
 }
 
+/* Either convention from a given frequency vector freqs[dim / 2] (the
+ * reference's own host loop computes it; see or_timestep_embedding_*): the
+ * argument t * f is one f32 product in both (T2's affine(f, t, 0) rounds the
+ * exact f64 product once), then [sin, cos] (T1) or [cos, sin] + 0 pad (T2). */
+void or_timestep_embedding_freqs(const float *t, int64_t n, const float *freqs, int64_t dim, int cos_first,
+                                 float *out) {
+  int64_t half = dim / 2;
+  for (int64_t r = 0; r < n; ++r) {
+    for (int64_t i = 0; i < half; ++i) {
+      float a = t[r] * freqs[i];
+      out[r * dim + i] = cos_first ? cosf(a) : sinf(a);
+      out[r * dim + half + i] = cos_first ? sinf(a) : cosf(a);
+    }
+    if (cos_first && dim % 2) out[r * dim + dim - 1] = 0.f;
+  }
+}
+
 /* T2 (trellis2_blocks.rs:189-203): nlp = -(ln(10000) as f64) as f32;
  * f = exp(nlp*i/half); args = f*t + 0 (affine); out = [cos, sin] (+0 pad). */
 void or_timestep_embedding_cos_first(const float *t, int64_t n, int64_t dim, float *out) {
@@ -952,6 +975,83 @@ void or_q8_0_linear_f32(const float *x, int64_t M, int64_t K, const uint8_t *blo
   ql_ctx c = {x, wf, bias, K, N, out_dt, y, abs_sum};
   parallel_rows(M, ql_rows, &c);
   free(wf);
+}
+
+/* ---- candle's CPU QMatMul for a Q8_0 weight ------------------------------
+ * Linear::forward's Quant branch (nn_blocks.rs:80-93) calls QMatMul::forward,
+ * which on the CPU is the QTensor custom op (f32 x only) running
+ * k_quants::matmul of the upstream candle-core crate (quantized/k_quants.rs
+ * of the fork FerrisMind/candle 9f6eed1, not vendored in the reference): every
+ * x row is first quantized to Q8_0 blocks (BlockQ8_0::from_float), then each
+ * output is the weight row's vec_dot with them, block by block, and the
+ * bias is broadcast-added. With no AVX target feature (the reference sets
+ * none: no .cargo/config) vec_dot takes the generic vec_dot_unopt:
+ *   sumf = 0; for each block b in order:
+ *     sumf += (f32)(sum_j wq[j] * xq[j]) * f32(w.d) * f32(x.d)
+ * the products left to right, each operation rounded in f32. */
+
+/* BlockQ8_0::from_float: amax = max |x| (NaN ignored, f32::max), d = amax /
+ * 127, id = d != 0 ? 1 / d : 0, q = round-half-away(x * id) saturated to
+ * int8 (NaN -> 0, Rust's `as i8`), d stored as f16 (half's from_f32: RNE). */
+void or_quantize_q8_0(const float *x, int64_t n, uint8_t *blocks) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float *xs = x + b * 32;
+    float amax = 0.f;
+    for (int j = 0; j < 32; ++j) {
+      float a = fabsf(xs[j]);
+      if (a > amax) amax = a; /* f32::max: a NaN operand yields the other (the compare is false) */
+    }
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = or_f32_to_f16(d);
+    uint8_t *o = blocks + b * 34;
+    o[0] = (uint8_t)(dh & 0xFF);
+    o[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 32; ++j) {
+      float r = roundf(xs[j] * id);
+      int q = isnan(r) ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
+      o[2 + j] = (uint8_t)(int8_t)q;
+    }
+  }
+}
+
+typedef struct {
+  const uint8_t *xb, *wb;
+  const float *bias;
+  int64_t nb, N;
+  float *y;
+} q8d_ctx;
+
+static void q8d_rows(const void *vc, int64_t r0, int64_t r1) {
+  const q8d_ctx *c = (const q8d_ctx *)vc;
+  for (int64_t m = r0; m < r1; ++m) {
+    const uint8_t *xr = c->xb + m * c->nb * 34;
+    for (int64_t n = 0; n < c->N; ++n) {
+      const uint8_t *wr = c->wb + n * c->nb * 34;
+      float sumf = 0.f;
+      for (int64_t b = 0; b < c->nb; ++b) {
+        const uint8_t *wq = wr + b * 34, *xq = xr + b * 34;
+        int32_t s = 0;
+        for (int j = 0; j < 32; ++j) s += (int32_t)(int8_t)wq[2 + j] * (int32_t)(int8_t)xq[2 + j];
+        const float wd = or_f16_to_f32((uint16_t)(wq[0] | (wq[1] << 8)));
+        const float xd = or_f16_to_f32((uint16_t)(xq[0] | (xq[1] << 8)));
+        /* each operation rounded (the oracle builds with -ffp-contract=off) */
+        sumf = sumf + ((float)s * wd) * xd;
+      }
+      c->y[m * c->N + n] = c->bias ? sumf + c->bias[n] : sumf;
+    }
+  }
+}
+
+void or_q8_0_linear_int8(const float *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N, const float *bias,
+                         float *y) {
+  const int64_t nb = K / 32;
+  uint8_t *xb = (uint8_t *)malloc((size_t)(M * nb * 34));
+  if (!xb) return;
+  for (int64_t m = 0; m < M; ++m) or_quantize_q8_0(x + m * K, K, xb + m * nb * 34);
+  q8d_ctx c = {xb, blocks, bias, nb, N, y};
+  parallel_rows(M, q8d_rows, &c);
+  free(xb);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -130,6 +130,9 @@ void or_silu(int dt, const void *x, int64_t n, void *y);
 void or_timestep_embedding_sin_first(const float *t, int64_t n, int64_t dim, float *out);
 /* T2: timestep_embedding (trellis2_blocks.rs:184-204), cos first. */
 void or_timestep_embedding_cos_first(const float *t, int64_t n, int64_t dim, float *out);
+/* Either convention (cos_first: T2) from a given frequency vector freqs[dim / 2]. */
+void or_timestep_embedding_freqs(const float *t, int64_t n, const float *freqs, int64_t dim, int cos_first,
+                                 float *out);
 
 /* ---- Q8_0 dequant -------------------------------------------------------- */
 /* GGML block_q8_0 = {f16 d; int8 qs[32]} (34 bytes); w = f32(d)*qs. */
@@ -146,6 +149,15 @@ void or_q8_0_linear(const uint16_t *x, int64_t M, int64_t K, const uint8_t *bloc
 /* The same with f32 x [M, K] and the exact f32 weights q * d. */
 void or_q8_0_linear_f32(const float *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N,
                         const float *bias, int out_dt, void *y, float *abs_sum);
+
+/* ---- Q8_0 quantized linear, candle's CPU semantics ------------------------- */
+/* BlockQ8_0::from_float: f32 x [n] (n % 32 == 0) -> GGML Q8_0 blocks. */
+void or_quantize_q8_0(const float *x, int64_t n, uint8_t *blocks);
+/* QMatMul::forward on the CPU + bias: x f32 [M, K] quantized per row to Q8_0,
+ * integer block dots with the weight blocks [N, K], scaled and summed in f32
+ * block order; y f32 [M, N]. */
+void or_q8_0_linear_int8(const float *x, int64_t M, int64_t K, const uint8_t *blocks, int64_t N, const float *bias,
+                         float *y);
 
 /* ---- TRELLIS.2 sparse ops (runtime/trellis2_sparse.rs) --------------------- */
 /* CoordMap + kernel_offset_delta: nbr[i][k] = row of coords[i] + delta(k), or

@@ -51,9 +51,12 @@ _SIG = {
     "or_silu": ([ctypes.c_int, _P, _I, _P], None),
     "or_timestep_embedding_sin_first": ([_P, _I, _I, _P], None),
     "or_timestep_embedding_cos_first": ([_P, _I, _I, _P], None),
+    "or_timestep_embedding_freqs": ([_P, _I, _P, _I, ctypes.c_int, _P], None),
     "or_dequant_q8_0": ([_P, _I, ctypes.c_int, _P], None),
     "or_q8_0_linear": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
     "or_q8_0_linear_f32": ([_P, _I, _I, _P, _I, _P, ctypes.c_int, _P, _P], None),
+    "or_quantize_q8_0": ([_P, _I, _P], None),
+    "or_q8_0_linear_int8": ([_P, _I, _I, _P, _I, _P, _P], None),
     "or_sparse_neighbors": ([_P, _I, _P], None),
     "or_sparse_conv3d": ([_P, _I, _I, _P, _P, _P, _I, _P, _P], None),
     "or_channel_to_spatial": ([_P, _I, _P, _I, _P, _P, _P, _P, _P], ctypes.c_int64),
@@ -311,12 +314,32 @@ def silu(x, dt=None):
     return _act(LIB.or_silu, x, dt)
 
 
-def timestep_embedding(t, dim, cos_first=True):
+def timestep_embedding(t, dim, cos_first=True, freqs=None):
+    """T1 / T2 with the frequencies the reference's host loop computes
+    (libm expf), or from a given frequency vector `freqs` [dim // 2]."""
     t = _f32(t).reshape(-1)
     out = np.empty((t.size, dim), dtype=np.float32)
+    if freqs is not None:
+        f = _f32(freqs).reshape(-1)
+        assert f.size == dim // 2
+        LIB.or_timestep_embedding_freqs(_ptr(t), t.size, _ptr(f), dim, 1 if cos_first else 0, _ptr(out))
+        return out
     fn = LIB.or_timestep_embedding_cos_first if cos_first else LIB.or_timestep_embedding_sin_first
     fn(_ptr(t), t.size, dim, _ptr(out))
     return out
+
+
+def timestep_freqs_rounded_once(dim):
+    """exp(x) evaluated in f64 and rounded once to f32, for the reference's
+    f32 argument x = (nlp * i) / half, nlp = f32(-ln 10000)
+    (trellis2_blocks.rs:189-194; triposg_dit.rs:286-291): the correctly
+    rounded frequency wherever the f64 exp is within half an f32 ulp's
+    margin, which tests/test_oracle_pins.py checks against exact values."""
+    import math
+    half = dim // 2
+    nlp = np.float32(-math.log(10000.0))
+    x = (nlp * np.arange(half, dtype=np.float32)) / np.float32(half)
+    return np.exp(x.astype(np.float64)).astype(np.float32)
 
 
 def dequant_q8_0(blocks, out_dt=BF16):
@@ -325,6 +348,27 @@ def dequant_q8_0(blocks, out_dt=BF16):
     out = np.empty(nb * 32, dtype=np.float32 if out_dt == F32 else np.uint16)
     LIB.or_dequant_q8_0(_ptr(blocks), nb, out_dt, _ptr(out))
     return out
+
+
+def quantize_q8_0(x):
+    """BlockQ8_0::from_float of f32 x [..., K] (K % 32 == 0): u8 blocks [rows * K/32 * 34]."""
+    x = _f32(x).reshape(-1)
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    LIB.or_quantize_q8_0(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def q8_0_linear_int8(x, blocks, n, bias=None):
+    """candle's CPU QMatMul for a Q8_0 weight (+ bias): f32 x [M, K], weight
+    blocks of [n, K] -> f32 [M, n]."""
+    x = _f32(x)
+    M, K = x.shape
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    assert blocks.size == n * (K // 32) * 34
+    y = np.empty((M, n), dtype=np.float32)
+    b = _f32(bias) if bias is not None else None
+    LIB.or_q8_0_linear_int8(_ptr(x), M, K, _ptr(blocks), n, _ptr(b) if b is not None else None, _ptr(y))
+    return y
 
 
 def q8_0_linear(x_bits, blocks, n, bias=None, out_dt=BF16, with_abs=False):

@@ -511,7 +511,7 @@ def test_activations(dev, ops, orc, synth, act, dt, n):
 # Timestep embeddings
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("dim,cos_first", [(256, True), (2048, False), (255, True)])
+@pytest.mark.parametrize("dim,cos_first", [(256, True), (2048, False), (2048, True), (256, False), (255, True)])
 def test_timestep_embedding(dev, ops, orc, synth, dim, cos_first):
     print(f"\n[case] timestep_embedding dim={dim} cos_first={cos_first}", flush=True)
     t = synth.uniform(synth.config_seed(2) + 4, 2, 0.0, 1000.0)
@@ -524,9 +524,14 @@ def test_timestep_embedding(dev, ops, orc, synth, dim, cos_first):
     got = y.cpu().numpy()
     # identical frequencies: only sin/cos rounding differs (<= 2 ulp of |v| <= 1)
     assert np.max(np.abs(got - want)) <= 2.5e-7
-    # device-computed frequencies: a 1-ulp frequency difference moves the
-    # argument by up to t * 2^-24 * f
-    assert np.max(np.abs(y_dev.cpu().numpy() - want)) <= 1000.0 * 2.0 ** -23
+    # device-computed frequencies (exp in f64, rounded once): bit for bit the
+    # rounded-once table (tests/test_oracle_pins.py pins it to the exact exp),
+    # and the same 2.5e-7 bar against the oracle given that table
+    cr = orc.timestep_freqs_rounded_once(dim)
+    y_cr = ops.timestep_embedding(td, dim, cos_first, freqs=torch.from_numpy(cr).to(dev))
+    sync()
+    assert np.array_equal(y_dev.cpu().numpy(), y_cr.cpu().numpy())
+    assert np.max(np.abs(y_dev.cpu().numpy() - orc.timestep_embedding(t, dim, cos_first, freqs=cr))) <= 2.5e-7
 
 
 # ---------------------------------------------------------------------------

@@ -487,9 +487,133 @@ def test_timestep_embedding_kat_and_conventions():
     assert np.max(np.abs(small[:128] - np.cos(10000.0 ** (-i / 128.0)))) < 2e-7
 
 
+def _libm_timestep_freqs(dim):
+    """The reference's host frequency loop: f32 argument, libm expf."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.argtypes, libm.expf.restype = [ctypes.c_float], ctypes.c_float
+    half = dim // 2
+    nlp = np.float32(-math.log(10000.0))
+    return np.array([libm.expf(float((nlp * np.float32(i)) / np.float32(half))) for i in range(half)], np.float32)
+
+
+def test_timestep_frequencies_rounded_once():
+    """The device path's frequencies, exp(x) in f64 rounded once to f32, are
+    the f32 nearest the exact exp(x) of the reference's f32 argument at the
+    configs' dims (mpmath at 200 bits); and the given-frequency form of the
+    oracle, fed the reference's libm table, reproduces its own T1 / T2 bit
+    for bit. glibc's expf is not correctly rounded everywhere (dim 2048,
+    i = 457: 0.5004 ulp), so that table and the rounded-once one can differ
+    in the last bit of a frequency; the GPU tests hold the device path to
+    the rounded-once table."""
+    mpmath = pytest.importorskip("mpmath")
+    mpmath.mp.prec = 200
+    for dim in (256, 2048, 255):
+        f = orc.timestep_freqs_rounded_once(dim)
+        half = dim // 2
+        nlp = np.float32(-math.log(10000.0))
+        x = (nlp * np.arange(half, dtype=np.float32)) / np.float32(half)
+        for i in range(half):
+            exact = mpmath.exp(mpmath.mpf(float(x[i])))
+            err = abs(mpmath.mpf(float(f[i])) - exact)
+            ulp = mpmath.mpf(float(np.spacing(f[i])))
+            assert err <= ulp / 2, (dim, i)
+        t = synth.uniform(72, 3, 0.0, 1000.0)
+        libm = _libm_timestep_freqs(dim)
+        for cos_first in (True, False):
+            if dim % 2 and not cos_first:
+                continue
+            assert np.array_equal(orc.timestep_embedding(t, dim, cos_first, freqs=libm),
+                                  orc.timestep_embedding(t, dim, cos_first))
+
+
 # ---------------------------------------------------------------------------
 # Q8_0
 # ---------------------------------------------------------------------------
+
+def _quantize_q8_0_py(x):
+    """BlockQ8_0::from_float restated independently (numpy f32 arithmetic,
+    numpy's own binary16 rounding)."""
+    x = np.asarray(x, np.float32).reshape(-1, 32)
+    out = np.empty((x.shape[0], 34), np.uint8)
+    for b, xs in enumerate(x):
+        a = np.abs(xs)
+        a = a[~np.isnan(a)]
+        amax = np.float32(a.max()) if a.size else np.float32(0.0)
+        amax = max(amax, np.float32(0.0))
+        d = np.float32(amax / np.float32(127.0))
+        idv = np.float32(1.0) / d if d != 0 else np.float32(0.0)
+        v = (xs * idv).astype(np.float32)
+        with np.errstate(invalid="ignore"):
+            r = np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))  # half away from zero
+            q = np.where(np.isnan(r), 0, np.clip(r, -128, 127)).astype(np.int8)
+        out[b, 0:2] = np.array([d], np.float16).view(np.uint8)
+        out[b, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_quantize_q8_0_matches_restatement_and_bounds():
+    """or_quantize_q8_0 (candle's BlockQ8_0::from_float, k_quants.rs) against
+    an independent numpy restatement on random and special blocks, plus what
+    the format fixes: |q| <= 127, the largest |x| of a block maps to +-127,
+    and q * d reconstructs x within d / 2 (+ the f16 rounding of d)."""
+    rng = np.random.default_rng(5)
+    blocks = [rng.normal(0, 1, 32), rng.normal(0, 1e-3, 32), rng.uniform(-1e4, 1e4, 32), np.zeros(32),
+              np.full(32, -2.5), np.arange(32) - 15.5, np.r_[np.full(31, 0.25), 127.0],
+              np.r_[np.nan, rng.normal(0, 1, 31)], np.r_[np.inf, rng.normal(0, 1, 31)],
+              np.r_[1e-40, np.zeros(31)], np.r_[70000.0, rng.normal(0, 1, 31)]]
+    x = np.concatenate([np.asarray(b, np.float32) for b in blocks])
+    got = orc.quantize_q8_0(x)
+    assert np.array_equal(got, _quantize_q8_0_py(x))
+    xr = rng.normal(0, 3, 32 * 64).astype(np.float32)
+    g = orc.quantize_q8_0(xr).reshape(-1, 34)
+    q = g[:, 2:].view(np.int8).astype(np.int32)
+    d = g[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    xb = xr.reshape(-1, 32)
+    assert np.abs(q).max() <= 127
+    assert np.all(np.abs(q[np.arange(len(xb)), np.abs(xb).argmax(1)]) == 127)
+    amax = np.abs(xb).max(1)
+    err = np.abs(q * d[:, None] - xb)
+    assert np.all(err <= (amax / 127.0)[:, None] * (0.5 + 127 * 2.0 ** -11) * 1.0001)
+
+
+def test_q8_0_linear_int8_brute_force():
+    """or_q8_0_linear_int8 (candle's CPU QMatMul for Q8_0: x quantized per row,
+    integer block dots, sumf += (f32)isum * wd * xd in block order, + bias)
+    against a Python loop in the same f32 order on tiny shapes; the integer
+    block dots against numpy int64; and one block in closed form."""
+    rng = np.random.default_rng(6)
+    M, N, K = 3, 5, 96
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    wblk = synth.q8_0_blocks(7, N * K // 32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    y = orc.q8_0_linear_int8(x, wblk, N, bias)
+    xq = orc.quantize_q8_0(x).reshape(M, K // 32, 34)
+    wq = wblk.reshape(N, K // 32, 34)
+    want = np.empty((M, N), np.float32)
+    for m in range(M):
+        for n in range(N):
+            s = np.float32(0.0)
+            for b in range(K // 32):
+                xi = xq[m, b, 2:].view(np.int8).astype(np.int64)
+                wi = wq[n, b, 2:].view(np.int8).astype(np.int64)
+                isum = int((xi * wi).sum())
+                assert abs(isum) < 2 ** 24  # exact in f32 as well
+                xd = np.float32(xq[m, b, 0:2].copy().view(np.float16)[0])
+                wd = np.float32(wq[n, b, 0:2].copy().view(np.float16)[0])
+                s = np.float32(s + np.float32(np.float32(np.float32(isum) * wd) * xd))
+            want[m, n] = np.float32(s + bias[n])
+    assert np.array_equal(y, want)
+    # one block, closed form: x = 127 * e_3 quantizes to d = 1, q = 127 e_3,
+    # so with weight values -16..15 at d = 1: y = 127 * (3 - 16)
+    x1 = np.zeros((1, 32), np.float32)
+    x1[0, 3] = 127.0
+    wb = np.zeros(34, np.uint8)
+    wb[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    wb[2:] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    assert orc.q8_0_linear_int8(x1, wb, 1)[0, 0] == np.float32(127 * -13)
+
 
 def test_q8_0_dequant_brute_force():
     scales = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0xBC00, 0x7BFF, 0xFBFF,
