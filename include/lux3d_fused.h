@@ -400,7 +400,10 @@ int lux3d_sparse_neighbors(const lux3d_tensor_t *coords, const lux3d_tensor_t *k
  * ends), so N is limited to 2^20 voxels (LUX3D_ERR_SHAPE beyond). Every call
  * on a GPU uses that GPU's one table: calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller. Same
- * kernels and outputs as lux3d_sparse_neighbors.                           */
+ * kernels and outputs as lux3d_sparse_neighbors. The first call on a device
+ * looks the table's address up (hipGetSymbolAddress, which may load the
+ * library's code object on that device): make one call per device outside
+ * graph capture before capturing calls of this entry.                      */
 int lux3d_sparse_neighbors_noalloc(const lux3d_tensor_t *coords, const lux3d_tensor_t *nbr,
                                    const lux3d_tensor_t *bad_coords, lux3d_stream_t stream);
 int lux3d_sparse_conv3d(const lux3d_tensor_t *x, const lux3d_tensor_t *nbr,
