@@ -7,6 +7,10 @@
         <kernel-substring> "<command>" > profiles/<name>.md
   python -m lux3d_fused.rocprof_summary counters <counter_collection.csv> <kernel-substring> "<command>" \
         > profiles/<name>.md
+  python -m lux3d_fused.rocprof_summary sweep <kernel_trace.csv> <stdout of the traced sweep> "<command>" \
+        [<stdout of the unprofiled sweep> "<its command>"] > profiles/ceiling_sweep.md
+  python -m lux3d_fused.rocprof_summary rotation <kernel_trace.csv> <kernel-substring> \
+        <stdout of bench.py --profile> "<command>" > profiles/rotation_<op>.md
 
 `trace` reports the kernels whose name contains <kernel-substring> (the op's
 own kernels, alternatives separated by `|`; the workload set-up kernels are
@@ -17,6 +21,17 @@ launch against <peak>), in a JSON block that bench.py reads back.
 `counters` reports the median per-dispatch value of every counter in the
 file for the matching kernels, and per-wavefront instruction counts when
 SQ_WAVES was collected.
+
+`sweep` reports the plain-copy sweep of `bench.py --ceiling-sweep`: the
+traced copies sliced per (size, variant) by the manifest that run printed
+(its timed graph replays only), their average duration and bandwidth, and
+the fastest variant per size; with the unprofiled run's stdout it adds that
+run's HIP-event table of the whole variant family.
+
+`rotation` splits the per-dispatch durations of one op's kernel (the trace
+of `bench.py --profile <op>`) by rotation set and by position in the timed
+graph, to show where the spread between the fastest and slowest launches
+comes from.
 
 `traffic` reports the per-dispatch HBM bytes of the kernels whose name
 contains <kernel-substring>, with FETCH_SIZE and WRITE_SIZE (KiB per
@@ -194,6 +209,103 @@ def traffic(fetch, write, cal_fetch, cal_write, kernel_sub, command):
     return "\n".join(lines) + "\n"
 
 
+def _trace_rows(path, kernel_sub):
+    subs = kernel_sub.split("|")
+    rows = [r for r in _rows(path) if any(s in r["Kernel_Name"] for s in subs)]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3) for r in rows]
+
+
+def _json_lines(log_path, key):
+    out = []
+    for line in open(log_path):
+        if line.startswith("{") and f'"{key}"' in line:
+            out.append(json.loads(line))
+    return out
+
+
+def sweep(trace_csv, log_path, command, events_log=None, events_command=None):
+    """Per (size, variant) average duration of the traced copies."""
+    man = _json_lines(log_path, "manifest")[0]["manifest"]
+    best_line = _json_lines(log_path, "sweep_best")[0]
+    iters = best_line["iters"]
+    durs = [d for _, d in _trace_rows(trace_csv, "best_kernel")]
+    pos, table = 0, {}
+    for e in man:
+        seg = durs[pos:pos + e["dispatches"]]
+        pos += e["dispatches"]
+        timed = seg[3 + iters:]  # skip the eager warm-ups and the first graph replay
+        table.setdefault(e["mb"], {})[e["variant"]] = sum(timed) / len(timed)
+    out = ["# Plain-copy ceiling by copy size (rocprofv3 kernel trace)", "",
+           f"Command: `{command}`", "", NOTE, "",
+           "Each size moves MB x 10^6 bytes per launch, half read and half written, over rotation sets "
+           "that together exceed the 256 MB Infinity Cache; durations are the traced average of the timed "
+           "graph replays. Variants: oneshot = one workgroup per tile; strided = a persistent grid of g "
+           "workgroups striding over tiles; prefetch = persistent, the next tile loaded before the current "
+           "one is stored; c = 16-byte chunks per thread per tile, b = threads per workgroup.", "",
+           "| MB | fastest variant | us | GB/s | of 8 TB/s | oneshot_c1_b256 us |", "|---|---|---|---|---|---|"]
+    res = {}
+    for mb, vs in table.items():
+        k = min(vs, key=vs.get)
+        gbs = mb * 1e6 / vs[k] / 1e3
+        res[mb] = {"variant": k, "us": round(vs[k], 3), "gbs": round(gbs, 1), "frac": round(gbs / 8000.0, 4),
+                   "all_us": {v: round(u, 3) for v, u in vs.items()}}
+        base = vs.get("oneshot_c1_b256")
+        out.append(f"| {mb} | {k} | {vs[k]:.3f} | {gbs:,.1f} | {gbs / 8000.0:.4f} | "
+                   + (f"{base:.3f}" if base else "-") + " |")
+    if events_log:
+        ev = _json_lines(events_log, "sweep_mb")
+        out += ["", f"The whole variant family, HIP events around the graph replays (unprofiled): "
+                    f"`{events_command}`", "",
+                "| MB | fastest | us | GB/s | of 8 TB/s | oneshot_c1_b256 | strided_c1_b256_g1024 |",
+                "|---|---|---|---|---|---|---|"]
+        for e in ev:
+            us = e["us"]
+            k = min(us, key=us.get)
+            gbs = e["bytes"] / us[k] / 1e3
+            out.append(f"| {e['sweep_mb']} | {k} | {us[k]:.3f} | {gbs:,.1f} | {gbs / 8000.0:.4f} | "
+                       f"{us.get('oneshot_c1_b256', float('nan')):.3f} | "
+                       f"{us.get('strided_c1_b256_g1024', float('nan')):.3f} |")
+    out += ["", "```json", json.dumps(res, indent=1), "```"]
+    return "\n".join(out) + "\n"
+
+
+def rotation(trace_csv, kernel_sub, log_path, command):
+    """Durations of one op's launches by rotation set and graph position."""
+    prof = next(line for line in open(log_path) if line.startswith("[profile]"))
+    sets = int(prof.split("sets=")[1].split()[0])
+    iters = int(prof.split("iters=")[1].split()[0])
+    d = [u for _, u in _trace_rows(trace_csv, kernel_sub)]
+    # time_graph: 3 eager launches (sets 0..2), then the graph of `iters`
+    # launches (launch i on set i % sets) replayed 6 times
+    graph = d[3:]
+    by_set, by_pos = {}, {}
+    for j, u in enumerate(graph):
+        i = j % iters
+        by_set.setdefault(i % sets, []).append(u)
+        by_pos.setdefault(min(i, 3) if i < 3 else "3+", []).append(u)
+    s = sorted(graph)
+    pct = lambda q: s[min(len(s) - 1, int(q * len(s)))]  # noqa: E731
+    out = ["# Per-launch durations by rotation set and graph position (rocprofv3 kernel trace)", "",
+           f"Command: `{command}`", "", NOTE, "",
+           f"Kernels matching `{kernel_sub}`: {len(graph)} graph launches ({iters} per replay, {sets} rotation "
+           f"sets). min {s[0]:.3f}, p10 {pct(0.1):.3f}, median {pct(0.5):.3f}, p90 {pct(0.9):.3f}, "
+           f"max {s[-1]:.3f} us.", "", "| rotation set | launches | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for k in sorted(by_set):
+        v = by_set[k]
+        out.append(f"| {k} | {len(v)} | {sum(v) / len(v):.3f} | {min(v):.3f} | {max(v):.3f} |")
+    out += ["", "| position in the graph | launches | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for k in [0, 1, 2, "3+"]:
+        v = by_pos.get(k, [])
+        if v:
+            out.append(f"| {k} | {len(v)} | {sum(v) / len(v):.3f} | {min(v):.3f} | {max(v):.3f} |")
+    res = {"sets": sets, "iters": iters, "launches": len(graph), "min": s[0], "median": pct(0.5), "max": s[-1],
+           "by_set_avg": {k: round(sum(v) / len(v), 3) for k, v in by_set.items()},
+           "by_position_avg": {str(k): round(sum(v) / len(v), 3) for k, v in by_pos.items()}}
+    out += ["", "```json", json.dumps(res, indent=1), "```"]
+    return "\n".join(out) + "\n"
+
+
 def main(argv):
     if argv[0] == "stats":
         sys.stdout.write(stats(argv[1], argv[2]))
@@ -203,6 +315,10 @@ def main(argv):
         sys.stdout.write(counters(*argv[1:4]))
     elif argv[0] == "traffic":
         sys.stdout.write(traffic(*argv[1:7]))
+    elif argv[0] == "sweep":
+        sys.stdout.write(sweep(*argv[1:6]))
+    elif argv[0] == "rotation":
+        sys.stdout.write(rotation(*argv[1:5]))
     else:
         raise SystemExit(__doc__)
 
