@@ -887,6 +887,85 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const l
 }
 
 namespace {
+// x f32 rows (16-byte aligned) and the Q8_0 quantization workspace for them:
+// xq int8 [rows, k] and xd f32 block-major [k/32, rows rounded up to 64],
+// both contiguous and 16-byte aligned.
+int q8_act(const char *fn, const lux3d_tensor_t *x, const lux3d_tensor_t *xq, const lux3d_tensor_t *xd,
+           Q8IntParams &p) {
+  int r;
+  RowView xv;
+  if ((r = row_tensor(x, fn, "x", LUX3D_F32, xv))) return r;
+  if ((r = check_desc(xq, fn, "xq")) || (r = check_desc(xd, fn, "xd"))) return r;
+  const int64_t k = xv.d;
+  if (k % 32 || k == 0) return fail(LUX3D_ERR_SHAPE, "%s: x rows must hold a positive multiple of 32 values", fn);
+  if (xq->dtype != LUX3D_I8 || !is_contiguous(xq) || numel(xq) != xv.rows * k)
+    return fail(LUX3D_ERR_SHAPE, "%s: xq must be a contiguous int8 [%lld, %lld]", fn, (long long)xv.rows,
+                (long long)k);
+  const int64_t mpad = (xv.rows + 63) / 64 * 64;
+  if (xd->dtype != LUX3D_F32 || !is_contiguous(xd) || numel(xd) != mpad * (k / 32))
+    return fail(LUX3D_ERR_SHAPE, "%s: xd must be a contiguous f32 [%lld, %lld] (block-major, rows rounded up to 64)",
+                fn, (long long)(k / 32), (long long)mpad);
+  if (!aligned16(x->data) || (xv.rows > 1 && (xv.rs * 4) % 16) || !aligned16(xq->data) || !aligned16(xd->data))
+    return fail(LUX3D_ERR_LAYOUT, "%s: x rows, xq and xd must be 16-byte aligned", fn);
+  p.x = reinterpret_cast<const float *>(xv.p);
+  p.ldx = xv.rs;
+  p.xq = reinterpret_cast<int8_t *>(xq->data);
+  p.xd = reinterpret_cast<float *>(xd->data);
+  p.ldxd = mpad;
+  p.M = xv.rows;
+  p.K = k;
+  return LUX3D_OK;
+}
+}  // namespace
+
+int lux3d_q8_0_quantize(const lux3d_tensor_t *x, const lux3d_tensor_t *xq, const lux3d_tensor_t *xd,
+                        lux3d_stream_t stream) {
+  const char *fn = "lux3d_q8_0_quantize";
+  Q8IntParams p;
+  int r;
+  if ((r = q8_act(fn, x, xq, xd, p))) return r;
+  return hip_status(launch_q8_0_quantize_rows(p, stream_of(stream)), fn);
+}
+
+int lux3d_q8_0_linear_int8(const lux3d_tensor_t *x, const lux3d_tensor_t *qs, const lux3d_tensor_t *scales,
+                           const lux3d_tensor_t *bias, const lux3d_tensor_t *xq, const lux3d_tensor_t *xd,
+                           const lux3d_tensor_t *y, lux3d_stream_t stream) {
+  const char *fn = "lux3d_q8_0_linear_int8";
+  Q8IntParams p;
+  int r;
+  if ((r = q8_act(fn, x, xq, xd, p))) return r;
+  if ((r = check_desc(qs, fn, "qs")) || (r = check_desc(scales, fn, "scales"))) return r;
+  if (qs->dtype != LUX3D_I8 || qs->rank != 2 || !is_contiguous(qs))
+    return fail(LUX3D_ERR_SHAPE, "%s: qs must be a contiguous int8 [n, k] (from lux3d_q8_0_repack)", fn);
+  const int64_t n = qs->shape[0];
+  if (qs->shape[1] != p.K)
+    return fail(LUX3D_ERR_SHAPE, "%s: x has %lld features, the weight %lld", fn, (long long)p.K,
+                (long long)qs->shape[1]);
+  if (scales->dtype != LUX3D_F32 || !is_contiguous(scales) || numel(scales) != n * (p.K / 32))
+    return fail(LUX3D_ERR_SHAPE, "%s: scales must be a contiguous f32 [n, k/32]", fn);
+  if (!aligned16(qs->data)) return fail(LUX3D_ERR_LAYOUT, "%s: qs must be 16-byte aligned", fn);
+  RowView yv;
+  if ((r = row_tensor(y, fn, "y", LUX3D_F32, yv))) return r;
+  if (yv.d != n || yv.rows != p.M)
+    return fail(LUX3D_ERR_SHAPE, "%s: y must be f32 [%lld, %lld]", fn, (long long)p.M, (long long)n);
+  if (bias) {
+    if ((r = check_desc(bias, fn, "bias"))) return r;
+    if (bias->dtype != LUX3D_F32 || !is_contiguous(bias) || numel(bias) != n)
+      return fail(LUX3D_ERR_SHAPE, "%s: bias must be a contiguous f32 [n]", fn);
+    p.bias = reinterpret_cast<const float *>(bias->data);
+  }
+  p.qs = reinterpret_cast<const int8_t *>(qs->data);
+  p.scales = reinterpret_cast<const float *>(scales->data);
+  p.y = reinterpret_cast<float *>(const_cast<void *>(yv.p));
+  p.ldy = yv.rs;
+  p.N = n;
+  hipStream_t s = stream_of(stream);
+  hipError_t e = launch_q8_0_quantize_rows(p, s);
+  if (e == hipSuccess) e = launch_q8_0_int8_gemm(p, s);
+  return hip_status(e, fn);
+}
+
+namespace {
 // Validates q, k, v, out for attention and fills the strides; `mfma` tells
 // whether every row is 16-byte aligned with D 64 / 128. `f32_out_ok`: out
 // may also be f32 when q, k, v are 2-byte.

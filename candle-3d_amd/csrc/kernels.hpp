@@ -116,6 +116,23 @@ struct Q8GemmParams {
 hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs, float *scales, hipStream_t s);
 hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s);
 
+// candle's CPU QMatMul for a Q8_0 weight: x f32 rows quantized to Q8_0
+// blocks (int8 values xq [M, K] + the f16 scale widened to f32, xd
+// block-major [K/32, ldxd]), then y = sum over blocks of (f32)(isum) * wd * xd in block
+// order (+ bias), f32 out. K % 32 == 0; every pointer 16-byte aligned.
+struct Q8IntParams {
+  const float *x = nullptr; int64_t ldx = 0;  // f32 rows
+  int8_t *xq = nullptr;                       // [M, K] contiguous (workspace)
+  float *xd = nullptr; int64_t ldxd = 0;      // block-major [K / 32, ldxd >= M rounded up to 64] (workspace)
+  const int8_t *qs = nullptr;                 // [N, K] from the repack
+  const float *scales = nullptr;              // [N, K / 32]
+  const float *bias = nullptr;                // [N] or null
+  float *y = nullptr; int64_t ldy = 0;        // [M, N] rows
+  int64_t M = 0, N = 0, K = 0;
+};
+hipError_t launch_q8_0_quantize_rows(const Q8IntParams &p, hipStream_t s);
+hipError_t launch_q8_0_int8_gemm(const Q8IntParams &p, hipStream_t s);
+
 // Scaled dot-product attention over [B, H, L, D] views (element strides per
 // batch, head and token; unit inner stride). out = softmax(q k^T * scale) v.
 // `mfma` selects the matrix-core kernels (D 64 or 128, every row

@@ -750,6 +750,157 @@ hipError_t launch_q8_0_repack(const uint8_t *blocks, int64_t nblocks, int8_t *qs
   return hipGetLastError();
 }
 
+// ---- integer-dot Q8_0 linear: candle's CPU QMatMul semantics ----------------
+//
+// The reference's quantized Linear::forward (runtime/nn_blocks.rs:80-93) on
+// the CPU quantizes each x row to Q8_0 blocks and takes integer dot
+// products with the weight blocks (candle-core quantized/k_quants.rs,
+// BlockQ8_0::from_float and vec_dot). Here:
+// - q8_0_quantize_rows_kernel: eight lanes per 32-value block (16 bytes
+//   each): amax = max |x| (NaN ignored, at least 0), d = amax / 127, id =
+//   d != 0 ? 1 / d : 0 (correctly rounded f32 divisions), q = round half
+//   away from zero of x * id, saturated to int8 with NaN -> 0, and d rounded
+//   to f16 (RNE) and widened back to f32;
+// - q8_0_int8_gemm_kernel: one v_mfma_i32_32x32x32_i8 per 32 x 32 tile and
+//   Q8_0 block gives that block's exact int32 dot products; each is then
+//   folded into the f32 sum as candle's generic vec_dot does, in block
+//   order: acc = acc + ((f32)isum * wd) * xd, every operation rounded
+//   (mul_rn / add_rn: no contraction), and y = acc + bias. The result is
+//   bit-identical to candle's CPU path. The f32 fold (4 VALU operations per
+//   output and block) bounds the kernel, not the int8 matrix rate.
+
+__global__ __launch_bounds__(256) void q8_0_quantize_rows_kernel(Q8IntParams p) {
+  const int64_t nb = p.K / 32;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t blk = g >> 3;
+  const int part = (int)(g & 7);
+  const bool live = blk < p.M * nb;
+  const int64_t bc = live ? blk : 0;
+  const int64_t m = bc / nb, b = bc - m * nb;
+  const float4 v = *reinterpret_cast<const float4 *>(p.x + m * p.ldx + b * 32 + part * 4);
+  const float xv[4] = {v.x, v.y, v.z, v.w};
+  // f32::max ignores a NaN operand; fmaxf (IEEE maxNum) does the same
+  float a = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
+  a = fmaxf(a, dpp<DPP_XOR1>(a));
+  a = fmaxf(a, dpp<DPP_XOR2>(a));
+  a = fmaxf(a, dpp<DPP_HALF_MIRROR>(a));  // the 8 lanes of the block
+  const float amax = fmaxf(a, 0.0f);       // candle starts its maximum at 0
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float r = roundf(mul_rn(xv[k], id));
+    const int q = r != r ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
+    packed |= ((uint32_t)(uint8_t)(int8_t)q) << (8 * k);
+  }
+  if (!live) return;
+  *reinterpret_cast<uint32_t *>(p.xq + m * p.K + b * 32 + part * 4) = packed;
+  if (part == 0) p.xd[b * p.ldxd + m] = (float)(_Float16)d;  // block-major
+}
+
+// 256 threads (2 x 2 wavefronts of 32 x 32 tiles) per 64 x 64 tile of y; a
+// stage is two Q8_0 blocks (k-step 64), double-buffered through LDS: rows of
+// 64 int8 at an 80-byte stride (conflict-free 16-byte fragment reads) and
+// the stage's block scales of the tile's 64 x rows and 64 weight rows. The
+// second block's MFMA is issued before the first block's f32 fold, so the
+// matrix core runs beside the fold's VALU work. An odd last block is loaded
+// twice and folded once.
+constexpr int kI8Tile = 64, kI8Row = 80;
+__global__ __launch_bounds__(256) void q8_0_int8_gemm_kernel(Q8IntParams p, int tiles_n) {
+  typedef int i32x4_t_ __attribute__((ext_vector_type(4)));
+  typedef int i32x16_t_ __attribute__((ext_vector_type(16)));
+  __shared__ __align__(16) int8_t As[2][kI8Tile * kI8Row];
+  __shared__ __align__(16) int8_t Bs[2][kI8Tile * kI8Row];
+  __shared__ __align__(16) float Ad[2][2][kI8Tile];  // [buffer][block of the stage][row]
+  __shared__ __align__(16) float Bd[2][2][kI8Tile];
+  (void)tiles_n;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * kI8Tile, n0 = (int64_t)blockIdx.x * kI8Tile;
+  const int64_t nb = p.K / 32, nst = (nb + 1) / 2;
+  // loaders: thread t moves the 16 bytes (t & 3) of x row t / 4 and of weight
+  // row t / 4 per stage (rows past M / N clamped: loaded, computed, never
+  // stored); threads 0-127 the x scales (block t / 64 of the stage, row
+  // t % 64), 128-255 the weight scales
+  const int lr = t >> 2, lq = t & 3;
+  const int64_t ra = m0 + lr < p.M ? m0 + lr : p.M - 1, rb = n0 + lr < p.N ? n0 + lr : p.N - 1;
+  const int8_t *sa = p.xq + ra * p.K + lq * 16, *sb = p.qs + rb * p.K + lq * 16;
+  const int so = lr * kI8Row + lq * 16;
+  const int sr = t & 63, sbk = (t >> 6) & 1;
+  const bool sx = t < 128;
+  const int64_t swr = n0 + sr < p.N ? n0 + sr : p.N - 1;
+  auto scale_at = [&](int64_t st) -> float {
+    int64_t kb = 2 * st + sbk;
+    kb = kb < nb ? kb : nb - 1;
+    return sx ? p.xd[kb * p.ldxd + m0 + sr] : p.scales[swr * nb + kb];
+  };
+  auto k_off = [&](int64_t st) -> int64_t {  // byte offset of this thread's 16 bytes in stage st
+    const int64_t k = st * 64 + lq * 16;
+    return k < p.K ? st * 64 : p.K - 64;  // an odd last block: its second half loads block nb - 1 again
+  };
+  uint4 va, vb;
+  float vs;
+  auto load = [&](int64_t st) {
+    const int64_t o = k_off(st);
+    va = *reinterpret_cast<const uint4 *>(sa + o);
+    vb = *reinterpret_cast<const uint4 *>(sb + o);
+    vs = scale_at(st);
+  };
+  auto store = [&](int buf) {
+    *reinterpret_cast<uint4 *>(&As[buf][so]) = va;
+    *reinterpret_cast<uint4 *>(&Bs[buf][so]) = vb;
+    (sx ? Ad[buf][sbk] : Bd[buf][sbk])[sr] = vs;
+  };
+  load(0);
+  store(0);
+  lds_barrier();
+
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  const int fr = lane & 31, fk = (lane >> 5) * 16;
+  auto fold = [&](const i32x16_t_ &c, int buf, int blk) {
+    const float wd = Bd[buf][blk][wn * 32 + fr];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // rows 8q + 4 (lane / 32) + 0..3 of the wavefront's 32
+      const float4 xd4 = *reinterpret_cast<const float4 *>(&Ad[buf][blk][wm * 32 + 8 * q + 4 * (lane >> 5)]);
+      const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * q + i;
+        acc[e] = add_rn(acc[e], mul_rn(mul_rn((float)c[e], wd), xd[i]));
+      }
+    }
+  };
+  for (int64_t st = 0; st < nst; ++st) {
+    const int buf = (int)(st & 1);
+    if (st + 1 < nst) load(st + 1);
+    const int8_t *a = &As[buf][(wm * 32 + fr) * kI8Row + fk], *b = &Bs[buf][(wn * 32 + fr) * kI8Row + fk];
+    const i32x16_t_ c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a),
+                                                               *reinterpret_cast<const i32x4_t_ *>(b), i32x16_t_{}, 0,
+                                                               0, 0);
+    const bool two = 2 * st + 1 < nb;
+    i32x16_t_ c1 = {};
+    if (two)
+      c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a + 32),
+                                                 *reinterpret_cast<const i32x4_t_ *>(b + 32), i32x16_t_{}, 0, 0, 0);
+    fold(c0, buf, 0);
+    if (two) fold(c1, buf, 1);
+    if (st + 1 < nst) store(buf ^ 1);
+    lds_barrier();
+  }
+  // lane holds y[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of its 32 x 32 tile
+  const int64_t col = n0 + wn * 32 + fr;
+  if (col >= p.N) return;
+  const float bias = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t row = m0 + wm * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+    if (row < p.M) p.y[row * p.ldy + col] = p.bias ? add_rn(acc[e], bias) : acc[e];
+  }
+}
+
 hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
   if (p.K <= 0 || p.K % kBK) return hipErrorInvalidValue;
@@ -762,6 +913,24 @@ hipError_t launch_q8_0_gemm(int out_dt, const Q8GemmParams &p, hipStream_t s) {
     case LUX3D_F32: return launch_tiles<F32>(p, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_q8_0_quantize_rows(const Q8IntParams &p, hipStream_t s) {
+  if (p.M <= 0) return hipSuccess;
+  if (p.K <= 0 || p.K % 32) return hipErrorInvalidValue;
+  const int64_t lanes = p.M * (p.K / 32) * 8;
+  if ((lanes + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(q8_0_quantize_rows_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_0_int8_gemm(const Q8IntParams &p, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (p.K <= 0 || p.K % 32 || p.ldxd < (p.M + kI8Tile - 1) / kI8Tile * kI8Tile) return hipErrorInvalidValue;
+  const int64_t tn = (p.N + kI8Tile - 1) / kI8Tile, tm = (p.M + kI8Tile - 1) / kI8Tile;
+  if (tn > INT32_MAX || tm > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(q8_0_int8_gemm_kernel, dim3((unsigned)tn, (unsigned)tm), dim3(256), 0, s, p, (int)tn);
+  return hipGetLastError();
 }
 
 }  // namespace lux3d

@@ -67,6 +67,8 @@ SIGNATURES = {
     "lux3d_dequant_q8_0": [TP, TP, S],
     "lux3d_q8_0_repack": [TP, ctypes.c_int64, ctypes.c_int64, TP, TP, S],
     "lux3d_q8_0_linear": [TP, TP, TP, TP, TP, S],
+    "lux3d_q8_0_linear_int8": [TP, TP, TP, TP, TP, TP, TP, S],
+    "lux3d_q8_0_quantize": [TP, TP, TP, S],
     "lux3d_sdpa": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_heads_f32": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_layernorm_rope2d": [TP, TP, TP, ctypes.c_float, TP, TP, TP, TP, ctypes.c_float, TP, S],

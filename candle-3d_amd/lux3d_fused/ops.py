@@ -379,6 +379,41 @@ def q8_0_linear(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, bias: O
     return y
 
 
+def q8_0_quantize(x: torch.Tensor):
+    """BlockQ8_0::from_float of f32 x [..., k] rows (candle-core
+    k_quants.rs, the first step of candle's CPU QMatMul): -> (xq int8
+    [rows, k], xd f32 [rows, k/32], the f16 block scales widened; a view of
+    the library's block-major workspace)."""
+    k = x.shape[-1]
+    rows = x.numel() // k
+    xq, xd = _q8_workspace(rows, k, x.device)
+    _lib.call("lux3d_q8_0_quantize", desc(x), desc(xq), desc(xd), _stream(x))
+    return xq, xd[:, :rows].t()
+
+
+def _q8_workspace(rows, k, device):
+    """xq int8 [rows, k] and the block-major xd f32 [k/32, rows rounded up to 64]."""
+    xq = torch.empty((rows, k), dtype=torch.int8, device=device)
+    xd = torch.empty((k // 32, (rows + 63) // 64 * 64), dtype=torch.float32, device=device)
+    return xq, xd
+
+
+def q8_0_linear_int8(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor,
+                     bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """`Linear::forward` for a Q8_0 weight with candle's CPU arithmetic
+    (runtime/nn_blocks.rs:83-93 -> QMatMul::forward on the CPU): x f32 rows
+    quantized to Q8_0 blocks, integer block dots, f32 block-order sum, +
+    bias; f32 [..., k] -> f32 [..., n]. The quantization workspace is
+    allocated here."""
+    n, k = qs.shape
+    rows = x.numel() // k
+    xq, xd = _q8_workspace(rows, k, x.device)
+    y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=torch.float32, device=x.device)
+    _lib.call("lux3d_q8_0_linear_int8", desc(x), desc(qs), desc(scales), desc(bias), desc(xq), desc(xd), desc(y),
+              _stream(x))
+    return y
+
+
 class QMatMul:
     """QMatMul over a Q8_0 weight [n, k] (the reference keeps the packed
     QTensor; here the blocks are repacked once to int8 + f32 scales)."""

@@ -531,6 +531,47 @@ def cfg2_q8_0_linear_f32(dev) -> Workload:
     return _q8_linear(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection", torch.float32)
 
 
+def _q8_linear_int8(dev, cfg, m, k, n, what) -> Workload:
+    """Q8_0 linear with candle's CPU arithmetic (f32 x quantized per 32 to
+    Q8_0, int32 block dots on the int8 matrix cores, f32 block-order fold,
+    + bias): two launches (quantize, GEMM) per op. Priced against the int8
+    matrix peak; the f32 fold (4 VALU operations per output and block) is
+    the bound."""
+    from . import _lib
+    s = synth.config_seed(cfg) + 520
+    x0 = _normal(s, (m, k), dev, torch.float32)
+    blocks = _t(synth.q8_0_blocks(s + 1, n * k // 32), dev)
+    qs, scales = ops.q8_0_repack(blocks, n, k)
+    bias = _normal(s + 2, (n,), dev, torch.float32, 0.0, 0.5)
+    nbytes = m * k * 4 + n * k + n * (k // 32) * 4 + n * 4 + m * n * 4
+    n_sets = _n_sets(m * k * 4 + m * n * 4)
+    xs = [_fill_like(x0, j) for j in range(n_sets)]
+    ys = [torch.empty((m, n), dtype=torch.float32, device=dev) for _ in range(n_sets)]
+    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
+    xd = torch.empty((k // 32, (m + 63) // 64 * 64), dtype=torch.float32, device=dev)
+    dx = [ops.desc(v) for v in xs]
+    dy = [ops.desc(v) for v in ys]
+    dq, dsc, db, dxq, dxd = ops.desc(qs), ops.desc(scales), ops.desc(bias), ops.desc(xq), ops.desc(xd)
+
+    def launch(i):
+        j = i % n_sets
+        _lib.call("lux3d_q8_0_linear_int8", dx[j], dq, dsc, db, dxq, dxd, dy[j], _cur())
+    wl = Workload("q8_0_linear_int8", cfg, "q8_0_quantize_rows_kernel + q8_0_int8_gemm_kernel",
+                  "f32 x quantized to Q8_0, int8 x int8 -> int32 per block, f32 fold", nbytes,
+                  f"x[{m},{k}] f32 @ W[{n},{k}]^T, candle CPU arithmetic ({what})", launch, n_sets,
+                  flops=2 * m * k * n, peak_tflops=5000.0)
+    wl._keep = (xs, ys, qs, scales, bias, blocks, xq, xd, dx, dy, dq, dsc, db, dxq, dxd)
+    return wl
+
+
+def cfg4_q8_0_linear_int8(dev) -> Workload:
+    return _q8_linear_int8(dev, 4, 1029, 1024, 4096, "configs[4] weight, 1029 tokens")
+
+
+def cfg2_q8_0_linear_int8(dev) -> Workload:
+    return _q8_linear_int8(dev, 2, 4096, 2048, 8192, "TripoSG FF up-projection")
+
+
 def _sdpa(dev, name, cfg, b, n, h, d, what, reps=50, dt=torch.bfloat16, heads_f32=False) -> Workload:
     """Attention over q, k, v taken as the permuted views of a fused
     [B, N, 3, H, D] qkv buffer (vggt.rs:161-168), output [B, H, N, D].
@@ -790,6 +831,8 @@ EXTRAS: List[Callable] = [
     cfg4_dinov3_rope,
     cfg4_q8_0_linear,
     cfg2_q8_0_linear,
+    cfg4_q8_0_linear_int8,
+    cfg2_q8_0_linear_int8,
     cfg2_q8_0_linear_f32,
     cfg1_sdpa_frame,
     cfg1_sdpa_frame_qln,

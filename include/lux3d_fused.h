@@ -347,6 +347,34 @@ int lux3d_q8_0_linear(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
                       const lux3d_tensor_t *scales, const lux3d_tensor_t *bias,
                       const lux3d_tensor_t *y, lux3d_stream_t stream);
 
+/* lux3d_q8_0_linear_int8: the same Linear::forward Quant branch with
+ * candle's CPU arithmetic (QMatMul::forward on the CPU: the QTensor custom
+ * op over upstream candle-core's k_quants::matmul), bit for bit: each f32 x
+ * row is quantized to Q8_0 blocks (lux3d_q8_0_quantize below), each output is
+ *   acc = 0; for each block b in order: acc += (f32)(sum_j w_q[j] x_q[j]) * w_d * x_d
+ * (int32 block dots on the int8 matrix cores, then every f32 operation
+ * rounded in that order), and y = acc + bias (broadcast_add).
+ *   x: f32 [..., k] rows, 16-byte aligned; qs, scales: lux3d_q8_0_repack;
+ *   bias: f32 [n] or NULL; y: f32 [..., n] rows;
+ *   xq: int8 [rows, k] and xd: f32 [k/32, rows rounded up to 64]
+ *   (block-major: a block's scales of consecutive rows are adjacent),
+ *   contiguous and 16-byte aligned -- a workspace that receives x's
+ *   quantized blocks.
+ * Two kernels (quantize, then the GEMM).
+ *
+ * lux3d_q8_0_quantize: BlockQ8_0::from_float of every 32-value block of each
+ * x row (candle-core k_quants.rs; the first step of the CPU QMatMul): amax =
+ * max |x| (NaN ignored), d = amax / 127, q = round-half-away(x / d as
+ * x * (1 / d)) saturated to int8 (NaN -> 0), d rounded to f16. xq receives
+ * the int8 values, xd (block-major, as above) the f16 scale widened to f32
+ * (exact). One kernel.                                                     */
+int lux3d_q8_0_linear_int8(const lux3d_tensor_t *x, const lux3d_tensor_t *qs,
+                           const lux3d_tensor_t *scales, const lux3d_tensor_t *bias,
+                           const lux3d_tensor_t *xq, const lux3d_tensor_t *xd,
+                           const lux3d_tensor_t *y, lux3d_stream_t stream);
+int lux3d_q8_0_quantize(const lux3d_tensor_t *x, const lux3d_tensor_t *xq,
+                        const lux3d_tensor_t *xd, lux3d_stream_t stream);
+
 /* ---- TRELLIS.2 sparse voxel ops (runtime/trellis2_sparse.rs) ----------------
  * lux3d_sparse_neighbors: CoordMap::new + the per-offset lookups of
  * SparseConv3d::forward (trellis2_sparse.rs:62-91, 205-222), on the device;
