@@ -496,6 +496,28 @@ __device__ __forceinline__ int64_t uniform(int64_t v) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// x / d for x < 2^31 from the launcher's (m, s) = (ceil(2^s / d), 31 +
+// ceil(log2 d)): x m / 2^s exceeds x / d by less than 2^31 / 2^s <= 1 / d,
+// which cannot reach the next integer. Three instructions instead of the
+// ~10 of a runtime 32-bit division.
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, uint32_t m, int s) {
+  return (uint32_t)(((uint64_t)x * m) >> s);
+}
+inline void div_magic(int64_t d, uint32_t &m, int &s) {
+  int l = 0;
+  while ((int64_t(1) << l) < d) ++l;
+  s = 31 + l;
+  m = (uint32_t)(((uint64_t(1) << s) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
+// Segment of dense row r (equal segments of rows_per_seg rows, magic (m, s)
+// of rows_per_seg from div_magic) when every row index is below 2^31:
+// three scalar instructions instead of a 64-bit division.
+__device__ __forceinline__ int64_t segment_of_dense(uint32_t r, uint32_t m, int s, int64_t nseg) {
+  const int64_t q = (int64_t)fdiv(r, m, s);
+  return q < nseg ? q : nseg - 1;
+}
+
 // Segment of row r given int64 offsets [nseg+1] (largest s with off[s] <= r),
 // or equal segments of `rows_per_seg` rows when `off` is NULL. Always returns
 // a value in [0, nseg-1], whatever the offsets hold.

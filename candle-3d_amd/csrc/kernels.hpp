@@ -35,6 +35,7 @@ struct RowParams {
   const void *g = nullptr; int g_dt = -1;       // LayerScale gamma
   const int64_t *seg_off = nullptr;             // [nseg+1] or NULL
   int64_t nseg = 1, rows_per_seg = 1;
+  uint32_t rps_m = 0; int rps_s = 0;            // set by the launcher: rows_per_seg's div_magic (dense, rows < 2^31)
   ModPiece shift, scale, gate;
 };
 

@@ -28,6 +28,13 @@ constexpr int kBlock = 256;
 // (1024-thread workgroups straddle more segment boundaries).
 constexpr int kStagedBlock = 512;
 
+// Segment of row r: the launcher's magic division for dense segments, the
+// scalar binary search over the offsets for ragged ones.
+__device__ __forceinline__ int64_t row_segment(const RowParams &p, int64_t r) {
+  if (p.rps_m) return segment_of_dense((uint32_t)r, p.rps_m, p.rps_s, p.nseg);
+  return segment_of(p.seg_off, p.nseg, p.rows_per_seg, r);
+}
+
 template <int TPR, int BLOCK = kBlock>
 __device__ __forceinline__ float row_total(float s, float *red) {
   s = wave_sum(s);
@@ -224,13 +231,13 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   if constexpr (SEGMENTED) {
     if constexpr (STAGE) {
       const int64_t last = row0 + RPB - 1 < p.rows ? row0 + RPB - 1 : p.rows - 1;
-      const int64_t seg0 = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row0);
-      staged = segment_of(p.seg_off, p.nseg, p.rows_per_seg, last) == seg0;  // uniform over the workgroup
+      const int64_t seg0 = row_segment(p, row0);
+      staged = row_segment(p, last) == seg0;  // uniform over the workgroup
       seg = seg0;
       if (staged) stage_pieces<MODE, BLOCK>(p, seg0, lds_pieces, st);
-      else seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
+      else seg = row_segment(p, row);
     } else {
-      seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
+      seg = row_segment(p, row);
     }
   }
 
@@ -365,7 +372,7 @@ template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void row_kernel_any(RowParams p) {
   __shared__ float red_a[kBlock / 64], red_b[kBlock / 64];
   const int64_t row = blockIdx.x;
-  const int64_t seg = segment_of(p.seg_off, p.nseg, p.rows_per_seg, row);
+  const int64_t seg = row_segment(p, row);
   auto piece = [&](const ModPiece &m, int64_t c, float dflt) -> float {
     float v = param1(m.p, m.dt, seg * m.ld + c, dflt);
     return m.base_dt >= 0 ? param1(m.base, m.base_dt, c, 0.f) + v : v;
@@ -414,8 +421,11 @@ __global__ __launch_bounds__(kBlock) void row_kernel_any(RowParams p) {
 }
 
 template <typename T, int MODE>
-hipError_t launch_typed(const RowParams &p, bool vec, hipStream_t s) {
-  if (p.rows <= 0) return hipSuccess;
+hipError_t launch_typed(const RowParams &p0, bool vec, hipStream_t s) {
+  if (p0.rows <= 0) return hipSuccess;
+  RowParams p = p0;
+  if (!p.seg_off && p.rows < (int64_t(1) << 31) && p.rows_per_seg > 0 && p.rows_per_seg < (int64_t(1) << 31))
+    div_magic(p.rows_per_seg, p.rps_m, p.rps_s);
   const int64_t chunks = p.d / 8;
   // Layout: threads per row (TPR), chunks per lane (NC) and workgroup size.
   // Short jobs (DINOv2/DINOv3's ~1k tokens) split each row over 2-4

@@ -65,20 +65,6 @@ __device__ __forceinline__ void head_param(const void *p, int dt, int64_t off, i
   }
 }
 
-// x / d for x < 2^31 from the launcher's (m, s) = (ceil(2^s / d), 31 +
-// ceil(log2 d)): x m / 2^s exceeds x / d by less than 2^31 / 2^s <= 1 / d,
-// which cannot reach the next integer. Three instructions instead of the
-// ~10 of a runtime 32-bit division.
-__device__ __forceinline__ uint32_t fdiv(uint32_t x, uint32_t m, int s) {
-  return (uint32_t)(((uint64_t)x * m) >> s);
-}
-void div_magic(int64_t d, uint32_t &m, int &s) {
-  int l = 0;
-  while ((int64_t(1) << l) < d) ++l;
-  s = 31 + l;
-  m = (uint32_t)(((uint64_t(1) << s) + (uint64_t)d - 1) / (uint64_t)d);
-}
-
 // Element offset of (b, h, n) + c in a [B, H, N, D] view. O32: the launcher
 // has checked that every byte offset of the views is below 2^31 and that
 // every index and every stride of an axis longer than 1 is below 2^24, so
