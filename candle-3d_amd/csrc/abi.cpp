@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <utility>
 
 #include "kernels.hpp"
 #include "lux3d_fused.h"
@@ -1026,10 +1027,117 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
       return r;
     return lux3d_sdpa(out, k, v, scale, out, stream);
   }
-  p.qln = true;
+  p.qpro = QP_LN_R1;
   p.qw = wp; p.qw_dt = wdt; p.qb = bp; p.qb_dt = bdt; p.eps = eps;
   p.tab_c = cos_full->data; p.tab_s = sin_alt_full->data; p.tab_dt = cos_full->dtype;
   p.tab_sB = cB; p.tab_sN = cN;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+int lux3d_sdpa_rms_norm_heads(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w, float eps, const lux3d_tensor_t *k,
+                              const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
+                              lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa_rms_norm_heads";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  if (!q_w) return fail(LUX3D_ERR_NULL, "%s: `q_w` is NULL", fn);
+  const void *wp;
+  int wdt;
+  if ((r = param_vec(q_w, p.D, fn, "q_w", wp, wdt))) return r;
+  if (!(eps >= 0.f)) return fail(LUX3D_ERR_VALUE, "%s: eps must be >= 0", fn);
+  const bool fused = p.mfma && q->dtype != LUX3D_F32 && aligned16(wp);
+  if (!fused) {
+    // the two launches, out holding the normalised q
+    if ((r = lux3d_rms_norm_heads(q, q_w, nullptr, nullptr, eps, out, nullptr, stream))) return r;
+    return lux3d_sdpa(out, k, v, scale, out, stream);
+  }
+  p.qpro = QP_RMS;
+  p.qw = wp; p.qw_dt = wdt; p.eps = eps;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+namespace {
+// The [B, L, H, D] view of a [B, H, L, D] descriptor (dims 1 and 2 swapped).
+lux3d_tensor_t swap_heads_tokens(const lux3d_tensor_t *t) {
+  lux3d_tensor_t u = *t;
+  std::swap(u.shape[1], u.shape[2]);
+  std::swap(u.stride[1], u.stride[2]);
+  return u;
+}
+// A rotation table [rows, cols] with a unit inner stride in f32 / bf16 / f16
+// (cos and sin alike); its row stride in sN.
+int rot_tables(const lux3d_tensor_t *cos, const lux3d_tensor_t *sin, int64_t rows, int64_t cols, const char *fn,
+               const char *what, int64_t &sN) {
+  int r;
+  if (!cos || !sin) return fail(LUX3D_ERR_NULL, "%s: pass both cos and sin tables", fn);
+  if ((r = check_desc(cos, fn, "cos")) || (r = check_desc(sin, fn, "sin"))) return r;
+  for (const lux3d_tensor_t *t : {cos, sin}) {
+    if (!is_float(t->dtype)) return fail(LUX3D_ERR_DTYPE, "%s: tables must be f32/bf16/f16", fn);
+    if (t->rank != 2 || t->shape[0] != rows || t->shape[1] != cols || (cols > 1 && t->stride[1] != 1))
+      return fail(LUX3D_ERR_SHAPE, "%s: tables must be %s = [%lld, %lld] with unit inner stride", fn, what,
+                  (long long)rows, (long long)cols);
+  }
+  if (cos->stride[0] != sin->stride[0] || cos->dtype != sin->dtype)
+    return fail(LUX3D_ERR_LAYOUT, "%s: cos and sin must share layout and dtype", fn);
+  sN = cos->stride[0];
+  return LUX3D_OK;
+}
+// Both tables 16-byte aligned with 16-byte aligned rows.
+bool tables_aligned(const lux3d_tensor_t *cos, const lux3d_tensor_t *sin, int64_t sN) {
+  return aligned16(cos->data) && aligned16(sin->data) && (sN * elem_bytes(cos->dtype)) % 16 == 0;
+}
+}  // namespace
+
+int lux3d_sdpa_l2norm_rope3d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_gamma, const lux3d_tensor_t *cos,
+                             const lux3d_tensor_t *sin, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                             const lux3d_tensor_t *out, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa_l2norm_rope3d";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  if (!q_gamma) return fail(LUX3D_ERR_NULL, "%s: `q_gamma` is NULL", fn);
+  const void *gp;
+  int gdt;
+  if ((r = param_vec(q_gamma, p.H * p.D, fn, "q_gamma", gp, gdt))) return r;
+  if (p.D % 2) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld must be even to rotate (re, im) pairs", fn, (long long)p.D);
+  int64_t sN;
+  if ((r = rot_tables(cos, sin, p.Lq, p.D / 2, fn, "[L, D/2]", sN))) return r;
+  const bool fused = p.mfma && q->dtype != LUX3D_F32 && aligned16(gp) && tables_aligned(cos, sin, sN);
+  if (!fused) {
+    // the two launches on the [B, L, H, D] views, out holding the rotated q
+    const lux3d_tensor_t qt = swap_heads_tokens(q), ot = swap_heads_tokens(out);
+    if ((r = lux3d_qk_l2norm_rope3d(&qt, q_gamma, nullptr, nullptr, cos, sin, nullptr, 0.f, &ot, nullptr, stream)))
+      return r;
+    return lux3d_sdpa(out, k, v, scale, out, stream);
+  }
+  p.qpro = QP_L2_R2;
+  p.qw = gp; p.qw_dt = gdt;
+  p.tab_c = cos->data; p.tab_s = sin->data; p.tab_dt = cos->dtype; p.tab_sN = sN;
+  return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
+}
+
+int lux3d_sdpa_dinov3_rope(const lux3d_tensor_t *q, const lux3d_tensor_t *cos, const lux3d_tensor_t *sin,
+                           int64_t num_prefix, const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                           const lux3d_tensor_t *out, lux3d_stream_t stream) {
+  const char *fn = "lux3d_sdpa_dinov3_rope";
+  AttnParams p;
+  int r;
+  if ((r = attn_params(fn, q, k, v, scale, out, p))) return r;
+  if (p.D % 2) return fail(LUX3D_ERR_SHAPE, "%s: head dim %lld must be even (rotate_half)", fn, (long long)p.D);
+  if (num_prefix < 0 || num_prefix > p.Lq) return fail(LUX3D_ERR_VALUE, "%s: num_prefix out of range", fn);
+  int64_t sN;
+  if ((r = rot_tables(cos, sin, p.Lq - num_prefix, p.D, fn, "[S - num_prefix, D]", sN))) return r;
+  const bool fused = p.mfma && (q->dtype == LUX3D_F32 || q->dtype == LUX3D_BF16) && tables_aligned(cos, sin, sN);
+  if (!fused) {
+    // the two launches, out holding the rotated q
+    if ((r = lux3d_dinov3_rope(q, nullptr, cos, sin, num_prefix, out, nullptr, stream))) return r;
+    return lux3d_sdpa_heads_f32(out, k, v, scale, out, stream);
+  }
+  p.exact_p = true;
+  p.qpro = QP_R3;
+  p.tab_c = cos->data; p.tab_s = sin->data; p.tab_dt = cos->dtype; p.tab_sN = sN;
+  p.prefix = num_prefix;
   return hip_status(launch_attention(q->dtype, p, stream_of(stream)), fn);
 }
 

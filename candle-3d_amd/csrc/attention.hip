@@ -130,14 +130,14 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
 // Measured on MI355X (TFLOP/s, VGGT frame / global, D 64): LAZY + DOT +
 // PHASED 617 / 795 against 579 / 700 without; D 128 (TripoSG / TRELLIS.2
 // 16k) LAZY + DOT 718 / 877 against 679 / 827, PHASED by key tile no gain.
-// QLN: q arrives raw; its LayerNorm and 2D RoPE (the QK kernel's arithmetic
-// and lane mapping, bit for bit) are applied while the Q fragments are
-// loaded, so the normalised q never goes through HBM.
+// QP (QP_*): q arrives raw; its head norm and rotation (the head kernels'
+// arithmetic and lane mapping, bit for bit) are applied while the Q
+// fragments are loaded, so the normalised q never goes through HBM.
 // EXACTP: f32 probabilities as three bf16 terms (see the file header).
-template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool QLN = false,
+template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, int QP = QP_NONE,
           bool DMA = false, bool EXACTP = false>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
-  static_assert(!EXACTP || (std::is_same<T, BF16>::value && !DOT && !QLN), "exact probabilities: bf16, f32 sums");
+  static_assert(!EXACTP || (std::is_same<T, BF16>::value && !DOT), "exact probabilities: bf16, f32 sums");
   using M = Mma<T>;
   using op_t = typename M::op_t;
   constexpr int BQ = 4 * 32 * QT;
@@ -171,25 +171,27 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   for (int qt = 0; qt < QT; ++qt) {
     int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
     qr = qr < Lq ? qr : Lq - 1;
-    if constexpr (!QLN) {
+    if constexpr (QP == QP_NONE) {
 #pragma unroll
       for (int c = 0; c < D / 16; ++c)
         qf[qt][c] = *reinterpret_cast<const op_t *>(qbase + (qr * p.q_st + c * 16 + 8 * hh) * 2);
     }
   }
-  if constexpr (QLN) {
-    // LayerNorm + RoPE of the wavefront's query rows with the QK kernel's
-    // mapping (D / 8 lanes per row, 8 elements per lane, the same DPP sums
-    // and partner exchange), written as bf16 / f16 into the K / V staging
-    // area, which is not in use yet; then each lane reads its fragments.
-    static_assert(D == 64 || D == 128, "QLN head dims");
+  if constexpr (QP != QP_NONE) {
+    // Head norm + rotation of the wavefront's query rows with the head
+    // kernels' mapping (D / 8 lanes per row, 8 elements per lane, the same
+    // DPP sums and partner exchange), written as bf16 / f16 into the K / V
+    // staging area, which is not in use yet; then each lane reads its
+    // fragments.
+    static_assert(D == 64 || D == 128, "Q prologue head dims");
     constexpr int LPR = D / 8, RPP = 64 / LPR;  // lanes per row, rows per pass
     static_assert(4 * QT * 32 * D <= 4 * BKV * KROW, "Q staging fits the K / V buffers");
     uint16_t *qs = smem + wave * (QT * 32 * D);
     const int ch = lane % LPR;
     float w8[8], b8[8];
-    param8(p.qw, p.qw_dt, ch * 8, 1.f, w8);
-    param8(p.qb, p.qb_dt, ch * 8, 0.f, b8);
+    if constexpr (QP == QP_LN_R1 || QP == QP_RMS) param8(p.qw, p.qw_dt, ch * 8, 1.f, w8);
+    if constexpr (QP == QP_LN_R1) param8(p.qb, p.qb_dt, ch * 8, 0.f, b8);
+    if constexpr (QP == QP_L2_R2) param8(p.qw, p.qw_dt, hi * D + ch * 8, 1.f, w8);  // gamma of head hi
     // the passes unrolled: their row loads are all in flight together
     static_assert((QT * 32) % RPP == 0, "whole passes");
 #pragma unroll
@@ -199,20 +201,57 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       qr = qr < Lq ? qr : Lq - 1;
       float x[8];
       Chunk<T>::template load<false>(qbase + (qr * p.q_st + ch * 8) * 2, x);
-      const float mean = group_sum<LPR>(ln_chunk_sum(x)) * (1.0f / D);
-      const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
-      ln_chunk_affine(x, rstd, w8, b8);
-      float C8[8], S8[8], pv[8];
-      const int64_t toff = bi * p.tab_sB + qr * p.tab_sN + ch * 8;
-      param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
-      param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
+      if constexpr (QP == QP_LN_R1) {
+        const float mean = group_sum<LPR>(ln_chunk_sum(x)) * (1.0f / D);
+        const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
+        ln_chunk_affine(x, rstd, w8, b8);
+      } else if constexpr (QP == QP_RMS) {
+        head_rms_chunk<LPR, D>(x, w8, p.eps);
+      } else if constexpr (QP == QP_L2_R2) {
+        head_l2_chunk<LPR, D>(x, w8);
+      }
+      // out[j] = x[j] * C[j] + x[j ^ M] * S[j] (rotate1)
+      float y[8];
+      if constexpr (QP == QP_LN_R1) {
+        // Rope2d: partner j ^ D/4, C / S the cos_full / sin_alt_full rows
+        float C8[8], S8[8], pv[8];
+        const int64_t toff = bi * p.tab_sB + qr * p.tab_sN + ch * 8;
+        param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
+        param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 32>(x[k]);  // element j ^ D/4
+        for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 32>(x[k]);  // element j ^ D/4
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = rotate1(x[k], C8[k], pv[k], S8[k]);
+      } else if constexpr (QP == QP_L2_R2) {
+        // TRELLIS.2 pairs (2a, 2a + 1) = (re, im): partner j ^ 1 in the lane,
+        // C = cos[n][a], S = -sin[n][a] for the re element, +sin for im
+        float c4[4], s4[4];
+        const int64_t toff = qr * p.tab_sN + ch * 4;
+        param4(p.tab_c, p.tab_dt, toff, 1.f, c4);
+        param4(p.tab_s, p.tab_dt, toff, 0.f, s4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = rotate1(x[k], c4[k >> 1], x[k ^ 1], (k & 1) ? s4[k >> 1] : -s4[k >> 1]);
+      } else if constexpr (QP == QP_R3) {
+        // DINOv3 rotate_half: partner j ^ D/2, S = -sin for j < D/2; tokens
+        // before the prefix pass through (their table row is clamped to 0
+        // and the rotation discarded, so no load depends on a branch)
+        float C8[8], S8[8], pv[8];
+        const bool rot = qr >= p.prefix;
+        const int64_t toff = (rot ? qr - p.prefix : 0) * p.tab_sN + ch * 8;
+        param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
+        param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 16>(x[k]);  // element j ^ D/2
+        const bool lo = ch * 8 < D / 2;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = rot ? rotate1(x[k], C8[k], pv[k], lo ? -S8[k] : S8[k]) : x[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = x[k];
+      }
       u32x4_t pk;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pk[e] = M::pack(rotate1(x[2 * e], C8[2 * e], pv[2 * e], S8[2 * e]),
-                        rotate1(x[2 * e + 1], C8[2 * e + 1], pv[2 * e + 1], S8[2 * e + 1]));
+      for (int e = 0; e < 4; ++e) pk[e] = M::pack(y[2 * e], y[2 * e + 1]);
       *reinterpret_cast<u32x4_t *>(qs + row * D + ch * 8) = pk;
     }
     lds_barrier();
@@ -606,7 +645,9 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 // of BKV keys are loaded as f32 (keys past Lk clamped to Lk - 1, their scores
 // masked), split in registers and stored as three bf16 planes each, [key][dim]
 // rows padded by 16 bytes, double-buffered.
-template <int D, int BKV, int MINW>
+// R3: DINOv3's rotate_half rotation of q (QP_R3) applied in the Q load with
+// the head kernel's per-element arithmetic (rotate1), bit for bit.
+template <int D, int BKV, int MINW, bool R3 = false>
 __global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   using op_t = bf16x8_t;
   using M = Mma<BF16>;
@@ -635,15 +676,35 @@ __global__ __launch_bounds__(256, MINW) void attn_f32x3_kernel(AttnParams p, int
     int64_t qr = qb * BQ + wave * 32 + l32;
     qr = qr < Lq ? qr : Lq - 1;
     const float *qrow = qbase + qr * p.q_st;
+    float xq[D / 16][8];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) Chunk<F32>::load<false>(qrow + c * 16 + 8 * hh, xq[c]);
+    if constexpr (R3) {
+      // element j = 16 c + 8 hh + e; its partner j ^ D/2 is element e of the
+      // lane's own chunk c ^ D/32; S = -sin for j < D/2. Tokens before the
+      // prefix pass through (table row clamped to 0, rotation discarded).
+      const bool rot = qr >= p.prefix;
+      const int64_t trow = (rot ? qr - p.prefix : 0) * p.tab_sN;
+      float yq[D / 16][8];
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        float C8[8], S8[8];
+        param8(p.tab_c, p.tab_dt, trow + c * 16 + 8 * hh, 1.f, C8);
+        param8(p.tab_s, p.tab_dt, trow + c * 16 + 8 * hh, 0.f, S8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          yq[c][e] = rot ? rotate1(xq[c][e], C8[e], xq[c ^ (D / 32)][e], c < D / 32 ? -S8[e] : S8[e]) : xq[c][e];
+      }
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xq[c][e] = yq[c][e];
+    }
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      const float4 a = *reinterpret_cast<const float4 *>(qrow + c * 16 + 8 * hh);
-      const float4 b = *reinterpret_cast<const float4 *>(qrow + c * 16 + 8 * hh + 4);
       u32x4_t x1, x2, x3;
-      split3_into(a.x, a.y, x1, x2, x3, 0);
-      split3_into(a.z, a.w, x1, x2, x3, 1);
-      split3_into(b.x, b.y, x1, x2, x3, 2);
-      split3_into(b.z, b.w, x1, x2, x3, 3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split3_into(xq[c][2 * e], xq[c][2 * e + 1], x1, x2, x3, e);
       q1[c] = __builtin_bit_cast(op_t, x1);
       q2[c] = __builtin_bit_cast(op_t, x2);
       q3[c] = __builtin_bit_cast(op_t, x3);
@@ -914,15 +975,34 @@ hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  if constexpr (EXACTP)
-    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, false, DMA, true>),
-                       dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
-  else if (p.qln)
-    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, true, DMA>), dim3((unsigned)nwg),
-                       dim3(256), 0, s, p, nqb, nwg);
-  else
-    hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, false, DMA>), dim3((unsigned)nwg),
-                       dim3(256), 0, s, p, nqb, nwg);
+  const dim3 grid((unsigned)nwg), block(256);
+  if constexpr (EXACTP) {
+    // exact_sdpa_heads: q as it is, or DINOv3's rotation in the Q load
+    if (p.qpro == QP_R3)
+      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_R3, DMA, true>), grid, block,
+                         0, s, p, nqb, nwg);
+    else
+      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_NONE, DMA, true>), grid,
+                         block, 0, s, p, nqb, nwg);
+  } else {
+    switch (p.qpro) {
+      case QP_LN_R1:
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_LN_R1, DMA>), grid, block, 0,
+                           s, p, nqb, nwg);
+        break;
+      case QP_RMS:
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_RMS, DMA>), grid, block, 0, s,
+                           p, nqb, nwg);
+        break;
+      case QP_L2_R2:
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_L2_R2, DMA>), grid, block, 0,
+                           s, p, nqb, nwg);
+        break;
+      default:
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_NONE, DMA>), grid, block, 0,
+                           s, p, nqb, nwg);
+    }
+  }
   return hipGetLastError();
 }
 
@@ -952,7 +1032,10 @@ hipError_t launch_f32x3(const AttnParams &p, hipStream_t s) {
   const int64_t nqb = (p.Lq + 127) / 128;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_f32x3_kernel<D, BKV, MINW>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  if (p.qpro == QP_R3)
+    hipLaunchKernelGGL((attn_f32x3_kernel<D, BKV, MINW, true>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
+  else
+    hipLaunchKernelGGL((attn_f32x3_kernel<D, BKV, MINW>), dim3((unsigned)nwg), dim3(256), 0, s, p, nqb, nwg);
   return hipGetLastError();
 }
 
@@ -986,8 +1069,14 @@ bool use_256_query(const AttnParams &p) {
 
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
-  if (p.qln && !(T::code != LUX3D_F32 && p.mfma && (p.D == 64 || p.D == 128))) return hipErrorInvalidValue;
-  if (p.qln && p.exact_p) return hipErrorInvalidValue;
+  // a Q prologue runs on the matrix-core kernels only: 2-byte types (or f32
+  // with DINOv3's rotation), D 64 / 128; exact_sdpa_heads takes QP_R3 only
+  if (p.qpro != QP_NONE) {
+    if (!p.mfma || (p.D != 64 && p.D != 128) || p.qpro < QP_LN_R1 || p.qpro > QP_R3) return hipErrorInvalidValue;
+    if (T::code == LUX3D_F32 && p.qpro != QP_R3) return hipErrorInvalidValue;
+    if ((p.qpro == QP_R3) != p.exact_p) return hipErrorInvalidValue;
+    if (p.qpro == QP_R3 && T::code == LUX3D_F16) return hipErrorInvalidValue;
+  }
   if (p.out_f32 && !p.exact_p && T::code != LUX3D_F32) return hipErrorInvalidValue;
   if (p.exact_p && T::code != LUX3D_F32) {
     // f32 probabilities: the bf16 matrix-core kernel with three-term P, else

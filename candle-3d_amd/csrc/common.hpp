@@ -479,6 +479,29 @@ __device__ __forceinline__ float ln_rstd(float sq_total, float inv_d, float eps)
 __device__ __forceinline__ float l2_rnorm(float s) {
   return __builtin_isinf(s) ? 1e-30f : rsqrt_f32(fmaxf(s, 1e-24f));
 }
+// Per-head RMSNorm and L2 norm of a head row held as 8-element chunks by
+// LPR lanes, shared by the head kernels and the attention kernel's Q load so
+// that the two agree bit for bit:
+//   rms: x = (x * rsqrt(sum(x^2) / D + eps)) * w
+//   l2:  x = ((x / clamp(||x||, 1e-12, 1e30)) * g) * sqrt(D)
+template <int LPR, int D>
+__device__ __forceinline__ void head_rms_chunk(float (&x)[8], const float (&w)[8], float eps) {
+  float s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
+  const float rr = rsqrt_f32(group_sum<LPR>(s2) * (1.0f / D) + eps);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = (x[k] * rr) * w[k];
+}
+template <int LPR, int D> __device__ __forceinline__ void head_l2_chunk(float (&x)[8], const float (&g)[8]) {
+  float s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
+  const float rr = l2_rnorm(group_sum<LPR>(s2));
+  const float scale = sqrtf((float)D);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = ((x[k] * rr) * g[k]) * scale;
+}
 
 // Workgroup barrier that orders LDS only: the fences are scoped to the
 // local (LDS) address space, so the wave waits for its own LDS accesses

@@ -151,17 +151,34 @@ struct AttnParams {
   // exact_p: f32 probabilities and sums whatever the input type (the
   // reference's exact_sdpa_heads); out_f32: out is f32 (exact_p or f32 inputs)
   bool exact_p = false, out_f32 = false;
-  // q LayerNorm + 2D RoPE applied in the Q load (matrix-core path): q is the
-  // raw head view; qw / qb the LayerNorm affine (D elements); tables the
-  // Rope2d cos_full / sin_alt_full, element (b, n, j) at b*tab_sB + n*tab_sN + j.
-  bool qln = false;
+  // Head norm / rotation of q applied in the Q load (matrix-core paths): q is
+  // the raw head view, qpro one of QP_*:
+  //   QP_LN_R1 LayerNorm (qw, qb: [D]) + Rope2d tables cos_full / sin_alt_full,
+  //            element (b, n, j) at b*tab_sB + n*tab_sN + j
+  //   QP_RMS   RMSNorm, weight qw [D]
+  //   QP_L2_R2 L2 norm with gamma qw [H, D] + TRELLIS.2 pair rotation, tables
+  //            [L, D/2], pair a of token n at n*tab_sN + a
+  //   QP_R3    DINOv3 rotate_half rotation, tables [L - prefix, D], row
+  //            n - prefix at (n - prefix)*tab_sN; tokens n < prefix unchanged
+  int qpro = 0;
   const void *qw = nullptr, *qb = nullptr;
   int qw_dt = -1, qb_dt = -1;
   float eps = 0.f;
   const void *tab_c = nullptr, *tab_s = nullptr;
   int tab_dt = -1;
   int64_t tab_sB = 0, tab_sN = 0;
+  int64_t prefix = 0;
+  // Key split (nsplit > 1): each (batch, head, query block) runs as nsplit
+  // workgroups over consecutive ranges of split_blocks key blocks; each
+  // writes its unnormalised partial O and (m, l) to ws_part and the last to
+  // arrive (counter ws_cnt[tile], zero on entry and left zero) merges the
+  // nsplit partials in split order and writes out.
+  int nsplit = 1;
+  int64_t split_blocks = 0;
+  float *ws_part = nullptr;
+  uint32_t *ws_cnt = nullptr;
 };
+enum { QP_NONE = 0, QP_LN_R1 = 1, QP_RMS = 2, QP_L2_R2 = 3, QP_R3 = 4 };
 hipError_t launch_attention(int dt, const AttnParams &p, hipStream_t s);
 
 // TRELLIS.2 sparse voxel ops.

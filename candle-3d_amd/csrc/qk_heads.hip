@@ -344,23 +344,12 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
         const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
         ln_chunk_affine(x, rstd, w[q], bias[q]);
       } else if constexpr (NORM == HN_RMS) {
-        float s2 = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
-        const float rr = rsqrt_f32(group_sum<LPR>(s2) * (1.0f / D) + p.eps);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = (x[k] * rr) * w[q][k];
+        head_rms_chunk<LPR, D>(x, w[q], p.eps);
       } else if constexpr (NORM == HN_L2) {
-        float s2 = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s2 += x[k] * x[k];
-        const float rr = l2_rnorm(group_sum<LPR>(s2));
-        const float scale = sqrtf((float)D);
         float g[8];
         if constexpr (EARLY) pdecode(qg[q][r], io.p0_dt, 1.f, g);
         else head_param<T, D>(io.p0, io.p0_dt, (int64_t)hh[r] * D, lane, 1.f, g);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = ((x[k] * rr) * g[k]) * scale;
+        head_l2_chunk<LPR, D>(x, g);
       }
       if constexpr (ROT != HR_NONE) {
         bool rotate = true;

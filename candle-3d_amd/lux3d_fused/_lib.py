@@ -72,6 +72,9 @@ SIGNATURES = {
     "lux3d_sdpa": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_heads_f32": [TP, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sdpa_layernorm_rope2d": [TP, TP, TP, ctypes.c_float, TP, TP, TP, TP, ctypes.c_float, TP, S],
+    "lux3d_sdpa_rms_norm_heads": [TP, TP, ctypes.c_float, TP, TP, ctypes.c_float, TP, S],
+    "lux3d_sdpa_l2norm_rope3d": [TP, TP, TP, TP, TP, TP, ctypes.c_float, TP, S],
+    "lux3d_sdpa_dinov3_rope": [TP, TP, TP, ctypes.c_int64, TP, TP, ctypes.c_float, TP, S],
     "lux3d_sparse_neighbors": [TP, TP, TP, TP, TP, S],
     "lux3d_sparse_neighbors_noalloc": [TP, TP, TP, S],
     "lux3d_sparse_conv3d": [TP, TP, TP, TP, TP, S],

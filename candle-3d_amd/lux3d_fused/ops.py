@@ -455,6 +455,44 @@ def sdpa_layernorm_rope2d(q_raw: torch.Tensor, q_norm, embeddings: "RopeEmbeddin
     return out
 
 
+def sdpa_rms_norm_heads(q_raw: torch.Tensor, q_w: torch.Tensor, eps: float, k: torch.Tensor, v: torch.Tensor,
+                       scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """exact_query_chunked_sdpa(rms_norm_heads(q_raw, q_w), k, v, scale)
+    (triposg_dit.rs:446-455) with q's per-head RMSNorm done in the attention
+    kernel's Q load; k already normalised."""
+    if out is None:
+        out = torch.empty(q_raw.shape, dtype=q_raw.dtype, device=q_raw.device)
+    _lib.call("lux3d_sdpa_rms_norm_heads", desc(q_raw), desc(q_w), float(eps), desc(k), desc(v), float(scale),
+              desc(out), _stream(q_raw))
+    return out
+
+
+def sdpa_l2norm_rope3d(q_raw: torch.Tensor, q_gamma: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                       k: torch.Tensor, v: torch.Tensor, scale: float,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Trellis2SelfAttention::attention (trellis2_blocks.rs:417-436) on
+    [B, H, L, D] views: exact_query_chunked_sdpa(rope(l2norm(q_raw)), k, v,
+    scale) with q's L2 norm (gamma [H, D]) and 3D RoPE (tables [L, D/2]) done
+    in the attention kernel's Q load; k already normalised and rotated."""
+    if out is None:
+        out = torch.empty(q_raw.shape, dtype=q_raw.dtype, device=q_raw.device)
+    _lib.call("lux3d_sdpa_l2norm_rope3d", desc(q_raw), desc(q_gamma), desc(cos), desc(sin), desc(k), desc(v),
+              float(scale), desc(out), _stream(q_raw))
+    return out
+
+
+def sdpa_dinov3_rope(q_raw: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_prefix: int, k: torch.Tensor,
+                     v: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """exact_sdpa_heads(apply_rotary_to_patches(q_raw), k, v, scale)
+    (trellis2_dino.rs:385-393) with q's rotate_half RoPE done in the
+    attention kernel's Q load; k already rotated."""
+    if out is None:
+        out = torch.empty(q_raw.shape, dtype=q_raw.dtype, device=q_raw.device)
+    _lib.call("lux3d_sdpa_dinov3_rope", desc(q_raw), desc(cos), desc(sin), int(num_prefix), desc(k), desc(v),
+              float(scale), desc(out), _stream(q_raw))
+    return out
+
+
 def exact_query_chunked_sdpa(q, k, v, scale: float, chunk_size: int = 0) -> torch.Tensor:
     """attention_math.rs:199-241. chunk_size only bounded the reference's
     scores buffer; this kernel keeps no such buffer, so it is ignored."""

@@ -522,6 +522,56 @@ int lux3d_sdpa_layernorm_rope2d(const lux3d_tensor_t *q, const lux3d_tensor_t *q
                                 const lux3d_tensor_t *v, float scale, const lux3d_tensor_t *out,
                                 lux3d_stream_t stream);
 
+/* lux3d_sdpa_rms_norm_heads: the TripoSG self-attention of
+ * triposg_dit.rs:446-455, exact_query_chunked_sdpa(rms_norm_heads(q, w), k,
+ * v, scale), with q's per-head RMSNorm (y = x / sqrt(mean(x^2) + eps) * w,
+ * RmsNormHeads::rms_norm_heads, triposg_dit.rs:509-522) applied inside the
+ * attention kernel's Q load. q is the raw [B, H, L, D] head view (any outer
+ * strides: the per-head third of cat([q, k, v]) passes as it is); q_w [D]
+ * any float dtype; k the already normalised keys (lux3d_rms_norm_heads);
+ * v, scale and out as lux3d_sdpa. The normalised q equals
+ * lux3d_rms_norm_heads' bit for bit, so the result equals that call
+ * followed by lux3d_sdpa. bf16 / f16, D = 64 / 128, 16-byte aligned rows
+ * and weight run fused; any other case runs exactly those two launches,
+ * with out as the intermediate q.                                             */
+int lux3d_sdpa_rms_norm_heads(const lux3d_tensor_t *q, const lux3d_tensor_t *q_w, float eps,
+                              const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                              const lux3d_tensor_t *out, lux3d_stream_t stream);
+
+/* lux3d_sdpa_l2norm_rope3d: the TRELLIS.2 self-attention of
+ * trellis2_blocks.rs:417-436 (Trellis2SelfAttention::attention),
+ * exact_query_chunked_sdpa(rope(l2norm(q)), k, v, scale), with q's L2 norm
+ * (y = x / clamp(||x||, 1e-12, 1e30) * gamma * sqrt(D), Trellis2QkRmsNorm,
+ * :306-319) and 3D RoPE pair rotation (Trellis2Rope3d::apply, :139-160)
+ * applied inside the attention kernel's Q load. q, k, v, out are
+ * [B, H, L, D] views (TRELLIS.2's [B, L, H, D] buffers pass as their
+ * permuted views); q_gamma [H, D]; cos, sin [L, D/2] (Trellis2Rope3d::cos_sin
+ * layout, any float dtype); k already normalised and rotated
+ * (lux3d_qk_l2norm_rope3d). The rotated q equals lux3d_qk_l2norm_rope3d's bit
+ * for bit, so the result equals that call followed by lux3d_sdpa. bf16 / f16,
+ * D = 64 / 128, 16-byte aligned rows, gamma and table rows run fused; any
+ * other case runs exactly those two launches, with out as the intermediate q.  */
+int lux3d_sdpa_l2norm_rope3d(const lux3d_tensor_t *q, const lux3d_tensor_t *q_gamma,
+                             const lux3d_tensor_t *cos, const lux3d_tensor_t *sin,
+                             const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                             const lux3d_tensor_t *out, lux3d_stream_t stream);
+
+/* lux3d_sdpa_dinov3_rope: the DINOv3 attention of trellis2_dino.rs:385-393,
+ * exact_sdpa_heads(apply_rotary_to_patches(q), k, v, scale), with q's
+ * rotate_half RoPE (tokens s >= num_prefix use row s - num_prefix of cos / sin
+ * [S - num_prefix, D]; earlier tokens pass through; :406-445) applied inside
+ * the attention kernel's Q load. q, k, v, out [B, H, S, D] of one dtype (f32,
+ * the reference's, or bf16); k already rotated (lux3d_dinov3_rope); the
+ * attention is lux3d_sdpa_heads_f32's. The rotated q equals
+ * lux3d_dinov3_rope's bit for bit, so the result equals that call followed by
+ * lux3d_sdpa_heads_f32. f32 / bf16, D = 64 / 128, 16-byte aligned rows and
+ * table rows run fused; any other case runs exactly those two launches,
+ * with out as the intermediate q.                                             */
+int lux3d_sdpa_dinov3_rope(const lux3d_tensor_t *q, const lux3d_tensor_t *cos,
+                           const lux3d_tensor_t *sin, int64_t num_prefix,
+                           const lux3d_tensor_t *k, const lux3d_tensor_t *v, float scale,
+                           const lux3d_tensor_t *out, lux3d_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
