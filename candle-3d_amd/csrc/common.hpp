@@ -579,12 +579,18 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, int64_t bytes) 
 }
 // Each lane reads 16 (4) bytes at voff + soff of the buffer; the wavefront
 // writes them in lane order at LDS byte address lds. Inline assembly rather
-// than the compiler's buffer-load-to-LDS builtin: the compiler then does not
-// know the LDS is written and inserts no vmcnt waits of its own (the callers
-// wait explicitly), which kept the Q8_0 ring 2% faster. hipcc warns that m0 is
-// a reserved register in the clobber list; the kernels of this library make
-// no m0 use of their own (their assembly holds m0 only in these pairs), so
-// nothing live is overwritten.
+// than the compiler's buffer-load-to-LDS builtin: with the builtin the
+// compiler knows the LDS is written by a vector-memory load and, unable to
+// tell the two buffers of a ring apart, waits for every such load
+// (vmcnt(0)) right after issuing the next block's loads in the attention
+// loop and after each barrier of the Q8_0 ring, which serialises both
+// pipelines; here the callers place their waits themselves. hipcc warns that
+// m0 is a reserved register in the clobber list: the statement overwrites
+// m0 without the compiler knowing its old value, which is safe only while
+// the compiler keeps nothing of its own in m0 in these kernels. The build
+// verifies that for every translation unit that calls these (check_m0.py
+// over its device assembly: no m0 use outside these pairs), and fails
+// otherwise.
 __device__ __forceinline__ void lds_load16(i32x4_t rs, uint32_t voff, uint32_t soff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rs), "s"(soff)
                : "memory", "m0");

@@ -656,6 +656,122 @@ def cfg1_sdpa_frame_qln(dev) -> Workload:
     return wl
 
 
+def _sdpa_qprologue(dev, name, cfg, kind, b, n, h, d, dt, fused=True, reps=50) -> Workload:
+    """Attention whose q takes its model's head norm / rotation first:
+    kind "rms" (TripoSG, triposg_dit.rs:446-455: q, k, v the per-head thirds
+    of cat([q, k, v]) as [B, L, H, 3D]), "l2r2" (TRELLIS.2,
+    trellis2_blocks.rs:417-436: L2 norm + 3D RoPE, [B, L, 3, H, D] buffer),
+    "r3" (DINOv3, trellis2_dino.rs:385-393: rotate_half RoPE past 5 prefix
+    tokens, exact_sdpa_heads). fused: the lux3d_sdpa_* entry that applies it
+    in the Q load; else the head op into a scratch q, then the attention
+    (the two launches it replaces).
+    k is taken as already normalised / rotated in both."""
+    from . import _lib
+    esz = torch.empty((), dtype=dt).element_size()
+    sd = synth.config_seed(cfg) + 740 + len(kind)
+    if kind == "rms":
+        buf0 = _normal(sd, (b, n, h, 3 * d), dev, dt)
+        views = lambda x: (x[..., :d].transpose(1, 2), x[..., d:2 * d].transpose(1, 2),  # noqa: E731
+                           x[..., 2 * d:].transpose(1, 2))
+    elif kind == "l2r2":
+        buf0 = _normal(sd, (b, n, 3, h, d), dev, dt)
+        views = lambda x: (x[:, :, 0].transpose(1, 2), x[:, :, 1].transpose(1, 2),  # noqa: E731
+                           x[:, :, 2].transpose(1, 2))
+    else:
+        buf0 = _normal(sd, (3, b, n, h, d), dev, dt)
+        views = lambda x: (x[0].transpose(1, 2), x[1].transpose(1, 2), x[2].transpose(1, 2))  # noqa: E731
+    n_sets = max(2, _n_sets(buf0.numel() * esz + b * h * n * d * esz))
+    bufs = [_fill_like(buf0, j) for j in range(n_sets)]
+    outs = [torch.empty((b, h, n, d), dtype=dt, device=dev) for _ in range(n_sets)]
+    qtmp = [torch.empty((b, n, h, d) if kind == "l2r2" else (b, h, n, d), dtype=dt, device=dev)
+            for _ in range(n_sets)] if not fused else []
+    keep = [bufs, outs, qtmp]
+    scale = 1.0 / float(d) ** 0.5
+    D = ops.desc
+    if kind == "rms":
+        w = _normal(sd + 1, (d,), dev, torch.float32, 1.0, 0.1)
+        keep.append(w)
+        params = (D(w),)
+    elif kind == "l2r2":
+        g = torch.Generator(device="cpu").manual_seed(sd)
+        coords = torch.randint(0, 64, (n, 3), generator=g, dtype=torch.int32).to(dev)
+        cos, sin = ops.Trellis2Rope3d(d).cos_sin(coords)
+        gamma = _normal(sd + 2, (h, d), dev, torch.float32, 1.0, 0.1)
+        keep += [cos, sin, gamma]
+        params = (D(gamma), D(cos), D(sin))
+    else:
+        ang = _normal(sd + 3, (n - 5, d), dev, torch.float32, 0.0, 2.0)
+        cos, sin = torch.cos(ang), torch.sin(ang)
+        keep += [cos, sin]
+        params = (D(cos), D(sin))
+    descs = []
+    for j in range(n_sets):
+        q, k, v = views(bufs[j])
+        descs.append((D(q), D(k), D(v), D(outs[j]), D(q.transpose(1, 2)) if kind == "l2r2" else None,
+                      D(qtmp[j]) if qtmp else None,
+                      D(qtmp[j].transpose(1, 2)) if qtmp and kind == "l2r2" else (D(qtmp[j]) if qtmp else None)))
+
+    def launch(i):
+        dq, dk, dv, do, dq_blhd, dtmp, dtmp_bhld = descs[i % n_sets]
+        if kind == "rms":
+            if fused:
+                _lib.call("lux3d_sdpa_rms_norm_heads", dq, params[0], 1e-6, dk, dv, scale, do, _cur())
+            else:
+                _lib.call("lux3d_rms_norm_heads", dq, params[0], None, None, 1e-6, dtmp, None, _cur())
+                _lib.call("lux3d_sdpa", dtmp_bhld, dk, dv, scale, do, _cur())
+        elif kind == "l2r2":
+            if fused:
+                _lib.call("lux3d_sdpa_l2norm_rope3d", dq, params[0], params[1], params[2], dk, dv, scale, do, _cur())
+            else:
+                _lib.call("lux3d_qk_l2norm_rope3d", dq_blhd, params[0], None, None, params[1], params[2], None, 0.0,
+                          dtmp, None, _cur())
+                _lib.call("lux3d_sdpa", dtmp_bhld, dk, dv, scale, do, _cur())
+        else:
+            if fused:
+                _lib.call("lux3d_sdpa_dinov3_rope", dq, params[0], params[1], 5, dk, dv, scale, do, _cur())
+            else:
+                _lib.call("lux3d_dinov3_rope", dq, None, params[0], params[1], 5, dtmp, None, _cur())
+                _lib.call("lux3d_sdpa_heads_f32", dtmp_bhld, dk, dv, scale, do, _cur())
+    f32 = dt == torch.float32
+    what = {"rms": "RMSNorm", "l2r2": "L2 norm + 3D RoPE", "r3": "rotate_half RoPE"}[kind]
+    how = "in the Q load" if fused else "head op, then attention (two launches)"
+    wl = Workload(name, cfg, f"attn_{'f32x3' if f32 else 'mfma'}_kernel<{d}, q prologue>",
+                  "f32 (three-term splits)" if f32 else "bf16 -> f32 acc", 4 * b * h * n * d * esz,
+                  f"q, k, v [{b},{h},{n},{d}]: q {what} {how}", launch, n_sets,
+                  flops=4 * b * h * n * n * d, reps=reps, peak_tflops=2500.0 / 6 if f32 else 0.0)
+    wl._keep = (keep, descs, params)
+    return wl
+
+
+def cfg2_sdpa_rms(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_rms_fused", 2, "rms", 2, 2048, 16, 128, torch.bfloat16)
+
+
+def cfg2_sdpa_rms_two(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_rms_two", 2, "rms", 2, 2048, 16, 128, torch.bfloat16, fused=False)
+
+
+def cfg3_sdpa_l2r2(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_l2r2_fused", 3, "l2r2", 1, 40000, 12, 128, torch.bfloat16, reps=5)
+
+
+def cfg3_sdpa_l2r2_two(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_l2r2_two", 3, "l2r2", 1, 40000, 12, 128, torch.bfloat16, fused=False, reps=5)
+
+
+def cfg4_sdpa_dinov3_rope(dev) -> Workload:
+    # the reference's DINOv3 runs f32 (trellis2_dino.rs:374-377, linear_f32)
+    return _sdpa_qprologue(dev, "sdpa_dinov3_rope_fused", 4, "r3", 1, 1029, 16, 64, torch.float32)
+
+
+def cfg4_sdpa_dinov3_rope_two(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_dinov3_rope_two", 4, "r3", 1, 1029, 16, 64, torch.float32, fused=False)
+
+
+def cfg4_sdpa_dinov3_rope_bf16(dev) -> Workload:
+    return _sdpa_qprologue(dev, "sdpa_dinov3_rope_bf16_fused", 4, "r3", 1, 1029, 16, 64, torch.bfloat16)
+
+
 def cfg1_sdpa_frame(dev) -> Workload:
     return _sdpa(dev, "sdpa_frame", 1, 8, 1374, 16, 64, "VGGT frame attention")
 
@@ -843,6 +959,13 @@ EXTRAS: List[Callable] = [
     cfg3_sdpa,
     cfg4_sdpa_dinov3,
     cfg4_sdpa_dinov3_f32,
+    cfg2_sdpa_rms,
+    cfg2_sdpa_rms_two,
+    cfg3_sdpa_l2r2,
+    cfg3_sdpa_l2r2_two,
+    cfg4_sdpa_dinov3_rope,
+    cfg4_sdpa_dinov3_rope_two,
+    cfg4_sdpa_dinov3_rope_bf16,
     cfg3_sparse_conv_c1024,
     cfg3_sparse_conv_c256,
     cfg3_sparse_conv_c256_output_stationary,
