@@ -135,17 +135,19 @@ __device__ __forceinline__ int64_t xcd_logical_id(int64_t pid, int64_t n) {
 // fragments are loaded, so the normalised q never goes through HBM.
 // EXACTP: f32 probabilities as three bf16 terms (see the file header).
 template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, int QP = QP_NONE,
-          bool DMA = false, bool EXACTP = false>
+          bool DMA = false, bool EXACTP = false, int KS = 1>
 __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int64_t nqb, int64_t nwg) {
   static_assert(!EXACTP || (std::is_same<T, BF16>::value && !DOT), "exact probabilities: bf16, f32 sums");
+  static_assert(KS == 1 || (!PHASED && (BKV / 32) % KS == 0), "key groups: whole 32-key tiles per wavefront");
   using M = Mma<T>;
   using op_t = typename M::op_t;
-  constexpr int BQ = 4 * 32 * QT;
+  constexpr int QG = 4 / KS;               // query groups per workgroup (KS wavefronts each)
+  constexpr int BQ = QG * 32 * QT;
   // 2-byte elements per K / V row in LDS: padded by 16 bytes, or (DMA)
   // unpadded with 16-byte chunk c of row r in slot c ^ ((r & 7) * D / 64)
   constexpr int KROW = DMA ? D : D + 8;
   constexpr int KCH = BKV * D / 8 / 256;   // 16-byte K (and V) chunks per thread per block
-  constexpr int NKT = BKV / 32;            // 32-key tiles per block
+  constexpr int NKT = BKV / 32 / KS;       // 32-key tiles of a block per wavefront
   constexpr int NDT = D / 32;              // 32-dim output tiles
   static_assert(KCH >= 1 && BKV % 32 == 0 && D % 32 == 0, "tile shape");
   __shared__ __align__(16) uint16_t smem[4 * BKV * KROW];
@@ -163,13 +165,16 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
+  // KS > 1: the KS wavefronts of query group qg hold the same queries and
+  // take key tiles kt0 .. kt0 + NKT - 1 of every block (key group kg)
+  const int qg = wave / KS, kg = wave % KS, kt0 = kg * NKT;
   const int64_t Lq = p.Lq, Lk = p.Lk;
 
   // Q as the B operand: lane holds Q[query l32][c * 16 + 8 * hh + e].
   op_t qf[QT][D / 16];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
+    int64_t qr = qb * BQ + (qg * QT + qt) * 32 + l32;
     qr = qr < Lq ? qr : Lq - 1;
     if constexpr (QP == QP_NONE) {
 #pragma unroll
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
 #pragma unroll
     for (int it = 0; it < QT * 32 / RPP; ++it) {
       const int row = lane / LPR + it * RPP;
-      int64_t qr = qb * BQ + wave * QT * 32 + row;
+      int64_t qr = qb * BQ + qg * QT * 32 + row;
       qr = qr < Lq ? qr : Lq - 1;
       float x[8];
       Chunk<T>::template load<false>(qbase + (qr * p.q_st + ch * 8) * 2, x);
@@ -386,7 +391,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) {
-            const int krow = kt * 32 + l32, kch = DMA ? ((2 * c + hh) ^ ((krow & 7) * SWZ)) : 2 * c + hh;
+            const int krow = (kt0 + kt) * 32 + l32, kch = DMA ? ((2 * c + hh) ^ ((krow & 7) * SWZ)) : 2 * c + hh;
             const op_t a = *reinterpret_cast<const op_t *>(&Ks[buf][krow * KROW + kch * 8]);
             s[qt][kt] = M::run(a, qf[qt][c], s[qt][kt]);
           }
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
-          const int krow = kt * 32 + l32, kch = DMA ? ((2 * c + hh) ^ ((krow & 7) * SWZ)) : 2 * c + hh;
+          const int krow = (kt0 + kt) * 32 + l32, kch = DMA ? ((2 * c + hh) ^ ((krow & 7) * SWZ)) : 2 * c + hh;
           const op_t a = *reinterpret_cast<const op_t *>(&Ks[buf][krow * KROW + kch * 8]);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) s[qt][kt] = M::run(a, qf[qt][c], s[qt][kt]);
@@ -407,7 +412,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          if (kt * 32 + 8 * (i >> 2) + (i & 3) >= lim) {
+          if ((kt0 + kt) * 32 + 8 * (i >> 2) + (i & 3) >= lim) {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) s[qt][kt][i] = -INFINITY;
           }
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
     auto vfrag = [&](int dt, int kt, int jj) {
       const int g16 = lane & 15;
-      const int vrow = kt * 32 + 16 * jj + 4 * hh + (g16 >> 2);
+      const int vrow = (kt0 + kt) * 32 + 16 * jj + 4 * hh + (g16 >> 2);
       const int vcol = dt * 32 + 16 * ((lane >> 4) & 1) + 4 * (g16 & 3);  // rows vrow and vrow + 8 swizzle alike
       const int vch = DMA ? ((vcol >> 3) ^ ((vrow & 7) * SWZ)) : vcol >> 3;
       const uint16_t *vr = &Vs[buf][vrow * KROW + vch * 8 + (vcol & 7)];
@@ -601,27 +606,82 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
   for (int64_t j = 0; j < nfull; ++j) step(j, std::false_type{});
   if (tail) step(nkv - 1, std::true_type{});
 
+  if constexpr (KS > 1) {
+    // The KS partial results of a query group -- O (unnormalised), the
+    // reference maximum m (log2 units) and the row-sum part l of each lane --
+    // go through LDS (the K / V buffers are free after the last block's
+    // barrier) and are merged in key-group order: M = max m_s,
+    // l = sum l_s 2^(m_s - M), O = sum O_s 2^(m_s - M). Wavefront kg of the
+    // group then owns the output dim tiles dt with dt % KS == kg. Lane-minor
+    // layout: each LDS access of a wavefront is 64 consecutive floats.
+    constexpr int PW = QT * (NDT * 16 + 2) * 64;  // floats per wavefront
+    static_assert(4 * PW * 4 <= (int)sizeof(smem), "partials fit the K / V buffers");
+    float *part = reinterpret_cast<float *>(smem);
+    float *mine = part + wave * PW;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mine[((qt * NDT + dt) * 16 + i) * 64 + lane] = o[qt][dt][i];
+      mine[(QT * NDT * 16 + 2 * qt) * 64 + lane] = m[qt];
+      mine[(QT * NDT * 16 + 2 * qt + 1) * 64 + lane] = l[qt];
+    }
+    lds_barrier();
+    const float *grp = part + qg * KS * PW;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float ms[KS], a[KS], mm = -INFINITY;
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2) {
+        ms[s2] = grp[s2 * PW + (QT * NDT * 16 + 2 * qt) * 64 + lane];
+        mm = fmaxf(mm, ms[s2]);
+      }
+      float lsum = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2) {
+        a[s2] = __builtin_amdgcn_exp2f(ms[s2] - mm);
+        lsum = lsum + grp[s2 * PW + (QT * NDT * 16 + 2 * qt + 1) * 64 + lane] * a[s2];
+      }
+      l[qt] = lsum;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        if (dt % KS != kg) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float acc = 0.f;
+#pragma unroll
+          for (int s2 = 0; s2 < KS; ++s2) acc = acc + grp[s2 * PW + ((qt * NDT + dt) * 16 + i) * 64 + lane] * a[s2];
+          o[qt][dt][i] = acc;
+        }
+      }
+    }
+  }
+
   // out[query][dim]: lane holds dims dt * 32 + 8 * g + 4 * hh + {0..3}, g = 0..3
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const int64_t qr = qb * BQ + (wave * QT + qt) * 32 + l32;
+    const int64_t qr = qb * BQ + (qg * QT + qt) * 32 + l32;
     const float inv = 1.f / half_swap_sum(l[qt]);
     if (qr >= Lq) continue;
     char *orow = obase + qr * p.o_st * ob;
     if (EXACTP && p.out_f32) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt) {
+        if (KS > 1 && dt % KS != kg) continue;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           *reinterpret_cast<float4 *>(orow + (dt * 32 + 8 * g + 4 * hh) * 4) =
               make_float4(o[qt][dt][4 * g] * inv, o[qt][dt][4 * g + 1] * inv, o[qt][dt][4 * g + 2] * inv,
                           o[qt][dt][4 * g + 3] * inv);
+      }
       continue;
     }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (KS > 1 && dt % KS != kg) continue;
         const uint2 w = make_uint2(M::pack(o[qt][dt][4 * g] * inv, o[qt][dt][4 * g + 1] * inv),
                                    M::pack(o[qt][dt][4 * g + 2] * inv, o[qt][dt][4 * g + 3] * inv));
         *reinterpret_cast<uint2 *>(orow + (dt * 32 + 8 * g + 4 * hh) * 2) = w;
@@ -969,9 +1029,9 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(AttnParams p, int64_t
 }
 
 template <typename T, int D, int QT, int BKV, int MINW, bool LAZY, bool DOT, bool PHASED, bool DMA,
-          bool EXACTP = false>
+          bool EXACTP = false, int KS = 1>
 hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
-  constexpr int BQ = 4 * 32 * QT;
+  constexpr int BQ = 4 / KS * 32 * QT;
   const int64_t nqb = (p.Lq + BQ - 1) / BQ;
   const int64_t nwg = p.B * p.H * nqb;
   if (nwg > INT32_MAX) return hipErrorInvalidValue;
@@ -979,27 +1039,27 @@ hipError_t launch_mfma(const AttnParams &p, hipStream_t s) {
   if constexpr (EXACTP) {
     // exact_sdpa_heads: q as it is, or DINOv3's rotation in the Q load
     if (p.qpro == QP_R3)
-      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_R3, DMA, true>), grid, block,
+      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_R3, DMA, true, KS>), grid, block,
                          0, s, p, nqb, nwg);
     else
-      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_NONE, DMA, true>), grid,
+      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, false, PHASED, QP_NONE, DMA, true, KS>), grid,
                          block, 0, s, p, nqb, nwg);
   } else {
     switch (p.qpro) {
       case QP_LN_R1:
-        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_LN_R1, DMA>), grid, block, 0,
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_LN_R1, DMA, false, KS>), grid, block, 0,
                            s, p, nqb, nwg);
         break;
       case QP_RMS:
-        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_RMS, DMA>), grid, block, 0, s,
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_RMS, DMA, false, KS>), grid, block, 0, s,
                            p, nqb, nwg);
         break;
       case QP_L2_R2:
-        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_L2_R2, DMA>), grid, block, 0,
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_L2_R2, DMA, false, KS>), grid, block, 0,
                            s, p, nqb, nwg);
         break;
       default:
-        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_NONE, DMA>), grid, block, 0,
+        hipLaunchKernelGGL((attn_mfma_kernel<T, D, QT, BKV, MINW, LAZY, DOT, PHASED, QP_NONE, DMA, false, KS>), grid, block, 0,
                            s, p, nqb, nwg);
     }
   }
@@ -1067,6 +1127,31 @@ bool use_256_query(const AttnParams &p) {
   return 100 * busiest_cu_time(n2, 2, t2) < 97 * busiest_cu_time(n1, 3, t1);
 }
 
+// Key groups per query tile (KS, D 64): with few 128-query tiles (DINOv3:
+// 16 heads x 9 tiles = 144 workgroups, one wavefront per SIMD on 144 of the
+// 256 CUs) the four wavefronts of a workgroup share 128 / KS queries and
+// split each key block KS ways, merging in LDS at the end: KS times the
+// workgroups, each wavefront with 1 / KS of the keys. These kernels are
+// VALU-bound (exact_sdpa_heads: about 370 VALU instructions per 64-key block
+// and wavefront against 32 MFMAs), so the busiest SIMD's share sets the
+// time; KS = 2 is taken while the doubled grid still fits three workgroups
+// per CU. Measured (exact_sdpa_heads bf16, D 64, us, KS = 1 / 2 / 4):
+// 16 heads x 1029 tokens 26.3 / 24.2 / 25.5, x 1024 22.6 / 17.3 / 16.4,
+// 8 x 1029 23.9 / 17.3 / 16.7, 2 x 16 x 1029 37.0 / 32.2 / 38.1, 4 x 4096
+// 78.3 / 55.0 / 50.5, 16 x 2048 45.7 / 43.2 / 50.9; KS = 4 (128-key blocks,
+// two workgroups per CU) gains little more where it gains and loses
+// elsewhere, so it is not chosen by default. Needs Lk >= the block (every
+// key group sees keys in block 0). LUX3D_ATTN_KS=1 / 2 / 4 forces a choice
+// (timing).
+int key_groups(const AttnParams &p) {
+  const int64_t tiles = p.B * p.H * ((p.Lq + 127) / 128);
+  int ks = 2 * tiles <= 3 * kCus ? 2 : 1;
+  if (const char *e = getenv("LUX3D_ATTN_KS")) ks = atoi(e);
+  if (ks == 4 && p.Lk >= 128) return 4;
+  if (ks == 2 && p.Lk >= 64) return 2;
+  return 1;
+}
+
 template <typename T>
 hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   // a Q prologue runs on the matrix-core kernels only: 2-byte types (or f32
@@ -1083,6 +1168,9 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
     // the generic kernel (f32 throughout)
     if constexpr (T::code == LUX3D_BF16) {
       if (p.mfma && p.D == 64) {
+        const int ks = key_groups(p);
+        if (ks == 4) return launch_mfma<T, 64, 1, 128, 2, true, false, false, false, true, 4>(p, s);
+        if (ks == 2) return launch_mfma<T, 64, 1, 64, 3, true, false, false, false, true, 2>(p, s);
         if (p.Lq <= kShortQ) return launch_mfma<T, 64, 1, 64, 3, true, false, false, false, true>(p, s);
         return launch_mfma<T, 64, 2, 64, 2, true, false, false, false, true>(p, s);
       }
@@ -1096,6 +1184,9 @@ hipError_t launch_t(const AttnParams &p, hipStream_t s) {
   if constexpr (T::code != LUX3D_F32) {
     if (p.mfma) {
       if (p.D == 64) {
+        const int ks = key_groups(p);
+        if (ks == 4) return launch_mfma<T, 64, 1, 128, 2, true, true, false, false, false, 4>(p, s);
+        if (ks == 2) return launch_mfma<T, 64, 1, 64, 3, true, true, false, false, false, 2>(p, s);
         if (!use_256_query(p))
           return launch_mfma<T, 64, 1, 64, 3, true, true, false, false>(p, s);
         return launch_mfma<T, 64, 2, 64, 2, true, true, true, false>(p, s);

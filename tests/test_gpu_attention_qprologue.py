@@ -246,3 +246,68 @@ def test_sdpa_dinov3_rope_against_oracle(dev, ops, orc, dt):
     plain = ops.exact_sdpa_heads(q, k, v, scale)
     torch.cuda.synchronize()
     assert torch.equal(fused[:, :, :prefix], plain[:, :, :prefix])
+
+
+# ---------------------------------------------------------------------------
+# Key groups: the wavefronts of a workgroup split each key block (D 64)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ks", [1, 2, 4])
+@pytest.mark.parametrize("b,lq,lk,h", [(1, 1029, 1029, 16), (2, 200, 700, 3), (1, 33, 128, 2)])
+def test_sdpa_key_groups_exact_heads(dev, ops, orc, monkeypatch, ks, b, lq, lk, h):
+    """exact_sdpa_heads (bf16 in, f32 out) with the keys of every block split
+    over 1, 2 or 4 wavefronts and merged in LDS: every output within the f32
+    bar of the oracle (|err| <= 1e-5 wabs + 2^-23 |want|), at the DINOv3
+    shape (partial last key block, a partial query tile) and cross shapes."""
+    monkeypatch.setenv("LUX3D_ATTN_KS", str(ks))
+    d = 64
+    _print_case(op="sdpa key groups exact", ks=ks, b=b, lq=lq, lk=lk, h=h)
+    g = torch.Generator(device="cpu").manual_seed(lq + lk + ks)
+    q = torch.randn((b, h, lq, d), generator=g).to(dev).to(torch.bfloat16)
+    k = (torch.randn((b, h, lk, d), generator=g) * 1.5).to(dev).to(torch.bfloat16)
+    v = torch.randn((b, h, lk, d), generator=g).to(dev).to(torch.bfloat16)
+    out = torch.empty((b, h, lq, d), dtype=torch.float32, device=dev)
+    ops.exact_sdpa_heads(q, k, v, 0.125, out=out)
+    torch.cuda.synchronize()
+    want, wabs = orc.sdpa(host(q, "bf16"), host(k, "bf16"), host(v, "bf16"), 0.125, dt=orc.BF16, out_dt=orc.F32,
+                          with_abs=True)
+    err = np.abs(out.cpu().numpy().astype(np.float64) - want.astype(np.float64))
+    bound = 1e-5 * wabs.astype(np.float64) + 2.0 ** -23 * np.abs(want.astype(np.float64))
+    assert np.all(err <= bound + 1e-30), f"worst err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("ks", [2, 4])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_sdpa_key_groups_rounded_probabilities(dev, ops, orc, monkeypatch, ks, dt):
+    """lux3d_sdpa (probabilities rounded to the input type) with key groups:
+    the matrix-core bound of test_gpu_attention.py against the oracle."""
+    monkeypatch.setenv("LUX3D_ATTN_KS", str(ks))
+    b, lq, lk, h, d = 1, 1029, 1029, 8, 64
+    _print_case(op="sdpa key groups", ks=ks, dt=dt)
+    g = torch.Generator(device="cpu").manual_seed(7 + ks)
+    qkv = torch.randn((b, lq, 3, h, d), generator=g).to(dev).to(TDT[dt]).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    got = ops.sdpa(q, k, v, 0.125)
+    torch.cuda.synchronize()
+    want, wabs = orc.sdpa(host(q, dt), host(k, dt), host(v, dt), 0.125, dt=odt(orc, dt), with_abs=True)
+    gg, w = to_f64(host(got, dt), dt), to_f64(want, dt)
+    bound = ULP[dt] * np.abs(w) + (ULP[dt] + 1e-6) * wabs.astype(np.float64)
+    err = np.abs(gg - w)
+    assert np.all(err <= bound + 1e-30), f"worst err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("ks", [2, 4])
+def test_sdpa_dinov3_rope_key_groups_equals_the_two_launches(dev, ops, orc, monkeypatch, ks):
+    """The fused DINOv3 rotation with key groups equals the rotation launch
+    followed by exact_sdpa_heads on the same key groups, bit for bit, and
+    repeated calls agree (the merge order is fixed)."""
+    monkeypatch.setenv("LUX3D_ATTN_KS", str(ks))
+    b, s, h, d, prefix = 1, 1029, 16, 64, 5
+    _print_case(op="sdpa_dinov3_rope key groups", ks=ks)
+    q, k, v, cos, sin = _dino_case(dev, orc, b, s, h, d, "bf16", prefix, seed=91, grid=32)
+    q_r, k_r = ops.apply_rotary_to_patches(q, k, cos, sin, prefix)
+    fused = ops.sdpa_dinov3_rope(q, cos, sin, prefix, k_r, v, 0.125)
+    again = ops.sdpa_dinov3_rope(q, cos, sin, prefix, k_r, v, 0.125)
+    two = ops.exact_sdpa_heads(q_r, k_r, v, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two) and torch.equal(fused, again)
