@@ -197,15 +197,42 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
     if constexpr (QP == QP_LN_R1 || QP == QP_RMS) param8(p.qw, p.qw_dt, ch * 8, 1.f, w8);
     if constexpr (QP == QP_LN_R1) param8(p.qb, p.qb_dt, ch * 8, 0.f, b8);
     if constexpr (QP == QP_L2_R2) param8(p.qw, p.qw_dt, hi * D + ch * 8, 1.f, w8);  // gamma of head hi
-    // the passes unrolled: their row loads are all in flight together
+    // Every pass's row, table and parameter loads are issued first (one
+    // fence keeps the scheduler from sinking them behind the reductions),
+    // so each wavefront waits on one memory round trip, not one per pass.
     static_assert((QT * 32) % RPP == 0, "whole passes");
+    constexpr int NP = QT * 32 / RPP;                                   // passes
+    constexpr int TW = QP == QP_L2_R2 ? 4 : (QP == QP_RMS ? 1 : 8);   // table values per lane and pass
+    float xs[NP][8], tc[NP][TW], tsn[NP][TW];
+    int64_t qrs[NP];
 #pragma unroll
-    for (int it = 0; it < QT * 32 / RPP; ++it) {
+    for (int it = 0; it < NP; ++it) {
       const int row = lane / LPR + it * RPP;
       int64_t qr = qb * BQ + qg * QT * 32 + row;
       qr = qr < Lq ? qr : Lq - 1;
-      float x[8];
-      Chunk<T>::template load<false>(qbase + (qr * p.q_st + ch * 8) * 2, x);
+      qrs[it] = qr;
+      Chunk<T>::template load<false>(qbase + (qr * p.q_st + ch * 8) * 2, xs[it]);
+      if constexpr (QP == QP_LN_R1) {
+        const int64_t toff = bi * p.tab_sB + qr * p.tab_sN + ch * 8;
+        param8(p.tab_c, p.tab_dt, toff, 1.f, tc[it]);
+        param8(p.tab_s, p.tab_dt, toff, 0.f, tsn[it]);
+      } else if constexpr (QP == QP_L2_R2) {
+        const int64_t toff = qr * p.tab_sN + ch * 4;
+        param4(p.tab_c, p.tab_dt, toff, 1.f, tc[it]);
+        param4(p.tab_s, p.tab_dt, toff, 0.f, tsn[it]);
+      } else if constexpr (QP == QP_R3) {
+        // tokens before the prefix read table row 0 (their rotation is discarded)
+        const int64_t toff = (qr >= p.prefix ? qr - p.prefix : 0) * p.tab_sN + ch * 8;
+        param8(p.tab_c, p.tab_dt, toff, 1.f, tc[it]);
+        param8(p.tab_s, p.tab_dt, toff, 0.f, tsn[it]);
+      }
+    }
+    issue_fence();
+#pragma unroll
+    for (int it = 0; it < NP; ++it) {
+      const int row = lane / LPR + it * RPP;
+      const int64_t qr = qrs[it];
+      float(&x)[8] = xs[it];
       if constexpr (QP == QP_LN_R1) {
         const float mean = group_sum<LPR>(ln_chunk_sum(x)) * (1.0f / D);
         const float rstd = ln_rstd(group_sum<LPR>(ln_chunk_center_sq(x, mean)), 1.0f / D, p.eps);
@@ -219,37 +246,27 @@ __global__ __launch_bounds__(256, MINW) void attn_mfma_kernel(AttnParams p, int6
       float y[8];
       if constexpr (QP == QP_LN_R1) {
         // Rope2d: partner j ^ D/4, C / S the cos_full / sin_alt_full rows
-        float C8[8], S8[8], pv[8];
-        const int64_t toff = bi * p.tab_sB + qr * p.tab_sN + ch * 8;
-        param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
-        param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
+        float pv[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 32>(x[k]);  // element j ^ D/4
 #pragma unroll
-        for (int k = 0; k < 8; ++k) y[k] = rotate1(x[k], C8[k], pv[k], S8[k]);
+        for (int k = 0; k < 8; ++k) y[k] = rotate1(x[k], tc[it][k], pv[k], tsn[it][k]);
       } else if constexpr (QP == QP_L2_R2) {
         // TRELLIS.2 pairs (2a, 2a + 1) = (re, im): partner j ^ 1 in the lane,
         // C = cos[n][a], S = -sin[n][a] for the re element, +sin for im
-        float c4[4], s4[4];
-        const int64_t toff = qr * p.tab_sN + ch * 4;
-        param4(p.tab_c, p.tab_dt, toff, 1.f, c4);
-        param4(p.tab_s, p.tab_dt, toff, 0.f, s4);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) y[k] = rotate1(x[k], c4[k >> 1], x[k ^ 1], (k & 1) ? s4[k >> 1] : -s4[k >> 1]);
+        for (int k = 0; k < 8; ++k)
+          y[k] = rotate1(x[k], tc[it][k >> 1], x[k ^ 1], (k & 1) ? tsn[it][k >> 1] : -tsn[it][k >> 1]);
       } else if constexpr (QP == QP_R3) {
         // DINOv3 rotate_half: partner j ^ D/2, S = -sin for j < D/2; tokens
-        // before the prefix pass through (their table row is clamped to 0
-        // and the rotation discarded, so no load depends on a branch)
-        float C8[8], S8[8], pv[8];
+        // before the prefix pass through
+        float pv[8];
         const bool rot = qr >= p.prefix;
-        const int64_t toff = (rot ? qr - p.prefix : 0) * p.tab_sN + ch * 8;
-        param8(p.tab_c, p.tab_dt, toff, 1.f, C8);
-        param8(p.tab_s, p.tab_dt, toff, 0.f, S8);
 #pragma unroll
         for (int k = 0; k < 8; ++k) pv[k] = lane_xor<D / 16>(x[k]);  // element j ^ D/2
         const bool lo = ch * 8 < D / 2;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) y[k] = rot ? rotate1(x[k], C8[k], pv[k], lo ? -S8[k] : S8[k]) : x[k];
+        for (int k = 0; k < 8; ++k) y[k] = rot ? rotate1(x[k], tc[it][k], pv[k], lo ? -tsn[it][k] : tsn[it][k]) : x[k];
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) y[k] = x[k];
