@@ -695,6 +695,29 @@ Tensor sdpa_layernorm_rope(const Tensor &q, const LayerNorm &q_norm, const RopeE
   return out;
 }
 
+Tensor sdpa_rms_norm_heads(const Tensor &q, const Tensor &q_w, const Tensor &k, const Tensor &v, float scale) {
+  Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
+  abi_check(lux3d_sdpa_rms_norm_heads(Desc(q).p(), Desc(q_w).p(), 1e-6f, Desc(k).p(), Desc(v).p(), scale,
+                                      Desc(out).p(), q.device().stream()));
+  return out;
+}
+
+Tensor sdpa_l2norm_rope3d(const Tensor &q, const Tensor &q_gamma, const Tensor &cos, const Tensor &sin,
+                          const Tensor &k, const Tensor &v, float scale) {
+  Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
+  abi_check(lux3d_sdpa_l2norm_rope3d(Desc(q).p(), Desc(q_gamma).p(), Desc(cos).p(), Desc(sin).p(), Desc(k).p(),
+                                     Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
+  return out;
+}
+
+Tensor sdpa_dinov3_rope(const Tensor &q, const Tensor &cos, const Tensor &sin, size_t num_prefix, const Tensor &k,
+                        const Tensor &v, float scale) {
+  Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());
+  abi_check(lux3d_sdpa_dinov3_rope(Desc(q).p(), Desc(cos).p(), Desc(sin).p(), (int64_t)num_prefix, Desc(k).p(),
+                                   Desc(v).p(), scale, Desc(out).p(), q.device().stream()));
+  return out;
+}
+
 Tensor exact_query_chunked_sdpa(const Tensor &q, const Tensor &k, const Tensor &v, float scale, size_t) {
   if (q.rank() != 4) fail(LUX3D_ERR_SHAPE, "sdpa: q must be [B, H, L, D], got " + dims_str(q.dims()));
   Tensor out = Tensor::empty(q.dims(), q.dtype(), q.device());

@@ -300,6 +300,21 @@ Tensor exact_sdpa_heads(const Tensor &q, const Tensor &k, const Tensor &v, float
 // two calls.
 Tensor sdpa_layernorm_rope(const Tensor &q, const class LayerNorm &q_norm, const struct RopeEmbeddings &embeddings,
                            const Tensor &k, const Tensor &v, float scale);
+// exact_query_chunked_sdpa(rms_norm_heads(q, q_w), k, v, scale)
+// (triposg_dit.rs:446-455) with q's per-head RMSNorm (eps 1e-6) in the Q
+// load; k already normalised. Bit-identical to the two calls.
+Tensor sdpa_rms_norm_heads(const Tensor &q, const Tensor &q_w, const Tensor &k, const Tensor &v, float scale);
+// Trellis2SelfAttention::attention (trellis2_blocks.rs:417-436) on
+// [B, H, L, D] views: exact_query_chunked_sdpa(rope(l2norm(q)), k, v, scale)
+// with q's L2 norm (gamma [H, D]) and 3D RoPE (cos / sin [L, D/2]) in the Q
+// load; k already normalised and rotated. Bit-identical to the two calls.
+Tensor sdpa_l2norm_rope3d(const Tensor &q, const Tensor &q_gamma, const Tensor &cos, const Tensor &sin,
+                          const Tensor &k, const Tensor &v, float scale);
+// exact_sdpa_heads(apply_rotary_to_patches(q), k, v, scale)
+// (trellis2_dino.rs:385-393) with q's rotate_half RoPE in the Q load; k
+// already rotated. Bit-identical to the two calls.
+Tensor sdpa_dinov3_rope(const Tensor &q, const Tensor &cos, const Tensor &sin, size_t num_prefix, const Tensor &k,
+                        const Tensor &v, float scale);
 
 // QMatMul over a Q8_0 weight [n, k] (QMatMul::from_qtensor and forward,
 // runtime/nn_blocks.rs:83-93, 145-150). from_q8_0 repacks the GGML blocks

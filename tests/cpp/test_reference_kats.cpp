@@ -311,6 +311,57 @@ void vggt_attention_fused_equals_two_calls(const Device &dev) {
   CHECK(fused.to_vec_u16() == two.to_vec_u16());
 }
 
+// TripoSG (triposg_dit.rs:446-455), TRELLIS.2 (trellis2_blocks.rs:417-436)
+// and DINOv3 (trellis2_dino.rs:385-393) attention with q's head norm /
+// rotation fused into the attention kernel equal the head op followed by the
+// attention bit for bit.
+void model_attentions_fused_equal_two_calls(const Device &dev) {
+  const int64_t B = 1, N = 200, H = 2, D = 128;
+  std::vector<float> x((size_t)(B * N * H * 3 * D));
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.017f * (float)i) * 1.5f + 0.2f;
+  std::vector<float> w(D), g(H * D);
+  for (int64_t j = 0; j < D; ++j) w[j] = 1.0f + 0.01f * (float)(j % 9);
+  for (int64_t j = 0; j < H * D; ++j) g[j] = 1.0f - 0.005f * (float)(j % 11);
+  // TripoSG: per-head thirds of cat([q, k, v]) as [B, L, H, 3D], heads-first views
+  const Tensor qkv = Tensor::from_f32(x, {B, N, H, 3 * D}, DType::BF16, dev);
+  const Tensor q = qkv.narrow(3, 0, D).transpose(1, 2), k = qkv.narrow(3, D, D).transpose(1, 2);
+  const Tensor v = qkv.narrow(3, 2 * D, D).transpose(1, 2);
+  const Tensor qw = Tensor::from_f32(w, {D}, DType::F32, dev);
+  const Tensor kn = rms_norm_heads(k, qw);
+  const Tensor f1 = sdpa_rms_norm_heads(q, qw, kn, v, 0.088f);
+  const Tensor t1 = exact_query_chunked_sdpa(rms_norm_heads(q, qw), kn, v, 0.088f);
+  CHECK(f1.to_vec_u16() == t1.to_vec_u16());
+  // TRELLIS.2: [B, L, H, D] buffers, L2 norm + 3D RoPE from voxel coords
+  const Tensor buf = Tensor::from_f32(x, {B, N, 3, H, D}, DType::BF16, dev);
+  std::vector<int64_t> coords((size_t)(N * 3));
+  for (int64_t i = 0; i < N * 3; ++i) coords[(size_t)i] = (i * 7) % 23;
+  const Trellis2Rope3d rope((size_t)D);
+  auto [cos, sin] = rope.cos_sin(coords, dev);
+  const Tensor gamma = Tensor::from_f32(g, {H, D}, DType::F32, dev);
+  const Tensor bq = buf.permute({2, 0, 1, 3, 4}).get(0), bk = buf.permute({2, 0, 1, 3, 4}).get(1);
+  const Tensor bv = buf.permute({2, 0, 1, 3, 4}).get(2);  // [B, L, H, D] views
+  // the two launches: the L2 norm + rotation head op (one rounding), then attention
+  const Tensor qn = Tensor::empty(bq.dims(), DType::BF16, dev), kr = Tensor::empty(bk.dims(), DType::BF16, dev);
+  const lux3d_tensor_t dbq = bq.desc(), dbk = bk.desc(), dg = gamma.desc(), dcos = cos.desc(), dsin = sin.desc();
+  const lux3d_tensor_t dqn = qn.desc(), dkr = kr.desc();
+  CHECK(lux3d_qk_l2norm_rope3d(&dbq, &dg, &dbk, &dg, &dcos, &dsin, nullptr, 0.f, &dqn, &dkr, dev.stream()) == 0);
+  const Tensor f2 = sdpa_l2norm_rope3d(bq.transpose(1, 2), gamma, cos, sin, kr.transpose(1, 2), bv.transpose(1, 2),
+                                       0.088f);
+  const Tensor t2 = exact_query_chunked_sdpa(qn.transpose(1, 2), kr.transpose(1, 2), bv.transpose(1, 2), 0.088f);
+  CHECK(f2.to_vec_u16() == t2.to_vec_u16());
+  // DINOv3 (f32, the reference's precision): 4 + 14 x 14 tokens, 4 prefix
+  const int64_t S = 4 + 14 * 14, DH = 64;
+  std::vector<float> xd((size_t)(3 * S * DH * H));
+  for (size_t i = 0; i < xd.size(); ++i) xd[i] = std::cos(0.011f * (float)i);
+  const Tensor dq = Tensor::from_f32(xd, {3, B, S, H, DH}, DType::F32, dev);
+  auto [dc, ds] = dinov3_rope_cos_sin((size_t)DH, 100.0f, 14, 14, dev);
+  const Tensor q3 = dq.get(0).transpose(1, 2), k3 = dq.get(1).transpose(1, 2), v3 = dq.get(2).transpose(1, 2);
+  auto [qr, kr3] = apply_rotary_to_patches(q3, k3, dc, ds, 4);
+  const Tensor f3 = sdpa_dinov3_rope(q3, dc, ds, 4, kr3, v3, 0.125f);
+  const Tensor t3 = exact_sdpa_heads(qr, kr3, v3, 0.125f);
+  CHECK(f3.to_vec_f32() == t3.to_vec_f32());
+}
+
 // Q8_0: w = f16(d) * int8(q), exact.
 void dequantize_q8_0_exact(const Device &dev) {
   std::vector<uint8_t> blk(34);
@@ -699,6 +750,7 @@ int main(int argc, char **argv) {
       {"sparse_attention_matches_naive", sparse_attention_matches_naive, true},
       {"exact_sdpa_heads_bf16_is_f32_arithmetic", exact_sdpa_heads_bf16_is_f32_arithmetic, true},
       {"vggt_attention_fused_equals_two_calls", vggt_attention_fused_equals_two_calls, true},
+      {"model_attentions_fused_equal_two_calls", model_attentions_fused_equal_two_calls, true},
       {"gguf_q8_linear_from_file", gguf_q8_linear_from_file, true},
       {"kernel_offset_deltas_cover_the_3x3x3_kernel", kernel_offset_deltas_cover_the_3x3x3_kernel, false},
       {"coord_map_builds_and_looks_up", coord_map_builds_and_looks_up, true},
