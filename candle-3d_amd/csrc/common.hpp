@@ -308,11 +308,7 @@ inline size_t lds_for_occupancy(hipStream_t s, int wg_per_cu, size_t used) {
 // it orders loads for latency and register pressure, not for vmcnt, and so
 // would sink a small early load (a position, a parameter) below the row
 // loads that a wait for it must then also wait for.
-__device__ __forceinline__ void issue_fence() {
-#ifndef LUX3D_XP_NOFENCE
-  __builtin_amdgcn_sched_barrier(0);
-#endif
-}
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Per-channel parameters in two steps, for the kernels whose activation
 // loads must stay in flight. vmcnt counts loads and stores together in issue
@@ -323,29 +319,6 @@ __device__ __forceinline__ void issue_fence() {
 // bounds-checked buffer loads (bytes past the vector read as 0, an absent
 // vector has a zero-size descriptor and reads nothing), and `pdecode`
 // converts them where they are used, after the kernel's one wait.
-#ifdef LUX3D_XP_GLOBAL
-struct rsrc_t { const char *p; };
-__device__ __forceinline__ rsrc_t param_rsrc(const void *p, int dt, int64_t n) {
-  return rsrc_t{(dt < 0 || n <= 0) ? nullptr : reinterpret_cast<const char *>(p)};
-}
-struct PRaw {
-  u32x4_t a, b;
-};
-__device__ __forceinline__ PRaw pissue(rsrc_t r, int dt, int64_t i, int64_t j) {
-  const int sh = dt == LUX3D_F32 ? 2 : 1;
-  PRaw q;
-  if (r.p) {
-    const uint4 a = *reinterpret_cast<const uint4 *>(r.p + (i << sh));
-    const uint4 b = *reinterpret_cast<const uint4 *>(r.p + (j << sh));
-    q.a = u32x4_t{a.x, a.y, a.z, a.w};
-    q.b = u32x4_t{b.x, b.y, b.z, b.w};
-  } else {
-    q.a = u32x4_t{0u, 0u, 0u, 0u};
-    q.b = q.a;
-  }
-  return q;
-}
-#else
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t param_rsrc(const void *p, int dt, int64_t n) {
   int64_t bytes = (dt < 0 || !p) ? 0 : n * (dt == LUX3D_F32 ? 4 : 2);
@@ -362,7 +335,6 @@ __device__ __forceinline__ PRaw pissue(rsrc_t r, int dt, int64_t i, int64_t j) {
   q.b = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(j << sh), 0, 0);
   return q;
 }
-#endif
 __device__ __forceinline__ void pdecode(const PRaw &q, int dt, float dflt, float (&v)[8]) {
   if (dt == LUX3D_F32) {
     v[0] = __uint_as_float(q.a.x); v[1] = __uint_as_float(q.a.y);
