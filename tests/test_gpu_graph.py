@@ -129,3 +129,74 @@ def test_graph_replays_of_the_newer_entries(dev):
             a = got.view(torch.int16) if got.dtype == torch.bfloat16 else got
             b = want.view(torch.int16) if want.dtype == torch.bfloat16 else want
             assert torch.equal(a, b), f"replay {rep} differs from eager"
+
+
+def test_graph_replays_of_the_fused_attentions(dev):
+    """Graph replays of the attention entries that normalise / rotate q in
+    the Q load (TripoSG RMSNorm, TRELLIS.2 L2 norm + 3D RoPE, DINOv3
+    rotation in f32 and bf16) and of the two-key-group attention (DINOv3's
+    1029 tokens, bf16 exact and rounded probabilities): every replay equals
+    the eager run bit for bit."""
+    print("\n[case] graph replay of the fused attentions + key groups", flush=True)
+    from lux3d_fused import ops, _lib
+    g = torch.Generator(device="cpu").manual_seed(21)
+
+    def rnd(shape, dt=torch.bfloat16, scale=1.0):
+        return (torch.randn(shape, generator=g) * scale).to(dev).to(dt)
+
+    # TripoSG: per-head thirds of [1, 300, 2, 3 * 128]
+    th = rnd((1, 300, 2, 384))
+    tq, tk, tv = (th[..., i * 128:(i + 1) * 128].transpose(1, 2) for i in range(3))
+    tw = rnd((128,), torch.float32, 0.1) + 1
+    to = torch.empty((1, 2, 300, 128), dtype=torch.bfloat16, device=dev)
+    # TRELLIS.2: [1, 257, 3, 2, 128], tables [257, 64]
+    tr = rnd((1, 257, 3, 2, 128))
+    coords = torch.randint(0, 40, (257, 3), generator=g, dtype=torch.int32).to(dev)
+    cos3, sin3 = ops.Trellis2Rope3d(128).cos_sin(coords)
+    gam = rnd((2, 128), torch.float32, 0.1) + 1
+    tro = torch.empty((1, 2, 257, 128), dtype=torch.bfloat16, device=dev)
+    # DINOv3: [1, 16, 1029, 64] f32 and bf16 (the bf16 exact path runs two key groups)
+    d32 = rnd((3, 1, 1029, 16, 64), torch.float32)
+    d16 = d32.to(torch.bfloat16)
+    ang = torch.rand((1024, 64), generator=g) * 6.3
+    dc, ds = torch.cos(ang).to(dev), torch.sin(ang).to(dev)
+    do32 = torch.empty((1, 16, 1029, 64), dtype=torch.float32, device=dev)
+    do16 = torch.empty((1, 16, 1029, 64), dtype=torch.bfloat16, device=dev)
+    dsd = torch.empty((1, 16, 1029, 64), dtype=torch.bfloat16, device=dev)
+    d = ops.desc
+
+    def run():
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("lux3d_sdpa_rms_norm_heads", d(tq), d(tw), 1e-6, d(tk), d(tv), 0.0884, d(to), s)
+        _lib.call("lux3d_sdpa_l2norm_rope3d", d(tr[:, :, 0].transpose(1, 2)), d(gam), d(cos3), d(sin3),
+                  d(tr[:, :, 1].transpose(1, 2)), d(tr[:, :, 2].transpose(1, 2)), 0.0884, d(tro), s)
+        _lib.call("lux3d_sdpa_dinov3_rope", d(d32[0].transpose(1, 2)), d(dc), d(ds), 5, d(d32[1].transpose(1, 2)),
+                  d(d32[2].transpose(1, 2)), 0.125, d(do32), s)
+        _lib.call("lux3d_sdpa_dinov3_rope", d(d16[0].transpose(1, 2)), d(dc), d(ds), 5, d(d16[1].transpose(1, 2)),
+                  d(d16[2].transpose(1, 2)), 0.125, d(do16), s)
+        _lib.call("lux3d_sdpa", d(d16[0].transpose(1, 2)), d(d16[1].transpose(1, 2)), d(d16[2].transpose(1, 2)),
+                  0.125, d(dsd), s)
+
+    outs = (to, tro, do32, do16, dsd)
+    run()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in outs]
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run()
+    for rep in range(4):
+        for t in outs:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(outs, eager):
+            a = got.view(torch.int16) if got.dtype == torch.bfloat16 else got.view(torch.int32)
+            b = want.view(torch.int16) if want.dtype == torch.bfloat16 else want.view(torch.int32)
+            assert torch.equal(a, b), f"replay {rep} differs from eager"
