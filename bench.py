@@ -562,6 +562,13 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    # the dominant kernel against the fastest plain copy of the same streams
+    # (ceiling.BEST_VARIANTS at the op's size), the ceiling its frac is judged by
+    dom_row = next((r for r in table if r["op"] == roofline["op"]), None)
+    if dom_row and "best_copy_us" in dom_row:
+        roofline["best_copy"] = {"us": dom_row["best_copy_us"], "variant": dom_row["best_copy_variant"],
+                                 "frac_peak": dom_row["best_copy_frac_peak"],
+                                 "kernel_over_copy": dom_row["frac_of_best_copy"]}
     # The full table (every op with its ceilings, traces and CPU rows) goes to
     # stderr and, on request, a file; the stdout line keeps the headline plus
     # one short entry per op so that it stays a few KB.

@@ -356,6 +356,42 @@ def test_sdpa_layernorm_rope2d_argument_errors():
     assert rc == _lib.ERR_VALUE
 
 
+def test_fused_model_attention_argument_errors():
+    """The TripoSG / TRELLIS.2 / DINOv3 entries that take q's norm / rotation
+    into the attention reject bad parameters and tables on the host (before
+    choosing between the fused kernel and the two launches)."""
+    q, k, v, o = T([1, 2, 40, 128]), T([1, 2, 40, 128]), T([1, 2, 40, 128]), T([1, 2, 40, 128])
+    w = T([128], _lib.F32)
+    rc, msg = status("lux3d_sdpa_rms_norm_heads", q, None, 1e-6, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_NULL and "q_w" in msg
+    rc, msg = status("lux3d_sdpa_rms_norm_heads", q, T([64], _lib.F32), 1e-6, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_sdpa_rms_norm_heads", q, w, -1.0, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_VALUE
+    rc, msg = status("lux3d_sdpa_rms_norm_heads", q, w, 1e-6, k, v, 0.1, T([1, 2, 39, 128]), None)
+    assert rc == _lib.ERR_SHAPE
+    gam, cs, sn = T([2, 128], _lib.F32), T([40, 64], _lib.F32), T([40, 64], _lib.F32)
+    rc, msg = status("lux3d_sdpa_l2norm_rope3d", q, None, cs, sn, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_NULL and "q_gamma" in msg
+    rc, msg = status("lux3d_sdpa_l2norm_rope3d", q, T([128], _lib.F32), cs, sn, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_SHAPE
+    rc, msg = status("lux3d_sdpa_l2norm_rope3d", q, gam, T([40, 128], _lib.F32), sn, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_SHAPE and "[L, D/2]" in msg
+    rc, msg = status("lux3d_sdpa_l2norm_rope3d", q, gam, cs, T([40, 64], _lib.BF16), k, v, 0.1, o, None)
+    assert rc == _lib.ERR_LAYOUT
+    rc, msg = status("lux3d_sdpa_l2norm_rope3d", q, gam, cs, None, k, v, 0.1, o, None)
+    assert rc == _lib.ERR_NULL
+    q3, k3, v3, o3 = T([1, 2, 40, 64], _lib.F32), T([1, 2, 40, 64], _lib.F32), T([1, 2, 40, 64], _lib.F32), \
+        T([1, 2, 40, 64], _lib.F32)
+    c3, s3 = T([35, 64], _lib.F32), T([35, 64], _lib.F32)
+    rc, msg = status("lux3d_sdpa_dinov3_rope", q3, c3, s3, 41, k3, v3, 0.125, o3, None)
+    assert rc == _lib.ERR_VALUE and "num_prefix" in msg
+    rc, msg = status("lux3d_sdpa_dinov3_rope", q3, c3, s3, 4, k3, v3, 0.125, o3, None)
+    assert rc == _lib.ERR_SHAPE and "[S - num_prefix, D]" in msg
+    rc, msg = status("lux3d_sdpa_dinov3_rope", q3, c3, s3, 5, k3, v3, 0.125, T([1, 2, 40, 64]), None)
+    assert rc == _lib.ERR_DTYPE
+
+
 def test_integration_ffi_block_lists_every_entry():
     """The Rust extern blocks of the integration guide at the repository root
     declare exactly the functions of include/lux3d_fused.h and
