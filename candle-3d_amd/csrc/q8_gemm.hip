@@ -815,36 +815,39 @@ __global__ __launch_bounds__(256) void q8_0_int8_gemm_kernel(Q8IntParams p, int 
   __shared__ __align__(16) float Ad[2][2][kI8Tile];  // [buffer][block of the stage][row]
   __shared__ __align__(16) float Bd[2][2][kI8Tile];
   (void)tiles_n;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave >> 1,
+            wn = wave & 1;
   const int64_t m0 = (int64_t)blockIdx.y * kI8Tile, n0 = (int64_t)blockIdx.x * kI8Tile;
   const int64_t nb = p.K / 32, nst = (nb + 1) / 2;
   // loaders: thread t moves the 16 bytes (t & 3) of x row t / 4 and of weight
   // row t / 4 per stage (rows past M / N clamped: loaded, computed, never
-  // stored); threads 0-127 the x scales (block t / 64 of the stage, row
-  // t % 64), 128-255 the weight scales
+  // stored); wavefronts 0-1 the x scales (block wave & 1 of the stage, row
+  // lane), 2-3 the weight scales
   const int lr = t >> 2, lq = t & 3;
   const int64_t ra = m0 + lr < p.M ? m0 + lr : p.M - 1, rb = n0 + lr < p.N ? n0 + lr : p.N - 1;
   const int8_t *sa = p.xq + ra * p.K + lq * 16, *sb = p.qs + rb * p.K + lq * 16;
   const int so = lr * kI8Row + lq * 16;
-  const int sr = t & 63, sbk = (t >> 6) & 1;
-  const bool sx = t < 128;
+  const int sr = lane, sbk = wave & 1;
+  const bool sx = wave < 2;
   const int64_t swr = n0 + sr < p.N ? n0 + sr : p.N - 1;
-  auto scale_at = [&](int64_t st) -> float {
-    int64_t kb = 2 * st + sbk;
-    kb = kb < nb ? kb : nb - 1;
-    return sx ? p.xd[kb * p.ldxd + m0 + sr] : p.scales[swr * nb + kb];
-  };
-  auto k_off = [&](int64_t st) -> int64_t {  // byte offset of this thread's 16 bytes in stage st
-    const int64_t k = st * 64 + lq * 16;
-    return k < p.K ? st * 64 : p.K - 64;  // an odd last block: its second half loads block nb - 1 again
-  };
+  // the thread's scale column: x scales are block-major (stride ldxd per
+  // block), weight scales row-major (stride 1); the stride is wave-uniform
+  const float *sp = sx ? p.xd + m0 + sr : p.scales + swr * nb;
+  const int64_t sstep = sx ? p.ldxd : 1;
+  // an odd last stage holds block nb - 1 in both halves: threads of the
+  // second half (lq 2, 3) read 32 bytes back, and both scale rows read it
+  const int back = lq >= 2 ? 32 : 0;
   uint4 va, vb;
   float vs;
   auto load = [&](int64_t st) {
-    const int64_t o = k_off(st);
+    int64_t o = st * 64, kb = 2 * st + sbk;
+    if (2 * st + 1 == nb) {
+      o -= back;
+      kb = 2 * st;
+    }
     va = *reinterpret_cast<const uint4 *>(sa + o);
     vb = *reinterpret_cast<const uint4 *>(sb + o);
-    vs = scale_at(st);
+    vs = sp[kb * sstep];
   };
   auto store = [&](int buf) {
     *reinterpret_cast<uint4 *>(&As[buf][so]) = va;
@@ -880,13 +883,13 @@ __global__ __launch_bounds__(256) void q8_0_int8_gemm_kernel(Q8IntParams p, int 
     const i32x16_t_ c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a),
                                                                *reinterpret_cast<const i32x4_t_ *>(b), i32x16_t_{}, 0,
                                                                0, 0);
-    const bool two = 2 * st + 1 < nb;
-    i32x16_t_ c1 = {};
-    if (two)
-      c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a + 32),
-                                                 *reinterpret_cast<const i32x4_t_ *>(b + 32), i32x16_t_{}, 0, 0, 0);
+    // an odd last stage holds block nb - 1 in both halves: its second product
+    // is computed and not folded
+    const i32x16_t_ c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a + 32),
+                                                               *reinterpret_cast<const i32x4_t_ *>(b + 32),
+                                                               i32x16_t_{}, 0, 0, 0);
     fold(c0, buf, 0);
-    if (two) fold(c1, buf, 1);
+    if (2 * st + 1 < nb) fold(c1, buf, 1);
     if (st + 1 < nst) store(buf ^ 1);
     lds_barrier();
   }
