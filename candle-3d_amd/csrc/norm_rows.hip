@@ -282,7 +282,51 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
     }
   }
 
-  if constexpr (MODE == ROW_RESID_LN) {
+  // One row per workgroup (the short jobs, where a row's latency is the
+  // job's): g arrives with the residual inputs as raw bytes, and w and b are
+  // issued right after them, ahead of the h store, so that they arrive while
+  // the statistics are reduced instead of after them. configs[4] F1 f32:
+  // 4.19 against 4.44 us (same-box A/B). The long jobs measured slower in
+  // this order (configs[1] F1 19.1 against 18.3 us) and load their
+  // parameters where they are used. The h store stays conditional on `live`:
+  // written unconditionally, the compiler dropped its non-temporal bit and
+  // the job took 4.9 us.
+  constexpr bool EARLY = MODE == ROW_RESID_LN && RPB == 1 && NC <= 2;
+  PRaw e_g[EARLY ? NC : 1], e_w[EARLY ? NC : 1], e_b[EARLY ? NC : 1];
+  if constexpr (EARLY) {
+    const char *ar = reinterpret_cast<const char *>(p.a) + row * p.a_rs * EB;
+    char *hr = reinterpret_cast<char *>(p.h) + row * p.h_rs * EB;
+    float av[NC][8], g[NC][8];
+    const rsrc_t r_g = param_rsrc(p.g, p.g_dt, p.d);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
+      ld_row<T>(ar, at, av[c]);
+      e_g[c] = pissue(r_g, p.g_dt, at.o0, at.o1);
+    }
+    issue_fence();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) pdecode(e_g[c], p.g_dt, 1.f, g[c]);
+    const rsrc_t r_w = param_rsrc(p.w, p.w_dt, p.d), r_b = param_rsrc(p.b, p.b_dt, p.d);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const ChunkAt at = chunk_at<T, TPR>(c, t);
+      e_w[c] = pissue(r_w, p.w_dt, at.o0, at.o1);
+      e_b[c] = pissue(r_b, p.b_dt, at.o0, at.o1);
+    }
+    issue_fence();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float ls = p.g_dt >= 0 ? mul_rn(av[c][k], g[c][k]) : av[c][k];
+        v[c][k] = Chunk<T>::round_trip(add_rn(ls, v[c][k]));  // the norm reads the stored h
+      }
+      if (live) st_row<T>(hr, chunk_at<T, TPR>(c, t), v[c]);
+    }
+  }
+
+  if constexpr (MODE == ROW_RESID_LN && !EARLY) {
     const char *ar = reinterpret_cast<const char *>(p.a) + row * p.a_rs * EB;
     char *hr = reinterpret_cast<char *>(p.h) + row * p.h_rs * EB;
 #pragma unroll
@@ -355,6 +399,9 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
       if constexpr (LN_UPFRONT) {
         pdecode(q_w[c], p.w_dt, 1.f, w);
         pdecode(q_b[c], p.b_dt, 0.f, b);
+      } else if constexpr (EARLY) {
+        pdecode(e_w[c], p.w_dt, 1.f, w);
+        pdecode(e_b[c], p.b_dt, 0.f, b);
       } else {
         param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
         param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);

@@ -162,6 +162,39 @@ def test_residual_layer_norm(dev, ops, orc, synth, dt, shape, gamma):
     check(y, yw, dt, "residual_layer_norm y")
 
 
+@pytest.mark.parametrize("dt,shape,gamma,pdt", [
+    ("bf16", (1, 700, 1024), None, None),           # no LayerScale, no affine
+    ("bf16", (1, 700, 1024), (1.0, 0.1), "bf16"),   # 2-byte parameters
+    ("f32", (1, 700, 1024), (1e-5, 1e-6), "f16"),
+    ("f32", (2, 300, 2048), None, "f32"),           # 2048-wide rows: 256 threads per row
+    ("bf16", (2, 300, 2048), (1.0, 0.1), "f32"),
+])
+def test_residual_layer_norm_short_jobs(dev, ops, orc, synth, dt, shape, gamma, pdt):
+    """Jobs under 2048 rows run one row per workgroup and issue the LayerNorm
+    parameters ahead of the residual store; every parameter dtype and the
+    absent ones take that path."""
+    print(f"\n[case] residual_layer_norm short job dt={dt} shape={shape} gamma={gamma} params={pdt}", flush=True)
+    n = int(np.prod(shape))
+    d = shape[-1]
+    seed = synth.config_seed(4) + 17
+    x = synth.normal(seed, n).reshape(shape)
+    a = synth.normal(seed + 1, n).reshape(shape)
+
+    def param(s, mean, std):
+        t = torch.from_numpy(synth.normal(s, d, mean, std)).to(dev).to(TDT[pdt if pdt else "f32"])
+        return t, t.float().cpu().numpy()
+
+    gd, g = param(seed + 2, *gamma) if gamma else (None, None)
+    wd, w = param(seed + 3, 1.0, 0.02) if pdt else (None, None)
+    bd, b = param(seed + 4, 0.0, 0.02) if pdt else (None, None)
+    xd, ad = dev_tensor(x, dt, dev), dev_tensor(a, dt, dev)
+    h, y = ops.residual_layer_norm(xd, ad, gd, wd, bd, 1e-5)
+    sync()
+    hw, yw = orc.residual_layer_norm(host_view(xd, dt), host_view(ad, dt), g, w, b, 1e-5, dt=oracle_dt(orc, dt))
+    assert np.array_equal(host_view(h, dt), hw), "residual stream h must be bit-exact"
+    check(y, yw, dt, "residual_layer_norm y (short job)")
+
+
 # ---------------------------------------------------------------------------
 # AdaLN modulate / gated residual (dense and ragged)
 # ---------------------------------------------------------------------------
