@@ -876,20 +876,25 @@ __global__ __launch_bounds__(256) void q8_0_int8_gemm_kernel(Q8IntParams p, int 
       }
     }
   };
+  // a wavefront whose 32 rows all lie past M (in the last row of tiles) only
+  // loads and synchronises: its products would never be stored
+  const bool rows_live = m0 + wm * 32 < p.M;  // wave-uniform
   for (int64_t st = 0; st < nst; ++st) {
     const int buf = (int)(st & 1);
     if (st + 1 < nst) load(st + 1);
-    const int8_t *a = &As[buf][(wm * 32 + fr) * kI8Row + fk], *b = &Bs[buf][(wn * 32 + fr) * kI8Row + fk];
-    const i32x16_t_ c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a),
-                                                               *reinterpret_cast<const i32x4_t_ *>(b), i32x16_t_{}, 0,
-                                                               0, 0);
-    // an odd last stage holds block nb - 1 in both halves: its second product
-    // is computed and not folded
-    const i32x16_t_ c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a + 32),
-                                                               *reinterpret_cast<const i32x4_t_ *>(b + 32),
-                                                               i32x16_t_{}, 0, 0, 0);
-    fold(c0, buf, 0);
-    if (2 * st + 1 < nb) fold(c1, buf, 1);
+    if (rows_live) {
+      const int8_t *a = &As[buf][(wm * 32 + fr) * kI8Row + fk], *b = &Bs[buf][(wn * 32 + fr) * kI8Row + fk];
+      const i32x16_t_ c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a),
+                                                                 *reinterpret_cast<const i32x4_t_ *>(b), i32x16_t_{},
+                                                                 0, 0, 0);
+      // an odd last stage holds block nb - 1 in both halves: its second
+      // product is computed and not folded
+      const i32x16_t_ c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(*reinterpret_cast<const i32x4_t_ *>(a + 32),
+                                                                 *reinterpret_cast<const i32x4_t_ *>(b + 32),
+                                                                 i32x16_t_{}, 0, 0, 0);
+      fold(c0, buf, 0);
+      if (2 * st + 1 < nb) fold(c1, buf, 1);
+    }
     if (st + 1 < nst) store(buf ^ 1);
     lds_barrier();
   }

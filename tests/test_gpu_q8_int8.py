@@ -76,7 +76,9 @@ def test_q8_0_quantize_bit_exact(dev, ops, orc, synth, case):
 @pytest.mark.parametrize("m,n,k,bias", [(1029, 4096, 1024, True),   # configs[4]: DINOv3 ViT-L MLP fc1 shape
                                          (3, 70, 96, False),          # ragged tiles, three blocks
                                          (130, 64, 32, True),         # one block
-                                         (65, 129, 2048, False)])
+                                         (65, 129, 2048, False),
+                                         (100, 130, 64, True),        # last tile: upper wavefronts partly live
+                                         (40, 64, 160, False)])       # one tile, upper wavefronts partly live
 def test_q8_0_linear_int8_bit_exact(dev, ops, orc, synth, m, n, k, bias):
     print(f"\n[case] q8_0_linear_int8 m={m} n={n} k={k} bias={bias}", flush=True)
     x = synth.normal(92, m * k).reshape(m, k).astype(np.float32)
