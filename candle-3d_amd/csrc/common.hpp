@@ -275,6 +275,19 @@ __device__ __forceinline__ void param4(const void *p, int dt, int64_t i, float d
     for (int k = 0; k < 4; ++k) v[k] = dflt;
   }
 }
+// Compute units of the stream's device, looked up once per device (256 on
+// MI355X, and the value used if the lookup fails).
+inline int cu_count(hipStream_t s) {
+  static std::atomic<int> cus[64];  // 0: not looked up yet
+  const int dev = hipGetStreamDeviceId(s);
+  if (dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 // Dynamic LDS bytes for a launch whose kernel uses `used` bytes, raised so
 // that at most `wg_per_cu` of its workgroups are resident on a CU (the extra
 // bytes are a reservation the kernel never touches). Some streaming kernels

@@ -413,6 +413,142 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
   }
 }
 
+// ---- persistent residual + LayerNorm (2-byte rows of 1024) ------------------
+//
+// The long F1 jobs (VGGT's [B * N, 1024] blocks in bf16 / f16). A workgroup of
+// 256 threads owns a pair of rows at a time (128 threads, one 8-element chunk
+// each, per row: the same element mapping, arithmetic and reduction order as
+// row_kernel<T, 128, 1, ROW_RESID_LN>, so the outputs are bit-identical) and
+// walks the pairs with a grid stride; the grid is two workgroups per CU.
+// - γ, w and b are loaded once per thread, not once per row.
+// - The next pair's rows are loaded before this pair's arithmetic and
+//   stores, as raw bytes through buffer loads on the (wave-uniform) row
+//   address, so no per-lane address arithmetic sits between the pairs.
+// - Loads and stores are unconditional, so the compiler's vmcnt waits are
+//   exact: the last pair of a workgroup re-reads its own rows, and a row past
+//   the end (an odd row count) stores through a descriptor of size 0, which
+//   drops the write.
+// - Two register sets alternate (the loop is unrolled by two), so no loaded
+//   value is copied, and each pair's store data stays allocated until the
+//   next pair's loads are issued: a load into a register a pending store
+//   still reads from waits for that store.
+// configs[1] F1: 17.3 against 18.2 µs for row_kernel (same-box A/B, graph-
+// timed, cold); one or three workgroups per CU: 19.1 / 17.6 µs; loading two
+// pairs ahead: no gain.
+template <typename T> __device__ __forceinline__ void decode8(uint4 u, float (&v)[8]) {
+  const uint32_t q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (T::code == LUX3D_BF16) {
+      v[2 * i] = __uint_as_float(q[i] << 16);
+      v[2 * i + 1] = __uint_as_float(q[i] & 0xFFFF0000u);
+    } else {
+      v[2 * i] = f16_bits_to_f32(q[i] & 0xFFFFu);
+      v[2 * i + 1] = f16_bits_to_f32(q[i] >> 16);
+    }
+  }
+}
+template <typename T> __device__ __forceinline__ u32x4_t encode8(const float (&v)[8]) {
+  u32x4_t u;
+  if constexpr (T::code == LUX3D_BF16) {
+    u.x = pack_bf16x2(v[0], v[1]); u.y = pack_bf16x2(v[2], v[3]);
+    u.z = pack_bf16x2(v[4], v[5]); u.w = pack_bf16x2(v[6], v[7]);
+  } else {
+    u.x = pack_f16x2(v[0], v[1]); u.y = pack_f16x2(v[2], v[3]);
+    u.z = pack_f16x2(v[4], v[5]); u.w = pack_f16x2(v[6], v[7]);
+  }
+  return u;
+}
+// a 16-byte access of one row through a descriptor covering `bytes` of it
+// (non-temporal: aux bit 1)
+__device__ __forceinline__ rsrc_t row_rsrc(const void *row, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(row), (short)0, bytes, 0x00020000);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void resid_ln_persist_kernel(RowParams p, int npairs) {
+  static_assert(T::bytes == 2, "2-byte rows");
+  constexpr int TPR = 128, EB = T::bytes, NT = 2;
+  __shared__ float red_a[4], red_b[4];
+  const int t = threadIdx.x & (TPR - 1);
+  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);  // the row of the pair (wave-uniform)
+  const ChunkAt at = chunk_at<T, TPR>(0, t);
+  const int off = (int)(at.o0 * EB);
+  float g[8], w[8], b[8];
+  param_at<T>(p.g, p.g_dt, 0, at, 1.f, g);
+  param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
+  param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);
+  const float inv_d = 1.0f / (float)p.d;
+  const bool has_g = p.g_dt >= 0;
+  const int rbytes = (int)(p.d * EB);
+  const char *xs = reinterpret_cast<const char *>(p.x), *as = reinterpret_cast<const char *>(p.a);
+  char *hs = reinterpret_cast<char *>(p.h), *ys = reinterpret_cast<char *>(p.y);
+  const int rows = (int)p.rows;  // < 2^31 (the launcher checks): row math in scalar 32-bit registers
+  auto row_of = [&](int pr) -> int {
+    const int r = pr * 2 + half;
+    return r < rows ? r : rows - 1;
+  };
+  auto ld = [&](const char *base, int64_t rs, int r) -> uint4 {
+    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(row_rsrc(base + (int64_t)r * rs * EB, rbytes), off, 0, NT);
+    return make_uint4(u.x, u.y, u.z, u.w);
+  };
+  // one pair: (cx, ca) hold its rows, the next pair's go into (nx, na);
+  // (phd, pyd) are the previous pair's store data, kept allocated until the
+  // loads are issued
+  const int stride = (int)gridDim.x;
+  auto pair_step = [&](int pr, const uint4 &cx, const uint4 &ca, uint4 &nx, uint4 &na, u32x4_t &hd, u32x4_t &yd,
+                       const u32x4_t &phd, const u32x4_t &pyd) {
+    const int64_t row = row_of(pr);
+    const int nr = row_of(pr + stride < npairs ? pr + stride : pr);
+    nx = ld(xs, p.x_rs, nr);
+    na = ld(as, p.a_rs, nr);
+    asm volatile("" ::"v"(phd), "v"(pyd));
+    const int live_bytes = pr * 2 + half < rows ? rbytes : 0;
+    float v[8], av[8];
+    decode8<T>(cx, v);
+    decode8<T>(ca, av);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // LayerScale product and residual add as two roundings, as row_kernel
+      const float ls = has_g ? mul_rn(av[k], g[k]) : av[k];
+      v[k] = Chunk<T>::round_trip(add_rn(ls, v[k]));
+    }
+    hd = encode8<T>(v);
+    __builtin_amdgcn_raw_buffer_store_b128(hd, row_rsrc(hs + row * p.h_rs * EB, live_bytes), off, 0, NT);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+    const float mean = row_total<TPR, 256>(s, red_a) * inv_d;
+    float s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float dv = v[k] - mean;
+      s2 += dv * dv;
+    }
+    const float var = row_total<TPR, 256>(s2, red_b) * inv_d;
+    const float rstd = 1.0f / sqrtf(var + p.eps);
+    float out[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = (v[k] - mean) * rstd * w[k] + b[k];
+    yd = encode8<T>(out);
+    __builtin_amdgcn_raw_buffer_store_b128(yd, row_rsrc(ys + row * p.y_rs * EB, live_bytes), off, 0, NT);
+  };
+  // the first pair is peeled off the loop, so that the loop is entered, as it
+  // is re-entered, with a pair's loads and stores in flight: the compiler's
+  // waits at the loop head then hold for the steady state (with nothing but
+  // loads in flight on entry, it waited there for the previous stores too)
+  int pr = (int)blockIdx.x;
+  uint4 x0 = ld(xs, p.x_rs, row_of(pr)), a0 = ld(as, p.a_rs, row_of(pr)), x1, a1;
+  u32x4_t h0 = {}, y0 = {}, h1 = {}, y1 = {};
+  pair_step(pr, x0, a0, x1, a1, h0, y0, h1, y1);
+  for (pr += stride; pr < npairs; pr += stride) {
+    pair_step(pr, x1, a1, x0, a0, h1, y1, h0, y0);
+    pr += stride;
+    if (pr >= npairs) break;
+    pair_step(pr, x0, a0, x1, a1, h0, y0, h1, y1);
+  }
+}
+
 // Fallback for any D and any alignment: one 256-thread block per row, three
 // passes over the row (the second and third hit L2).
 template <typename T, int MODE>
@@ -514,6 +650,16 @@ hipError_t launch_typed(const RowParams &p0, bool vec, hipStream_t s) {
   if (!tpr) {  // any width / alignment: one 256-thread block per row
     hipLaunchKernelGGL((row_kernel_any<T, MODE>), dim3((unsigned)p.rows), dim3(kBlock), 0, s, p);
     return hipGetLastError();
+  }
+  // the long residual + LayerNorm jobs on 2-byte rows of 1024: the persistent
+  // kernel, two workgroups per CU
+  if constexpr (MODE == ROW_RESID_LN && T::bytes == 2) {
+    if (tpr == 128 && nc == 1 && !row_per_block && p.rows < INT32_MAX) {
+      const int64_t npairs = (p.rows + 1) / 2, cap = 2 * (int64_t)cu_count(s);
+      const int64_t grid = npairs < cap ? npairs : cap;
+      hipLaunchKernelGGL((resid_ln_persist_kernel<T>), dim3((unsigned)grid), dim3(256), 0, s, p, (int)npairs);
+      return hipGetLastError();
+    }
   }
   int block = row_per_block ? tpr : kBlock;
   // staged segment pieces: larger workgroups stage them for more rows

@@ -138,6 +138,8 @@ def test_layer_norm_empty_and_errors(dev, ops):
     ("bf16", (1, 1029, 1024), (1e-5, 1e-6)),
     ("bf16", (2, 2049, 2048), None),            # TripoSG plain residual + LN (F3)
     ("f32", (3, 7, 200), (1.0, 0.1)),           # generic kernel
+    ("bf16", (1, 4099, 1024), (1.0, 0.02)),     # persistent rows: odd row count (a row past the end)
+    ("f16", (3, 1373, 1024), None),             # persistent rows: f16, no LayerScale, odd row count
 ])
 def test_residual_layer_norm(dev, ops, orc, synth, dt, shape, gamma):
     print(f"\n[case] residual_layer_norm dt={dt} shape={shape} gamma={gamma}", flush=True)
@@ -160,6 +162,49 @@ def test_residual_layer_norm(dev, ops, orc, synth, dt, shape, gamma):
     else:
         assert np.array_equal(host_view(h, dt), hw), "residual stream h must be bit-exact"
     check(y, yw, dt, "residual_layer_norm y")
+
+
+def test_residual_layer_norm_strided_rows(dev, ops, orc, synth):
+    """Row-strided x and branch views on the long-job path (rows of 1024 in
+    2048-wide buffers)."""
+    print("\n[case] residual_layer_norm strided rows bf16 [5000, 1024] of [5000, 2048]", flush=True)
+    rows, d = 5000, 1024
+    seed = synth.config_seed(1) + 31
+    xw = synth.normal(seed, rows * 2 * d).reshape(rows, 2 * d)
+    aw = synth.normal(seed + 1, rows * 2 * d).reshape(rows, 2 * d)
+    g = synth.normal(seed + 2, d, 1.0, 0.02)
+    w = synth.normal(seed + 3, d, 1.0, 0.02)
+    b = synth.normal(seed + 4, d, 0.0, 0.02)
+    xwd, awd = dev_tensor(xw, "bf16", dev), dev_tensor(aw, "bf16", dev)
+    xd, ad = xwd[:, d:], awd[:, :d]
+    h, y = ops.residual_layer_norm(xd, ad, torch.from_numpy(g).to(dev), torch.from_numpy(w).to(dev),
+                                   torch.from_numpy(b).to(dev), 1e-5)
+    sync()
+    hw, yw = orc.residual_layer_norm(host_view(xd, "bf16"), host_view(ad, "bf16"), g, w, b, 1e-5, dt=orc.BF16)
+    assert np.array_equal(host_view(h, "bf16"), hw), "residual stream h must be bit-exact"
+    check(y, yw, "bf16", "residual_layer_norm y (strided rows)")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_residual_layer_norm_persistent_equals_row_kernel(dev, ops, synth, dt):
+    """The long jobs (>= 2048 rows of 1024, 2-byte) run the persistent kernel,
+    the short ones row_kernel; both compute each row with the same element
+    mapping, arithmetic and reduction order, so a row's h and y do not depend
+    on which of them ran: the first 2000 rows of a 6001-row job, run again as
+    a job of their own, come out bit for bit the same."""
+    print(f"\n[case] residual_layer_norm persistent vs row kernel dt={dt}", flush=True)
+    rows, d, part = 6001, 1024, 2000
+    seed = synth.config_seed(1) + 57
+    x = dev_tensor(synth.normal(seed, rows * d).reshape(rows, d), dt, dev)
+    a = dev_tensor(synth.normal(seed + 1, rows * d).reshape(rows, d), dt, dev)
+    g = torch.from_numpy(synth.normal(seed + 2, d, 1.0, 0.02)).to(dev)
+    w = torch.from_numpy(synth.normal(seed + 3, d, 1.0, 0.02)).to(dev)
+    b = torch.from_numpy(synth.normal(seed + 4, d, 0.0, 0.02)).to(dev)
+    h, y = ops.residual_layer_norm(x, a, g, w, b, 1e-5)
+    h2, y2 = ops.residual_layer_norm(x[:part].contiguous(), a[:part].contiguous(), g, w, b, 1e-5)
+    sync()
+    assert torch.equal(h[:part].view(torch.int16), h2.view(torch.int16))
+    assert torch.equal(y[:part].view(torch.int16), y2.view(torch.int16))
 
 
 @pytest.mark.parametrize("dt,shape,gamma,pdt", [
