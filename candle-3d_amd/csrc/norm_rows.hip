@@ -415,26 +415,32 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(RowParams p) {
 
 // ---- persistent residual + LayerNorm (2-byte rows of 1024) ------------------
 //
-// The long F1 jobs (VGGT's [B * N, 1024] blocks in bf16 / f16). A workgroup of
-// 256 threads owns a pair of rows at a time (128 threads, one 8-element chunk
-// each, per row: the same element mapping, arithmetic and reduction order as
-// row_kernel<T, 128, 1, ROW_RESID_LN>, so the outputs are bit-identical) and
-// walks the pairs with a grid stride; the grid is two workgroups per CU.
+// The long F1 jobs (VGGT's [B * N, 1024] blocks in bf16 / f16). One
+// 256-thread workgroup per CU; each wavefront owns a row at a time (lane l:
+// the 8-element chunks at 8 l and 512 + 8 l) and walks rows with a grid
+// stride, on its own: no LDS, no barrier.
 // - γ, w and b are loaded once per thread, not once per row.
-// - The next pair's rows are loaded before this pair's arithmetic and
-//   stores, as raw bytes through buffer loads on the (wave-uniform) row
-//   address, so no per-lane address arithmetic sits between the pairs.
+// - The next row is loaded before this row's arithmetic and stores, as raw
+//   bytes through buffer loads on the (wave-uniform) row address, so no
+//   per-lane address arithmetic sits between the rows; 32-bit scalar row
+//   math (a 64-bit signed compare of scalars takes a VGPR, and the compiler
+//   took one that a pending load also wrote: a wait).
 // - Loads and stores are unconditional, so the compiler's vmcnt waits are
-//   exact: the last pair of a workgroup re-reads its own rows, and a row past
-//   the end (an odd row count) stores through a descriptor of size 0, which
-//   drops the write.
-// - Two register sets alternate (the loop is unrolled by two), so no loaded
-//   value is copied, and each pair's store data stays allocated until the
-//   next pair's loads are issued: a load into a register a pending store
-//   still reads from waits for that store.
-// configs[1] F1: 17.3 against 18.2 µs for row_kernel (same-box A/B, graph-
-// timed, cold); one or three workgroups per CU: 19.1 / 17.6 µs; loading two
-// pairs ahead: no gain.
+//   exact: a wavefront's last row re-reads its own data.
+// - Two register sets alternate (the loop is unrolled by two, the first row
+//   peeled so that the loop is entered as it is re-entered), and each row's
+//   store data stays allocated until the next row's loads are issued (an
+//   empty asm use): a load into a register that a pending store still reads
+//   from waits for that store.
+// - Statistics: each chunk is wave-summed on its own and the two totals are
+//   added, chunk 0 first: chunk c of lane l is what lane l of wavefront c
+//   holds in row_kernel<T, 128, 1, ROW_RESID_LN>, whose row total adds its
+//   two wavefronts' sums in that order, so every output is bit-identical to
+//   row_kernel's (and to the short jobs').
+// configs[1] F1: 16.8 against 17.6-17.8 µs for two-wavefront rows walked the
+// same way and 18.2 µs for row_kernel (same box, graph-timed, cold); two
+// workgroups per CU or more, 64-thread workgroups, or loading two rows
+// ahead: slower.
 template <typename T> __device__ __forceinline__ void decode8(uint4 u, float (&v)[8]) {
   const uint32_t q[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -466,86 +472,103 @@ __device__ __forceinline__ rsrc_t row_rsrc(const void *row, int bytes) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void resid_ln_persist_kernel(RowParams p, int npairs) {
-  static_assert(T::bytes == 2, "2-byte rows");
-  constexpr int TPR = 128, EB = T::bytes, NT = 2;
-  __shared__ float red_a[4], red_b[4];
-  const int t = threadIdx.x & (TPR - 1);
-  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);  // the row of the pair (wave-uniform)
-  const ChunkAt at = chunk_at<T, TPR>(0, t);
-  const int off = (int)(at.o0 * EB);
-  float g[8], w[8], b[8];
-  param_at<T>(p.g, p.g_dt, 0, at, 1.f, g);
-  param_at<T>(p.w, p.w_dt, 0, at, 1.f, w);
-  param_at<T>(p.b, p.b_dt, 0, at, 0.f, b);
+__global__ __launch_bounds__(256) void resid_ln_persist_kernel(RowParams p, int rows) {
+  static_assert(T::bytes == 2, "2-byte rows of 1024");
+  constexpr int EB = T::bytes, NT = 2;
+  const int lane = threadIdx.x & 63;
+  const int wpb = (int)(blockDim.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * wpb + (threadIdx.x >> 6)));
+  const int nw = (int)gridDim.x * wpb;
+  const ChunkAt a0 = chunk_at<T, 64>(0, lane), a1 = chunk_at<T, 64>(1, lane);
+  const int off0 = (int)(a0.o0 * EB), off1 = (int)(a1.o0 * EB);
+  float g[2][8], w[2][8], b[2][8];
+  param_at<T>(p.g, p.g_dt, 0, a0, 1.f, g[0]);
+  param_at<T>(p.g, p.g_dt, 0, a1, 1.f, g[1]);
+  param_at<T>(p.w, p.w_dt, 0, a0, 1.f, w[0]);
+  param_at<T>(p.w, p.w_dt, 0, a1, 1.f, w[1]);
+  param_at<T>(p.b, p.b_dt, 0, a0, 0.f, b[0]);
+  param_at<T>(p.b, p.b_dt, 0, a1, 0.f, b[1]);
   const float inv_d = 1.0f / (float)p.d;
   const bool has_g = p.g_dt >= 0;
   const int rbytes = (int)(p.d * EB);
   const char *xs = reinterpret_cast<const char *>(p.x), *as = reinterpret_cast<const char *>(p.a);
   char *hs = reinterpret_cast<char *>(p.h), *ys = reinterpret_cast<char *>(p.y);
-  const int rows = (int)p.rows;  // < 2^31 (the launcher checks): row math in scalar 32-bit registers
-  auto row_of = [&](int pr) -> int {
-    const int r = pr * 2 + half;
-    return r < rows ? r : rows - 1;
+  struct Raw {
+    uint4 x0, x1, a0, a1;
   };
-  auto ld = [&](const char *base, int64_t rs, int r) -> uint4 {
-    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(row_rsrc(base + (int64_t)r * rs * EB, rbytes), off, 0, NT);
+  struct Out {
+    u32x4_t h0, h1, y0, y1;
+  };
+  auto ld = [&](const rsrc_t &r, int off) -> uint4 {
+    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT);
     return make_uint4(u.x, u.y, u.z, u.w);
   };
-  // one pair: (cx, ca) hold its rows, the next pair's go into (nx, na);
-  // (phd, pyd) are the previous pair's store data, kept allocated until the
-  // loads are issued
-  const int stride = (int)gridDim.x;
-  auto pair_step = [&](int pr, const uint4 &cx, const uint4 &ca, uint4 &nx, uint4 &na, u32x4_t &hd, u32x4_t &yd,
-                       const u32x4_t &phd, const u32x4_t &pyd) {
-    const int64_t row = row_of(pr);
-    const int nr = row_of(pr + stride < npairs ? pr + stride : pr);
-    nx = ld(xs, p.x_rs, nr);
-    na = ld(as, p.a_rs, nr);
-    asm volatile("" ::"v"(phd), "v"(pyd));
-    const int live_bytes = pr * 2 + half < rows ? rbytes : 0;
-    float v[8], av[8];
-    decode8<T>(cx, v);
-    decode8<T>(ca, av);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      // LayerScale product and residual add as two roundings, as row_kernel
-      const float ls = has_g ? mul_rn(av[k], g[k]) : av[k];
-      v[k] = Chunk<T>::round_trip(add_rn(ls, v[k]));
-    }
-    hd = encode8<T>(v);
-    __builtin_amdgcn_raw_buffer_store_b128(hd, row_rsrc(hs + row * p.h_rs * EB, live_bytes), off, 0, NT);
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) s += v[k];
-    const float mean = row_total<TPR, 256>(s, red_a) * inv_d;
-    float s2 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float dv = v[k] - mean;
-      s2 += dv * dv;
-    }
-    const float var = row_total<TPR, 256>(s2, red_b) * inv_d;
-    const float rstd = 1.0f / sqrtf(var + p.eps);
-    float out[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = (v[k] - mean) * rstd * w[k] + b[k];
-    yd = encode8<T>(out);
-    __builtin_amdgcn_raw_buffer_store_b128(yd, row_rsrc(ys + row * p.y_rs * EB, live_bytes), off, 0, NT);
+  auto ldrow = [&](int r) -> Raw {
+    const rsrc_t rx = row_rsrc(xs + (int64_t)r * p.x_rs * EB, rbytes);
+    const rsrc_t ra = row_rsrc(as + (int64_t)r * p.a_rs * EB, rbytes);
+    return Raw{ld(rx, off0), ld(rx, off1), ld(ra, off0), ld(ra, off1)};
   };
-  // the first pair is peeled off the loop, so that the loop is entered, as it
-  // is re-entered, with a pair's loads and stores in flight: the compiler's
-  // waits at the loop head then hold for the steady state (with nothing but
-  // loads in flight on entry, it waited there for the previous stores too)
-  int pr = (int)blockIdx.x;
-  uint4 x0 = ld(xs, p.x_rs, row_of(pr)), a0 = ld(as, p.a_rs, row_of(pr)), x1, a1;
-  u32x4_t h0 = {}, y0 = {}, h1 = {}, y1 = {};
-  pair_step(pr, x0, a0, x1, a1, h0, y0, h1, y1);
-  for (pr += stride; pr < npairs; pr += stride) {
-    pair_step(pr, x1, a1, x0, a0, h1, y1, h0, y0);
-    pr += stride;
-    if (pr >= npairs) break;
-    pair_step(pr, x0, a0, x1, a1, h0, y0, h1, y1);
+  // one row: c holds it, the next row goes into n; po is the previous row's
+  // store data, kept allocated until the loads are issued
+  auto step = [&](int r, const Raw &c, Raw &n, Out &o, const Out &po) {
+    n = ldrow(r + nw < rows ? r + nw : r);
+    asm volatile("" ::"v"(po.h0), "v"(po.h1), "v"(po.y0), "v"(po.y1));
+    issue_fence();  // the loads stay ahead of this row's arithmetic
+    float v[2][8], av[2][8];
+    decode8<T>(c.x0, v[0]);
+    decode8<T>(c.x1, v[1]);
+    decode8<T>(c.a0, av[0]);
+    decode8<T>(c.a1, av[1]);
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        // LayerScale product and residual add as two roundings, as row_kernel
+        const float ls = has_g ? mul_rn(av[cc][k], g[cc][k]) : av[cc][k];
+        v[cc][k] = Chunk<T>::round_trip(add_rn(ls, v[cc][k]));
+      }
+    const rsrc_t rh = row_rsrc(hs + (int64_t)r * p.h_rs * EB, rbytes);
+    const rsrc_t ry = row_rsrc(ys + (int64_t)r * p.y_rs * EB, rbytes);
+    o.h0 = encode8<T>(v[0]);
+    o.h1 = encode8<T>(v[1]);
+    __builtin_amdgcn_raw_buffer_store_b128(o.h0, rh, off0, 0, NT);
+    __builtin_amdgcn_raw_buffer_store_b128(o.h1, rh, off1, 0, NT);
+    float s[2] = {0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s[cc] += v[cc][k];
+    const float mean = (wave_sum(s[0]) + wave_sum(s[1])) * inv_d;
+    float q[2] = {0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float dv = v[cc][k] - mean;
+        q[cc] += dv * dv;
+      }
+    const float var = (wave_sum(q[0]) + wave_sum(q[1])) * inv_d;
+    const float rstd = 1.0f / sqrtf(var + p.eps);
+    float out[2][8];
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) out[cc][k] = (v[cc][k] - mean) * rstd * w[cc][k] + b[cc][k];
+    o.y0 = encode8<T>(out[0]);
+    o.y1 = encode8<T>(out[1]);
+    __builtin_amdgcn_raw_buffer_store_b128(o.y0, ry, off0, 0, NT);
+    __builtin_amdgcn_raw_buffer_store_b128(o.y1, ry, off1, 0, NT);
+  };
+  int r = wv;
+  if (r >= rows) return;  // wave-uniform; no barrier follows
+  Raw c0 = ldrow(r), c1;
+  Out o0 = {}, o1 = {};
+  step(r, c0, c1, o0, o1);
+  for (r += nw; r < rows; r += nw) {
+    step(r, c1, c0, o1, o0);
+    r += nw;
+    if (r >= rows) break;
+    step(r, c0, c1, o0, o1);
   }
 }
 
@@ -653,11 +676,13 @@ hipError_t launch_typed(const RowParams &p0, bool vec, hipStream_t s) {
   }
   // the long residual + LayerNorm jobs on 2-byte rows of 1024: the persistent
   // kernel, two workgroups per CU
+  // the long residual + LayerNorm jobs on 2-byte rows of 1024: the persistent
+  // kernel, one 256-thread workgroup per CU
   if constexpr (MODE == ROW_RESID_LN && T::bytes == 2) {
     if (tpr == 128 && nc == 1 && !row_per_block && p.rows < INT32_MAX) {
-      const int64_t npairs = (p.rows + 1) / 2, cap = 2 * (int64_t)cu_count(s);
-      const int64_t grid = npairs < cap ? npairs : cap;
-      hipLaunchKernelGGL((resid_ln_persist_kernel<T>), dim3((unsigned)grid), dim3(256), 0, s, p, (int)npairs);
+      const int64_t need = (p.rows + 3) / 4, cap = cu_count(s);
+      const int64_t grid = need < cap ? need : cap;
+      hipLaunchKernelGGL((resid_ln_persist_kernel<T>), dim3((unsigned)grid), dim3(256), 0, s, p, (int)p.rows);
       return hipGetLastError();
     }
   }
