@@ -125,9 +125,11 @@ def _residual_ln(dev, cfg, shape, dt, gamma_ms, eps, name="residual_layer_norm")
     def launch(i):
         dx, da, dh, dy = D[i % n]
         _lib.call("lux3d_residual_layer_norm", dx, da, dg, dw, dbb, eps, dh, dy, _cur())
-    wl = Workload(name, cfg, "row_kernel<RESID_LN>", "bf16" if dt == torch.bfloat16 else "f32", nbytes,
-                  str(list(shape)), launch, n)
     rows = x0.numel() // d
+    # 2-byte rows of 1024 in jobs of >= 2048 rows take the persistent kernel
+    persist = esz == 2 and d == 1024 and rows >= 2048
+    wl = Workload(name, cfg, "resid_ln_persist_kernel" if persist else "row_kernel<RESID_LN>",
+                  "bf16" if dt == torch.bfloat16 else "f32", nbytes, str(list(shape)), launch, n)
     # 128 threads per row, one chunk each (d = 1024); a row per workgroup below 2048 rows
     wl.pattern = {"kind": "rows", "nin": 2, "nout": 2, "rows": rows, "row_bytes": d * esz, "eb": esz, "tpr": 128,
                   "row_per_block": rows < 2048}
