@@ -223,6 +223,23 @@ __device__ __forceinline__ void phase_finish(const HeadParams &p, int tb, int e,
   }
 }
 
+// Rotation tables (R1_TAB) issued before the head rows: the raw bits of the
+// table elements a thread stages (up to two), decoded into LDS after the
+// rows are in flight (as stage_phases would read them: C defaults to 1, S to
+// 0 for an absent table). Loaded after the rows and converted at once, their
+// wait had to wait for every row too.
+__device__ __forceinline__ uint32_t tab_raw(const void *p, int dt, int64_t i) {
+  if (dt == LUX3D_F32) return reinterpret_cast<const uint32_t *>(p)[i];
+  if (dt == LUX3D_BF16 || dt == LUX3D_F16) return reinterpret_cast<const uint16_t *>(p)[i];
+  return 0;
+}
+__device__ __forceinline__ float tab_decode(uint32_t v, int dt, float dflt) {
+  if (dt == LUX3D_F32) return __uint_as_float(v);
+  if (dt == LUX3D_BF16) return bf16_bits_to_f32(v);
+  if (dt == LUX3D_F16) return f16_bits_to_f32(v);
+  return dflt;
+}
+
 // Grid: x = tiles of `tb` consecutive tokens; y = tensor (q, k) when NTB = 1,
 // or 1 when NTB = 2 (each workgroup then handles q and k of its tokens, whose
 // rows lie side by side in a packed qkv buffer, and stages the phases once).
@@ -276,6 +293,26 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
   const int e0 = threadIdx.x;
   PhaseSrc ps{};
   if constexpr (SRC) ps = phase_issue<ROT, D>(p, tok0, tb, ntok, N, e0);
+  // R1_TAB: this thread's (up to two) table elements, issued first when the
+  // tile's tb * D elements fit two per thread (always, for the launcher's
+  // tiles); otherwise stage_phases reads them after the rows
+  constexpr bool TABE = ROT == HR_R1_TAB;
+  const bool tab_early = TABE && tb * D <= 2 * (int)blockDim.x;
+  uint32_t tcr[2] = {0u, 0u}, tsr[2] = {0u, 0u};
+  if constexpr (TABE) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int e = e0 + i * (int)blockDim.x;
+      if (e >= tb * D) e = 0;
+      const int t = e / D, j = e % D;
+      uint32_t tok = tok0 + t;
+      tok = tok < ntok ? tok : ntok - 1;
+      const uint32_t b = fdiv(tok, p.div_n_m, p.div_n_s), n = tok - b * N;
+      const int64_t off = (int64_t)b * p.tab_sB + (int64_t)n * p.tab_sN + j;
+      tcr[i] = tab_raw(p.tab_c, p.tab_dt, off);
+      tsr[i] = tab_raw(p.tab_s, p.tab_dt, off);
+    }
+  }
   issue_fence();
 
   float v[NTB][R][8];
@@ -319,6 +356,15 @@ __global__ __launch_bounds__(256) void head_kernel(HeadParams p, int tb) {
       // tiles with more angles than threads: the rest the plain way
       for (int e = e0 + (int)blockDim.x; e < tb * (D / 2); e += blockDim.x)
         phase_finish<ROT, D>(p, tb, e, phase_issue<ROT, D>(p, tok0, tb, ntok, N, e), Cs, Ss);
+    } else if (tab_early) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = e0 + i * (int)blockDim.x;
+        if (e < tb * D) {
+          Cs[e] = tab_decode(tcr[i], p.tab_dt, 1.f);
+          Ss[e] = tab_decode(tsr[i], p.tab_dt, 0.f);
+        }
+      }
     } else {
       stage_phases<ROT, D>(p, tok0, tb, ntok, N, Cs, Ss);
     }
