@@ -67,6 +67,47 @@ def test_graph_replays_match_eager(dev):
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep} differs from eager"
 
 
+def test_graph_replays_of_the_persistent_residual_layer_norm(dev):
+    """Long 2-byte jobs of rows of 1024 run the persistent residual +
+    LayerNorm kernel (its grid is sized from the device's CU count, looked up
+    on the first launch): captured and replayed, bit-identical to eager."""
+    print("\n[case] graph replay of the persistent residual_layer_norm [2, 2501, 1024] bf16", flush=True)
+    from lux3d_fused import ops, synth, _lib
+    B, N, C = 2, 2501, 1024
+    T = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dt or torch.float32)  # noqa: E731
+    x = T(synth.normal(21, B * N * C).reshape(B, N, C), torch.bfloat16)
+    a = T(synth.normal(22, B * N * C).reshape(B, N, C), torch.bfloat16)
+    g, w, b = T(synth.normal(23, C, 1.0, 0.02)), T(synth.normal(24, C, 1.0, 0.02)), T(synth.normal(25, C, 0.0, 0.02))
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+
+    def run():
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("lux3d_residual_layer_norm", ops.desc(x), ops.desc(a), ops.desc(g), ops.desc(w), ops.desc(b),
+                  1e-5, ops.desc(h), ops.desc(y), s)
+
+    run()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in (h, y)]
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        run()
+    for rep in range(4):
+        for t in (h, y):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((h, y), eager):
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {rep} differs from eager"
+
+
 def test_graph_replays_of_the_newer_entries(dev):
     """The same check for the fused gated residual + modulate, exact_sdpa_heads
     on bf16 (three-term probabilities), f32 attention (three-term splits) and
