@@ -140,6 +140,8 @@ def test_layer_norm_empty_and_errors(dev, ops):
     ("f32", (3, 7, 200), (1.0, 0.1)),           # generic kernel
     ("bf16", (1, 4099, 1024), (1.0, 0.02)),     # persistent rows: odd row count (a row past the end)
     ("f16", (3, 1373, 1024), None),             # persistent rows: f16, no LayerScale, odd row count
+    ("bf16", (1, 2048, 1024), (1.0, 0.02)),     # the first job size on the persistent kernel
+    ("bf16", (1, 65537, 1024), (1.0, 0.02)),    # 64 rows per wavefront, one more for some
 ])
 def test_residual_layer_norm(dev, ops, orc, synth, dt, shape, gamma):
     print(f"\n[case] residual_layer_norm dt={dt} shape={shape} gamma={gamma}", flush=True)
