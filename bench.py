@@ -576,11 +576,21 @@ def main():
     if args.table_out:
         with open(args.table_out, "w") as f:
             json.dump({**out, "ops": table}, f, indent=1)
-    out["ops"] = [{"op": r["op"], "us": r["us"], "frac": r["frac_peak"],
-                   **({"best_copy_us": r["best_copy_us"]} if "best_copy_us" in r else {}),
-                   **({"frac_mfma": r["frac_mfma_peak"]} if "frac_mfma_peak" in r else {})}
-                  for r in table if r["target_70pct"] or "frac_mfma_peak" in r]
-    print(json.dumps(out, separators=(",", ":")), flush=True)
+    print(headline_json(out, table), flush=True)
+
+
+def headline_json(out, table):
+    """The final stdout line the driver parses: the headline fields of `out`
+    plus one short entry per target or matrix-core op of the per-op table
+    (op, us, fraction of peak, best copy), on one line. The full table goes
+    elsewhere: with every row's ceilings, traces and CPU figures the line
+    grew to ~28 KB and no longer fit the driver's stdout tail."""
+    line = dict(out)
+    line["ops"] = [{"op": r["op"], "us": r["us"], "frac": r["frac_peak"],
+                    **({"best_copy_us": r["best_copy_us"]} if "best_copy_us" in r else {}),
+                    **({"frac_mfma": r["frac_mfma_peak"]} if "frac_mfma_peak" in r else {})}
+                   for r in table if r["target_70pct"] or "frac_mfma_peak" in r]
+    return json.dumps(line, separators=(",", ":"))
 
 
 if __name__ == "__main__":
