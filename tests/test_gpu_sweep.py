@@ -1,0 +1,185 @@
+"""GPU parity sweep over the row kernels' launch layouts: row widths that
+pick one, two or four wavefronts per row and one to eight 16-byte chunks per
+lane (and the generic fallback), row counts either side of the 2048-row
+switch between one-row workgroups and multi-row ones (and the persistent
+residual + LayerNorm kernel), and every activation dtype, for each row op
+against the oracle at the usual bars (residual streams bit-exact, bf16 / f16
+within 2 ulp, f32 within 1e-5 of the output scale; see conftest.py).
+Inputs are seeded N(0, 1) rows and N(1, 0.05) / N(0, 0.1) parameters.
+
+Rows of 8192 (wider than any config) are allowed 4e-5 instead of 1e-5 of
+their elements on the absolute floor: there the reference's single-pass
+statistics (sum2 / d - mean^2, which the oracle restates) are themselves
+that noisy near zero. Against a float64 LayerNorm of the same bf16 rows the
+oracle has 264 of 16,777,216 elements (1.6e-5) beyond 2 ulp that pass only
+through the floor at d = 8192 (46 of 4,194,304 at d = 2048); the GPU kernel
+against the oracle had 263."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+from conftest import assert_bf16_close, assert_f16_close, assert_f32_close  # noqa: E402
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops(dev):
+    from lux3d_fused import ops as _ops
+    return _ops
+
+
+@pytest.fixture(scope="module")
+def orc():
+    import lux3d_oracle as o
+    o.set_threads(16)
+    return o
+
+
+def _dev(a, dt, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).to(TDT[dt])
+
+
+def _host(t, dt):
+    t = t.detach().contiguous().cpu()
+    if dt == "f32":
+        return t.numpy()
+    if dt == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _odt(orc, dt):
+    return {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}[dt]
+
+
+def _check(got, want, dt, what, d):
+    g = _host(got, dt)
+    ff = 4e-5 if d >= 8192 else None
+    if dt == "f32":
+        return assert_f32_close(g, want, what=what, floor_frac=ff)
+    if dt == "bf16":
+        return assert_bf16_close(g, want, what=what, floor_frac=ff)
+    return assert_f16_close(g.view(np.uint16), np.asarray(want).view(np.uint16), what=what, floor_frac=ff)
+
+
+def _rows(seed, rows, d):
+    return np.random.default_rng(seed).normal(0.0, 1.0, (rows, d)).astype(np.float32)
+
+
+def _vec(seed, n, mean, std, lead=()):
+    return np.random.default_rng(seed).normal(mean, std, lead + (n,)).astype(np.float32)
+
+
+# (width, rows, dtype): 512 / 1024 / 1536 / 2048 / 3072 / 4096 / 8192 cover
+# 1-8 chunks per lane on one wavefront and 2- / 4-wavefront rows; 640 and 200
+# (chunk counts no layout divides) take the generic kernel.
+LN_CASES = [(512, 5, "bf16"), (1024, 1, "f32"), (1024, 2047, "bf16"), (1024, 2048, "f16"), (1536, 2049, "bf16"),
+            (2048, 1023, "f32"), (3072, 2050, "bf16"), (4096, 2048, "bf16"), (4096, 100, "f32"),
+            (8192, 2048, "bf16"), (8192, 7, "f16"), (640, 300, "bf16"), (200, 9, "f32")]
+
+
+@pytest.mark.parametrize("d,rows,dt", LN_CASES)
+def test_sweep_layer_norm(dev, ops, orc, d, rows, dt):
+    print(f"\n[case] sweep layer_norm d={d} rows={rows} dt={dt}", flush=True)
+    x = _dev(_rows(d * 7 + rows, rows, d), dt, dev)
+    w, b = _vec(1, d, 1.0, 0.05), _vec(2, d, 0.0, 0.1)
+    y = ops.layer_norm(x, torch.from_numpy(w).to(dev), torch.from_numpy(b).to(dev), 1e-5)
+    torch.cuda.synchronize()
+    _check(y, orc.layer_norm(_host(x, dt), w, b, 1e-5, dt=_odt(orc, dt)), dt, f"layer_norm {d}x{rows}", d)
+
+
+# 2-byte rows of 1024 from 2048 rows on take the persistent kernel (at 2051
+# rows some wavefronts take one row more than others); the rest row_kernel
+RESID_CASES = [(1024, 2048, "bf16"), (1024, 2051, "f16"), (1024, 1, "bf16"), (1024, 2047, "f32"),
+               (2048, 2049, "bf16"), (4096, 2048, "f32"), (1536, 64, "bf16"), (8192, 2049, "bf16")]
+
+
+@pytest.mark.parametrize("d,rows,dt", RESID_CASES)
+def test_sweep_residual_layer_norm(dev, ops, orc, d, rows, dt):
+    print(f"\n[case] sweep residual_layer_norm d={d} rows={rows} dt={dt}", flush=True)
+    x = _dev(_rows(d * 11 + rows, rows, d), dt, dev)
+    a = _dev(_rows(d * 13 + rows, rows, d), dt, dev)
+    g, w, b = _vec(3, d, 1.0, 0.05), _vec(4, d, 1.0, 0.05), _vec(5, d, 0.0, 0.1)
+    T = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    h, y = ops.residual_layer_norm(x, a, T(g), T(w), T(b), 1e-5)
+    torch.cuda.synchronize()
+    hw, yw = orc.residual_layer_norm(_host(x, dt), _host(a, dt), g, w, b, 1e-5, dt=_odt(orc, dt))
+    assert np.array_equal(_host(h, dt), hw), "residual stream h must be bit-exact"
+    _check(y, yw, dt, f"residual_layer_norm y {d}x{rows}", d)
+
+
+# (width, segment sizes, dtype, with the M1' output gate)
+MOD_CASES = [(2048, (2048, 2048), "bf16", False), (1536, (1000, 1, 1048), "bf16", True),
+             (1024, (350, 350), "f32", False), (4096, (1025, 1025), "f16", True),
+             (3072, (1024, 1024), "bf16", False), (8192, (1024, 1024), "bf16", False),
+             (640, (7, 9), "bf16", True)]
+
+
+def _pieces(seed, S, d, n):
+    return [_vec(seed + k, d, 0.0, 0.1, (S,)) for k in range(n)]
+
+
+@pytest.mark.parametrize("d,sizes,dt,gated", MOD_CASES)
+def test_sweep_adaln_modulate(dev, ops, orc, d, sizes, dt, gated):
+    print(f"\n[case] sweep adaln_modulate d={d} segments={sizes} dt={dt} gate={gated}", flush=True)
+    n, S = sum(sizes), len(sizes)
+    x = _dev(_rows(d * 17 + n, n, d), dt, dev)
+    sh, sc, gt = _pieces(20, S, d, 3)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    T = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    y = ops.adaln_modulate(x, T(sh), T(sc), T(gt) if gated else None, seg_offsets=T(offs), eps=1e-6)
+    torch.cuda.synchronize()
+    want = orc.adaln_modulate(_host(x, dt), offs, sh, sc, gt if gated else None, eps=1e-6, dt=_odt(orc, dt))
+    _check(y, want, dt, f"adaln_modulate {d} {sizes}", d)
+
+
+GATE_CASES = [(2048, (2048, 2048), "bf16"), (1536, (1000, 1049), "f32"), (1024, (50, 50), "bf16"),
+              (4096, (1024, 1024), "f16"), (640, (5, 6), "bf16")]
+
+
+@pytest.mark.parametrize("d,sizes,dt", GATE_CASES)
+def test_sweep_gated_residual(dev, ops, orc, d, sizes, dt):
+    print(f"\n[case] sweep gated_residual d={d} segments={sizes} dt={dt}", flush=True)
+    n, S = sum(sizes), len(sizes)
+    x = _dev(_rows(d * 19 + n, n, d), dt, dev)
+    h = _dev(_rows(d * 23 + n, n, d), dt, dev)
+    (gt,) = _pieces(30, S, d, 1)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    T = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    out = ops.gated_residual(x, h, T(gt), seg_offsets=T(offs))
+    torch.cuda.synchronize()
+    want = orc.gated_residual(_host(x, dt), _host(h, dt), offs, gt, dt=_odt(orc, dt))
+    assert np.array_equal(_host(out, dt), want), "x + h * gate must be bit-exact"
+
+
+GMOD_CASES = [(2048, (1024, 1024), "bf16", True), (1536, (1000, 1049), "bf16", True),
+              (1024, (350, 350), "f32", False), (4096, (1025, 1025), "f16", True), (640, (5, 6), "f32", True)]
+
+
+@pytest.mark.parametrize("d,sizes,dt,gated", GMOD_CASES)
+def test_sweep_gated_residual_adaln_modulate(dev, ops, orc, d, sizes, dt, gated):
+    print(f"\n[case] sweep gated_residual_adaln_modulate d={d} segments={sizes} dt={dt} gate={gated}", flush=True)
+    n, S = sum(sizes), len(sizes)
+    x = _dev(_rows(d * 29 + n, n, d), dt, dev)
+    h = _dev(_rows(d * 31 + n, n, d), dt, dev)
+    gt, sh, sc = _pieces(40, S, d, 3)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    T = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    xo, y = ops.gated_residual_adaln_modulate(x, h, T(gt) if gated else None, T(sh), T(sc), seg_offsets=T(offs),
+                                              eps=1e-6)
+    torch.cuda.synchronize()
+    xw, yw = orc.gated_residual_modulate(_host(x, dt), _host(h, dt), offs, gt if gated else None, sh, sc, eps=1e-6,
+                                         dt=_odt(orc, dt))
+    assert np.array_equal(_host(xo, dt), xw), "the residual stream x' must be bit-exact"
+    _check(y, yw, dt, f"gated_residual_adaln_modulate {d} {sizes}", d)
