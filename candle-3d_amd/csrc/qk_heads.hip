@@ -631,7 +631,12 @@ hipError_t launch_dn(int norm, int rot, const HeadParams &p0, hipStream_t s) {
   if (threads > 256) threads = 256;
   const int64_t ipp = threads / LPR;
   int64_t tb = (R * ipp) / p0.H;
-  if (tb < 1) return hipErrorInvalidValue;  // more heads than one pass holds (H*D > 2048)
+  // more heads than R passes of a workgroup hold (H * D / 8 > 256 R): the
+  // generic kernel, one wavefront per row
+  if (tb < 1) {
+    if (p0.B * p0.H * p0.N > INT32_MAX / 2) return hipErrorInvalidValue;
+    return launch_any<T>(norm, rot, p0, s);
+  }
   HeadParams p = p0;
   div_magic(p.H, p.div_h_m, p.div_h_s);
   div_magic(p.N, p.div_n_m, p.div_n_s);

@@ -183,3 +183,80 @@ def test_sweep_gated_residual_adaln_modulate(dev, ops, orc, d, sizes, dt, gated)
                                          dt=_odt(orc, dt))
     assert np.array_equal(_host(xo, dt), xw), "the residual stream x' must be bit-exact"
     _check(y, yw, dt, f"gated_residual_adaln_modulate {d} {sizes}", d)
+
+
+# ---- head kernels -------------------------------------------------------------
+#
+# The launcher fits whole heads into a workgroup pass (threads = a multiple of
+# H * D / 8 rounded to wavefronts, at most 256) and takes tb tokens per
+# workgroup; H = 1, 3, 12, 24, 48, 64 give tiles of 64 down to one token and
+# passes with dead items, and more heads than one workgroup holds (96 or 80
+# heads of 64, 80 of 128) take the generic kernel. 2-byte rows run two rows
+# per thread (four for unrotated rows of 128), f32 rows one.
+
+
+def _synth():
+    from lux3d_fused import synth as s
+    return s
+
+
+@pytest.mark.parametrize("B,ph,pw,H,dt", [(2, 5, 7, 1, "bf16"), (1, 9, 9, 3, "f32"), (2, 9, 11, 12, "bf16"),
+                                          (1, 13, 13, 24, "f16"), (1, 6, 6, 48, "bf16"), (1, 4, 5, 64, "bf16"),
+                                          (1, 3, 3, 96, "bf16"), (1, 3, 3, 80, "f32")])
+@pytest.mark.parametrize("source", ["positions", "tables"])
+def test_sweep_qk_layernorm_rope2d(dev, ops, orc, B, ph, pw, H, dt, source):
+    print(f"\n[case] sweep qk_layernorm_rope2d B={B} grid={ph}x{pw} H={H} dt={dt} source={source}", flush=True)
+    s, D = _synth(), 64
+    N = 5 + ph * pw
+    qkv = _dev(_rows(H * 37 + N, B * N * 3 * H, D).reshape(B, N, 3, H, D), dt, dev)
+    perm = qkv.permute(2, 0, 3, 1, 4)  # [3, B, H, N, D] views of the packed buffer
+    q, k = perm[0], perm[1]
+    pos = s.vggt_positions(B, ph, pw)
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)  # noqa: E731
+    qw, qb, kw, kb = _vec(51, D, 1.0, 0.05), _vec(52, D, 0.0, 0.1), _vec(53, D, 1.0, 0.05), _vec(54, D, 0.0, 0.1)
+    cos, sin = orc.rope2d_tables(pos, D, 100.0)
+    if source == "tables":
+        emb = ops.RopeEmbeddings(T(cos).unsqueeze(1), T(sin).unsqueeze(1))
+        qo, ko = ops.qk_layernorm_rope2d(q, k, (T(qw), T(qb), 1e-5), (T(kw), T(kb), 1e-5), emb)
+    else:
+        qo, ko = ops.qk_layernorm_rope2d(q, k, (T(qw), T(qb), 1e-5), (T(kw), T(kb), 1e-5), positions=T(pos),
+                                         base=100.0)
+    torch.cuda.synchronize()
+    odt = _odt(orc, dt)
+    _check(qo, orc.layernorm_rope2d(np.ascontiguousarray(_host(q, dt)), qw, qb, 1e-5, cos, sin, dt=odt), dt,
+           f"q H={H}", D)
+    _check(ko, orc.layernorm_rope2d(np.ascontiguousarray(_host(k, dt)), kw, kb, 1e-5, cos, sin, dt=odt), dt,
+           f"k H={H}", D)
+
+
+@pytest.mark.parametrize("B,L,H,D,dt", [(2, 33, 16, 128, "bf16"), (1, 70, 4, 64, "f32"), (1, 40, 24, 128, "bf16"),
+                                        (1, 10, 64, 128, "bf16"), (1, 5, 80, 128, "f16"), (3, 17, 1, 64, "bf16")])
+def test_sweep_rms_norm_heads(dev, ops, orc, B, L, H, D, dt):
+    print(f"\n[case] sweep rms_norm_heads B={B} L={L} H={H} D={D} dt={dt}", flush=True)
+    qkv = _dev(_rows(H * 41 + L, B * L * H, 3 * D).reshape(B, L, H, 3 * D), dt, dev)
+    q, k = qkv[..., 0:D].transpose(1, 2), qkv[..., D:2 * D].transpose(1, 2)  # [B, H, L, D] strided
+    wq, wk = _vec(61, D, 1.0, 0.05), _vec(62, D, 1.0, 0.05)
+    T = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    qo, ko = ops.rms_norm_heads(q, T(wq), 1e-6, k=k, k_weight=T(wk))
+    torch.cuda.synchronize()
+    odt = _odt(orc, dt)
+    _check(qo, orc.rms_norm_heads(np.ascontiguousarray(_host(q, dt)), wq, 1e-6, dt=odt), dt, f"q H={H} D={D}", D)
+    _check(ko, orc.rms_norm_heads(np.ascontiguousarray(_host(k, dt)), wk, 1e-6, dt=odt), dt, f"k H={H} D={D}", D)
+
+
+@pytest.mark.parametrize("N,H,D,dt", [(500, 12, 128, "bf16"), (300, 3, 128, "f32"), (200, 16, 64, "bf16"),
+                                      (64, 40, 128, "bf16"), (129, 1, 128, "f16")])
+def test_sweep_qk_l2norm_rope3d(dev, ops, orc, N, H, D, dt):
+    print(f"\n[case] sweep qk_l2norm_rope3d N={N} H={H} D={D} dt={dt}", flush=True)
+    coords = _synth().unique_voxels(71 + N, N, 64)
+    qkv = _dev(_rows(H * 43 + N, N * 3 * H, D).reshape(1, N, 3, H, D), dt, dev)
+    q, k = qkv[:, :, 0], qkv[:, :, 1]  # [1, N, H, D] views
+    gq, gk = _vec(63, D, 1.0, 0.05, (H,)), _vec(64, D, 1.0, 0.05, (H,))
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)  # noqa: E731
+    qo, ko = ops.qk_l2norm_rope3d(q, k, T(gq), T(gk), coords=T(coords))
+    torch.cuda.synchronize()
+    cos, sin = orc.rope3d_tables(coords, D)
+    odt = _odt(orc, dt)
+    for got, x, g, what in ((qo, q, gq, "q"), (ko, k, gk, "k")):
+        want = orc.qk_l2norm_rope3d(np.ascontiguousarray(_host(x, dt)).reshape(N, H, D), g, cos, sin, dt=odt)
+        _check(got, want.reshape(1, N, H, D), dt, f"{what} H={H} D={D}", D)
