@@ -260,3 +260,24 @@ def test_sweep_qk_l2norm_rope3d(dev, ops, orc, N, H, D, dt):
     for got, x, g, what in ((qo, q, gq, "q"), (ko, k, gk, "k")):
         want = orc.qk_l2norm_rope3d(np.ascontiguousarray(_host(x, dt)).reshape(N, H, D), g, cos, sin, dt=odt)
         _check(got, want.reshape(1, N, H, D), dt, f"{what} H={H} D={D}", D)
+
+
+# ---- activations: sizes around the 8-element chunk and unaligned starts -------
+#
+# A 16-byte aligned start takes the vector kernel (8 elements per thread and a
+# tail); any other start the element-wise one.
+
+
+@pytest.mark.parametrize("act", ["gelu_tanh", "gelu_erf", "silu"])
+@pytest.mark.parametrize("dt,n,offset", [("bf16", 1, 0), ("f32", 7, 0), ("f16", 9, 0), ("bf16", 17, 1),
+                                         ("f32", 1000003, 3), ("bf16", 65536, 5), ("f16", 4096, 8)])
+def test_sweep_activations(dev, ops, orc, act, dt, n, offset):
+    print(f"\n[case] sweep {act} dt={dt} n={n} offset={offset}", flush=True)
+    x = np.random.default_rng(n + offset).normal(0.0, 3.0, n + offset).astype(np.float32)
+    x[offset:offset + min(n, 6)] = [0.0, -0.0, -9.0, 9.0, -30.0, 30.0][:min(n, 6)]
+    xd = _dev(x, dt, dev)[offset:]  # a contiguous view starting `offset` elements in
+    fn = {"gelu_tanh": ops.gelu, "gelu_erf": ops.gelu_erf, "silu": ops.silu}[act]
+    y = fn(xd)
+    torch.cuda.synchronize()
+    ofn = {"gelu_tanh": orc.gelu_tanh, "gelu_erf": orc.gelu_erf, "silu": orc.silu}[act]
+    _check(y, ofn(np.ascontiguousarray(_host(xd, dt)), dt=_odt(orc, dt)), dt, f"{act} n={n} offset={offset}", 0)
