@@ -281,3 +281,27 @@ def test_sweep_activations(dev, ops, orc, act, dt, n, offset):
     torch.cuda.synchronize()
     ofn = {"gelu_tanh": orc.gelu_tanh, "gelu_erf": orc.gelu_erf, "silu": orc.silu}[act]
     _check(y, ofn(np.ascontiguousarray(_host(xd, dt)), dt=_odt(orc, dt)), dt, f"{act} n={n} offset={offset}", 0)
+
+
+# ---- Q8_0 dequant: block counts around the staging tile, 2-byte aligned blocks --
+#
+# GGUF places a tensor's blocks at 2-byte alignment: a block buffer that is
+# not 16-byte aligned reads its blocks with 2-byte loads, an aligned one
+# stages them through LDS in tiles of blocks; every output bit-exact.
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("nblocks,offset", [(1, 0), (3, 2), (63, 0), (64, 2), (65, 0), (1001, 2), (100003, 0)])
+def test_sweep_dequant_q8_0(dev, ops, orc, out, nblocks, offset):
+    print(f"\n[case] sweep dequant_q8_0 nblocks={nblocks} offset={offset} -> {out}", flush=True)
+    blocks = _synth().q8_0_blocks(900 + nblocks, nblocks)
+    buf = torch.zeros(offset + blocks.size, dtype=torch.uint8, device=dev)
+    buf[offset:] = torch.from_numpy(blocks).to(dev)
+    y = ops.dequantize_q8_0(buf[offset:], (nblocks * 32,), TDT[out])
+    torch.cuda.synchronize()
+    want = orc.dequant_q8_0(blocks, _odt(orc, out))
+    got = _host(y, out).reshape(-1)
+    if out == "f32":
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.array_equal(got.view(np.uint16), np.asarray(want).view(np.uint16))
