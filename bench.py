@@ -358,7 +358,7 @@ def cpu_baselines(runs):
         print(f"[cpu] {tag}: {out[tag]['gbs']} GB/s on {threads} threads, {out[tag]['gbs_1thread']} on 1",
               file=sys.stderr, flush=True)
     facts = {"os_cpu_count": nproc, "affinity_cpus": avail, "threads_used": threads,
-             "what": "C restatement of candle's CPU path (oracle/lux3d_oracle.c, gcc -O2), rows split over "
+             "what": "C restatement of candle's CPU path (oracle/lux3d_oracle.c, gcc -O3 -march=x86-64-v3), rows split over "
                      "threads like candle's rayon-over-rows; candle itself is not buildable here",
              "statistic": f"median of {runs} runs after 3 warm-ups, per thread count"}
     return out, facts

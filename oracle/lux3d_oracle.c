@@ -2,7 +2,8 @@
  * lux3d_oracle.c -- CPU restatement of candle-3d's fused transformer-layer op
  * arithmetic. TEST INFRASTRUCTURE ONLY (the checker; see lux3d_oracle.h).
  *
- * Build: gcc -O2 -ffp-contract=off -fPIC -shared -pthread (oracle/Makefile).
+ * Build: gcc -O3 -march=x86-64-v3 -ffp-contract=off -fno-fast-math -fPIC -shared -pthread
+ * (oracle/Makefile).
  * -ffp-contract=off keeps every a*b+c as two IEEE roundings, which is what the
  * reference's Rust (which never contracts) computes.
  *
