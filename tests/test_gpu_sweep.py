@@ -305,3 +305,44 @@ def test_sweep_dequant_q8_0(dev, ops, orc, out, nblocks, offset):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     else:
         assert np.array_equal(got.view(np.uint16), np.asarray(want).view(np.uint16))
+
+
+# ---- attention at key-block boundaries on the key-group path ------------------
+#
+# Short launches (few 128-query tiles) split each 64-key block over two key
+# groups of a workgroup (D 64); these cases put Lk just below, at and above
+# the block and group sizes, with 1, 31, 64, 129 and 257 queries, through
+# lux3d_sdpa (bf16 / f16, the rounded-probability bound of the attention
+# tests) and exact_sdpa_heads (bf16 in, f32 arithmetic, the f32 bar).
+
+_ATTN_CASES = [(1, 63, 64, "bf16"), (31, 64, 64, "bf16"), (129, 65, 64, "bf16"), (1, 127, 64, "bf16"),
+               (31, 128, 64, "bf16"), (129, 129, 64, "bf16"), (129, 192, 64, "bf16"), (257, 1029, 64, "bf16"),
+               (33, 65, 64, "f16"), (64, 128, 64, "f16"), (31, 65, 128, "bf16"), (129, 127, 128, "bf16")]
+
+
+def _attn_inputs(dev, lq, lk, d, dt):
+    g = torch.Generator(device="cpu").manual_seed(lq * 131 + lk * 7 + d)
+    q = torch.randn((1, 3, lq, d), generator=g).to(dev).to(TDT[dt])
+    k = (2 * torch.randn((1, 3, lk, d), generator=g)).to(dev).to(TDT[dt])
+    v = torch.randn((1, 3, lk, d), generator=g).to(dev).to(TDT[dt])
+    return q, k, v
+
+
+@pytest.mark.parametrize("lq,lk,d,dt", _ATTN_CASES)
+def test_sweep_sdpa_key_blocks(dev, ops, orc, lq, lk, d, dt):
+    from test_gpu_attention import assert_attn_close, oracle
+    print(f"\n[case] sweep sdpa lq={lq} lk={lk} d={d} dt={dt}", flush=True)
+    q, k, v = _attn_inputs(dev, lq, lk, d, dt)
+    scale = 1.0 / np.sqrt(d)
+    out = ops.sdpa(q, k, v, scale)
+    torch.cuda.synchronize()
+    want, wabs = oracle(orc, q, k, v, scale, dt)
+    assert_attn_close(out, want, wabs, dt, True, f"sdpa {lq}x{lk}x{d} {dt}")
+
+
+@pytest.mark.parametrize("lq,lk,d", [(c[0], c[1], c[2]) for c in _ATTN_CASES if c[3] == "bf16"])
+def test_sweep_exact_sdpa_heads_key_blocks(dev, ops, orc, lq, lk, d):
+    from test_gpu_sdpa_heads_f32 import _check as check_exact
+    print(f"\n[case] sweep exact_sdpa_heads lq={lq} lk={lk} d={d}", flush=True)
+    q, k, v = _attn_inputs(dev, lq, lk, d, "bf16")
+    check_exact(ops, orc, q, k, v, 1.0 / np.sqrt(d), "bf16", f"exact_sdpa_heads {lq}x{lk}x{d}")
