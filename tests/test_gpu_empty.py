@@ -1,10 +1,11 @@
-"""Empty inputs through the C ABI: zero rows, zero tokens, zero elements and
-zero Q8_0 blocks. candle's ops return empty tensors for them (an empty
-`Tensor` flows through `layer_norm`, `rope`, `gelu`, `dequantize` with no
-work done); every entry point here must accept them, launch nothing and
-return LUX3D_OK, so that the stream stays clean for the next call. Each
-test ends with a synchronize (which raises on a stream error) and one
-non-empty call of the same entry point checked against the oracle."""
+"""Empty inputs through the C ABI: zero rows, zero tokens, zero elements,
+zero Q8_0 blocks, no queries and no voxels. candle's ops return empty
+tensors for them (an empty `Tensor` flows through `layer_norm`, `rope`,
+`gelu`, `dequantize` with no work done); every entry point here must accept
+them, launch no work over the empty input (sparse_neighbors still clears its
+hash table) and return LUX3D_OK, so that the stream stays clean for the next
+call. Each test ends with a synchronize (which raises on a stream error) and
+one non-empty call checked against the oracle."""
 import numpy as np
 import pytest
 
@@ -139,3 +140,25 @@ def test_empty_pointwise(dev, ops, orc, dt):
     torch.cuda.synchronize()
     want = orc.dequant_q8_0(raw.reshape(-1), out_dt=orc.F32).reshape(nb, 32)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_empty_next_rows(dev, ops, orc):
+    print("\n[case] empty: sdpa (no queries), q8_0_linear / q8_0_linear_int8 (no rows), sparse_neighbors "
+          "(no voxels)", flush=True)
+    q0 = torch.empty((1, 4, 0, 64), dtype=torch.bfloat16, device=dev)
+    kv = torch.zeros((1, 4, 10, 64), dtype=torch.bfloat16, device=dev)
+    assert ops.sdpa(q0, kv, kv, 0.125).shape == (1, 4, 0, 64)
+    n, k = 32, 64
+    raw = np.random.default_rng(6).integers(0, 256, (n * k // 32, 34), dtype=np.uint8)
+    raw[:, 0:2] = np.frombuffer(np.full(n * k // 32, 0.02, np.float16).tobytes(), np.uint8).reshape(-1, 2)
+    qs, scales = ops.q8_0_repack(torch.from_numpy(raw.reshape(-1)).to(dev), n, k)
+    assert ops.q8_0_linear(torch.empty((0, k), dtype=torch.bfloat16, device=dev), qs, scales).shape == (0, n)
+    assert ops.q8_0_linear_int8(torch.empty((0, k), dtype=torch.float32, device=dev), qs, scales).shape == (0, n)
+    assert ops.sparse_neighbors(torch.empty((0, 3), dtype=torch.int32, device=dev)).shape == (0, 27)
+    torch.cuda.synchronize()
+    # the next non-empty call on the same stream: neighbour indices, exact
+    g = np.stack(np.meshgrid(np.arange(3), np.arange(3), np.arange(4), indexing="ij"), -1).reshape(-1, 3)
+    c = np.ascontiguousarray(g[::-1], dtype=np.int32)  # 36 distinct voxels, not in scan order
+    nbr = ops.sparse_neighbors(torch.from_numpy(c).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(nbr.cpu().numpy(), orc.sparse_neighbors(c))
